@@ -1,0 +1,82 @@
+"""Drop-in for the reference extension module ``flexkv.c_ext`` (transfer path).
+
+``transfer_kv_blocks`` keeps the reference's 15 positional arguments
+(csrc/bindings.cpp:25-32, bound without keywords at :108-109) and semantics:
+it unpacks the tensors into raw pointers, runs on the *current* torch stream
+(bindings.cpp:44), returns after that stream has drained (transfer.cu:131),
+and raises RuntimeError on failure (bindings.cpp:51-54).  The work is done by
+the HIP C-ABI entry ``fkv_transfer_kv_blocks``.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+__all__ = ["transfer_kv_blocks"]
+
+
+def _require_int64_host(t: torch.Tensor, name: str) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.dtype != torch.int64:
+        raise TypeError(f"{name} must be int64, got {t.dtype}")
+    if t.device.type != "cpu":
+        raise RuntimeError(f"{name} must be a host tensor (pinned), got device {t.device}")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+
+
+def transfer_kv_blocks(gpu_block_id_tensor: torch.Tensor,
+                       gpu_layer_ptrs_tensor: torch.Tensor,
+                       gpu_kv_stride_in_bytes: int,
+                       gpu_block_stride_in_bytes: int,
+                       cpu_block_id_tensor: torch.Tensor,
+                       cpu_tensor: torch.Tensor,
+                       cpu_kv_stride_in_bytes: int,
+                       cpu_layer_stride_in_bytes: int,
+                       cpu_block_stride_in_bytes: int,
+                       chunk_size_in_bytes: int,
+                       start_layer_id: int,
+                       transfer_sms: int = -1,
+                       is_host_to_device: bool = True,
+                       use_ce_transfer=False,
+                       is_mla: bool = False) -> None:
+    """Copy KV blocks between the per-layer GPU cache and the host cache.
+
+    ``use_ce_transfer``: False -> zero-copy wavefront kernel; True -> copy
+    engines behind an on-device gather/scatter through staging; the integer 2
+    selects the reference's one-DMA-per-chunk loop (csrc/transfer.cu:97-121).
+    ``transfer_sms`` bounds the compute units of the zero-copy kernel
+    (-1 = automatic).
+    """
+    _require_int64_host(gpu_block_id_tensor, "gpu_block_id_tensor")
+    _require_int64_host(cpu_block_id_tensor, "cpu_block_id_tensor")
+    _require_int64_host(gpu_layer_ptrs_tensor, "gpu_layer_ptrs_tensor")
+    if not isinstance(cpu_tensor, torch.Tensor):
+        raise TypeError(f"cpu_tensor must be a torch.Tensor, got {type(cpu_tensor).__name__}")
+    num_blocks = gpu_block_id_tensor.numel()          # bindings.cpp:33
+    num_layers = gpu_layer_ptrs_tensor.numel()        # bindings.cpp:34
+    if cpu_block_id_tensor.numel() != num_blocks:
+        raise RuntimeError(
+            f"gpu_block_id_tensor has {num_blocks} ids but cpu_block_id_tensor has "
+            f"{cpu_block_id_tensor.numel()}")
+    if isinstance(use_ce_transfer, bool):
+        mode = _lib.FKV_XFER_CE if use_ce_transfer else _lib.FKV_XFER_KERNEL
+    else:
+        mode = int(use_ce_transfer)
+    if not torch.cuda.is_available():
+        raise RuntimeError("transfer_kv_blocks needs a HIP device; none is visible")
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = lib.fkv_transfer_kv_blocks(
+        int(num_blocks), int(start_layer_id), int(num_layers),
+        gpu_block_id_tensor.data_ptr(), gpu_layer_ptrs_tensor.data_ptr(),
+        int(gpu_kv_stride_in_bytes), int(gpu_block_stride_in_bytes),
+        cpu_block_id_tensor.data_ptr(), cpu_tensor.data_ptr(),
+        int(cpu_kv_stride_in_bytes), int(cpu_layer_stride_in_bytes),
+        int(cpu_block_stride_in_bytes), 0, int(chunk_size_in_bytes),
+        stream, int(transfer_sms), 1 if is_host_to_device else 0, mode,
+        1 if is_mla else 0)
+    if rc != 0:
+        raise RuntimeError(_lib.last_error() or f"fkv_transfer_kv_blocks failed ({rc})")

@@ -1,0 +1,865 @@
+// kv_transfer.hip - GPU<->CPU KV-block transfer for MI355X (gfx950).
+//
+// One kernel template moves "chunks": the (layer, K|V, block) pieces of the
+// KV cache, each `chunk_size` contiguous bytes on both sides
+// (csrc/transfer.cu:39-53 gives the reference addressing).  It is used twice:
+//   * zero-copy mode: the "CPU side" is the pinned host cache itself and the
+//     kernel's 16-byte loads/stores travel over PCIe;
+//   * copy-engine mode: the "CPU side" is a contiguous HBM staging buffer laid
+//     out [block][layer][K|V][chunk]; the DMA engines then move maximal
+//     contiguous host runs between staging and the host cache.
+//
+// Work decomposition: a workgroup (4 wavefronts) owns a tile of consecutive
+// blocks; it stages the tile's (gpu_id, cpu_id) pairs in LDS, then its
+// wavefronts stream the tile's rows (64 lanes x 16 B = 1 KiB) in groups of
+// kUnroll rows, issuing all loads of a group before any store.  Rows are
+// ordered block -> layer -> K|V -> offset, which is host-address order for the
+// block-wise host layout.  Layer base pointers travel in the kernel argument
+// block (scalar loads, no PCIe round trip per chunk).
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "flexkv_hip.h"
+
+namespace {
+
+constexpr int kThreads = 256;               // 4 wavefronts of 64 lanes
+constexpr int kWaves = kThreads / 64;
+constexpr int kUnroll = 8;                  // rows in flight per wavefront
+constexpr int kMaxLayersPerLaunch = 128;    // layer pointers in kernel args
+constexpr int kMaxTileBlocks = 64;
+constexpr int kMaxDevices = 64;
+constexpr size_t kDefaultStagingBytes = size_t(256) << 20;
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+// Every address the kernel touches is global memory (HBM or mapped pinned
+// host memory); saying so lets the compiler emit global_* instead of flat_*.
+typedef __attribute__((address_space(1))) u32x4 gvec;
+
+struct CopyArgs {
+  const int64_t* ids;        // device-visible (gpu_id, cpu_id) pairs
+  char* cpu_base;            // CPU side incl. start layer and start offset
+  int64_t gpu_kv_stride;
+  int64_t gpu_block_stride;
+  int64_t cpu_kv_stride;
+  int64_t cpu_layer_stride;
+  int64_t cpu_block_stride;
+  int64_t chunk_vec;         // 16-byte vectors per chunk
+  int32_t rows_per_chunk;    // ceil(chunk_vec / 64)
+  int32_t num_blocks;
+  int32_t num_layers;        // layers in this launch (<= kMaxLayersPerLaunch)
+  int32_t kv_dim;
+  int32_t tile_blocks;
+  int32_t num_tiles;
+  uint64_t layer_ptr[kMaxLayersPerLaunch];
+};
+
+// kH2D: copy CPU side -> GPU side.  kIotaCpu: the CPU side is staging and
+// block i of the launch sits at CPU-side block index i (ids[2i+1] unused).
+template <bool kH2D, bool kIotaCpu>
+__global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
+  __shared__ int64_t s_gid[kMaxTileBlocks];
+  __shared__ int64_t s_cid[kMaxTileBlocks];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t kv = static_cast<uint32_t>(a.kv_dim);
+  const uint32_t rpc = static_cast<uint32_t>(a.rows_per_chunk);
+  const uint32_t items_per_block = static_cast<uint32_t>(a.num_layers) * kv;
+
+  for (int tile = blockIdx.x; tile < a.num_tiles; tile += gridDim.x) {
+    const int b0 = tile * a.tile_blocks;
+    const int nb = min(a.tile_blocks, a.num_blocks - b0);
+    __syncthreads();  // previous tile's readers are done with the LDS ids
+    if (threadIdx.x < nb) {
+      const int64_t* pr = a.ids + 2 * static_cast<int64_t>(b0 + threadIdx.x);
+      s_gid[threadIdx.x] = pr[0];
+      s_cid[threadIdx.x] = kIotaCpu ? static_cast<int64_t>(b0 + threadIdx.x) : pr[1];
+    }
+    __syncthreads();
+
+    const uint32_t rows = static_cast<uint32_t>(nb) * items_per_block * rpc;
+    for (uint32_t g = static_cast<uint32_t>(wave) * kUnroll; g < rows;
+         g += kWaves * kUnroll) {
+      // Decompose the group's first row once; later rows advance a cursor.
+      uint32_t item = g / rpc;
+      uint32_t rr = g - item * rpc;
+      uint32_t bi = item / items_per_block;
+      uint32_t rem = item - bi * items_per_block;
+      uint32_t l = rem / kv;
+      uint32_t k = rem - l * kv;
+
+      const char* src[kUnroll];
+      char* dst[kUnroll];
+      bool live[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t vec = static_cast<int64_t>(rr) * 64 + lane;
+        live[u] = (g + u < rows) && (vec < a.chunk_vec);
+        const uint32_t bsafe = min(bi, static_cast<uint32_t>(nb - 1));
+        char* gpu = reinterpret_cast<char*>(a.layer_ptr[min(l, items_per_block / kv - 1)]) +
+                    static_cast<int64_t>(k) * a.gpu_kv_stride +
+                    s_gid[bsafe] * a.gpu_block_stride + vec * 16;
+        char* cpu = a.cpu_base + static_cast<int64_t>(l) * a.cpu_layer_stride +
+                    static_cast<int64_t>(k) * a.cpu_kv_stride +
+                    s_cid[bsafe] * a.cpu_block_stride + vec * 16;
+        src[u] = kH2D ? cpu : gpu;
+        dst[u] = kH2D ? gpu : cpu;
+        // advance the cursor by one row
+        if (++rr == rpc) {
+          rr = 0;
+          if (++k == kv) {
+            k = 0;
+            if (++l == items_per_block / kv) {
+              l = 0;
+              ++bi;
+            }
+          }
+        }
+      }
+      u32x4 v[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (live[u]) v[u] = __builtin_nontemporal_load((const gvec*)src[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (live[u]) __builtin_nontemporal_store(v[u], (gvec*)dst[u]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Errors
+
+thread_local std::string t_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  t_err = buf;
+  return code;
+}
+
+#define FKV_HIP(call)                                                          \
+  do {                                                                         \
+    hipError_t e_ = (call);                                                    \
+    if (e_ != hipSuccess) {                                                    \
+      return fail(static_cast<int>(e_), "%s failed: %s (%s:%d)", #call,        \
+                  hipGetErrorString(e_), __FILE__, __LINE__);                  \
+    }                                                                          \
+  } while (0)
+
+constexpr int kInval = static_cast<int>(hipErrorInvalidValue);
+
+// ---------------------------------------------------------------------------
+// Pointer classification and bounds
+
+struct PtrInfo {
+  bool host = false;     // pinned host memory
+  bool device = false;   // device memory
+  char* dev_ptr = nullptr;  // device-visible address of the queried pointer
+  char* base = nullptr;     // allocation start (host address space)
+  size_t size = 0;          // allocation size
+};
+
+// Returns 0 and fills `out` if p lies in memory known to the HIP runtime.
+int query_ptr(const void* p, PtrInfo* out) {
+  hipPointerAttribute_t at;
+  memset(&at, 0, sizeof(at));
+  hipError_t e = hipPointerGetAttributes(&at, p);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return kInval;
+  }
+  if (at.type == hipMemoryTypeHost) {
+    out->host = true;
+    void* dp = nullptr;
+    if (hipHostGetDevicePointer(&dp, const_cast<void*>(p), 0) != hipSuccess || dp == nullptr) {
+      (void)hipGetLastError();
+      return kInval;
+    }
+    out->dev_ptr = static_cast<char*>(dp);
+  } else if (at.type == hipMemoryTypeDevice) {
+    out->device = true;
+    out->dev_ptr = static_cast<char*>(const_cast<void*>(p));
+  } else {
+    return kInval;
+  }
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  e = hipMemGetAddressRange(&base, &size, const_cast<void*>(p));
+  if (e != hipSuccess || base == nullptr) {
+    (void)hipGetLastError();
+    return kInval;
+  }
+  out->base = static_cast<char*>(base);
+  out->size = size;
+  return 0;
+}
+
+// [p + lo, p + hi) must lie inside the allocation described by info.
+bool range_inside(const char* p, __int128 lo, __int128 hi, const PtrInfo& info) {
+  const __int128 start = static_cast<__int128>(reinterpret_cast<uintptr_t>(p)) + lo;
+  const __int128 end = static_cast<__int128>(reinterpret_cast<uintptr_t>(p)) + hi;
+  const __int128 a0 = static_cast<__int128>(reinterpret_cast<uintptr_t>(info.base));
+  const __int128 a1 = a0 + static_cast<__int128>(info.size);
+  return lo <= hi && start >= a0 && end <= a1;
+}
+
+// ---------------------------------------------------------------------------
+// Per-device state: staging buffer, side stream, events, occupancy.
+
+struct DeviceState {
+  std::mutex mu;            // serialises copy-engine transfers on the device
+  bool init = false;
+  int num_cus = 0;
+  int occ_zero_copy[2] = {0, 0};
+  int occ_staged[2] = {0, 0};
+  char* staging = nullptr;
+  size_t staging_bytes = 0;
+  hipStream_t side = nullptr;
+  hipEvent_t ev_fill[2] = {nullptr, nullptr};   // staging half filled
+  hipEvent_t ev_drain[2] = {nullptr, nullptr};  // staging half consumed
+};
+
+DeviceState g_dev[kMaxDevices];
+std::mutex g_init_mu;
+std::atomic<size_t> g_staging_request{0};
+
+// Profiling
+std::atomic<bool> g_prof_on{false};
+std::mutex g_prof_mu;
+fkv_profile g_prof{};
+
+template <bool H, bool I>
+void* kernel_ptr() {
+  return reinterpret_cast<void*>(&kv_chunk_copy_kernel<H, I>);
+}
+
+int ensure_device_basics(int dev) {
+  DeviceState& d = g_dev[dev];
+  std::lock_guard<std::mutex> lk(g_init_mu);
+  if (d.init) return 0;
+  FKV_HIP(hipDeviceGetAttribute(&d.num_cus, hipDeviceAttributeMultiprocessorCount, dev));
+  int o = 0;
+  FKV_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, kernel_ptr<false, false>(), kThreads, 0));
+  d.occ_zero_copy[0] = std::max(1, o);
+  FKV_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, kernel_ptr<true, false>(), kThreads, 0));
+  d.occ_zero_copy[1] = std::max(1, o);
+  FKV_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, kernel_ptr<false, true>(), kThreads, 0));
+  d.occ_staged[0] = std::max(1, o);
+  FKV_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, kernel_ptr<true, true>(), kThreads, 0));
+  d.occ_staged[1] = std::max(1, o);
+  d.init = true;
+  return 0;
+}
+
+struct DeviceGuard {
+  int prev = -1;
+  bool changed = false;
+  int set(int dev) {
+    FKV_HIP(hipGetDevice(&prev));
+    if (prev != dev) {
+      FKV_HIP(hipSetDevice(dev));
+      changed = true;
+    }
+    return 0;
+  }
+  ~DeviceGuard() {
+    if (changed) (void)hipSetDevice(prev);
+  }
+};
+
+// Thread-local pinned buffer holding the packed (gpu_id, cpu_id) pairs the
+// kernels read.  Calls are synchronous, so the previous call's kernels have
+// finished before the buffer is rewritten or regrown.  Buffers are not freed
+// at thread exit (the runtime may already be gone at process exit).
+struct PinnedIds {
+  int64_t* p = nullptr;
+  char* dev = nullptr;
+  size_t cap = 0;  // bytes
+};
+thread_local PinnedIds t_ids;
+
+int pinned_ids(size_t bytes, int64_t** host, char** dev) {
+  if (bytes > t_ids.cap) {
+    if (t_ids.p) FKV_HIP(hipHostFree(t_ids.p));
+    t_ids.p = nullptr;
+    t_ids.cap = 0;
+    size_t cap = std::max<size_t>(bytes, 64 << 10);
+    void* p = nullptr;
+    FKV_HIP(hipHostMalloc(&p, cap, hipHostMallocPortable | hipHostMallocMapped | hipHostMallocCoherent));
+    void* dp = nullptr;
+    FKV_HIP(hipHostGetDevicePointer(&dp, p, 0));
+    t_ids.p = static_cast<int64_t*>(p);
+    t_ids.dev = static_cast<char*>(dp);
+    t_ids.cap = cap;
+  }
+  *host = t_ids.p;
+  *dev = t_ids.dev;
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Geometry validated on the host before anything is launched.
+
+struct Geometry {
+  int num_blocks, start_layer, num_layers, kv;
+  const int64_t* gids;
+  const int64_t* cids;
+  void* const* layer_ptrs;
+  int64_t gks, gbs, cks, cls, cbs, startoff, chunk;
+  char* cpu_ptr;
+  PtrInfo cpu_info;
+  int64_t min_gid, max_gid, min_cid, max_cid;
+};
+
+int validate(Geometry& g, int mode) {
+  if (g.num_blocks < 0 || g.num_layers < 0 || g.start_layer < 0)
+    return fail(kInval, "negative count: num_blocks=%d num_layers=%d start_layer_id=%d",
+                g.num_blocks, g.num_layers, g.start_layer);
+  if (!g.gids || !g.cids || !g.layer_ptrs || !g.cpu_ptr)
+    return fail(kInval, "null pointer argument");
+  if (g.chunk <= 0) return fail(kInval, "chunk_size_in_bytes must be positive, got %lld", (long long)g.chunk);
+  if (g.gks < 0 || g.gbs < 0 || g.cks < 0 || g.cls < 0 || g.cbs < 0 || g.startoff < 0)
+    return fail(kInval, "strides and cpu_startoff_inside_chunks must be non-negative");
+  const bool vec_mode = (mode == FKV_XFER_KERNEL || mode == FKV_XFER_CE);
+  if (vec_mode) {
+    const int64_t vals[] = {g.chunk, g.gks, g.gbs, g.cks, g.cls, g.cbs, g.startoff};
+    for (int64_t v : vals)
+      if (v % 16 != 0)
+        return fail(kInval,
+                    "kernel/CE transfer needs chunk size, strides and start offset in "
+                    "multiples of 16 bytes (chunk=%lld gkv=%lld gblk=%lld ckv=%lld "
+                    "clayer=%lld cblk=%lld startoff=%lld)",
+                    (long long)g.chunk, (long long)g.gks, (long long)g.gbs, (long long)g.cks,
+                    (long long)g.cls, (long long)g.cbs, (long long)g.startoff);
+    if (reinterpret_cast<uintptr_t>(g.cpu_ptr) % 16 != 0)
+      return fail(kInval, "cpu_ptr is not 16-byte aligned");
+  }
+  // Host must be able to read ids and the layer table.
+  g.min_gid = g.min_cid = INT64_MAX;
+  g.max_gid = g.max_cid = -1;
+  for (int i = 0; i < g.num_blocks; ++i) {
+    const int64_t a = g.gids[i], b = g.cids[i];
+    if (a < 0 || b < 0)
+      return fail(kInval, "negative block id at position %d (gpu %lld, cpu %lld)", i,
+                  (long long)a, (long long)b);
+    g.min_gid = std::min(g.min_gid, a);
+    g.max_gid = std::max(g.max_gid, a);
+    g.min_cid = std::min(g.min_cid, b);
+    g.max_cid = std::max(g.max_cid, b);
+  }
+  if (query_ptr(g.cpu_ptr, &g.cpu_info) != 0)
+    return fail(kInval, "cpu_ptr %p is not pinned host or device memory known to HIP "
+                "(allocate the host cache with fkv_host_alloc / pin_memory=True)", g.cpu_ptr);
+  const __int128 lo = static_cast<__int128>(g.start_layer) * g.cls +
+                      static_cast<__int128>(g.min_cid) * g.cbs + g.startoff;
+  const __int128 hi = static_cast<__int128>(g.start_layer + g.num_layers - 1) * g.cls +
+                      static_cast<__int128>(g.kv - 1) * g.cks +
+                      static_cast<__int128>(g.max_cid) * g.cbs + g.startoff + g.chunk;
+  if (!range_inside(g.cpu_ptr, lo, hi, g.cpu_info))
+    return fail(kInval,
+                "cpu block ids [%lld, %lld] with layers [%d, %d) address bytes outside the "
+                "host cache allocation (%zu bytes)",
+                (long long)g.min_cid, (long long)g.max_cid, g.start_layer,
+                g.start_layer + g.num_layers, g.cpu_info.size);
+  const __int128 glo = static_cast<__int128>(g.min_gid) * g.gbs;
+  const __int128 ghi = static_cast<__int128>(g.kv - 1) * g.gks +
+                       static_cast<__int128>(g.max_gid) * g.gbs + g.chunk;
+  // Layer tables usually repeat one allocation per layer; query each pointer.
+  for (int l = 0; l < g.num_layers; ++l) {
+    const char* p = static_cast<const char*>(g.layer_ptrs[l]);
+    if (!p) return fail(kInval, "gpu layer pointer %d is null", l);
+    if (vec_mode && reinterpret_cast<uintptr_t>(p) % 16 != 0)
+      return fail(kInval, "gpu layer pointer %d is not 16-byte aligned", l);
+    PtrInfo pi;
+    if (query_ptr(p, &pi) != 0 || !pi.device)
+      return fail(kInval, "gpu layer pointer %d (%p) is not device memory", l, p);
+    if (!range_inside(p, glo, ghi, pi))
+      return fail(kInval,
+                  "gpu block ids [%lld, %lld] address bytes outside the allocation of "
+                  "layer %d (%zu bytes)",
+                  (long long)g.min_gid, (long long)g.max_gid, l, pi.size);
+  }
+  return 0;
+}
+
+void prof_add_kernel(double ms, int64_t bytes) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  g_prof.kernel_launches += 1;
+  g_prof.kernel_ms += ms;
+  g_prof.kernel_bytes += bytes;
+}
+
+void prof_add_dma(double ms, int64_t copies, int64_t bytes) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  g_prof.dma_batches += 1;
+  g_prof.dma_copies += copies;
+  g_prof.dma_ms += ms;
+  g_prof.dma_bytes += bytes;
+}
+
+// Event pairs recorded around launches when profiling is on; read after the
+// final synchronisation.
+struct ProfSpan {
+  hipEvent_t a, b;
+  int64_t bytes;
+  int64_t copies;
+  bool dma;
+};
+
+struct ProfRecorder {
+  bool on = g_prof_on.load(std::memory_order_relaxed);
+  std::vector<ProfSpan> spans;
+  int begin(hipStream_t s, hipEvent_t* a) {
+    if (!on) return 0;
+    FKV_HIP(hipEventCreate(a));
+    FKV_HIP(hipEventRecord(*a, s));
+    return 0;
+  }
+  int end(hipStream_t s, hipEvent_t a, int64_t bytes, int64_t copies, bool dma) {
+    if (!on) return 0;
+    hipEvent_t b;
+    FKV_HIP(hipEventCreate(&b));
+    FKV_HIP(hipEventRecord(b, s));
+    spans.push_back({a, b, bytes, copies, dma});
+    return 0;
+  }
+  void flush() {
+    for (auto& sp : spans) {
+      float ms = 0.f;
+      if (hipEventElapsedTime(&ms, sp.a, sp.b) == hipSuccess) {
+        if (sp.dma)
+          prof_add_dma(ms, sp.copies, sp.bytes);
+        else
+          prof_add_kernel(ms, sp.bytes);
+      }
+      (void)hipEventDestroy(sp.a);
+      (void)hipEventDestroy(sp.b);
+    }
+    spans.clear();
+  }
+  ~ProfRecorder() {
+    for (auto& sp : spans) {
+      (void)hipEventDestroy(sp.a);
+      (void)hipEventDestroy(sp.b);
+    }
+  }
+};
+
+// Fill the per-launch part of CopyArgs and launch over `nb` blocks starting at
+// block `b0` of the (already packed) id list, for GPU layers [l0, l0 + nl).
+// `cpu_base` is the CPU-side address of launch layer 0 of block index 0.
+template <bool kH2D, bool kIota>
+int launch_copy(const Geometry& g, char* ids_dev, char* cpu_base, int64_t cks, int64_t cls,
+                int64_t cbs, int b0, int nb, int l0, int nl, int grid_cap,
+                hipStream_t stream, ProfRecorder& prof) {
+  CopyArgs a;
+  memset(&a, 0, sizeof(a));
+  a.ids = reinterpret_cast<const int64_t*>(ids_dev) + 2 * static_cast<int64_t>(b0);
+  a.cpu_base = cpu_base;
+  a.gpu_kv_stride = g.gks;
+  a.gpu_block_stride = g.gbs;
+  a.cpu_kv_stride = cks;
+  a.cpu_layer_stride = cls;
+  a.cpu_block_stride = cbs;
+  a.chunk_vec = g.chunk / 16;
+  a.rows_per_chunk = static_cast<int32_t>((a.chunk_vec + 63) / 64);
+  a.num_blocks = nb;
+  a.num_layers = nl;
+  a.kv_dim = g.kv;
+  for (int l = 0; l < nl; ++l) a.layer_ptr[l] = reinterpret_cast<uint64_t>(g.layer_ptrs[l0 + l]);
+  // Tile: enough tiles to keep every workgroup of the grid busy several
+  // times over, at most kMaxTileBlocks blocks, and rows within uint32.
+  const int64_t rows_per_block = static_cast<int64_t>(nl) * g.kv * a.rows_per_chunk;
+  int tb = static_cast<int>(std::max<int64_t>(1, nb / std::max(1, 4 * grid_cap)));
+  tb = std::min(tb, kMaxTileBlocks);
+  while (tb > 1 && rows_per_block * tb > (int64_t(1) << 31)) tb /= 2;
+  a.tile_blocks = tb;
+  a.num_tiles = (nb + tb - 1) / tb;
+  const int grid = std::max(1, std::min(grid_cap, a.num_tiles));
+  hipEvent_t ev = nullptr;
+  if (prof.begin(stream, &ev)) return kInval;
+  hipLaunchKernelGGL((kv_chunk_copy_kernel<kH2D, kIota>), dim3(grid), dim3(kThreads), 0, stream, a);
+  FKV_HIP(hipGetLastError());
+  return prof.end(stream, ev, static_cast<int64_t>(nb) * nl * g.kv * g.chunk, 0, false);
+}
+
+// Pack ids into the thread's pinned buffer as (gpu_id, cpu_id) pairs.
+int pack_ids(const Geometry& g, char** ids_dev) {
+  int64_t* h = nullptr;
+  int rc = pinned_ids(static_cast<size_t>(g.num_blocks) * 16, &h, ids_dev);
+  if (rc) return rc;
+  for (int i = 0; i < g.num_blocks; ++i) {
+    h[2 * i] = g.gids[i];
+    h[2 * i + 1] = g.cids[i];
+  }
+  return 0;
+}
+
+int stream_device(hipStream_t s, int* dev) {
+  if (s == nullptr) {
+    FKV_HIP(hipGetDevice(dev));
+  } else {
+    FKV_HIP(hipStreamGetDevice(s, dev));
+  }
+  if (*dev < 0 || *dev >= kMaxDevices) return fail(kInval, "device %d out of range", *dev);
+  return 0;
+}
+
+int transfer_zero_copy(const Geometry& g, hipStream_t stream, int dev, int transfer_cus,
+                       bool h2d) {
+  DeviceState& d = g_dev[dev];
+  char* ids_dev = nullptr;
+  int rc = pack_ids(g, &ids_dev);
+  if (rc) return rc;
+  int cus = transfer_cus <= 0 ? std::min(32, d.num_cus) : std::min(transfer_cus, d.num_cus);
+  const int grid_cap = cus * (h2d ? d.occ_zero_copy[1] : d.occ_zero_copy[0]);
+  char* cpu_dev = g.cpu_info.dev_ptr + g.startoff +
+                  static_cast<int64_t>(g.start_layer) * g.cls;
+  ProfRecorder prof;
+  for (int l0 = 0; l0 < g.num_layers; l0 += kMaxLayersPerLaunch) {
+    const int nl = std::min(kMaxLayersPerLaunch, g.num_layers - l0);
+    char* base = cpu_dev + static_cast<int64_t>(l0) * g.cls;
+    rc = h2d ? launch_copy<true, false>(g, ids_dev, base, g.cks, g.cls, g.cbs, 0,
+                                        g.num_blocks, l0, nl, grid_cap, stream, prof)
+             : launch_copy<false, false>(g, ids_dev, base, g.cks, g.cls, g.cbs, 0,
+                                         g.num_blocks, l0, nl, grid_cap, stream, prof);
+    if (rc) return rc;
+  }
+  FKV_HIP(hipStreamSynchronize(stream));
+  prof.flush();
+  return 0;
+}
+
+// One contiguous DMA between staging and the host cache.
+struct Run {
+  int64_t staging_off;
+  char* host;
+  int64_t bytes;
+};
+
+// Host runs for blocks [b0, b0+nb) of a piece whose staging layout is
+// [block][layer][kv][chunk] over `nl` layers starting at `l0`.
+void build_runs(const Geometry& g, int b0, int nb, int l0, int nl, std::vector<Run>& runs) {
+  runs.clear();
+  const int64_t row_chunks = static_cast<int64_t>(nl) * g.kv;
+  const bool row_contig = (g.kv == 1 || g.cks == g.chunk) && (nl == 1 || g.cls == g.kv * g.chunk);
+  char* host0 = g.cpu_ptr + g.startoff + static_cast<int64_t>(g.start_layer + l0) * g.cls;
+  int64_t soff = 0;
+  auto push = [&](char* h, int64_t bytes) {
+    if (!runs.empty() && runs.back().host + runs.back().bytes == h &&
+        runs.back().staging_off + runs.back().bytes == soff) {
+      runs.back().bytes += bytes;
+    } else {
+      runs.push_back({soff, h, bytes});
+    }
+    soff += bytes;
+  };
+  for (int i = b0; i < b0 + nb; ++i) {
+    char* hb = host0 + g.cids[i] * g.cbs;
+    if (row_contig) {
+      push(hb, row_chunks * g.chunk);
+    } else {
+      for (int l = 0; l < nl; ++l)
+        for (int k = 0; k < g.kv; ++k) push(hb + l * g.cls + k * g.cks, g.chunk);
+    }
+  }
+}
+
+int ensure_staging(DeviceState& d, int dev, size_t need_half) {
+  size_t want = g_staging_request.load();
+  if (want == 0) want = kDefaultStagingBytes;
+  want = std::max(want, 2 * need_half);
+  want = (want + 4095) & ~size_t(4095);
+  if (!d.side) {
+    FKV_HIP(hipStreamCreateWithFlags(&d.side, hipStreamNonBlocking));
+    for (int h = 0; h < 2; ++h) {
+      FKV_HIP(hipEventCreateWithFlags(&d.ev_fill[h], hipEventDisableTiming));
+      FKV_HIP(hipEventCreateWithFlags(&d.ev_drain[h], hipEventDisableTiming));
+    }
+  }
+  if (d.staging && d.staging_bytes == want) return 0;
+  if (d.staging) {
+    FKV_HIP(hipFree(d.staging));
+    d.staging = nullptr;
+    d.staging_bytes = 0;
+  }
+  void* p = nullptr;
+  FKV_HIP(hipMalloc(&p, want));
+  d.staging = static_cast<char*>(p);
+  d.staging_bytes = want;
+  (void)dev;
+  return 0;
+}
+
+int issue_runs(const std::vector<Run>& runs, char* staging, bool h2d, hipStream_t s) {
+  for (const Run& r : runs) {
+    if (h2d) {
+      FKV_HIP(hipMemcpyAsync(staging + r.staging_off, r.host, r.bytes, hipMemcpyHostToDevice, s));
+    } else {
+      FKV_HIP(hipMemcpyAsync(r.host, staging + r.staging_off, r.bytes, hipMemcpyDeviceToHost, s));
+    }
+  }
+  return 0;
+}
+
+int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
+  DeviceState& d = g_dev[dev];
+  std::lock_guard<std::mutex> lk(d.mu);
+  DeviceGuard guard;
+  int rc = guard.set(dev);
+  if (rc) return rc;
+  char* ids_dev = nullptr;
+  rc = pack_ids(g, &ids_dev);
+  if (rc) return rc;
+
+  // A piece is a run of whole blocks over a layer window; the window covers
+  // all layers unless one block row would not fit a staging half.
+  const size_t half_default = (g_staging_request.load() ? g_staging_request.load() : kDefaultStagingBytes) / 2;
+  int nl_piece = std::min(g.num_layers, kMaxLayersPerLaunch);
+  while (nl_piece > 1 && static_cast<size_t>(nl_piece) * g.kv * g.chunk > half_default) nl_piece /= 2;
+  const size_t row_bytes = static_cast<size_t>(nl_piece) * g.kv * g.chunk;
+  rc = ensure_staging(d, dev, row_bytes);
+  if (rc) return rc;
+  const size_t half = d.staging_bytes / 2;
+  const int blocks_per_piece = static_cast<int>(std::max<size_t>(1, half / row_bytes));
+  const int grid_cap = d.num_cus * (h2d ? d.occ_staged[1] : d.occ_staged[0]);
+
+  ProfRecorder prof;
+  bool used[2] = {false, false};
+  std::vector<Run> runs;
+  int piece = 0;
+  for (int l0 = 0; l0 < g.num_layers; l0 += nl_piece) {
+    const int nl = std::min(nl_piece, g.num_layers - l0);
+    const int64_t cls = static_cast<int64_t>(g.kv) * g.chunk;   // staging layer stride
+    const int64_t cbs = static_cast<int64_t>(nl) * cls;         // staging block stride
+    for (int b0 = 0; b0 < g.num_blocks; b0 += blocks_per_piece, ++piece) {
+      const int nb = std::min(blocks_per_piece, g.num_blocks - b0);
+      const int h = piece & 1;
+      char* stg = d.staging + h * half;
+      build_runs(g, b0, nb, l0, nl, runs);
+      const int64_t bytes = static_cast<int64_t>(nb) * nl * g.kv * g.chunk;
+      hipEvent_t ev = nullptr;
+      if (!h2d) {
+        // gather GPU -> staging on the caller's stream, then DMA staging -> host
+        if (used[h]) FKV_HIP(hipStreamWaitEvent(stream, d.ev_drain[h], 0));
+        rc = launch_copy<false, true>(g, ids_dev, stg, g.kv == 1 ? 0 : g.chunk, cls, cbs, b0, nb,
+                                      l0, nl, grid_cap, stream, prof);
+        if (rc) return rc;
+        FKV_HIP(hipEventRecord(d.ev_fill[h], stream));
+        FKV_HIP(hipStreamWaitEvent(d.side, d.ev_fill[h], 0));
+        if ((rc = prof.begin(d.side, &ev))) return rc;
+        if ((rc = issue_runs(runs, stg, false, d.side))) return rc;
+        if ((rc = prof.end(d.side, ev, bytes, static_cast<int64_t>(runs.size()), true))) return rc;
+        FKV_HIP(hipEventRecord(d.ev_drain[h], d.side));
+      } else {
+        // DMA host -> staging on the side stream, then scatter on the caller's
+        if (used[h]) FKV_HIP(hipStreamWaitEvent(d.side, d.ev_drain[h], 0));
+        if ((rc = prof.begin(d.side, &ev))) return rc;
+        if ((rc = issue_runs(runs, stg, true, d.side))) return rc;
+        if ((rc = prof.end(d.side, ev, bytes, static_cast<int64_t>(runs.size()), true))) return rc;
+        FKV_HIP(hipEventRecord(d.ev_fill[h], d.side));
+        FKV_HIP(hipStreamWaitEvent(stream, d.ev_fill[h], 0));
+        rc = launch_copy<true, true>(g, ids_dev, stg, g.kv == 1 ? 0 : g.chunk, cls, cbs, b0, nb,
+                                     l0, nl, grid_cap, stream, prof);
+        if (rc) return rc;
+        FKV_HIP(hipEventRecord(d.ev_drain[h], stream));
+      }
+      used[h] = true;
+    }
+  }
+  // The caller's stream must not run ahead of the last DMA.
+  for (int h = 0; h < 2; ++h)
+    if (used[h]) FKV_HIP(hipStreamWaitEvent(stream, d.ev_drain[h], 0));
+  FKV_HIP(hipStreamSynchronize(stream));
+  FKV_HIP(hipStreamSynchronize(d.side));
+  prof.flush();
+  return 0;
+}
+
+// The reference copy-engine loop, csrc/transfer.cu:97-121: one async copy per
+// (layer, K|V, block) chunk, issued layer-major then K|V then block.
+int transfer_ce_per_chunk(const Geometry& g, hipStream_t stream, bool h2d) {
+  ProfRecorder prof;
+  hipEvent_t ev = nullptr;
+  int rc = prof.begin(stream, &ev);
+  if (rc) return rc;
+  for (int l = 0; l < g.num_layers; ++l) {
+    char* gl = static_cast<char*>(g.layer_ptrs[l]);
+    for (int k = 0; k < g.kv; ++k) {
+      for (int i = 0; i < g.num_blocks; ++i) {
+        char* cpu = g.cpu_ptr + static_cast<int64_t>(l + g.start_layer) * g.cls + k * g.cks +
+                    g.cids[i] * g.cbs + g.startoff;
+        char* gpu = gl + k * g.gks + g.gids[i] * g.gbs;
+        if (h2d) {
+          FKV_HIP(hipMemcpyAsync(gpu, cpu, g.chunk, hipMemcpyHostToDevice, stream));
+        } else {
+          FKV_HIP(hipMemcpyAsync(cpu, gpu, g.chunk, hipMemcpyDeviceToHost, stream));
+        }
+      }
+    }
+  }
+  const int64_t copies = static_cast<int64_t>(g.num_layers) * g.kv * g.num_blocks;
+  if ((rc = prof.end(stream, ev, copies * g.chunk, copies, true))) return rc;
+  FKV_HIP(hipStreamSynchronize(stream));
+  prof.flush();
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fkv_transfer_kv_blocks(int num_blocks, int start_layer_id, int num_layers,
+                           const int64_t* gpu_block_ids, void* const* gpu_layer_ptrs,
+                           int64_t gpu_kv_stride_bytes, int64_t gpu_block_stride_bytes,
+                           const int64_t* cpu_block_ids, void* cpu_ptr,
+                           int64_t cpu_kv_stride_bytes, int64_t cpu_layer_stride_bytes,
+                           int64_t cpu_block_stride_bytes, int64_t cpu_startoff_inside_chunks,
+                           int64_t chunk_size_bytes, fkv_stream_t stream, int transfer_cus,
+                           int is_host_to_device, int use_ce_transfer, int is_mla) {
+  try {
+    t_err.clear();
+    if (use_ce_transfer < FKV_XFER_KERNEL || use_ce_transfer > FKV_XFER_CE_PER_CHUNK)
+      return fail(kInval, "use_ce_transfer must be 0 (kernel), 1 (CE) or 2 (CE per chunk), got %d",
+                  use_ce_transfer);
+    if (num_blocks == 0 || num_layers == 0) return 0;
+    Geometry g;
+    g.num_blocks = num_blocks;
+    g.start_layer = start_layer_id;
+    g.num_layers = num_layers;
+    g.kv = is_mla ? 1 : 2;
+    g.gids = gpu_block_ids;
+    g.cids = cpu_block_ids;
+    g.layer_ptrs = gpu_layer_ptrs;
+    g.gks = gpu_kv_stride_bytes;
+    g.gbs = gpu_block_stride_bytes;
+    g.cks = cpu_kv_stride_bytes;
+    g.cls = cpu_layer_stride_bytes;
+    g.cbs = cpu_block_stride_bytes;
+    g.startoff = cpu_startoff_inside_chunks;
+    g.chunk = chunk_size_bytes;
+    g.cpu_ptr = static_cast<char*>(cpu_ptr);
+    int rc = validate(g, use_ce_transfer);
+    if (rc) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int dev = 0;
+    if ((rc = stream_device(s, &dev))) return rc;
+    if ((rc = ensure_device_basics(dev))) return rc;
+    const bool h2d = is_host_to_device != 0;
+    switch (use_ce_transfer) {
+      case FKV_XFER_KERNEL:
+        return transfer_zero_copy(g, s, dev, transfer_cus, h2d);
+      case FKV_XFER_CE:
+        return transfer_staged(g, s, dev, h2d);
+      default:
+        return transfer_ce_per_chunk(g, s, h2d);
+    }
+  } catch (const std::exception& e) {
+    return fail(static_cast<int>(hipErrorUnknown), "exception: %s", e.what());
+  } catch (...) {
+    return fail(static_cast<int>(hipErrorUnknown), "unknown exception");
+  }
+}
+
+const char* fkv_last_error(void) { return t_err.c_str(); }
+
+int fkv_host_alloc(void** out_ptr, size_t bytes, unsigned flags) {
+  t_err.clear();
+  if (!out_ptr) return fail(kInval, "out_ptr is null");
+  *out_ptr = nullptr;
+  if (bytes == 0) return fail(kInval, "zero-byte host allocation");
+  unsigned hf = hipHostMallocPortable | hipHostMallocMapped;
+  if (flags == FKV_HOST_COHERENT) hf |= hipHostMallocCoherent;
+  else if (flags == FKV_HOST_NONCOHERENT) hf |= hipHostMallocNonCoherent;
+  else if (flags != FKV_HOST_DEFAULT) return fail(kInval, "unknown host alloc flags %u", flags);
+  FKV_HIP(hipHostMalloc(out_ptr, bytes, hf));
+  return 0;
+}
+
+int fkv_host_free(void* ptr) {
+  t_err.clear();
+  if (!ptr) return 0;
+  FKV_HIP(hipHostFree(ptr));
+  return 0;
+}
+
+int fkv_host_register(void* ptr, size_t bytes, unsigned flags) {
+  t_err.clear();
+  (void)flags;
+  if (!ptr || bytes == 0) return fail(kInval, "null or empty range");
+  PtrInfo pi;
+  if (query_ptr(ptr, &pi) != 0 || !pi.host)
+    return fail(kInval,
+                "host range %p is not pinned; allocate the host cache pinned "
+                "(fkv_host_alloc or pin_memory=True) instead of registering pageable memory",
+                ptr);
+  if (!range_inside(static_cast<char*>(ptr), 0, static_cast<__int128>(bytes), pi))
+    return fail(kInval, "host range %p + %zu exceeds its pinned allocation (%zu bytes)", ptr,
+                bytes, pi.size);
+  return 0;
+}
+
+int fkv_host_unregister(void* ptr) {
+  (void)ptr;
+  t_err.clear();
+  return 0;
+}
+
+int fkv_set_staging_bytes(size_t bytes) {
+  t_err.clear();
+  g_staging_request.store(bytes);
+  return 0;
+}
+
+int fkv_release_staging(void) {
+  t_err.clear();
+  for (int dev = 0; dev < kMaxDevices; ++dev) {
+    DeviceState& d = g_dev[dev];
+    std::lock_guard<std::mutex> lk(d.mu);
+    if (d.staging) {
+      DeviceGuard guard;
+      int rc = guard.set(dev);
+      if (rc) return rc;
+      FKV_HIP(hipFree(d.staging));
+      d.staging = nullptr;
+      d.staging_bytes = 0;
+    }
+  }
+  return 0;
+}
+
+int fkv_profile_enable(int on) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  g_prof = fkv_profile{};
+  g_prof_on.store(on != 0);
+  return 0;
+}
+
+int fkv_profile_read(fkv_profile* out) {
+  if (!out) return kInval;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  *out = g_prof;
+  return 0;
+}
+
+const char* fkv_version(void) { return "flexkv_hip 0.1 gfx950"; }
+
+}  // extern "C"

@@ -1,0 +1,269 @@
+"""Transfer workers for the GPU<->CPU path.
+
+Same API as the reference's worker module for the single-GPU case
+(flexkv/transfer/worker.py:49-342): WorkerTransferOp, TransferWorkerBase
+(create_worker spawns a process fed through a Pipe, run() polls and batches
+ops, finished op ids go to a queue), WorkerHandle (submit_transfer, shutdown)
+and GPUCPUTransferWorker (_transfer_impl, launch_transfer).  The transfer
+itself is flexkv_amd.c_ext.transfer_kv_blocks.
+
+Differences from the reference, all on failure paths:
+  * the host cache must already be pinned (CPUAllocator pin_memory=True);
+    page-locking existing pageable memory is not supported, so host_register
+    checks the buffer instead of registering it (worker.py:35-41 registers);
+  * an op that fails is still reported complete (worker.py:159-169), and is
+    also recorded in ``failed_ops`` of the worker and logged at error level.
+"""
+from __future__ import annotations
+
+import multiprocessing as mp
+import time
+from abc import ABC, abstractmethod
+from multiprocessing.connection import Connection
+from typing import Any, List, Optional, Sequence, Union
+
+import ctypes
+import numpy as np
+import torch
+
+from .. import _lib
+from ..c_ext import transfer_kv_blocks
+from ..common.debug import flexkv_logger
+from ..common.memory_handle import TensorSharedHandle
+from ..common.storage import KVCacheLayout, KVCacheLayoutType
+from ..common.transfer import TransferOp, TransferType
+
+
+def host_register(tensor: torch.Tensor) -> None:
+    """Check that `tensor` is pinned host memory the device can address
+    (the reference registers it with cudaHostRegister, worker.py:35-41)."""
+    size = tensor.numel() * tensor.element_size()
+    lib = _lib.load()
+    _lib.check(lib.fkv_host_register(ctypes.c_void_p(tensor.data_ptr()), size, 1),
+               "fkv_host_register")
+
+
+def host_unregister(tensor: torch.Tensor) -> None:
+    _lib.load().fkv_host_unregister(ctypes.c_void_p(tensor.data_ptr()))
+
+
+class WorkerTransferOp:
+    """Picklable op record sent to a worker (worker.py:49-68)."""
+
+    def __init__(self, transfer_op: TransferOp) -> None:
+        self.transfer_op_id = transfer_op.op_id
+        self.transfer_graph_id = transfer_op.graph_id
+        self.transfer_type = transfer_op.transfer_type
+        self.src_block_ids = transfer_op.src_descriptor.physical_block_ids.numpy()
+        self.dst_block_ids = transfer_op.dst_descriptor.physical_block_ids.numpy()
+        self.layer_id = transfer_op.layer_id
+        self.layer_granularity = transfer_op.layer_granularity
+
+    def __repr__(self) -> str:
+        return (f"WorkerTransferOp(id={self.transfer_op_id}, graph={self.transfer_graph_id}, "
+                f"type={self.transfer_type.name}, blocks={len(self.src_block_ids)}, "
+                f"layer_id={self.layer_id}, granularity={self.layer_granularity})")
+
+
+class TransferWorkerBase(ABC):
+    def __init__(self, worker_id: int, transfer_conn: Optional[Connection],
+                 finished_ops_queue: Optional[Any]) -> None:
+        self.worker_id = worker_id
+        self.transfer_conn = transfer_conn
+        self.finished_ops_queue = finished_ops_queue
+        self.failed_ops: List[int] = []
+
+    @staticmethod
+    def _get_layer_ptrs(layer_blocks: Union[Sequence[torch.Tensor], torch.Tensor]) -> torch.Tensor:
+        """Pinned int64 table of per-layer base addresses (worker.py:79-90)."""
+        if isinstance(layer_blocks, torch.Tensor):
+            layer_blocks = [layer_blocks]
+        ptrs = torch.tensor([t.data_ptr() for t in layer_blocks], dtype=torch.int64)
+        return ptrs.pin_memory() if torch.cuda.is_available() else ptrs
+
+    @classmethod
+    def create_worker(cls, worker_id: int, finished_ops_queue: Any, *args: Any,
+                      **kwargs: Any) -> "WorkerHandle":
+        """Start the worker in a spawned process (worker.py:92-106)."""
+        ctx = mp.get_context("spawn")
+        parent_conn, child_conn = ctx.Pipe()
+        ready_event = ctx.Event()
+        process = ctx.Process(target=cls._worker_process,
+                              args=(worker_id, child_conn, finished_ops_queue, ready_event, *args),
+                              kwargs=kwargs, daemon=True)
+        process.start()
+        return WorkerHandle(worker_id, parent_conn, process, ready_event)
+
+    @classmethod
+    def _worker_process(cls, worker_id: int, transfer_conn: Connection, finished_ops_queue: Any,
+                        ready_event: Any, *args: Any, **kwargs: Any) -> None:
+        worker = cls(worker_id, transfer_conn, finished_ops_queue, *args, **kwargs)
+        ready_event.set()
+        worker.run()
+
+    @abstractmethod
+    def _transfer_impl(self, src_block_ids: np.ndarray, dst_block_ids: np.ndarray,
+                       transfer_type: TransferType, layer_id: int, layer_granularity: int,
+                       **kwargs: Any) -> None:
+        ...
+
+    @abstractmethod
+    def launch_transfer(self, transfer_op: WorkerTransferOp) -> None:
+        ...
+
+    def _log_transfer_performance(self, transfer_op: WorkerTransferOp, transfer_size: int,
+                                  start_time: float, end_time: float) -> None:
+        dt = max(end_time - start_time, 1e-12)
+        flexkv_logger.info(
+            f"{transfer_op.transfer_type.name} transfer request: {transfer_op.transfer_op_id} "
+            f"finished transfer data size: {transfer_size / 2**30} GB "
+            f"transfer time: {dt:.4f} s transfer bandwidth: {transfer_size / dt / 1e9:.2f} GB/s")
+
+    def _execute(self, op: WorkerTransferOp) -> None:
+        try:
+            self.launch_transfer(op)
+        except Exception as e:
+            self.failed_ops.append(op.transfer_op_id)
+            flexkv_logger.error(f"Error launching transfer: {e}\nFailed transfer op: {op}")
+        if self.finished_ops_queue is not None:
+            self.finished_ops_queue.put(op.transfer_op_id)
+
+    def run(self) -> None:
+        """Main loop: poll the pipe (100 us), drain whatever else is queued,
+        run the batch in order, report each op id (worker.py:144-177)."""
+        while True:
+            try:
+                if not self.transfer_conn.poll(timeout=0.0001):
+                    continue
+                op = self.transfer_conn.recv()
+                if op is None:
+                    break
+                batch = [op]
+                stop = False
+                while self.transfer_conn.poll(timeout=0):
+                    nxt = self.transfer_conn.recv()
+                    if nxt is None:
+                        stop = True
+                        break
+                    batch.append(nxt)
+                for item in batch:
+                    self._execute(item)
+                if stop:
+                    break
+            except EOFError:
+                break
+            except Exception as e:  # keep serving; the reference does the same
+                flexkv_logger.error(f"Error in worker run loop: {e}")
+
+
+class WorkerHandle:
+    """Parent-side handle of a worker process (worker.py:179-205)."""
+
+    def __init__(self, worker_id: int, transfer_conn: Connection, process: Any,
+                 ready_event: Any) -> None:
+        self.worker_id = worker_id
+        self.transfer_conn = transfer_conn
+        self.process = process
+        self.ready_event = ready_event
+
+    def submit_transfer(self, op: TransferOp) -> None:
+        self.transfer_conn.send(WorkerTransferOp(op))
+
+    def shutdown(self) -> None:
+        try:
+            self.transfer_conn.send(None)
+            self.transfer_conn.close()
+        except (BrokenPipeError, OSError):
+            pass
+        self.process.join(timeout=5)
+        if self.process.is_alive():
+            flexkv_logger.warning("force terminate the worker process")
+            self.process.terminate()
+            self.process.join()
+
+    def __del__(self) -> None:
+        try:
+            if self.process.is_alive():
+                self.shutdown()
+        except Exception:
+            pass
+
+
+class GPUCPUTransferWorker(TransferWorkerBase):
+    """Moves KV blocks between one GPU's per-layer cache and the host cache
+    (worker.py:207-342; single GPU, no TP)."""
+
+    def __init__(self, worker_id: int, transfer_conn: Optional[Connection],
+                 finished_ops_queue: Optional[Any],
+                 gpu_blocks: Sequence[Union[TensorSharedHandle, torch.Tensor]],
+                 cpu_blocks: torch.Tensor, gpu_kv_layout: KVCacheLayout,
+                 cpu_kv_layout: KVCacheLayout, dtype: torch.dtype, gpu_device_id: int,
+                 use_ce_transfer_h2d: bool = False, use_ce_transfer_d2h: bool = False,
+                 transfer_sms_h2d: int = 8, transfer_sms_d2h: int = 8) -> None:
+        super().__init__(worker_id, transfer_conn, finished_ops_queue)
+        if gpu_kv_layout.type != KVCacheLayoutType.LAYERWISE:
+            raise ValueError("Only layerwise layout is supported for GPU")
+        if gpu_device_id != -1:
+            torch.cuda.set_device(gpu_device_id)
+        host_register(cpu_blocks)
+        self.gpu_blocks = [h.get_tensor() if isinstance(h, TensorSharedHandle) else h
+                           for h in gpu_blocks]
+        self.gpu_layer_ptrs = self._get_layer_ptrs(self.gpu_blocks)
+        self.cpu_tensor = cpu_blocks
+        self.dtype = dtype
+        self.is_mla = gpu_kv_layout.is_mla
+        self.num_layers = gpu_kv_layout.num_layer
+        per_layer = gpu_kv_layout.div_layer(self.num_layers)
+        es = dtype.itemsize
+        self.chunk_size_in_bytes = per_layer.get_chunk_size() * es
+        self.gpu_kv_stride_in_bytes = per_layer.get_kv_stride() * es
+        self.gpu_block_stride_in_bytes = per_layer.get_block_stride() * es
+        self.cpu_layer_stride_in_bytes = cpu_kv_layout.get_layer_stride() * es
+        self.cpu_kv_stride_in_bytes = cpu_kv_layout.get_kv_stride() * es
+        self.cpu_block_stride_in_bytes = cpu_kv_layout.get_block_stride() * es
+        self.transfer_stream = torch.cuda.Stream()
+        self.transfer_sms_h2d = transfer_sms_h2d
+        self.transfer_sms_d2h = transfer_sms_d2h
+        self.use_ce_transfer_h2d = use_ce_transfer_h2d
+        self.use_ce_transfer_d2h = use_ce_transfer_d2h
+
+    def _transfer_impl(self, src_block_ids: np.ndarray, dst_block_ids: np.ndarray,
+                       transfer_type: TransferType, layer_id: int, layer_granularity: int,
+                       **kwargs: Any) -> None:
+        assert src_block_ids.dtype == np.int64
+        assert dst_block_ids.dtype == np.int64
+        assert len(src_block_ids) == len(dst_block_ids)
+        if transfer_type == TransferType.H2D:
+            gpu_ids, cpu_ids = dst_block_ids, src_block_ids
+            use_ce, sms = self.use_ce_transfer_h2d, self.transfer_sms_h2d
+        elif transfer_type == TransferType.D2H:
+            gpu_ids, cpu_ids = src_block_ids, dst_block_ids
+            use_ce, sms = self.use_ce_transfer_d2h, self.transfer_sms_d2h
+        else:
+            raise ValueError(f"Invalid transfer type: {transfer_type} for GPUCPUTransferWorker")
+        if len(gpu_ids) == 0:
+            return
+        gpu_id_t = torch.from_numpy(np.ascontiguousarray(gpu_ids)).pin_memory()
+        cpu_id_t = torch.from_numpy(np.ascontiguousarray(cpu_ids)).pin_memory()
+        if layer_id < 0 or layer_granularity < 1 or layer_id + layer_granularity > self.num_layers:
+            raise ValueError(f"layer range [{layer_id}, {layer_id + layer_granularity}) is outside "
+                             f"[0, {self.num_layers})")
+        layer_ptrs = self.gpu_layer_ptrs[layer_id:layer_id + layer_granularity].contiguous().pin_memory()
+        transfer_kv_blocks(gpu_id_t, layer_ptrs, self.gpu_kv_stride_in_bytes,
+                           self.gpu_block_stride_in_bytes, cpu_id_t, self.cpu_tensor,
+                           self.cpu_kv_stride_in_bytes, self.cpu_layer_stride_in_bytes,
+                           self.cpu_block_stride_in_bytes, self.chunk_size_in_bytes, layer_id,
+                           sms, transfer_type == TransferType.H2D, use_ce, self.is_mla)
+
+    def launch_transfer(self, transfer_op: WorkerTransferOp) -> None:
+        layer_id = 0 if transfer_op.layer_id == -1 else transfer_op.layer_id
+        granularity = self.num_layers if transfer_op.layer_granularity == -1 \
+            else transfer_op.layer_granularity
+        with torch.cuda.stream(self.transfer_stream):
+            start = time.time()
+            self._transfer_impl(transfer_op.src_block_ids, transfer_op.dst_block_ids,
+                                transfer_op.transfer_type, layer_id, granularity)
+            end = time.time()
+        kv_dim = 1 if self.is_mla else 2
+        size = self.chunk_size_in_bytes * granularity * len(transfer_op.src_block_ids) * kv_dim
+        self._log_transfer_performance(transfer_op, size, start, end)

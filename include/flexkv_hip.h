@@ -1,0 +1,142 @@
+/*
+ * flexkv_hip.h - C ABI of libflexkv_hip.so, the MI355X (gfx950) GPU<->CPU
+ * KV-block transfer library.
+ *
+ * Every entry point takes plain pointers and sizes (no torch types), returns
+ * 0 on success or a non-zero status, and never lets a C++ exception cross the
+ * boundary.  On failure a message describing the first error is available from
+ * fkv_last_error() in the calling thread.  Status values are hipError_t codes:
+ * hipErrorInvalidValue (1) for rejected arguments, other hipError_t values for
+ * runtime failures.
+ *
+ * Reference interfaces replaced (paths are relative to the FlexKV source tree):
+ *   fkv_transfer_kv_blocks   <- flexkv::transfer_kv_blocks, csrc/transfer.cu:63-132,
+ *                               and its pybind wrapper transfer_kv_blocks_binding,
+ *                               csrc/bindings.cpp:25-55 (+ m.def at :108-109)
+ *   fkv_host_alloc/free      <- CPUAllocator.allocate(pin_memory=True),
+ *                               flexkv/storage/allocator.py:93-113
+ *   fkv_host_register/...    <- cudaHostRegister / cudaHostUnregister via ctypes,
+ *                               flexkv/transfer/worker.py:33-47
+ */
+#ifndef FLEXKV_HIP_H_
+#define FLEXKV_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Opaque stream handle: a hipStream_t (0 = the legacy default stream). */
+typedef void* fkv_stream_t;
+
+/* Values of `use_ce_transfer` in fkv_transfer_kv_blocks. */
+enum {
+  /* Wavefront gather/scatter kernel that loads and stores pinned host memory
+   * directly (zero-copy over PCIe).  Same role as the reference kernel mode,
+   * csrc/transfer.cu:123-129. */
+  FKV_XFER_KERNEL = 0,
+  /* Copy-engine path: a gather kernel packs the selected chunks into a
+   * contiguous HBM staging buffer and the DMA engines move maximal contiguous
+   * host runs (D2H); H2D is DMA into staging followed by a scatter kernel.
+   * Staging pieces are double-buffered across the caller's stream and a side
+   * stream.  Same role as the reference CE mode, csrc/transfer.cu:97-121. */
+  FKV_XFER_CE = 1,
+  /* The reference's copy-engine algorithm restated literally: one
+   * hipMemcpyAsync per (layer, K|V, block) chunk, csrc/transfer.cu:97-121.
+   * Kept as a comparison baseline. */
+  FKV_XFER_CE_PER_CHUNK = 2
+};
+
+/*
+ * Move `num_blocks` KV blocks between the per-layer GPU cache and the host
+ * cache, for layers [0, num_layers) of `gpu_layer_ptrs` which correspond to
+ * host layers [start_layer_id, start_layer_id + num_layers).
+ *
+ * For chunk (l, k, i), l < num_layers, k < (is_mla ? 1 : 2), i < num_blocks:
+ *   gpu chunk = gpu_layer_ptrs[l] + k*gpu_kv_stride_bytes
+ *               + gpu_block_ids[i]*gpu_block_stride_bytes
+ *   cpu chunk = cpu_ptr + (l + start_layer_id)*cpu_layer_stride_bytes
+ *               + k*cpu_kv_stride_bytes + cpu_block_ids[i]*cpu_block_stride_bytes
+ *               + cpu_startoff_inside_chunks
+ * and chunk_size_bytes bytes are copied cpu->gpu if is_host_to_device, else
+ * gpu->cpu (csrc/transfer.cu:39-53).
+ *
+ * Arguments follow flexkv::transfer_kv_blocks (csrc/transfer.cu:63-70) one for
+ * one; `transfer_cus` plays the role of `transfer_sms` (compute units the
+ * zero-copy kernel may occupy; -1 = automatic).
+ *
+ * Host requirements (checked; violations return hipErrorInvalidValue):
+ *   - gpu_block_ids, cpu_block_ids: host memory, num_blocks int64 each,
+ *     every id >= 0; gpu_layer_ptrs: host memory, num_layers pointers.
+ *   - cpu_ptr: pinned host memory (or device memory) for the kernel and CE
+ *     modes; every addressed byte lies inside the allocation holding cpu_ptr,
+ *     and every GPU chunk inside the allocation holding its layer pointer.
+ *   - kernel and CE modes: chunk_size_bytes, every stride, cpu_startoff and
+ *     every base pointer are multiples of 16 bytes.  (The reference kernel
+ *     silently drops a tail of chunk_size % 16 bytes, csrc/transfer.cu:35;
+ *     this library refuses such geometry instead.)
+ * The call is synchronous: it returns after `stream` has drained
+ * (csrc/transfer.cu:131).  Different host threads may call concurrently.
+ */
+int fkv_transfer_kv_blocks(int num_blocks, int start_layer_id, int num_layers,
+                           const int64_t* gpu_block_ids,
+                           void* const* gpu_layer_ptrs,
+                           int64_t gpu_kv_stride_bytes,
+                           int64_t gpu_block_stride_bytes,
+                           const int64_t* cpu_block_ids, void* cpu_ptr,
+                           int64_t cpu_kv_stride_bytes,
+                           int64_t cpu_layer_stride_bytes,
+                           int64_t cpu_block_stride_bytes,
+                           int64_t cpu_startoff_inside_chunks,
+                           int64_t chunk_size_bytes, fkv_stream_t stream,
+                           int transfer_cus, int is_host_to_device,
+                           int use_ce_transfer, int is_mla);
+
+/* Message of the last failed call made by this thread ("" if none). */
+const char* fkv_last_error(void);
+
+/* Pinned, device-mapped host allocation (hipHostMalloc).  flags: 0 = runtime
+ * default, FKV_HOST_COHERENT / FKV_HOST_NONCOHERENT select the coherence
+ * mode explicitly.  Replaces the pinned torch.empty of CPUAllocator. */
+enum { FKV_HOST_DEFAULT = 0, FKV_HOST_COHERENT = 1, FKV_HOST_NONCOHERENT = 2 };
+int fkv_host_alloc(void** out_ptr, size_t bytes, unsigned flags);
+int fkv_host_free(void* ptr);
+
+/* Check that [ptr, ptr+bytes) is pinned host memory usable by the transfer
+ * kernels (worker.py:35-41 registers the host cache at worker start).  This
+ * library never page-locks existing pageable memory: allocate the host cache
+ * with fkv_host_alloc instead.  Returns 0 if the range is pinned, else
+ * hipErrorInvalidValue.  fkv_host_unregister is the matching no-op. */
+int fkv_host_register(void* ptr, size_t bytes, unsigned flags);
+int fkv_host_unregister(void* ptr);
+
+/* Staging buffer used by FKV_XFER_CE on each device (bytes, split in two
+ * halves).  Takes effect at the next allocation on a device; 0 = default
+ * (256 MiB).  fkv_release_staging frees every device's buffer. */
+int fkv_set_staging_bytes(size_t bytes);
+int fkv_release_staging(void);
+
+/* Optional per-process timing of the library's kernels and DMA batches,
+ * measured with HIP events on the stream each one runs on. */
+typedef struct fkv_profile {
+  int64_t kernel_launches;   /* gather/scatter/zero-copy kernel launches */
+  double kernel_ms;          /* sum of their event-measured durations */
+  int64_t kernel_bytes;      /* algorithmic bytes they moved */
+  int64_t dma_batches;       /* DMA batches issued by FKV_XFER_CE */
+  int64_t dma_copies;        /* individual contiguous DMA copies */
+  double dma_ms;             /* sum of event-measured DMA batch durations */
+  int64_t dma_bytes;
+} fkv_profile;
+int fkv_profile_enable(int on);     /* also clears the counters */
+int fkv_profile_read(fkv_profile* out);
+
+/* Library version string, e.g. "flexkv_hip 0.1 gfx950". */
+const char* fkv_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLEXKV_HIP_H_ */

@@ -1,0 +1,102 @@
+"""CPU oracle for the GPU<->CPU KV-block transfer.
+
+TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()``
+and the ``cpu_baseline`` leg of ``bench.py`` as the checker / CPU baseline.
+The product package ``flexkv_amd`` never imports it.
+
+``transfer_kv_blocks`` calls the C restatement in ``kv_oracle.c`` (built into
+``liboracle.so`` by the Makefile beside it).  Its arguments mirror the
+reference binding ``transfer_kv_blocks`` (csrc/bindings.cpp:25-32) with the
+"GPU" side given as host arrays.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from typing import Sequence, Union
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+ArrayLike = Union[np.ndarray, "torch.Tensor"]  # noqa: F821
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with gcc (make) and return its path."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-s", "-B" if force else "all"], cwd=_HERE, check=True)
+    return _LIB_PATH
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        lib = ctypes.CDLL(_LIB_PATH)
+        f = lib.oracle_transfer_kv_blocks
+        f.restype = ctypes.c_int
+        f.argtypes = [
+            ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+            ctypes.c_int64, ctypes.c_int64,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+        ]
+        _lib = lib
+    return _lib
+
+
+def _addr(x) -> int:
+    """Host address of a C-contiguous numpy array or CPU torch tensor."""
+    if isinstance(x, np.ndarray):
+        if not x.flags["C_CONTIGUOUS"]:
+            raise ValueError("oracle needs C-contiguous arrays")
+        return x.ctypes.data
+    if hasattr(x, "data_ptr"):
+        if x.device.type != "cpu":
+            raise ValueError("oracle works on host memory only")
+        if not x.is_contiguous():
+            raise ValueError("oracle needs contiguous tensors")
+        return x.data_ptr()
+    raise TypeError(f"unsupported buffer type {type(x)!r}")
+
+
+def _ids(x) -> np.ndarray:
+    if hasattr(x, "numpy"):
+        x = x.numpy()
+    a = np.ascontiguousarray(np.asarray(x, dtype=np.int64))
+    if a.ndim != 1:
+        raise ValueError("block ids must be 1-D")
+    return a
+
+
+def transfer_kv_blocks(gpu_block_ids, gpu_layers: Sequence, gpu_kv_stride_in_bytes: int,
+                       gpu_block_stride_in_bytes: int, cpu_block_ids, cpu_buffer,
+                       cpu_kv_stride_in_bytes: int, cpu_layer_stride_in_bytes: int,
+                       cpu_block_stride_in_bytes: int, chunk_size_in_bytes: int,
+                       start_layer_id: int, is_host_to_device: bool,
+                       use_ce_transfer: bool = False, is_mla: bool = False,
+                       cpu_startoff_inside_chunks: int = 0, num_threads: int = 1) -> None:
+    """Oracle transfer, in place.  ``gpu_layers`` is one host buffer per layer
+    (the slice [start_layer_id, start_layer_id + len) of the engine's layers,
+    as in worker.py:293-295); ``cpu_buffer`` is the flat host cache."""
+    gids = _ids(gpu_block_ids)
+    cids = _ids(cpu_block_ids)
+    if gids.shape != cids.shape:
+        raise ValueError("gpu and cpu block id lists differ in length")
+    ptrs = np.array([_addr(t) for t in gpu_layers], dtype=np.uint64)
+    rc = _load().oracle_transfer_kv_blocks(
+        int(gids.size), int(start_layer_id), int(len(gpu_layers)),
+        gids.ctypes.data, ptrs.ctypes.data, int(gpu_kv_stride_in_bytes),
+        int(gpu_block_stride_in_bytes), cids.ctypes.data, _addr(cpu_buffer),
+        int(cpu_kv_stride_in_bytes), int(cpu_layer_stride_in_bytes),
+        int(cpu_block_stride_in_bytes), int(cpu_startoff_inside_chunks),
+        int(chunk_size_in_bytes), int(bool(is_host_to_device)), int(use_ce_transfer),
+        int(bool(is_mla)), int(num_threads))
+    if rc != 0:
+        raise ValueError(f"oracle rejected arguments (rc={rc})")

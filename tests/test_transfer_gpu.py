@@ -1,0 +1,291 @@
+"""GPU parity: the HIP transfer paths against the CPU oracle, byte for byte.
+
+Each case runs the oracle (oracle/kv_oracle.c) and the device path on the same
+inputs and compares every byte of the destination, including blocks that must
+stay untouched.  Modes: 0 = zero-copy kernel, 1 = copy engines through HBM
+staging, 2 = one DMA per chunk (the reference's CE loop).
+"""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import inputs
+from kvcase import KVCase
+
+pytestmark = pytest.mark.gpu
+
+MODES = [0, 1, 2]
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module")
+def dev():
+    from flexkv_amd import _lib
+    _lib.load()
+    return torch.device("cuda:0")
+
+
+def _oracle_d2h(case, gids, cids, mode):
+    s = case.strides()
+    host = case.host.copy()
+    oracle.transfer_kv_blocks(gids, case.gpu, s["gpu_kv"], s["gpu_block"], cids, host,
+                              s["cpu_kv"], s["cpu_layer"], s["cpu_block"], s["chunk"],
+                              case.start_layer, False, use_ce_transfer=(mode != 0),
+                              is_mla=case.kv == 1, cpu_startoff_inside_chunks=s["startoff"])
+    return host
+
+
+def _oracle_h2d(case, gids, cids, gpu_init, mode):
+    s = case.strides()
+    out = [g.copy() for g in gpu_init]
+    oracle.transfer_kv_blocks(gids, out, s["gpu_kv"], s["gpu_block"], cids, case.host,
+                              s["cpu_kv"], s["cpu_layer"], s["cpu_block"], s["chunk"],
+                              case.start_layer, True, use_ce_transfer=(mode != 0),
+                              is_mla=case.kv == 1, cpu_startoff_inside_chunks=s["startoff"])
+    return out
+
+
+def check_case(case, gids, cids, mode, transfer_cus=-1):
+    from gpu_util import DeviceCase, abi_transfer
+    print(f"case L={case.num_layers} kv={case.kv} n={len(gids)} chunk={case.strides()['chunk']} "
+          f"layout={case.layout} mode={mode}", flush=True)
+    dc = DeviceCase(case)
+    abi_transfer(dc, gids, cids, h2d=False, mode=mode, transfer_cus=transfer_cus)
+    torch.cuda.synchronize()
+    want = _oracle_d2h(case, gids, cids, mode)
+    got = dc.host_np()
+    assert np.array_equal(got, want), "D2H differs from the oracle"
+    # H2D from a host cache holding fresh values into a sentinel-filled GPU
+    case2 = KVCase(**{k: getattr(case, k) for k in (
+        "layers_total", "num_layers", "start_layer", "kv", "ng", "nh", "tokens", "heads", "dim",
+        "dtype", "layout", "tp", "rank")})
+    case2.fill(seed=99)
+    case2.host = want ^ np.asarray(0x1234, dtype=case.dtype)
+    init = case2.gpu
+    dc.set_host(case2.host)
+    dc.set_gpu(init)
+    abi_transfer(dc, gids, cids, h2d=True, mode=mode, transfer_cus=transfer_cus)
+    torch.cuda.synchronize()
+    want_g = _oracle_h2d(case2, gids, cids, init, mode)
+    for l, (g, w) in enumerate(zip(dc.gpu_np(), want_g)):
+        assert np.array_equal(g, w), f"H2D differs from the oracle at layer {l}"
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_tiny_fixture_vectors(dev, mode):
+    fx = np.load(os.path.join(GOLDEN, "tiny_vectors.npz"), allow_pickle=False)
+    meta = json.loads(str(fx["meta"]))
+    from gpu_util import DeviceCase, abi_transfer
+    for i, m in enumerate(meta):
+        case = KVCase(**m["shape"])
+        case.gpu = [fx[f"c{i}_gpu{l}"] for l in range(case.num_layers)]
+        case.host = fx[f"c{i}_host"]
+        gids, cids = fx[f"c{i}_gids"], fx[f"c{i}_cids"]
+        dc = DeviceCase(case)
+        abi_transfer(dc, gids, cids, h2d=False, mode=mode)
+        torch.cuda.synchronize()
+        assert np.array_equal(dc.host_np(), fx[f"c{i}_want_host"]), m
+        dc.set_gpu([np.zeros_like(g) for g in case.gpu])
+        abi_transfer(dc, gids, cids, h2d=True, mode=mode)
+        torch.cuda.synchronize()
+        for l, g in enumerate(dc.gpu_np()):
+            assert np.array_equal(g, fx[f"c{i}_want_gpu{l}"]), m
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_config0_digests(dev, mode):
+    """The CPU-plumbing configuration on the GPU reproduces the committed digests."""
+    from golden.gen_golden import config0_case, config0_ids
+    from gpu_util import DeviceCase, abi_transfer
+    with open(os.path.join(GOLDEN, "config0_digests.json")) as fh:
+        want = json.load(fh)
+    case = config0_case()
+    gids, cids = config0_ids()
+    dc = DeviceCase(case)
+    abi_transfer(dc, gids, cids, h2d=False, mode=mode)
+    torch.cuda.synchronize()
+    assert hashlib.sha256(dc.host_np().tobytes()).hexdigest() == want["d2h_host_sha256"]
+    dc.set_gpu([np.zeros_like(g) for g in case.gpu])
+    abi_transfer(dc, gids, cids, h2d=True, mode=mode)
+    torch.cuda.synchronize()
+    got = b"".join(g.tobytes() for g in dc.gpu_np())
+    assert hashlib.sha256(got).hexdigest() == want["h2d_gpu_sha256"]
+
+
+GEOMETRIES = [
+    # (layers_total, num_layers, start, kv, ng, nh, tokens, heads, dim, dtype, layout, tp, rank, n)
+    (4, 4, 0, 2, 64, 96, 16, 8, 128, np.uint16, "BLOCKWISE", 1, 0, 40),
+    (4, 4, 0, 2, 64, 96, 16, 8, 128, np.uint16, "LAYERWISE", 1, 0, 40),
+    (6, 3, 2, 2, 50, 70, 16, 1, 128, np.uint16, "BLOCKWISE", 1, 0, 33),   # 4 KiB chunks, layer window
+    (5, 5, 0, 1, 30, 40, 64, 1, 576, np.uint16, "BLOCKWISE", 1, 0, 20),   # MLA latent, 72 KiB chunks
+    (3, 3, 0, 2, 20, 20, 1, 1, 24, np.uint16, "BLOCKWISE", 1, 0, 7),      # 48 B chunk: partial row
+    (3, 2, 1, 2, 20, 30, 1, 5, 104, np.uint16, "LAYERWISE", 1, 0, 9),     # 1040 B = 65 vectors
+    (2, 2, 0, 2, 40, 40, 16, 2, 128, np.uint16, "BLOCKWISE", 4, 3, 25),   # TP host chunk, rank 3
+    (130, 130, 0, 2, 6, 8, 1, 1, 64, np.uint16, "BLOCKWISE", 1, 0, 5),    # >128 layers: 2 launches
+    (2, 2, 0, 2, 600, 700, 2, 2, 32, np.uint32, "BLOCKWISE", 1, 0, 520),  # many tiles
+]
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("geo", GEOMETRIES, ids=[f"g{i}" for i in range(len(GEOMETRIES))])
+def test_geometries_match_oracle(dev, geo, mode):
+    lt, nl, st, kv, ng, nh, t, h, d, dt, layout, tp, rank, n = geo
+    case = KVCase(layers_total=lt, num_layers=nl, start_layer=st, kv=kv, ng=ng, nh=nh, tokens=t,
+                  heads=h, dim=d, dtype=dt, layout=layout, tp=tp, rank=rank).fill(seed=lt * 7 + n)
+    gids = inputs.distinct_ids(n + 1, n, ng)
+    cids = inputs.distinct_ids(n + 2, n, nh)
+    check_case(case, gids, cids, mode)
+
+
+@pytest.mark.parametrize("cus", [1, 3, 256])
+def test_zero_copy_cu_limits(dev, cus):
+    case = KVCase(layers_total=4, num_layers=4, start_layer=0, kv=2, ng=80, nh=80, tokens=16,
+                  heads=2, dim=128).fill(seed=cus)
+    check_case(case, inputs.distinct_ids(1, 64, 80), inputs.distinct_ids(2, 64, 80), 0, cus)
+
+
+@pytest.mark.parametrize("run", [1, 8, 64])
+def test_staged_runs_and_small_staging(dev, run):
+    """Copy-engine path with a tiny staging buffer: many pieces, run merging
+    across consecutive host ids, and a layer window split."""
+    from flexkv_amd import _lib
+    _lib.set_staging_bytes(1 << 20)
+    try:
+        case = KVCase(layers_total=8, num_layers=8, start_layer=0, kv=2, ng=256, nh=512,
+                      tokens=16, heads=2, dim=128).fill(seed=run)
+        gids = inputs.run_ids(3, 128, 256, run)
+        cids = inputs.run_ids(4, 128, 512, run)
+        check_case(case, gids, cids, 1)
+        # one block row (8*2*8 KiB = 128 KiB) per half would not fit 64 KiB
+        _lib.release_staging()
+        _lib.set_staging_bytes(128 << 10)
+        check_case(case, gids, cids, 1)
+    finally:
+        _lib.release_staging()
+        _lib.set_staging_bytes(0)
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_duplicate_sources_and_single_block(dev, mode):
+    case = KVCase(layers_total=2, num_layers=2, start_layer=0, kv=2, ng=8, nh=16, tokens=16,
+                  heads=2, dim=64).fill(seed=2)
+    gids = np.array([3, 3, 5, 3], dtype=np.int64)
+    cids = np.array([0, 9, 4, 15], dtype=np.int64)
+    from gpu_util import DeviceCase, abi_transfer
+    dc = DeviceCase(case)
+    abi_transfer(dc, gids, cids, h2d=False, mode=mode)
+    torch.cuda.synchronize()
+    assert np.array_equal(dc.host_np(), _oracle_d2h(case, gids, cids, mode))
+    check_case(case, gids[:1], cids[:1], mode)
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_empty_transfer_is_noop(dev, mode):
+    case = KVCase(layers_total=2, num_layers=2, start_layer=0, kv=2, ng=8, nh=8, tokens=16,
+                  heads=2, dim=64).fill(seed=1)
+    from gpu_util import DeviceCase, abi_transfer
+    dc = DeviceCase(case)
+    empty = np.zeros(0, np.int64)
+    abi_transfer(dc, empty, empty, h2d=False, mode=mode)
+    abi_transfer(dc, empty, empty, h2d=True, mode=mode)
+    torch.cuda.synchronize()
+    assert np.array_equal(dc.host_np(), case.host)
+    for g, w in zip(dc.gpu_np(), case.gpu):
+        assert np.array_equal(g, w)
+
+
+def test_rejected_arguments_launch_nothing(dev):
+    """Bad geometry is refused on the host with RuntimeError; nothing moves."""
+    from gpu_util import DeviceCase, abi_transfer
+    case = KVCase(layers_total=2, num_layers=2, start_layer=0, kv=2, ng=8, nh=8, tokens=16,
+                  heads=2, dim=64).fill(seed=1)
+    dc = DeviceCase(case)
+    ok = np.array([1, 2], np.int64)
+    # Bounds are checked against the allocation holding each pointer (torch
+    # may place small tensors inside one larger segment), so use ids far past it.
+    far = 1 << 22
+    bad_cases = [
+        (np.array([1, far], np.int64), ok, {}),          # gpu id past the layer allocation
+        (ok, np.array([far, 1], np.int64), {}),          # cpu id past the host cache
+        (np.array([-1, 2], np.int64), ok, {}),           # negative id
+    ]
+    for mode in MODES:
+        for g, c, ov in bad_cases:
+            with pytest.raises(RuntimeError):
+                abi_transfer(dc, g, c, h2d=False, mode=mode, **ov)
+    for mode in (0, 1):
+        with pytest.raises(RuntimeError, match="multiples of 16"):
+            abi_transfer(dc, ok, ok, h2d=False, mode=mode, chunk=24)
+    with pytest.raises(RuntimeError, match="use_ce_transfer"):
+        abi_transfer(dc, ok, ok, h2d=False, mode=7)
+    with pytest.raises(RuntimeError):
+        abi_transfer(dc, ok, ok, h2d=False, mode=0, start_layer=far)  # layer past host cache
+    torch.cuda.synchronize()
+    assert np.array_equal(dc.host_np(), case.host)
+
+
+def test_pageable_host_cache_is_refused(dev):
+    from flexkv_amd import c_ext
+    gpu = torch.zeros(2, 4, 16, 2, 64, dtype=torch.int16, device=dev)
+    ptrs = torch.tensor([gpu.data_ptr()], dtype=torch.int64)
+    host = torch.zeros(4 * 2 * 16 * 2 * 64, dtype=torch.int16)  # pageable
+    ids = torch.tensor([0, 1], dtype=torch.int64)
+    with pytest.raises(RuntimeError, match="pinned"):
+        c_ext.transfer_kv_blocks(ids, ptrs, gpu[0].numel() * 2, gpu[0, 0].numel() * 2, ids, host,
+                                 16 * 2 * 64 * 2, 2 * 16 * 2 * 64 * 2, 2 * 16 * 2 * 64 * 2,
+                                 16 * 2 * 64 * 2, 0, -1, False, False, False)
+
+
+def test_unaligned_chunk_per_chunk_ce_matches_oracle(dev):
+    """24-byte chunks: the per-chunk copy-engine loop copies them exactly,
+    like the reference CE mode (csrc/transfer.cu:113-117)."""
+    case = KVCase(layers_total=2, num_layers=2, start_layer=0, kv=2, ng=10, nh=12, tokens=1,
+                  heads=1, dim=12).fill(seed=8)
+    check_case(case, inputs.distinct_ids(1, 6, 10), inputs.distinct_ids(2, 6, 12), 2)
+
+
+@pytest.mark.parametrize("use_ce", [False, True])
+def test_c_ext_dropin_on_side_stream(dev, use_ce):
+    """The reference call shape: 15 positional args, pinned id tensors, on the
+    current (non-default) stream."""
+    from flexkv_amd import c_ext
+    from flexkv_amd.common.storage import KVCacheLayout, KVCacheLayoutType
+    from flexkv_amd.storage.allocator import CPUAllocator
+    L, NG, NH = 4, 32, 64
+    gl = KVCacheLayout(KVCacheLayoutType.LAYERWISE, L, NG, 16, 8, 128)
+    cl = KVCacheLayout(KVCacheLayoutType.BLOCKWISE, L, NH, 16, 8, 128)
+    dt = torch.float16
+    gen = torch.Generator().manual_seed(5)
+    src = [torch.randn(gl.kv_shape[1:], generator=gen, dtype=torch.float32).to(dt) for _ in range(L)]
+    layers = [s.to(dev) for s in src]
+    cache = CPUAllocator.allocate(cl, dt).get_tensor()
+    cache.zero_()
+    chunk, gkv, _, gblk = gl.div_layer(L).byte_strides(dt)
+    _, ckv, clay, cblk = cl.byte_strides(dt)
+    gids = torch.tensor([5, 1, 30, 7], dtype=torch.int64).pin_memory()
+    cids = torch.tensor([60, 2, 33, 0], dtype=torch.int64).pin_memory()
+    ptrs = torch.tensor([t.data_ptr() for t in layers], dtype=torch.int64).pin_memory()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        c_ext.transfer_kv_blocks(gids, ptrs, gkv, gblk, cids, cache, ckv, clay, cblk, chunk, 0,
+                                 8, False, use_ce, False)
+    view = cache.view(NH, L, 2, 16, 8, 128)
+    for i in range(4):
+        for l in range(L):
+            assert torch.equal(view[cids[i], l], src[l][:, gids[i]])
+    assert torch.count_nonzero(view[torch.tensor([3, 4, 5])]) == 0
+    for t in layers:
+        t.zero_()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        c_ext.transfer_kv_blocks(gids, ptrs, gkv, gblk, cids, cache, ckv, clay, cblk, chunk, 0,
+                                 8, True, use_ce, False)
+    torch.cuda.synchronize()
+    for l in range(L):
+        assert torch.equal(layers[l][:, gids].cpu(), src[l][:, gids])
