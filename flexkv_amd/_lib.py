@@ -28,6 +28,8 @@ FKV_HOST_NONCOHERENT = 2
 # Names declared in include/flexkv_hip.h; tests check the library exports all.
 EXPORTED_SYMBOLS = (
     "fkv_transfer_kv_blocks",
+    "fkv_gather_kv_blocks",
+    "fkv_scatter_kv_blocks",
     "fkv_last_error",
     "fkv_host_alloc",
     "fkv_host_free",
@@ -66,6 +68,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     f.restype = c_int
     f.argtypes = [c_int, c_int, c_int, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64,
                   c_i64, c_i64, c_i64, c_vp, c_int, c_int, c_int, c_int]
+    for name in ("fkv_gather_kv_blocks", "fkv_scatter_kv_blocks"):
+        g = getattr(lib, name)
+        g.restype = c_int
+        g.argtypes = [c_int, c_int, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_sz, c_vp, c_int]
     lib.fkv_last_error.restype = ctypes.c_char_p
     lib.fkv_last_error.argtypes = []
     lib.fkv_host_alloc.restype = c_int

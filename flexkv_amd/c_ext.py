@@ -13,7 +13,7 @@ import torch
 
 from . import _lib
 
-__all__ = ["transfer_kv_blocks"]
+__all__ = ["transfer_kv_blocks", "gather_kv_blocks", "scatter_kv_blocks"]
 
 
 def _require_int64_host(t: torch.Tensor, name: str) -> None:
@@ -80,3 +80,41 @@ def transfer_kv_blocks(gpu_block_id_tensor: torch.Tensor,
         1 if is_mla else 0)
     if rc != 0:
         raise RuntimeError(_lib.last_error() or f"fkv_transfer_kv_blocks failed ({rc})")
+
+
+def _contiguous(fn_name: str, gpu_block_id_tensor, gpu_layer_ptrs_tensor, gpu_kv_stride_in_bytes,
+                gpu_block_stride_in_bytes, chunk_size_in_bytes, buffer, is_mla) -> None:
+    _require_int64_host(gpu_block_id_tensor, "gpu_block_id_tensor")
+    _require_int64_host(gpu_layer_ptrs_tensor, "gpu_layer_ptrs_tensor")
+    if not isinstance(buffer, torch.Tensor) or not buffer.is_contiguous():
+        raise TypeError("buffer must be a contiguous torch.Tensor")
+    if not torch.cuda.is_available():
+        raise RuntimeError(f"{fn_name} needs a HIP device; none is visible")
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = getattr(lib, fn_name)(
+        int(gpu_block_id_tensor.numel()), int(gpu_layer_ptrs_tensor.numel()),
+        gpu_block_id_tensor.data_ptr(), gpu_layer_ptrs_tensor.data_ptr(),
+        int(gpu_kv_stride_in_bytes), int(gpu_block_stride_in_bytes), int(chunk_size_in_bytes),
+        buffer.data_ptr(), buffer.numel() * buffer.element_size(), stream, 1 if is_mla else 0)
+    if rc != 0:
+        raise RuntimeError(_lib.last_error() or f"{fn_name} failed ({rc})")
+
+
+def gather_kv_blocks(gpu_block_id_tensor: torch.Tensor, gpu_layer_ptrs_tensor: torch.Tensor,
+                     gpu_kv_stride_in_bytes: int, gpu_block_stride_in_bytes: int,
+                     chunk_size_in_bytes: int, buffer: torch.Tensor, is_mla: bool = False) -> None:
+    """Pack the selected blocks of every layer into `buffer`, laid out
+    [block][layer][K|V][chunk] (extension; no reference counterpart)."""
+    _contiguous("fkv_gather_kv_blocks", gpu_block_id_tensor, gpu_layer_ptrs_tensor,
+                gpu_kv_stride_in_bytes, gpu_block_stride_in_bytes, chunk_size_in_bytes, buffer,
+                is_mla)
+
+
+def scatter_kv_blocks(gpu_block_id_tensor: torch.Tensor, gpu_layer_ptrs_tensor: torch.Tensor,
+                      gpu_kv_stride_in_bytes: int, gpu_block_stride_in_bytes: int,
+                      chunk_size_in_bytes: int, buffer: torch.Tensor, is_mla: bool = False) -> None:
+    """Inverse of gather_kv_blocks: unpack `buffer` into the selected blocks."""
+    _contiguous("fkv_scatter_kv_blocks", gpu_block_id_tensor, gpu_layer_ptrs_tensor,
+                gpu_kv_stride_in_bytes, gpu_block_stride_in_bytes, chunk_size_in_bytes, buffer,
+                is_mla)

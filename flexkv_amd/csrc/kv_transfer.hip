@@ -24,6 +24,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -33,12 +34,46 @@
 
 namespace {
 
+// Rows (64 lanes x 16 B) each wavefront keeps in flight: the zero-copy
+// kernel is PCIe-latency bound, the staging gather/scatter HBM bound.
+#ifndef FKV_UNROLL
+#define FKV_UNROLL 8
+#endif
+#ifndef FKV_UNROLL_HBM
+#define FKV_UNROLL_HBM 32
+#endif
+// Staging gather/scatter launch shape: 1 = one workgroup per tile (grid =
+// tiles), 0 = an occupancy-sized grid looping over tiles.
+#ifndef FKV_HBM_ONEPASS
+#define FKV_HBM_ONEPASS 1
+#endif
+// Tiles per occupancy slot the tiling aims for (zero-copy / staging).
+#ifndef FKV_TILE_FACTOR
+#define FKV_TILE_FACTOR 4
+#endif
+#ifndef FKV_TILE_FACTOR_HBM
+#define FKV_TILE_FACTOR_HBM 16
+#endif
+#ifndef FKV_NT_LOAD
+#define FKV_NT_LOAD 1
+#endif
+#ifndef FKV_NT_STORE
+#define FKV_NT_STORE 1
+#endif
+
 constexpr int kThreads = 256;               // 4 wavefronts of 64 lanes
 constexpr int kWaves = kThreads / 64;
-constexpr int kUnroll = 8;                  // rows in flight per wavefront
+constexpr int kUnrollZeroCopy = FKV_UNROLL;
+constexpr int kUnrollHbm = FKV_UNROLL_HBM;
 constexpr int kMaxLayersPerLaunch = 128;    // layer pointers in kernel args
 constexpr int kMaxTileBlocks = 64;
 constexpr int kMaxDevices = 64;
+constexpr int kMaxDmaStreams = 8;
+constexpr int kDefaultDmaStreams = 2;
+// Compute units of the zero-copy kernel when the caller passes -1: enough
+// loads/stores in flight to saturate the PCIe Gen5 x16 link (measured on
+// MI355X: 8 CUs reach the link's copy rate; more add contention).
+constexpr int kAutoZeroCopyCus = 8;
 constexpr size_t kDefaultStagingBytes = size_t(256) << 20;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -48,7 +83,7 @@ typedef __attribute__((address_space(1))) u32x4 gvec;
 
 struct CopyArgs {
   const int64_t* ids;        // device-visible (gpu_id, cpu_id) pairs
-  char* cpu_base;            // CPU side incl. start layer and start offset
+  char* cpu_base;            // CPU side of launch layer 0, block index 0
   int64_t gpu_kv_stride;
   int64_t gpu_block_stride;
   int64_t cpu_kv_stride;
@@ -59,27 +94,46 @@ struct CopyArgs {
   int32_t num_blocks;
   int32_t num_layers;        // layers in this launch (<= kMaxLayersPerLaunch)
   int32_t kv_dim;
-  int32_t tile_blocks;
+  int32_t tile_blocks;       // a tile is tile_blocks blocks x tile_layers layers
+  int32_t tile_layers;
+  int32_t tiles_b;           // tiles along the block axis
   int32_t num_tiles;
   uint64_t layer_ptr[kMaxLayersPerLaunch];
 };
 
+// A value every lane of the wavefront holds, moved to a scalar register.
+__device__ inline int64_t wave_uniform(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(x) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // kH2D: copy CPU side -> GPU side.  kIotaCpu: the CPU side is staging and
 // block i of the launch sits at CPU-side block index i (ids[2i+1] unused).
+// Row addresses are wave-uniform (scalar registers); each lane adds its own
+// 16-byte slot, so one 32-bit lane offset serves every access.
 template <bool kH2D, bool kIotaCpu>
 __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
+  constexpr int kUnroll = kIotaCpu ? kUnrollHbm : kUnrollZeroCopy;
   __shared__ int64_t s_gid[kMaxTileBlocks];
   __shared__ int64_t s_cid[kMaxTileBlocks];
 
   const int lane = threadIdx.x & 63;
+  const uint32_t lane_off = static_cast<uint32_t>(lane) * 16;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t kv = static_cast<uint32_t>(a.kv_dim);
   const uint32_t rpc = static_cast<uint32_t>(a.rows_per_chunk);
-  const uint32_t items_per_block = static_cast<uint32_t>(a.num_layers) * kv;
+  // true when every row of a chunk is a full 64-lane row
+  const bool full_rows = (a.chunk_vec & 63) == 0;
 
   for (int tile = blockIdx.x; tile < a.num_tiles; tile += gridDim.x) {
-    const int b0 = tile * a.tile_blocks;
+    const int tb = tile % a.tiles_b;
+    const int tl = tile / a.tiles_b;
+    const int b0 = tb * a.tile_blocks;
     const int nb = min(a.tile_blocks, a.num_blocks - b0);
+    const int l0 = tl * a.tile_layers;
+    const uint32_t nl = static_cast<uint32_t>(min(a.tile_layers, a.num_layers - l0));
+    const uint32_t items_per_block = nl * kv;
     __syncthreads();  // previous tile's readers are done with the LDS ids
     if (threadIdx.x < nb) {
       const int64_t* pr = a.ids + 2 * static_cast<int64_t>(b0 + threadIdx.x);
@@ -91,7 +145,8 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
     const uint32_t rows = static_cast<uint32_t>(nb) * items_per_block * rpc;
     for (uint32_t g = static_cast<uint32_t>(wave) * kUnroll; g < rows;
          g += kWaves * kUnroll) {
-      // Decompose the group's first row once; later rows advance a cursor.
+      // Decompose the group's first row once; later rows advance a cursor
+      // over (block, layer, K|V, row) in that order.
       uint32_t item = g / rpc;
       uint32_t rr = g - item * rpc;
       uint32_t bi = item / items_per_block;
@@ -104,15 +159,17 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
       bool live[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        const int64_t vec = static_cast<int64_t>(rr) * 64 + lane;
-        live[u] = (g + u < rows) && (vec < a.chunk_vec);
         const uint32_t bsafe = min(bi, static_cast<uint32_t>(nb - 1));
-        char* gpu = reinterpret_cast<char*>(a.layer_ptr[min(l, items_per_block / kv - 1)]) +
-                    static_cast<int64_t>(k) * a.gpu_kv_stride +
-                    s_gid[bsafe] * a.gpu_block_stride + vec * 16;
-        char* cpu = a.cpu_base + static_cast<int64_t>(l) * a.cpu_layer_stride +
-                    static_cast<int64_t>(k) * a.cpu_kv_stride +
-                    s_cid[bsafe] * a.cpu_block_stride + vec * 16;
+        const uint32_t layer = static_cast<uint32_t>(l0) + min(l, nl - 1);
+        const int64_t gid = wave_uniform(s_gid[bsafe]);
+        const int64_t cid = wave_uniform(s_cid[bsafe]);
+        const int64_t row_off = static_cast<int64_t>(rr) * (64 * 16);
+        char* gpu = reinterpret_cast<char*>(a.layer_ptr[layer]) +
+                    static_cast<int64_t>(k) * a.gpu_kv_stride + gid * a.gpu_block_stride + row_off;
+        char* cpu = a.cpu_base + static_cast<int64_t>(layer) * a.cpu_layer_stride +
+                    static_cast<int64_t>(k) * a.cpu_kv_stride + cid * a.cpu_block_stride + row_off;
+        live[u] = (g + u < rows) &&
+                  (full_rows || static_cast<int64_t>(rr) * 64 + lane < a.chunk_vec);
         src[u] = kH2D ? cpu : gpu;
         dst[u] = kH2D ? gpu : cpu;
         // advance the cursor by one row
@@ -120,7 +177,7 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
           rr = 0;
           if (++k == kv) {
             k = 0;
-            if (++l == items_per_block / kv) {
+            if (++l == nl) {
               l = 0;
               ++bi;
             }
@@ -130,11 +187,25 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
       u32x4 v[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        if (live[u]) v[u] = __builtin_nontemporal_load((const gvec*)src[u]);
+        if (live[u]) {
+          const gvec* p = (const gvec*)(src[u] + lane_off);
+#if FKV_NT_LOAD
+          v[u] = __builtin_nontemporal_load(p);
+#else
+          v[u] = *p;
+#endif
+        }
       }
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        if (live[u]) __builtin_nontemporal_store(v[u], (gvec*)dst[u]);
+        if (live[u]) {
+          gvec* p = (gvec*)(dst[u] + lane_off);
+#if FKV_NT_STORE
+          __builtin_nontemporal_store(v[u], p);
+#else
+          *p = v[u];
+#endif
+        }
       }
     }
   }
@@ -232,9 +303,12 @@ struct DeviceState {
   int occ_staged[2] = {0, 0};
   char* staging = nullptr;
   size_t staging_bytes = 0;
-  hipStream_t side = nullptr;
-  hipEvent_t ev_fill[2] = {nullptr, nullptr};   // staging half filled
-  hipEvent_t ev_drain[2] = {nullptr, nullptr};  // staging half consumed
+  // DMA side streams (one SDMA queue each) and the events ordering them
+  // against the caller's stream, per staging half.
+  int num_dma = 0;
+  hipStream_t dma[kMaxDmaStreams] = {};
+  hipEvent_t ev_compute[2] = {nullptr, nullptr};   // recorded on the caller's stream
+  hipEvent_t ev_dma[2][kMaxDmaStreams] = {};       // recorded on each DMA stream
 };
 
 DeviceState g_dev[kMaxDevices];
@@ -463,6 +537,29 @@ struct ProfRecorder {
   }
 };
 
+// Tiles are tb blocks x tl layers.  Start from whole block rows (one block,
+// every layer) and halve the layer window until there are about `factor`
+// tiles per occupancy slot of the grid; when blocks are plentiful, group
+// several per tile so one LDS id load serves more rows.  Rows per tile stay
+// below 2^31.  Measured on MI355X (2 GiB gather at the Llama-3-8B shape):
+// 32 rows in flight per wavefront with one workgroup per tile and 16 tiles
+// per slot reaches the device's plain-copy rate (~5.9 TB/s).
+void choose_tiles(int nb, int nl, int kv, int rpc, int grid_cap, int factor, CopyArgs* a) {
+  const int64_t target = factor * static_cast<int64_t>(std::max(1, grid_cap));
+  auto tiles = [&](int tb, int tl) {
+    return static_cast<int64_t>((nb + tb - 1) / tb) * ((nl + tl - 1) / tl);
+  };
+  int tb = 1, tl = nl;
+  while (tl > 1 && tiles(tb, tl) < target) tl = (tl + 1) / 2;
+  while (tb < kMaxTileBlocks && tiles(tb * 2, tl) >= target) tb *= 2;
+  while (tb > 1 && static_cast<int64_t>(tb) * tl * kv * rpc >= (int64_t(1) << 31)) tb /= 2;
+  while (tl > 1 && static_cast<int64_t>(tb) * tl * kv * rpc >= (int64_t(1) << 31)) tl = (tl + 1) / 2;
+  a->tile_blocks = tb;
+  a->tile_layers = tl;
+  a->tiles_b = (nb + tb - 1) / tb;
+  a->num_tiles = static_cast<int32_t>(tiles(tb, tl));
+}
+
 // Fill the per-launch part of CopyArgs and launch over `nb` blocks starting at
 // block `b0` of the (already packed) id list, for GPU layers [l0, l0 + nl).
 // `cpu_base` is the CPU-side address of launch layer 0 of block index 0.
@@ -485,15 +582,10 @@ int launch_copy(const Geometry& g, char* ids_dev, char* cpu_base, int64_t cks, i
   a.num_layers = nl;
   a.kv_dim = g.kv;
   for (int l = 0; l < nl; ++l) a.layer_ptr[l] = reinterpret_cast<uint64_t>(g.layer_ptrs[l0 + l]);
-  // Tile: enough tiles to keep every workgroup of the grid busy several
-  // times over, at most kMaxTileBlocks blocks, and rows within uint32.
-  const int64_t rows_per_block = static_cast<int64_t>(nl) * g.kv * a.rows_per_chunk;
-  int tb = static_cast<int>(std::max<int64_t>(1, nb / std::max(1, 4 * grid_cap)));
-  tb = std::min(tb, kMaxTileBlocks);
-  while (tb > 1 && rows_per_block * tb > (int64_t(1) << 31)) tb /= 2;
-  a.tile_blocks = tb;
-  a.num_tiles = (nb + tb - 1) / tb;
-  const int grid = std::max(1, std::min(grid_cap, a.num_tiles));
+  choose_tiles(nb, nl, g.kv, a.rows_per_chunk, grid_cap,
+               kIota ? FKV_TILE_FACTOR_HBM : FKV_TILE_FACTOR, &a);
+  int grid = std::max(1, std::min(grid_cap, a.num_tiles));
+  if (kIota && FKV_HBM_ONEPASS) grid = a.num_tiles;
   hipEvent_t ev = nullptr;
   if (prof.begin(stream, &ev)) return kInval;
   hipLaunchKernelGGL((kv_chunk_copy_kernel<kH2D, kIota>), dim3(grid), dim3(kThreads), 0, stream, a);
@@ -529,7 +621,8 @@ int transfer_zero_copy(const Geometry& g, hipStream_t stream, int dev, int trans
   char* ids_dev = nullptr;
   int rc = pack_ids(g, &ids_dev);
   if (rc) return rc;
-  int cus = transfer_cus <= 0 ? std::min(32, d.num_cus) : std::min(transfer_cus, d.num_cus);
+  int cus = transfer_cus <= 0 ? std::min(kAutoZeroCopyCus, d.num_cus)
+                              : std::min(transfer_cus, d.num_cus);
   const int grid_cap = cus * (h2d ? d.occ_zero_copy[1] : d.occ_zero_copy[0]);
   char* cpu_dev = g.cpu_info.dev_ptr + g.startoff +
                   static_cast<int64_t>(g.start_layer) * g.cls;
@@ -583,17 +676,28 @@ void build_runs(const Geometry& g, int b0, int nb, int l0, int nl, std::vector<R
   }
 }
 
-int ensure_staging(DeviceState& d, int dev, size_t need_half) {
+int dma_streams_wanted() {
+  const char* e = getenv("FLEXKV_DMA_STREAMS");
+  int n = e ? atoi(e) : kDefaultDmaStreams;
+  return std::max(1, std::min(n, kMaxDmaStreams));
+}
+
+int ensure_staging(DeviceState& d, size_t need_half) {
   size_t want = g_staging_request.load();
   if (want == 0) want = kDefaultStagingBytes;
   want = std::max(want, 2 * need_half);
   want = (want + 4095) & ~size_t(4095);
-  if (!d.side) {
-    FKV_HIP(hipStreamCreateWithFlags(&d.side, hipStreamNonBlocking));
-    for (int h = 0; h < 2; ++h) {
-      FKV_HIP(hipEventCreateWithFlags(&d.ev_fill[h], hipEventDisableTiming));
-      FKV_HIP(hipEventCreateWithFlags(&d.ev_drain[h], hipEventDisableTiming));
-    }
+  const int nd = dma_streams_wanted();
+  if (!d.ev_compute[0]) {
+    for (int h = 0; h < 2; ++h)
+      FKV_HIP(hipEventCreateWithFlags(&d.ev_compute[h], hipEventDisableTiming));
+  }
+  while (d.num_dma < nd) {
+    const int s = d.num_dma;
+    FKV_HIP(hipStreamCreateWithFlags(&d.dma[s], hipStreamNonBlocking));
+    for (int h = 0; h < 2; ++h)
+      FKV_HIP(hipEventCreateWithFlags(&d.ev_dma[h][s], hipEventDisableTiming));
+    d.num_dma = s + 1;
   }
   if (d.staging && d.staging_bytes == want) return 0;
   if (d.staging) {
@@ -605,12 +709,28 @@ int ensure_staging(DeviceState& d, int dev, size_t need_half) {
   FKV_HIP(hipMalloc(&p, want));
   d.staging = static_cast<char*>(p);
   d.staging_bytes = want;
-  (void)dev;
   return 0;
 }
 
-int issue_runs(const std::vector<Run>& runs, char* staging, bool h2d, hipStream_t s) {
-  for (const Run& r : runs) {
+// Split `runs` into `parts` consecutive groups of about equal bytes; group i
+// is runs[cut[i], cut[i+1]).
+void split_runs(const std::vector<Run>& runs, int parts, std::vector<size_t>& cut) {
+  cut.assign(parts + 1, runs.size());
+  cut[0] = 0;
+  int64_t total = 0;
+  for (const Run& r : runs) total += r.bytes;
+  int64_t acc = 0;
+  int next = 1;
+  for (size_t i = 0; i < runs.size() && next < parts; ++i) {
+    acc += runs[i].bytes;
+    while (next < parts && acc * parts >= total * next) cut[next++] = i + 1;
+  }
+}
+
+int issue_runs(const std::vector<Run>& runs, size_t lo, size_t hi, char* staging, bool h2d,
+               hipStream_t s) {
+  for (size_t i = lo; i < hi; ++i) {
+    const Run& r = runs[i];
     if (h2d) {
       FKV_HIP(hipMemcpyAsync(staging + r.staging_off, r.host, r.bytes, hipMemcpyHostToDevice, s));
     } else {
@@ -620,6 +740,13 @@ int issue_runs(const std::vector<Run>& runs, char* staging, bool h2d, hipStream_
   return 0;
 }
 
+// Copy-engine transfer through double-buffered HBM staging.
+//  D2H, per piece: [caller stream] wait until every DMA stream drained this
+//  half -> gather kernel -> event; [DMA stream s] wait event -> its share of
+//  the host runs -> event.
+//  H2D, per piece: [DMA stream s] wait until the scatter of this half's
+//  previous piece finished -> its share of the runs -> event; [caller stream]
+//  wait all DMA events -> scatter kernel -> event.
 int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   DeviceState& d = g_dev[dev];
   std::lock_guard<std::mutex> lk(d.mu);
@@ -632,19 +759,23 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
 
   // A piece is a run of whole blocks over a layer window; the window covers
   // all layers unless one block row would not fit a staging half.
-  const size_t half_default = (g_staging_request.load() ? g_staging_request.load() : kDefaultStagingBytes) / 2;
+  const size_t req = g_staging_request.load();
+  const size_t half_default = (req ? req : kDefaultStagingBytes) / 2;
   int nl_piece = std::min(g.num_layers, kMaxLayersPerLaunch);
   while (nl_piece > 1 && static_cast<size_t>(nl_piece) * g.kv * g.chunk > half_default) nl_piece /= 2;
   const size_t row_bytes = static_cast<size_t>(nl_piece) * g.kv * g.chunk;
-  rc = ensure_staging(d, dev, row_bytes);
+  rc = ensure_staging(d, row_bytes);
   if (rc) return rc;
   const size_t half = d.staging_bytes / 2;
   const int blocks_per_piece = static_cast<int>(std::max<size_t>(1, half / row_bytes));
   const int grid_cap = d.num_cus * (h2d ? d.occ_staged[1] : d.occ_staged[0]);
+  const int nd = std::min(d.num_dma, dma_streams_wanted());
 
   ProfRecorder prof;
   bool used[2] = {false, false};
+  bool dma_used[2][kMaxDmaStreams] = {};
   std::vector<Run> runs;
+  std::vector<size_t> cut;
   int piece = 0;
   for (int l0 = 0; l0 < g.num_layers; l0 += nl_piece) {
     const int nl = std::min(nl_piece, g.num_layers - l0);
@@ -655,43 +786,125 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
       const int h = piece & 1;
       char* stg = d.staging + h * half;
       build_runs(g, b0, nb, l0, nl, runs);
-      const int64_t bytes = static_cast<int64_t>(nb) * nl * g.kv * g.chunk;
-      hipEvent_t ev = nullptr;
+      const int parts = std::max(1, std::min<int>(nd, static_cast<int>(runs.size())));
+      split_runs(runs, parts, cut);
       if (!h2d) {
-        // gather GPU -> staging on the caller's stream, then DMA staging -> host
-        if (used[h]) FKV_HIP(hipStreamWaitEvent(stream, d.ev_drain[h], 0));
+        for (int s = 0; s < nd; ++s)
+          if (dma_used[h][s]) FKV_HIP(hipStreamWaitEvent(stream, d.ev_dma[h][s], 0));
         rc = launch_copy<false, true>(g, ids_dev, stg, g.kv == 1 ? 0 : g.chunk, cls, cbs, b0, nb,
                                       l0, nl, grid_cap, stream, prof);
         if (rc) return rc;
-        FKV_HIP(hipEventRecord(d.ev_fill[h], stream));
-        FKV_HIP(hipStreamWaitEvent(d.side, d.ev_fill[h], 0));
-        if ((rc = prof.begin(d.side, &ev))) return rc;
-        if ((rc = issue_runs(runs, stg, false, d.side))) return rc;
-        if ((rc = prof.end(d.side, ev, bytes, static_cast<int64_t>(runs.size()), true))) return rc;
-        FKV_HIP(hipEventRecord(d.ev_drain[h], d.side));
+        FKV_HIP(hipEventRecord(d.ev_compute[h], stream));
+        for (int s = 0; s < parts; ++s) {
+          hipEvent_t ev = nullptr;
+          int64_t bytes = 0;
+          for (size_t i = cut[s]; i < cut[s + 1]; ++i) bytes += runs[i].bytes;
+          FKV_HIP(hipStreamWaitEvent(d.dma[s], d.ev_compute[h], 0));
+          if ((rc = prof.begin(d.dma[s], &ev))) return rc;
+          if ((rc = issue_runs(runs, cut[s], cut[s + 1], stg, false, d.dma[s]))) return rc;
+          if ((rc = prof.end(d.dma[s], ev, bytes, static_cast<int64_t>(cut[s + 1] - cut[s]), true)))
+            return rc;
+          FKV_HIP(hipEventRecord(d.ev_dma[h][s], d.dma[s]));
+          dma_used[h][s] = true;
+        }
       } else {
-        // DMA host -> staging on the side stream, then scatter on the caller's
-        if (used[h]) FKV_HIP(hipStreamWaitEvent(d.side, d.ev_drain[h], 0));
-        if ((rc = prof.begin(d.side, &ev))) return rc;
-        if ((rc = issue_runs(runs, stg, true, d.side))) return rc;
-        if ((rc = prof.end(d.side, ev, bytes, static_cast<int64_t>(runs.size()), true))) return rc;
-        FKV_HIP(hipEventRecord(d.ev_fill[h], d.side));
-        FKV_HIP(hipStreamWaitEvent(stream, d.ev_fill[h], 0));
+        for (int s = 0; s < parts; ++s) {
+          hipEvent_t ev = nullptr;
+          int64_t bytes = 0;
+          for (size_t i = cut[s]; i < cut[s + 1]; ++i) bytes += runs[i].bytes;
+          if (used[h]) FKV_HIP(hipStreamWaitEvent(d.dma[s], d.ev_compute[h], 0));
+          if ((rc = prof.begin(d.dma[s], &ev))) return rc;
+          if ((rc = issue_runs(runs, cut[s], cut[s + 1], stg, true, d.dma[s]))) return rc;
+          if ((rc = prof.end(d.dma[s], ev, bytes, static_cast<int64_t>(cut[s + 1] - cut[s]), true)))
+            return rc;
+          FKV_HIP(hipEventRecord(d.ev_dma[h][s], d.dma[s]));
+          FKV_HIP(hipStreamWaitEvent(stream, d.ev_dma[h][s], 0));
+        }
         rc = launch_copy<true, true>(g, ids_dev, stg, g.kv == 1 ? 0 : g.chunk, cls, cbs, b0, nb,
                                      l0, nl, grid_cap, stream, prof);
         if (rc) return rc;
-        FKV_HIP(hipEventRecord(d.ev_drain[h], stream));
+        FKV_HIP(hipEventRecord(d.ev_compute[h], stream));
       }
       used[h] = true;
     }
   }
   // The caller's stream must not run ahead of the last DMA.
   for (int h = 0; h < 2; ++h)
-    if (used[h]) FKV_HIP(hipStreamWaitEvent(stream, d.ev_drain[h], 0));
+    for (int s = 0; s < nd; ++s)
+      if (dma_used[h][s]) FKV_HIP(hipStreamWaitEvent(stream, d.ev_dma[h][s], 0));
   FKV_HIP(hipStreamSynchronize(stream));
-  FKV_HIP(hipStreamSynchronize(d.side));
+  for (int s = 0; s < nd; ++s) FKV_HIP(hipStreamSynchronize(d.dma[s]));
   prof.flush();
   return 0;
+}
+
+// Gather (to_gpu = false) or scatter between the GPU cache and a contiguous
+// buffer laid out [block][layer][K|V][chunk]; g.cpu_ptr is the buffer and
+// g.cids is 0..n-1.  Uses every compute unit: the copy is HBM-bound.
+int transfer_contiguous(const Geometry& g, hipStream_t stream, int dev, bool to_gpu) {
+  DeviceState& d = g_dev[dev];
+  char* ids_dev = nullptr;
+  int rc = pack_ids(g, &ids_dev);
+  if (rc) return rc;
+  const int grid_cap = d.num_cus * (to_gpu ? d.occ_staged[1] : d.occ_staged[0]);
+  ProfRecorder prof;
+  for (int l0 = 0; l0 < g.num_layers; l0 += kMaxLayersPerLaunch) {
+    const int nl = std::min(kMaxLayersPerLaunch, g.num_layers - l0);
+    char* base = g.cpu_info.dev_ptr + static_cast<int64_t>(l0) * g.cls;
+    rc = to_gpu ? launch_copy<true, true>(g, ids_dev, base, g.cks, g.cls, g.cbs, 0, g.num_blocks,
+                                          l0, nl, grid_cap, stream, prof)
+                : launch_copy<false, true>(g, ids_dev, base, g.cks, g.cls, g.cbs, 0, g.num_blocks,
+                                           l0, nl, grid_cap, stream, prof);
+    if (rc) return rc;
+  }
+  FKV_HIP(hipStreamSynchronize(stream));
+  prof.flush();
+  return 0;
+}
+
+int contiguous_entry(int num_blocks, int num_layers, const int64_t* gpu_block_ids,
+                     void* const* gpu_layer_ptrs, int64_t gpu_kv_stride_bytes,
+                     int64_t gpu_block_stride_bytes, int64_t chunk_size_bytes, void* buffer,
+                     size_t buffer_bytes, fkv_stream_t stream, int is_mla, bool to_gpu) {
+  try {
+    t_err.clear();
+    if (num_blocks == 0 || num_layers == 0) return 0;
+    if (num_blocks < 0 || num_layers < 0)
+      return fail(kInval, "negative count: num_blocks=%d num_layers=%d", num_blocks, num_layers);
+    std::vector<int64_t> iota(static_cast<size_t>(num_blocks));
+    for (int i = 0; i < num_blocks; ++i) iota[i] = i;
+    Geometry g;
+    g.num_blocks = num_blocks;
+    g.start_layer = 0;
+    g.num_layers = num_layers;
+    g.kv = is_mla ? 1 : 2;
+    g.gids = gpu_block_ids;
+    g.cids = iota.data();
+    g.layer_ptrs = gpu_layer_ptrs;
+    g.gks = gpu_kv_stride_bytes;
+    g.gbs = gpu_block_stride_bytes;
+    g.chunk = chunk_size_bytes;
+    g.cks = g.kv == 1 ? 0 : chunk_size_bytes;
+    g.cls = static_cast<int64_t>(g.kv) * chunk_size_bytes;
+    g.cbs = static_cast<int64_t>(num_layers) * g.cls;
+    g.startoff = 0;
+    g.cpu_ptr = static_cast<char*>(buffer);
+    const __int128 need = static_cast<__int128>(num_blocks) * g.cbs;
+    if (need > static_cast<__int128>(buffer_bytes))
+      return fail(kInval, "buffer holds %zu bytes, the blocks need %lld", buffer_bytes,
+                  static_cast<long long>(need));
+    int rc = validate(g, FKV_XFER_KERNEL);
+    if (rc) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int dev = 0;
+    if ((rc = stream_device(s, &dev))) return rc;
+    if ((rc = ensure_device_basics(dev))) return rc;
+    return transfer_contiguous(g, s, dev, to_gpu);
+  } catch (const std::exception& e) {
+    return fail(static_cast<int>(hipErrorUnknown), "exception: %s", e.what());
+  } catch (...) {
+    return fail(static_cast<int>(hipErrorUnknown), "unknown exception");
+  }
 }
 
 // The reference copy-engine loop, csrc/transfer.cu:97-121: one async copy per
@@ -777,6 +990,25 @@ int fkv_transfer_kv_blocks(int num_blocks, int start_layer_id, int num_layers,
   } catch (...) {
     return fail(static_cast<int>(hipErrorUnknown), "unknown exception");
   }
+}
+
+int fkv_gather_kv_blocks(int num_blocks, int num_layers, const int64_t* gpu_block_ids,
+                         void* const* gpu_layer_ptrs, int64_t gpu_kv_stride_bytes,
+                         int64_t gpu_block_stride_bytes, int64_t chunk_size_bytes, void* buffer,
+                         size_t buffer_bytes, fkv_stream_t stream, int is_mla) {
+  return contiguous_entry(num_blocks, num_layers, gpu_block_ids, gpu_layer_ptrs,
+                          gpu_kv_stride_bytes, gpu_block_stride_bytes, chunk_size_bytes, buffer,
+                          buffer_bytes, stream, is_mla, false);
+}
+
+int fkv_scatter_kv_blocks(int num_blocks, int num_layers, const int64_t* gpu_block_ids,
+                          void* const* gpu_layer_ptrs, int64_t gpu_kv_stride_bytes,
+                          int64_t gpu_block_stride_bytes, int64_t chunk_size_bytes,
+                          const void* buffer, size_t buffer_bytes, fkv_stream_t stream,
+                          int is_mla) {
+  return contiguous_entry(num_blocks, num_layers, gpu_block_ids, gpu_layer_ptrs,
+                          gpu_kv_stride_bytes, gpu_block_stride_bytes, chunk_size_bytes,
+                          const_cast<void*>(buffer), buffer_bytes, stream, is_mla, true);
 }
 
 const char* fkv_last_error(void) { return t_err.c_str(); }

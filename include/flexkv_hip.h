@@ -94,6 +94,24 @@ int fkv_transfer_kv_blocks(int num_blocks, int start_layer_id, int num_layers,
                            int transfer_cus, int is_host_to_device,
                            int use_ce_transfer, int is_mla);
 
+/* Device-side gather / scatter between the per-layer GPU cache and one
+ * contiguous buffer laid out [num_blocks][num_layers][K|V][chunk] (block i of
+ * the id list at byte offset i * num_layers * kv * chunk).  This is the
+ * on-device half of FKV_XFER_CE exposed on its own, for callers that move the
+ * packed blocks themselves (RDMA, file I/O, peer GPUs).  The buffer may be
+ * device or pinned host memory; buffer_bytes must cover every block.  Same
+ * checks and synchronous return as fkv_transfer_kv_blocks.  No counterpart in
+ * the reference, which only ever copies between the two caches. */
+int fkv_gather_kv_blocks(int num_blocks, int num_layers, const int64_t* gpu_block_ids,
+                         void* const* gpu_layer_ptrs, int64_t gpu_kv_stride_bytes,
+                         int64_t gpu_block_stride_bytes, int64_t chunk_size_bytes,
+                         void* buffer, size_t buffer_bytes, fkv_stream_t stream, int is_mla);
+int fkv_scatter_kv_blocks(int num_blocks, int num_layers, const int64_t* gpu_block_ids,
+                          void* const* gpu_layer_ptrs, int64_t gpu_kv_stride_bytes,
+                          int64_t gpu_block_stride_bytes, int64_t chunk_size_bytes,
+                          const void* buffer, size_t buffer_bytes, fkv_stream_t stream,
+                          int is_mla);
+
 /* Message of the last failed call made by this thread ("" if none). */
 const char* fkv_last_error(void);
 

@@ -289,3 +289,62 @@ def test_c_ext_dropin_on_side_stream(dev, use_ce):
     torch.cuda.synchronize()
     for l in range(L):
         assert torch.equal(layers[l][:, gids].cpu(), src[l][:, gids])
+
+
+@pytest.mark.parametrize("geo", [(4, 2, 64, 16, 8, 128, 37), (130, 2, 8, 1, 1, 64, 5),
+                                 (5, 1, 30, 64, 1, 576, 11), (3, 2, 20, 1, 1, 24, 7)],
+                         ids=["8b-like", "130-layers", "mla", "48B-chunk"])
+@pytest.mark.parametrize("buffer_on_host", [False, True])
+def test_gather_scatter_match_oracle(dev, geo, buffer_on_host):
+    """fkv_gather/scatter_kv_blocks against the oracle with the contiguous
+    buffer described as a block-wise cache [n, L, kv, chunk] and ids 0..n-1."""
+    import ctypes
+    from flexkv_amd import _lib
+    from flexkv_amd.storage.allocator import pinned_empty
+    from gpu_util import to_torch, to_numpy
+    L, kv, ng, t, h, d, n = geo
+    case = KVCase(layers_total=L, num_layers=L, start_layer=0, kv=kv, ng=ng, nh=n, tokens=t,
+                  heads=h, dim=d).fill(seed=L + n)
+    gids = inputs.distinct_ids(n + 9, n, ng)
+    local = np.arange(n, dtype=np.int64)
+    s = case.strides()
+    want = case.host.copy()
+    oracle.transfer_kv_blocks(gids, case.gpu, s["gpu_kv"], s["gpu_block"], local, want,
+                              s["cpu_kv"], s["cpu_layer"], s["cpu_block"], s["chunk"], 0, False,
+                              use_ce_transfer=True, is_mla=kv == 1)
+    layers = [to_torch(g).to(dev) for g in case.gpu]
+    ptrs = (ctypes.c_void_p * L)(*[x.data_ptr() for x in layers])
+    nbytes = want.nbytes
+    if buffer_on_host:
+        buf = pinned_empty(nbytes // 2, torch.int16)
+    else:
+        buf = torch.empty(nbytes // 2, dtype=torch.int16, device=dev)
+    lib = _lib.load()
+    st = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.fkv_gather_kv_blocks(n, L, gids.ctypes.data, ptrs, s["gpu_kv"], s["gpu_block"],
+                                        s["chunk"], buf.data_ptr(), nbytes, st, kv == 1),
+               "gather")
+    assert np.array_equal(to_numpy(buf, np.uint16).reshape(want.shape), want)
+    # too small a buffer is refused
+    with pytest.raises(RuntimeError, match="buffer holds"):
+        _lib.check(lib.fkv_gather_kv_blocks(n, L, gids.ctypes.data, ptrs, s["gpu_kv"],
+                                            s["gpu_block"], s["chunk"], buf.data_ptr(),
+                                            nbytes - 16, st, kv == 1), "gather")
+    # scatter fresh values back into sentinel-filled layers
+    fresh = (want ^ np.uint16(0x0F0F)).reshape(-1)
+    buf.copy_(to_torch(fresh))
+    init = [np.full_like(g, 0x7777) for g in case.gpu]
+    for x, i in zip(layers, init):
+        x.copy_(to_torch(i))
+    _lib.check(lib.fkv_scatter_kv_blocks(n, L, gids.ctypes.data, ptrs, s["gpu_kv"], s["gpu_block"],
+                                         s["chunk"], buf.data_ptr(), nbytes, st, kv == 1),
+               "scatter")
+    exp = [i.copy() for i in init]
+    host_case = KVCase(layers_total=L, num_layers=L, start_layer=0, kv=kv, ng=ng, nh=n, tokens=t,
+                       heads=h, dim=d)
+    host_case.host = fresh.reshape(want.shape)
+    oracle.transfer_kv_blocks(gids, exp, s["gpu_kv"], s["gpu_block"], local, host_case.host,
+                              s["cpu_kv"], s["cpu_layer"], s["cpu_block"], s["chunk"], 0, True,
+                              use_ce_transfer=True, is_mla=kv == 1)
+    for x, e in zip(layers, exp):
+        assert np.array_equal(to_numpy(x, np.uint16), e)
