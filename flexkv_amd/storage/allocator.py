@@ -98,6 +98,22 @@ def pinned_empty(numel: int, dtype: torch.dtype, coherence: int = _lib.FKV_HOST_
     return flat.view(dtype)
 
 
+@dataclass
+class HostCacheSpec:
+    """A host cache to be allocated, pinned, by the process that uses it.
+
+    Pinned host memory cannot be handed to a spawned worker by pickling (the
+    copy the child would receive is ordinary shared memory, and this library
+    does not page-lock existing memory), so a worker in its own process is
+    given this spec and allocates the cache itself."""
+    layout: KVCacheLayout
+    dtype: torch.dtype
+    coherence: int = _lib.FKV_HOST_DEFAULT
+
+    def allocate(self) -> torch.Tensor:
+        return pinned_empty(self.layout.get_total_elements(), self.dtype, self.coherence)
+
+
 class GPUAllocator:
     @classmethod
     def allocate(cls, layout: KVCacheLayout, dtype: torch.dtype, **kwargs: Any) -> StorageHandle:

@@ -7,10 +7,12 @@ ops, finished op ids go to a queue), WorkerHandle (submit_transfer, shutdown)
 and GPUCPUTransferWorker (_transfer_impl, launch_transfer).  The transfer
 itself is flexkv_amd.c_ext.transfer_kv_blocks.
 
-Differences from the reference, all on failure paths:
+Differences from the reference:
   * the host cache must already be pinned (CPUAllocator pin_memory=True);
     page-locking existing pageable memory is not supported, so host_register
-    checks the buffer instead of registering it (worker.py:35-41 registers);
+    checks the buffer instead of registering it (worker.py:35-41 registers).
+    A worker in a spawned process takes a HostCacheSpec and allocates its
+    pinned cache itself;
   * an op that fails is still reported complete (worker.py:159-169), and is
     also recorded in ``failed_ops`` of the worker and logged at error level.
 """
@@ -32,6 +34,7 @@ from ..common.debug import flexkv_logger
 from ..common.memory_handle import TensorSharedHandle
 from ..common.storage import KVCacheLayout, KVCacheLayoutType
 from ..common.transfer import TransferOp, TransferType
+from ..storage.allocator import HostCacheSpec
 
 
 def host_register(tensor: torch.Tensor) -> None:
@@ -196,7 +199,7 @@ class GPUCPUTransferWorker(TransferWorkerBase):
     def __init__(self, worker_id: int, transfer_conn: Optional[Connection],
                  finished_ops_queue: Optional[Any],
                  gpu_blocks: Sequence[Union[TensorSharedHandle, torch.Tensor]],
-                 cpu_blocks: torch.Tensor, gpu_kv_layout: KVCacheLayout,
+                 cpu_blocks: Union[torch.Tensor, HostCacheSpec], gpu_kv_layout: KVCacheLayout,
                  cpu_kv_layout: KVCacheLayout, dtype: torch.dtype, gpu_device_id: int,
                  use_ce_transfer_h2d: bool = False, use_ce_transfer_d2h: bool = False,
                  transfer_sms_h2d: int = 8, transfer_sms_d2h: int = 8) -> None:
@@ -205,6 +208,8 @@ class GPUCPUTransferWorker(TransferWorkerBase):
             raise ValueError("Only layerwise layout is supported for GPU")
         if gpu_device_id != -1:
             torch.cuda.set_device(gpu_device_id)
+        if isinstance(cpu_blocks, HostCacheSpec):
+            cpu_blocks = cpu_blocks.allocate()
         host_register(cpu_blocks)
         self.gpu_blocks = [h.get_tensor() if isinstance(h, TensorSharedHandle) else h
                            for h in gpu_blocks]
