@@ -30,6 +30,12 @@ EXPORTED_SYMBOLS = (
     "fkv_transfer_kv_blocks",
     "fkv_gather_kv_blocks",
     "fkv_scatter_kv_blocks",
+    "fkv_transfer_kv_blocks_layerwise",
+    "fkv_handle_num_groups",
+    "fkv_handle_query",
+    "fkv_handle_wait",
+    "fkv_handle_stream_wait",
+    "fkv_handle_release",
     "fkv_last_error",
     "fkv_host_alloc",
     "fkv_host_free",
@@ -72,6 +78,16 @@ def _declare(lib: ctypes.CDLL) -> None:
         g = getattr(lib, name)
         g.restype = c_int
         g.argtypes = [c_int, c_int, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_sz, c_vp, c_int]
+    f = lib.fkv_transfer_kv_blocks_layerwise
+    f.restype = c_int
+    f.argtypes = [c_int, c_int, c_int, c_int, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64,
+                  c_i64, c_i64, c_i64, c_vp, c_int, c_int, c_int, ctypes.POINTER(c_vp)]
+    for name, extra in (("fkv_handle_num_groups", []), ("fkv_handle_query", [c_int]),
+                        ("fkv_handle_wait", [c_int]), ("fkv_handle_stream_wait", [c_int, c_vp]),
+                        ("fkv_handle_release", [])):
+        fn = getattr(lib, name)
+        fn.restype = c_int
+        fn.argtypes = [c_vp] + extra
     lib.fkv_last_error.restype = ctypes.c_char_p
     lib.fkv_last_error.argtypes = []
     lib.fkv_host_alloc.restype = c_int

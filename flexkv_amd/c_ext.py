@@ -13,7 +13,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["transfer_kv_blocks", "gather_kv_blocks", "scatter_kv_blocks"]
+__all__ = ["transfer_kv_blocks", "gather_kv_blocks", "scatter_kv_blocks",
+           "transfer_kv_blocks_layerwise", "LayerwiseTransfer"]
 
 
 def _require_int64_host(t: torch.Tensor, name: str) -> None:
@@ -118,3 +119,101 @@ def scatter_kv_blocks(gpu_block_id_tensor: torch.Tensor, gpu_layer_ptrs_tensor: 
     _contiguous("fkv_scatter_kv_blocks", gpu_block_id_tensor, gpu_layer_ptrs_tensor,
                 gpu_kv_stride_in_bytes, gpu_block_stride_in_bytes, chunk_size_in_bytes, buffer,
                 is_mla)
+
+
+class LayerwiseTransfer:
+    """Handle of an asynchronous, layer-grouped transfer
+    (fkv_transfer_kv_blocks_layerwise).  Group g covers layers
+    [g * granularity, (g + 1) * granularity) of the call."""
+
+    def __init__(self, handle: int, keep_alive: tuple) -> None:
+        self._h = handle
+        self._keep = keep_alive
+        lib = _lib.load()
+        self.num_groups = lib.fkv_handle_num_groups(handle) if handle else 0
+
+    def _check_group(self, group: int) -> None:
+        if self._h is None:
+            raise RuntimeError("transfer handle already released")
+        if not 0 <= group < self.num_groups:
+            raise IndexError(f"group {group} out of range [0, {self.num_groups})")
+
+    def query(self, group: int) -> bool:
+        """True once every layer of `group` has landed."""
+        self._check_group(group)
+        rc = _lib.load().fkv_handle_query(self._h, group)
+        if rc < 0:
+            raise RuntimeError(_lib.last_error())
+        return rc == 1
+
+    def wait(self, group: int = None) -> None:
+        """Block the host until `group` (default: the last group) is done."""
+        if self.num_groups == 0:
+            return
+        group = self.num_groups - 1 if group is None else group
+        self._check_group(group)
+        _lib.check(_lib.load().fkv_handle_wait(self._h, group), "fkv_handle_wait")
+
+    def stream_wait(self, group: int, stream: torch.cuda.Stream = None) -> None:
+        """Make `stream` (default: the current stream) wait on the device
+        until `group` is done; the host does not block."""
+        self._check_group(group)
+        st = (stream or torch.cuda.current_stream()).cuda_stream
+        _lib.check(_lib.load().fkv_handle_stream_wait(self._h, group, st),
+                   "fkv_handle_stream_wait")
+
+    def release(self) -> None:
+        """Wait for every group, then free the handle (idempotent)."""
+        h, self._h = self._h, None
+        self._keep = ()
+        if h:
+            _lib.check(_lib.load().fkv_handle_release(h), "fkv_handle_release")
+
+    def __enter__(self) -> "LayerwiseTransfer":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.release()
+
+    def __del__(self) -> None:
+        try:
+            self.release()
+        except Exception:
+            pass
+
+
+def transfer_kv_blocks_layerwise(gpu_block_id_tensor: torch.Tensor,
+                                 gpu_layer_ptrs_tensor: torch.Tensor,
+                                 gpu_kv_stride_in_bytes: int, gpu_block_stride_in_bytes: int,
+                                 cpu_block_id_tensor: torch.Tensor, cpu_tensor: torch.Tensor,
+                                 cpu_kv_stride_in_bytes: int, cpu_layer_stride_in_bytes: int,
+                                 cpu_block_stride_in_bytes: int, chunk_size_in_bytes: int,
+                                 start_layer_id: int, layer_granularity: int,
+                                 transfer_sms: int = -1, is_host_to_device: bool = True,
+                                 is_mla: bool = False) -> LayerwiseTransfer:
+    """Enqueue the transfer of every layer group on the current stream and
+    return at once (extension; the reference issues one synchronous call per
+    layer group).  Arguments as transfer_kv_blocks plus layer_granularity."""
+    import ctypes
+
+    _require_int64_host(gpu_block_id_tensor, "gpu_block_id_tensor")
+    _require_int64_host(cpu_block_id_tensor, "cpu_block_id_tensor")
+    _require_int64_host(gpu_layer_ptrs_tensor, "gpu_layer_ptrs_tensor")
+    if cpu_block_id_tensor.numel() != gpu_block_id_tensor.numel():
+        raise RuntimeError("gpu and cpu block id tensors differ in length")
+    if not torch.cuda.is_available():
+        raise RuntimeError("transfer_kv_blocks_layerwise needs a HIP device; none is visible")
+    lib = _lib.load()
+    out = ctypes.c_void_p()
+    rc = lib.fkv_transfer_kv_blocks_layerwise(
+        int(gpu_block_id_tensor.numel()), int(start_layer_id),
+        int(gpu_layer_ptrs_tensor.numel()), int(layer_granularity),
+        gpu_block_id_tensor.data_ptr(), gpu_layer_ptrs_tensor.data_ptr(),
+        int(gpu_kv_stride_in_bytes), int(gpu_block_stride_in_bytes),
+        cpu_block_id_tensor.data_ptr(), cpu_tensor.data_ptr(), int(cpu_kv_stride_in_bytes),
+        int(cpu_layer_stride_in_bytes), int(cpu_block_stride_in_bytes), 0,
+        int(chunk_size_in_bytes), torch.cuda.current_stream().cuda_stream, int(transfer_sms),
+        1 if is_host_to_device else 0, 1 if is_mla else 0, ctypes.byref(out))
+    if rc != 0:
+        raise RuntimeError(_lib.last_error() or f"fkv_transfer_kv_blocks_layerwise failed ({rc})")
+    return LayerwiseTransfer(out.value, (cpu_tensor,))

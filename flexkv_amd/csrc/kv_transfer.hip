@@ -588,9 +588,17 @@ int launch_copy(const Geometry& g, char* ids_dev, char* cpu_base, int64_t cks, i
   if (kIota && FKV_HBM_ONEPASS) grid = a.num_tiles;
   hipEvent_t ev = nullptr;
   if (prof.begin(stream, &ev)) return kInval;
+  (void)hipGetLastError();  // a stale error from elsewhere must not be blamed on this launch
   hipLaunchKernelGGL((kv_chunk_copy_kernel<kH2D, kIota>), dim3(grid), dim3(kThreads), 0, stream, a);
   FKV_HIP(hipGetLastError());
   return prof.end(stream, ev, static_cast<int64_t>(nb) * nl * g.kv * g.chunk, 0, false);
+}
+
+void pack_ids_into(const Geometry& g, int64_t* h) {
+  for (int i = 0; i < g.num_blocks; ++i) {
+    h[2 * i] = g.gids[i];
+    h[2 * i + 1] = g.cids[i];
+  }
 }
 
 // Pack ids into the thread's pinned buffer as (gpu_id, cpu_id) pairs.
@@ -598,10 +606,7 @@ int pack_ids(const Geometry& g, char** ids_dev) {
   int64_t* h = nullptr;
   int rc = pinned_ids(static_cast<size_t>(g.num_blocks) * 16, &h, ids_dev);
   if (rc) return rc;
-  for (int i = 0; i < g.num_blocks; ++i) {
-    h[2 * i] = g.gids[i];
-    h[2 * i + 1] = g.cids[i];
-  }
+  pack_ids_into(g, h);
   return 0;
 }
 
@@ -936,6 +941,135 @@ int transfer_ce_per_chunk(const Geometry& g, hipStream_t stream, bool h2d) {
   return 0;
 }
 
+// ---------------------------------------------------------------------------
+// Asynchronous layer-grouped transfers.  A handle owns a pinned id buffer
+// from a process-wide pool (returned at release) and one event per group.
+
+struct PoolBuf {
+  int64_t* host = nullptr;
+  char* dev = nullptr;
+  size_t cap = 0;
+};
+std::mutex g_pool_mu;
+std::vector<PoolBuf> g_pool;   // free buffers
+
+int pool_get(size_t bytes, PoolBuf* out) {
+  {
+    std::lock_guard<std::mutex> lk(g_pool_mu);
+    size_t best = g_pool.size();
+    for (size_t i = 0; i < g_pool.size(); ++i)
+      if (g_pool[i].cap >= bytes && (best == g_pool.size() || g_pool[i].cap < g_pool[best].cap))
+        best = i;
+    if (best != g_pool.size()) {
+      *out = g_pool[best];
+      g_pool.erase(g_pool.begin() + static_cast<long>(best));
+      return 0;
+    }
+  }
+  PoolBuf b;
+  b.cap = std::max<size_t>(bytes, 64 << 10);
+  void* p = nullptr;
+  FKV_HIP(hipHostMalloc(&p, b.cap, hipHostMallocPortable | hipHostMallocMapped | hipHostMallocCoherent));
+  void* dp = nullptr;
+  hipError_t e = hipHostGetDevicePointer(&dp, p, 0);
+  if (e != hipSuccess) {
+    (void)hipHostFree(p);
+    return fail(static_cast<int>(e), "hipHostGetDevicePointer failed: %s", hipGetErrorString(e));
+  }
+  b.host = static_cast<int64_t*>(p);
+  b.dev = static_cast<char*>(dp);
+  *out = b;
+  return 0;
+}
+
+void pool_put(const PoolBuf& b) {
+  std::lock_guard<std::mutex> lk(g_pool_mu);
+  g_pool.push_back(b);
+}
+
+}  // namespace
+
+struct fkv_transfer_handle_s {
+  int dev = 0;
+  hipStream_t stream = nullptr;
+  std::vector<hipEvent_t> done;   // one per layer group, in order
+  PoolBuf ids;
+  ProfRecorder prof;
+};
+
+namespace {
+
+int layerwise_enqueue(const Geometry& g, hipStream_t stream, int dev, int transfer_cus, bool h2d,
+                      int granularity, fkv_transfer_handle_s* h) {
+  DeviceState& d = g_dev[dev];
+  int rc = pool_get(static_cast<size_t>(g.num_blocks) * 16, &h->ids);
+  if (rc) return rc;
+  pack_ids_into(g, h->ids.host);
+  const int cus = transfer_cus <= 0 ? std::min(kAutoZeroCopyCus, d.num_cus)
+                                    : std::min(transfer_cus, d.num_cus);
+  const int grid_cap = cus * (h2d ? d.occ_zero_copy[1] : d.occ_zero_copy[0]);
+  char* cpu_dev = g.cpu_info.dev_ptr + g.startoff + static_cast<int64_t>(g.start_layer) * g.cls;
+  for (int g0 = 0; g0 < g.num_layers; g0 += granularity) {
+    const int gend = std::min(g.num_layers, g0 + granularity);
+    for (int l0 = g0; l0 < gend; l0 += kMaxLayersPerLaunch) {
+      const int nl = std::min(kMaxLayersPerLaunch, gend - l0);
+      char* base = cpu_dev + static_cast<int64_t>(l0) * g.cls;
+      rc = h2d ? launch_copy<true, false>(g, h->ids.dev, base, g.cks, g.cls, g.cbs, 0,
+                                          g.num_blocks, l0, nl, grid_cap, stream, h->prof)
+               : launch_copy<false, false>(g, h->ids.dev, base, g.cks, g.cls, g.cbs, 0,
+                                           g.num_blocks, l0, nl, grid_cap, stream, h->prof);
+      if (rc) return rc;
+    }
+    hipEvent_t ev = nullptr;
+    FKV_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    h->done.push_back(ev);
+    FKV_HIP(hipEventRecord(ev, stream));
+  }
+  return 0;
+}
+
+// Wait for everything the handle enqueued, then free it.  Safe on a handle
+// whose enqueue failed part-way.
+int handle_destroy(fkv_transfer_handle_s* h) {
+  int rc = 0;
+  if (!h->done.empty()) {
+    hipError_t e = hipEventSynchronize(h->done.back());
+    if (e != hipSuccess) rc = fail(static_cast<int>(e), "hipEventSynchronize: %s", hipGetErrorString(e));
+  } else if (h->ids.host) {  // enqueue failed after taking ids: drain what was issued
+    hipError_t e = hipStreamSynchronize(h->stream);
+    if (e != hipSuccess) rc = fail(static_cast<int>(e), "hipStreamSynchronize: %s", hipGetErrorString(e));
+  }
+  h->prof.flush();
+  for (hipEvent_t ev : h->done) (void)hipEventDestroy(ev);
+  if (h->ids.host) pool_put(h->ids);
+  delete h;
+  return rc;
+}
+
+Geometry make_geometry(int num_blocks, int start_layer_id, int num_layers,
+                       const int64_t* gpu_block_ids, void* const* gpu_layer_ptrs,
+                       int64_t gpu_kv_stride_bytes, int64_t gpu_block_stride_bytes,
+                       const int64_t* cpu_block_ids, void* cpu_ptr, int64_t cpu_kv_stride_bytes,
+                       int64_t cpu_layer_stride_bytes, int64_t cpu_block_stride_bytes,
+                       int64_t cpu_startoff_inside_chunks, int64_t chunk_size_bytes, int is_mla) {
+  Geometry g;
+  g.num_blocks = num_blocks;
+  g.start_layer = start_layer_id;
+  g.num_layers = num_layers;
+  g.kv = is_mla ? 1 : 2;
+  g.gids = gpu_block_ids;
+  g.cids = cpu_block_ids;
+  g.layer_ptrs = gpu_layer_ptrs;
+  g.gks = gpu_kv_stride_bytes;
+  g.gbs = gpu_block_stride_bytes;
+  g.cks = cpu_kv_stride_bytes;
+  g.cls = cpu_layer_stride_bytes;
+  g.cbs = cpu_block_stride_bytes;
+  g.startoff = cpu_startoff_inside_chunks;
+  g.chunk = chunk_size_bytes;
+  g.cpu_ptr = static_cast<char*>(cpu_ptr);
+  return g;
+}
 }  // namespace
 
 extern "C" {
@@ -954,22 +1088,11 @@ int fkv_transfer_kv_blocks(int num_blocks, int start_layer_id, int num_layers,
       return fail(kInval, "use_ce_transfer must be 0 (kernel), 1 (CE) or 2 (CE per chunk), got %d",
                   use_ce_transfer);
     if (num_blocks == 0 || num_layers == 0) return 0;
-    Geometry g;
-    g.num_blocks = num_blocks;
-    g.start_layer = start_layer_id;
-    g.num_layers = num_layers;
-    g.kv = is_mla ? 1 : 2;
-    g.gids = gpu_block_ids;
-    g.cids = cpu_block_ids;
-    g.layer_ptrs = gpu_layer_ptrs;
-    g.gks = gpu_kv_stride_bytes;
-    g.gbs = gpu_block_stride_bytes;
-    g.cks = cpu_kv_stride_bytes;
-    g.cls = cpu_layer_stride_bytes;
-    g.cbs = cpu_block_stride_bytes;
-    g.startoff = cpu_startoff_inside_chunks;
-    g.chunk = chunk_size_bytes;
-    g.cpu_ptr = static_cast<char*>(cpu_ptr);
+    Geometry g = make_geometry(num_blocks, start_layer_id, num_layers, gpu_block_ids,
+                               gpu_layer_ptrs, gpu_kv_stride_bytes, gpu_block_stride_bytes,
+                               cpu_block_ids, cpu_ptr, cpu_kv_stride_bytes,
+                               cpu_layer_stride_bytes, cpu_block_stride_bytes,
+                               cpu_startoff_inside_chunks, chunk_size_bytes, is_mla);
     int rc = validate(g, use_ce_transfer);
     if (rc) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1009,6 +1132,88 @@ int fkv_scatter_kv_blocks(int num_blocks, int num_layers, const int64_t* gpu_blo
   return contiguous_entry(num_blocks, num_layers, gpu_block_ids, gpu_layer_ptrs,
                           gpu_kv_stride_bytes, gpu_block_stride_bytes, chunk_size_bytes,
                           const_cast<void*>(buffer), buffer_bytes, stream, is_mla, true);
+}
+
+int fkv_transfer_kv_blocks_layerwise(
+    int num_blocks, int start_layer_id, int num_layers, int layer_granularity,
+    const int64_t* gpu_block_ids, void* const* gpu_layer_ptrs, int64_t gpu_kv_stride_bytes,
+    int64_t gpu_block_stride_bytes, const int64_t* cpu_block_ids, void* cpu_ptr,
+    int64_t cpu_kv_stride_bytes, int64_t cpu_layer_stride_bytes, int64_t cpu_block_stride_bytes,
+    int64_t cpu_startoff_inside_chunks, int64_t chunk_size_bytes, fkv_stream_t stream,
+    int transfer_cus, int is_host_to_device, int is_mla, fkv_transfer_handle* out) {
+  try {
+    t_err.clear();
+    if (!out) return fail(kInval, "out handle pointer is null");
+    *out = nullptr;
+    if (layer_granularity < 1) return fail(kInval, "layer_granularity must be >= 1");
+    if (num_blocks < 0 || num_layers < 0)
+      return fail(kInval, "negative count: num_blocks=%d num_layers=%d", num_blocks, num_layers);
+    Geometry g = make_geometry(num_blocks, start_layer_id, num_layers, gpu_block_ids,
+                               gpu_layer_ptrs, gpu_kv_stride_bytes, gpu_block_stride_bytes,
+                               cpu_block_ids, cpu_ptr, cpu_kv_stride_bytes,
+                               cpu_layer_stride_bytes, cpu_block_stride_bytes,
+                               cpu_startoff_inside_chunks, chunk_size_bytes, is_mla);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto* h = new fkv_transfer_handle_s();
+    h->stream = s;
+    int rc = 0;
+    if (num_blocks > 0 && num_layers > 0) {
+      if ((rc = validate(g, FKV_XFER_KERNEL)) || (rc = stream_device(s, &h->dev)) ||
+          (rc = ensure_device_basics(h->dev)) ||
+          (rc = layerwise_enqueue(g, s, h->dev, transfer_cus, is_host_to_device != 0,
+                                  layer_granularity, h))) {
+        const std::string msg = t_err;
+        (void)handle_destroy(h);
+        t_err = msg;
+        return rc;
+      }
+    }
+    *out = h;
+    return 0;
+  } catch (const std::exception& e) {
+    return fail(static_cast<int>(hipErrorUnknown), "exception: %s", e.what());
+  } catch (...) {
+    return fail(static_cast<int>(hipErrorUnknown), "unknown exception");
+  }
+}
+
+int fkv_handle_num_groups(fkv_transfer_handle h) {
+  t_err.clear();
+  if (!h) return fail(-1, "null handle");
+  return static_cast<int>(h->done.size());
+}
+
+int fkv_handle_query(fkv_transfer_handle h, int group) {
+  t_err.clear();
+  if (!h || group < 0 || group >= static_cast<int>(h->done.size()))
+    return fail(-1, "bad handle or group %d", group);
+  hipError_t e = hipEventQuery(h->done[group]);
+  if (e == hipSuccess) return 1;
+  (void)hipGetLastError();
+  if (e == hipErrorNotReady) return 0;
+  return fail(-static_cast<int>(e), "hipEventQuery: %s", hipGetErrorString(e));
+}
+
+int fkv_handle_wait(fkv_transfer_handle h, int group) {
+  t_err.clear();
+  if (!h || group < 0 || group >= static_cast<int>(h->done.size()))
+    return fail(kInval, "bad handle or group %d", group);
+  FKV_HIP(hipEventSynchronize(h->done[group]));
+  return 0;
+}
+
+int fkv_handle_stream_wait(fkv_transfer_handle h, int group, fkv_stream_t other) {
+  t_err.clear();
+  if (!h || group < 0 || group >= static_cast<int>(h->done.size()))
+    return fail(kInval, "bad handle or group %d", group);
+  FKV_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(other), h->done[group], 0));
+  return 0;
+}
+
+int fkv_handle_release(fkv_transfer_handle h) {
+  t_err.clear();
+  if (!h) return 0;
+  return handle_destroy(h);
 }
 
 const char* fkv_last_error(void) { return t_err.c_str(); }

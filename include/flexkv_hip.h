@@ -112,6 +112,36 @@ int fkv_scatter_kv_blocks(int num_blocks, int num_layers, const int64_t* gpu_blo
                           const void* buffer, size_t buffer_bytes, fkv_stream_t stream,
                           int is_mla);
 
+/* Asynchronous, layer-grouped transfer (zero-copy kernel path).  Layers
+ * [0, num_layers) move in groups of `layer_granularity` consecutive layers,
+ * in order, on `stream`; an event marks the end of each group.  The call
+ * returns once everything is enqueued, with a handle the caller polls or waits
+ * on per group: on the host (fkv_handle_query / fkv_handle_wait) or on the
+ * device (fkv_handle_stream_wait makes another stream, e.g. the one running
+ * layer l of the model, wait for group g without a host round trip).
+ * Arguments and checks as in fkv_transfer_kv_blocks; the id lists are copied
+ * before the call returns.  The caller keeps the GPU cache and host cache
+ * alive until the handle is released; fkv_handle_release waits for all groups
+ * and frees the handle.
+ *
+ * The reference reaches the same layer-wise schedule with one synchronous
+ * call per layer group (worker.py:293-295, layer-wise ops of
+ * flexkv/cache/transfer_pattern.py:370-428) and host polling
+ * (kvmanager.py:480 wait_at_layer_group). */
+typedef struct fkv_transfer_handle_s* fkv_transfer_handle;
+int fkv_transfer_kv_blocks_layerwise(
+    int num_blocks, int start_layer_id, int num_layers, int layer_granularity,
+    const int64_t* gpu_block_ids, void* const* gpu_layer_ptrs, int64_t gpu_kv_stride_bytes,
+    int64_t gpu_block_stride_bytes, const int64_t* cpu_block_ids, void* cpu_ptr,
+    int64_t cpu_kv_stride_bytes, int64_t cpu_layer_stride_bytes, int64_t cpu_block_stride_bytes,
+    int64_t cpu_startoff_inside_chunks, int64_t chunk_size_bytes, fkv_stream_t stream,
+    int transfer_cus, int is_host_to_device, int is_mla, fkv_transfer_handle* out);
+int fkv_handle_num_groups(fkv_transfer_handle h);             /* groups, or -1 */
+int fkv_handle_query(fkv_transfer_handle h, int group);       /* 1 done, 0 pending, <0 error */
+int fkv_handle_wait(fkv_transfer_handle h, int group);        /* host blocks until done */
+int fkv_handle_stream_wait(fkv_transfer_handle h, int group, fkv_stream_t other);
+int fkv_handle_release(fkv_transfer_handle h);
+
 /* Message of the last failed call made by this thread ("" if none). */
 const char* fkv_last_error(void);
 

@@ -1,0 +1,159 @@
+"""Asynchronous layer-grouped transfers (fkv_transfer_kv_blocks_layerwise)
+against the oracle, and the ordering their per-group events give."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import inputs
+from kvcase import KVCase
+
+pytestmark = pytest.mark.gpu
+
+
+def _abi_layerwise(dc, gids, cids, h2d, gran, stream=None, cus=-1):
+    from flexkv_amd import _lib
+    from flexkv_amd.c_ext import LayerwiseTransfer
+    case = dc.case
+    s = case.strides()
+    gids = np.ascontiguousarray(gids, dtype=np.int64)
+    cids = np.ascontiguousarray(cids, dtype=np.int64)
+    ptrs = (ctypes.c_void_p * len(dc.gpu))(*[t.data_ptr() for t in dc.gpu])
+    st = (stream or torch.cuda.current_stream()).cuda_stream
+    out = ctypes.c_void_p()
+    lib = _lib.load()
+    rc = lib.fkv_transfer_kv_blocks_layerwise(
+        len(gids), case.start_layer, len(dc.gpu), gran, gids.ctypes.data, ptrs, s["gpu_kv"],
+        s["gpu_block"], cids.ctypes.data, dc.host.data_ptr(), s["cpu_kv"], s["cpu_layer"],
+        s["cpu_block"], s["startoff"], s["chunk"], st, cus, int(h2d), int(case.kv == 1),
+        ctypes.byref(out))
+    _lib.check(rc, "fkv_transfer_kv_blocks_layerwise")
+    # ids were copied by the call: overwrite ours to prove the handle kept its own
+    gids[:] = -1
+    cids[:] = -1
+    return LayerwiseTransfer(out.value, ())
+
+
+@pytest.mark.parametrize("gran", [1, 3, 4, 200])
+@pytest.mark.parametrize("geo", [(4, 2, 64, 96, 16, 8, 128, 40), (130, 2, 6, 8, 1, 1, 64, 5),
+                                 (6, 1, 30, 40, 64, 1, 576, 9)], ids=["8b-like", "130-layers", "mla"])
+def test_layerwise_matches_oracle(geo, gran):
+    from gpu_util import DeviceCase
+    L, kv, ng, nh, t, h, d, n = geo
+    case = KVCase(layers_total=L, num_layers=L, start_layer=0, kv=kv, ng=ng, nh=nh, tokens=t,
+                  heads=h, dim=d).fill(seed=L * gran)
+    gids = inputs.distinct_ids(gran, n, ng)
+    cids = inputs.distinct_ids(gran + 1, n, nh)
+    s = case.strides()
+    dc = DeviceCase(case)
+    hnd = _abi_layerwise(dc, gids.copy(), cids.copy(), False, gran)
+    assert hnd.num_groups == -(-L // gran)
+    hnd.release()
+    want = case.host.copy()
+    oracle.transfer_kv_blocks(gids, case.gpu, s["gpu_kv"], s["gpu_block"], cids, want, s["cpu_kv"],
+                              s["cpu_layer"], s["cpu_block"], s["chunk"], 0, False, is_mla=kv == 1)
+    assert np.array_equal(dc.host_np(), want)
+    # H2D of fresh host values into zeroed layers
+    fresh = want ^ np.uint16(0x3C3C)
+    dc.set_host(fresh)
+    zeros = [np.zeros_like(g) for g in case.gpu]
+    dc.set_gpu(zeros)
+    with _abi_layerwise(dc, gids.copy(), cids.copy(), True, gran) as hnd:
+        for g in range(hnd.num_groups):
+            hnd.wait(g)
+            assert hnd.query(g)
+    exp = [z.copy() for z in zeros]
+    case.host = fresh
+    oracle.transfer_kv_blocks(gids, exp, s["gpu_kv"], s["gpu_block"], cids, case.host,
+                              s["cpu_kv"], s["cpu_layer"], s["cpu_block"], s["chunk"], 0, True,
+                              is_mla=kv == 1)
+    for got, e in zip(dc.gpu_np(), exp):
+        assert np.array_equal(got, e)
+
+
+def test_stream_wait_orders_consumers():
+    """A consumer stream that waits on group g sees layer g's blocks, with no
+    host synchronisation between the transfer and the consumer."""
+    from gpu_util import DeviceCase
+    L, n = 16, 256
+    case = KVCase(layers_total=L, num_layers=L, start_layer=0, kv=2, ng=512, nh=1024, tokens=16,
+                  heads=8, dim=128).fill(seed=5)
+    gids = inputs.distinct_ids(1, n, 512)
+    cids = inputs.distinct_ids(2, n, 1024)
+    dc = DeviceCase(case)
+    # host holds random values that must arrive; the device starts at zero
+    src = KVCase(layers_total=L, num_layers=L, start_layer=0, kv=2, ng=512, nh=1024, tokens=16,
+                 heads=8, dim=128)
+    size = int(np.prod(src.host_shape()))
+    src.host = (inputs.splitmix64(np.arange(size, dtype=np.uint64)) & np.uint64(0xFFFF)) \
+        .astype(np.uint16).reshape(src.host_shape())
+    dc.set_host(src.host)
+    dc.set_gpu([np.zeros_like(g) for g in case.gpu])
+    g_dev = torch.from_numpy(gids).to("cuda")
+    torch.cuda.synchronize()
+    xfer = torch.cuda.Stream()
+    consumer = torch.cuda.Stream()
+    outs = []
+    with torch.cuda.stream(xfer):
+        hnd = _abi_layerwise(dc, gids.copy(), cids.copy(), True, 1, stream=xfer, cus=1)
+    with torch.cuda.stream(consumer):
+        for l in range(L):
+            hnd.stream_wait(l, consumer)
+            outs.append(dc.gpu[l][:, g_dev].clone())
+    consumer.synchronize()
+    hnd.release()
+    hv = src.host_view(src.host)
+    for l in range(L):
+        want = np.stack([hv[c, l, :, 0] for c in cids], axis=1)   # [kv, n, t, h, d]
+        assert np.array_equal(outs[l].cpu().numpy().view(np.uint16), want), f"layer {l}"
+
+
+def test_concurrent_handles_keep_their_ids():
+    from gpu_util import DeviceCase
+    a = KVCase(layers_total=8, num_layers=8, start_layer=0, kv=2, ng=128, nh=128, tokens=16,
+               heads=4, dim=128).fill(seed=11)
+    b = KVCase(layers_total=8, num_layers=8, start_layer=0, kv=2, ng=128, nh=128, tokens=16,
+               heads=4, dim=128).fill(seed=12)
+    da, db = DeviceCase(a), DeviceCase(b)
+    ga, ca = inputs.distinct_ids(3, 100, 128), inputs.distinct_ids(4, 100, 128)
+    gb, cb = inputs.distinct_ids(5, 60, 128), inputs.distinct_ids(6, 60, 128)
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    ha = _abi_layerwise(da, ga.copy(), ca.copy(), False, 2, stream=sa)
+    hb = _abi_layerwise(db, gb.copy(), cb.copy(), False, 3, stream=sb)
+    hb.release()
+    ha.release()
+    for case, dc, g, c in ((a, da, ga, ca), (b, db, gb, cb)):
+        assert np.array_equal(dc.host_np(), case.expect_d2h(g, c))
+
+
+def test_empty_and_rejected():
+    from flexkv_amd import c_ext
+    from gpu_util import DeviceCase
+    case = KVCase(layers_total=2, num_layers=2, start_layer=0, kv=2, ng=8, nh=8, tokens=16,
+                  heads=2, dim=64).fill(seed=1)
+    dc = DeviceCase(case)
+    h = _abi_layerwise(dc, np.zeros(0, np.int64), np.zeros(0, np.int64), False, 1)
+    assert h.num_groups == 0
+    h.wait()
+    h.release()
+    h.release()
+    with pytest.raises(RuntimeError):
+        _abi_layerwise(dc, np.array([1, 1 << 22]), np.array([0, 1]), False, 1)
+    with pytest.raises(RuntimeError, match="granularity"):
+        _abi_layerwise(dc, np.array([1]), np.array([0]), False, 0)
+    ptrs = torch.tensor([t.data_ptr() for t in dc.gpu], dtype=torch.int64)
+    s = case.strides()
+    ids = torch.tensor([1, 2], dtype=torch.int64)
+    hnd = c_ext.transfer_kv_blocks_layerwise(ids, ptrs, s["gpu_kv"], s["gpu_block"], ids, dc.host,
+                                             s["cpu_kv"], s["cpu_layer"], s["cpu_block"],
+                                             s["chunk"], 0, 1, -1, False, False)
+    assert hnd.num_groups == 2
+    hnd.wait(1)
+    with pytest.raises(IndexError):
+        hnd.query(2)
+    hnd.release()
+    with pytest.raises(RuntimeError, match="released"):
+        hnd.query(0)
+    assert np.array_equal(dc.host_np(), case.expect_d2h(np.array([1, 2]), np.array([1, 2])))
