@@ -190,6 +190,114 @@ def link_peaks(wl: Workload, reps: int = 8):
     return res
 
 
+def layerwise_h2d(wl: Workload, steps: int):
+    """H2D of the step's blocks one layer group per layer.
+
+    * reference schedule: one synchronous call per layer (the layer-wise read
+      graph's ops, each run by the worker with its own stream sync);
+    * async: fkv_transfer_kv_blocks_layerwise, host waits per group;
+    * overlap: a compute stream waits on each group's event on the device, then
+      runs a per-layer GEMM; compared with the same GEMMs after a synchronous
+      transfer.
+    """
+    from flexkv_amd import c_ext
+    L = wl.w["layers"]
+    args = (wl.gkv, wl.gblk, wl.cids_p, wl.host, wl.ckv, wl.clay, wl.cblk, wl.chunk)
+    layer_ptrs = [wl.ptrs[l:l + 1].clone().pin_memory() for l in range(L)]
+
+    def per_layer_sync():
+        for l in range(L):
+            c_ext.transfer_kv_blocks(wl.gids_p, layer_ptrs[l], wl.gkv, wl.gblk, wl.cids_p,
+                                     wl.host, wl.ckv, wl.clay, wl.cblk, wl.chunk, l, -1, True,
+                                     False, wl.mla)
+
+    ref_s, _, _ = time_steps(per_layer_sync, steps, 1)
+    xfer = c_ext.transfer_stream()   # own hardware queue, every CU
+    first, total = [], []
+    for _ in range(steps + 1):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with torch.cuda.stream(xfer):
+            h = c_ext.transfer_kv_blocks_layerwise(wl.gids_p, wl.ptrs, wl.gkv, wl.gblk, *args[2:],
+                                                   0, 1, -1, True, wl.mla)
+        h.wait(0)
+        t1 = time.perf_counter()
+        h.wait()
+        t2 = time.perf_counter()
+        h.release()
+        first.append(t1 - t0)
+        total.append(t2 - t0)
+    first, total = first[1:], total[1:]
+    # compute proxy: per layer, bf16 GEMMs of [8192 x 4096] x [4096 x 4096]
+    a = torch.randn(8192, 4096, device=wl.dev, dtype=torch.bfloat16)
+    b = torch.randn(4096, 4096, device=wl.dev, dtype=torch.bfloat16)
+    c = torch.empty(8192, 4096, device=wl.dev, dtype=torch.bfloat16)
+    reps = 4
+    comp = torch.cuda.Stream()
+
+    def compute_layers(hnd=None):
+        with torch.cuda.stream(comp):
+            for l in range(L):
+                if hnd is not None:
+                    hnd.stream_wait(l, comp)
+                for _ in range(reps):
+                    torch.mm(a, b, out=c)
+
+    def serial():
+        wl.transfer(True, False)
+        compute_layers()
+        comp.synchronize()
+
+    def overlapped():
+        with torch.cuda.stream(xfer):
+            hnd = c_ext.transfer_kv_blocks_layerwise(wl.gids_p, wl.ptrs, wl.gkv, wl.gblk,
+                                                     *args[2:], 0, 1, -1, True, wl.mla)
+        compute_layers(hnd)
+        comp.synchronize()
+        hnd.release()
+
+    def compute_only():
+        compute_layers()
+        comp.synchronize()
+
+    comp_s, _, _ = time_steps(compute_only, steps, 1)
+    ser_s, _, _ = time_steps(serial, steps, 1)
+    ovl_s, _, _ = time_steps(overlapped, steps, 1)
+    gb = wl.bytes_per_op / 1e9
+    return {
+        "granularity_layers": 1,
+        "reference_schedule_ms": round(ref_s * 1e3, 2),
+        "reference_schedule_gbps": round(gb / ref_s, 2),
+        "async_total_ms": round(statistics.median(total) * 1e3, 2),
+        "async_gbps": round(gb / statistics.median(total), 2),
+        "async_first_group_ms": round(statistics.median(first) * 1e3, 3),
+        "overlap": {"compute_only_ms": round(comp_s * 1e3, 2),
+                    "transfer_then_compute_ms": round(ser_s * 1e3, 2),
+                    "layerwise_overlapped_ms": round(ovl_s * 1e3, 2),
+                    "compute_proxy": f"{reps} bf16 GEMMs [8192x4096]x[4096x4096] per layer"},
+    }
+
+
+def call_latency(wl: Workload, reps: int = 200):
+    """Wall time of small synchronous calls (1 block x 1 layer, 16 blocks x 1
+    layer, 16 blocks x all layers), zero-copy path, median of `reps`."""
+    from flexkv_amd import c_ext
+    out = {}
+    L = wl.w["layers"]
+    for nb, nl in ((1, 1), (16, 1), (16, L)):
+        g = wl.gids_p[:nb].clone().pin_memory()
+        c = wl.cids_p[:nb].clone().pin_memory()
+        p = wl.ptrs[:nl].clone().pin_memory()
+        ts = []
+        for i in range(reps + 5):
+            t0 = time.perf_counter()
+            c_ext.transfer_kv_blocks(g, p, wl.gkv, wl.gblk, c, wl.host, wl.ckv, wl.clay, wl.cblk,
+                                     wl.chunk, 0, -1, i % 2 == 0, False, wl.mla)
+            ts.append(time.perf_counter() - t0)
+        out[f"{nb}blk_{nl}layer_us"] = round(statistics.median(ts[5:]) * 1e6, 1)
+    return out
+
+
 def cpu_baseline(wl: Workload, budget_s: float):
     """The oracle's block-partitioned memcpy (oracle/kv_oracle.c) on this host's
     cores: D2H from host-resident copies of the selected GPU blocks into the
@@ -413,6 +521,10 @@ def main() -> int:
             "what": "reference copy-engine algorithm restated with HIP: one hipMemcpyAsync per "
                     "(layer, K|V, block) chunk (csrc/transfer.cu:97-121), D2H, one op"}
         log(f"CE per-chunk loop: {gb / el:.2f} GB/s")
+        result["layerwise_h2d"] = layerwise_h2d(wl, args.steps)
+        log(f"layer-wise H2D: {result['layerwise_h2d']}")
+        result["call_latency"] = call_latency(wl)
+        log(f"call latency: {result['call_latency']}")
         threads, cpu = cpu_baseline(wl, args.cpu_budget)
         v, reps, el = cpu[threads]
         v1, reps1, el1 = cpu[1]

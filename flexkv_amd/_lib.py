@@ -36,6 +36,8 @@ EXPORTED_SYMBOLS = (
     "fkv_handle_wait",
     "fkv_handle_stream_wait",
     "fkv_handle_release",
+    "fkv_stream_create",
+    "fkv_stream_destroy",
     "fkv_last_error",
     "fkv_host_alloc",
     "fkv_host_free",
@@ -88,6 +90,10 @@ def _declare(lib: ctypes.CDLL) -> None:
         fn = getattr(lib, name)
         fn.restype = c_int
         fn.argtypes = [c_vp] + extra
+    lib.fkv_stream_create.restype = c_int
+    lib.fkv_stream_create.argtypes = [c_int, ctypes.POINTER(c_vp)]
+    lib.fkv_stream_destroy.restype = c_int
+    lib.fkv_stream_destroy.argtypes = [c_vp]
     lib.fkv_last_error.restype = ctypes.c_char_p
     lib.fkv_last_error.argtypes = []
     lib.fkv_host_alloc.restype = c_int

@@ -14,7 +14,7 @@ import torch
 from . import _lib
 
 __all__ = ["transfer_kv_blocks", "gather_kv_blocks", "scatter_kv_blocks",
-           "transfer_kv_blocks_layerwise", "LayerwiseTransfer"]
+           "transfer_kv_blocks_layerwise", "LayerwiseTransfer", "transfer_stream"]
 
 
 def _require_int64_host(t: torch.Tensor, name: str) -> None:
@@ -217,3 +217,15 @@ def transfer_kv_blocks_layerwise(gpu_block_id_tensor: torch.Tensor,
     if rc != 0:
         raise RuntimeError(_lib.last_error() or f"fkv_transfer_kv_blocks_layerwise failed ({rc})")
     return LayerwiseTransfer(out.value, (cpu_tensor,))
+
+
+def transfer_stream(num_cus: int = 0) -> torch.cuda.ExternalStream:
+    """A torch stream on its own hardware queue (fkv_stream_create) for
+    transfers meant to overlap with compute; num_cus = 0 keeps every compute
+    unit.  The stream lives until the process ends."""
+    import ctypes
+
+    lib = _lib.load()
+    out = ctypes.c_void_p()
+    _lib.check(lib.fkv_stream_create(int(num_cus), ctypes.byref(out)), "fkv_stream_create")
+    return torch.cuda.ExternalStream(out.value)

@@ -1216,6 +1216,31 @@ int fkv_handle_release(fkv_transfer_handle h) {
   return handle_destroy(h);
 }
 
+int fkv_stream_create(int num_cus, fkv_stream_t* out) {
+  t_err.clear();
+  if (!out) return fail(kInval, "out stream pointer is null");
+  *out = nullptr;
+  int dev = 0;
+  FKV_HIP(hipGetDevice(&dev));
+  int ncu = 0;
+  FKV_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+  if (num_cus < 0 || num_cus > ncu)
+    return fail(kInval, "num_cus must be in [0, %d], got %d", ncu, num_cus);
+  const int use = num_cus == 0 ? ncu : num_cus;
+  std::vector<uint32_t> mask(static_cast<size_t>((ncu + 31) / 32), 0u);
+  for (int c = 0; c < use; ++c) mask[c / 32] |= 1u << (c % 32);
+  hipStream_t st = nullptr;
+  FKV_HIP(hipExtStreamCreateWithCUMask(&st, static_cast<uint32_t>(mask.size()), mask.data()));
+  *out = st;
+  return 0;
+}
+
+int fkv_stream_destroy(fkv_stream_t s) {
+  t_err.clear();
+  if (s) FKV_HIP(hipStreamDestroy(static_cast<hipStream_t>(s)));
+  return 0;
+}
+
 const char* fkv_last_error(void) { return t_err.c_str(); }
 
 int fkv_host_alloc(void** out_ptr, size_t bytes, unsigned flags) {

@@ -142,6 +142,17 @@ int fkv_handle_wait(fkv_transfer_handle h, int group);        /* host blocks unt
 int fkv_handle_stream_wait(fkv_transfer_handle h, int group, fkv_stream_t other);
 int fkv_handle_release(fkv_transfer_handle h);
 
+/* A stream on its own hardware queue, for transfers that must overlap with
+ * compute.  The HIP runtime spreads ordinary streams over a small pool of
+ * hardware queues (4 per process by default), so a transfer stream and a
+ * compute stream can land on the same queue and run one after the other; a
+ * stream created with a CU mask gets a queue of its own.  num_cus = 0 keeps
+ * every compute unit; num_cus = n confines the stream's kernels to the first
+ * n.  No counterpart in the reference (its worker uses torch.cuda.Stream(),
+ * worker.py:253). */
+int fkv_stream_create(int num_cus, fkv_stream_t* out);
+int fkv_stream_destroy(fkv_stream_t s);
+
 /* Message of the last failed call made by this thread ("" if none). */
 const char* fkv_last_error(void);
 

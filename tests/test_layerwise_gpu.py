@@ -157,3 +157,25 @@ def test_empty_and_rejected():
     with pytest.raises(RuntimeError, match="released"):
         hnd.query(0)
     assert np.array_equal(dc.host_np(), case.expect_d2h(np.array([1, 2]), np.array([1, 2])))
+
+
+@pytest.mark.parametrize("num_cus", [0, 8])
+def test_transfer_stream_helper(num_cus):
+    """fkv_stream_create: a transfer on a stream with its own hardware queue
+    (optionally confined to num_cus compute units) moves the same bytes."""
+    from flexkv_amd import c_ext, _lib
+    from gpu_util import DeviceCase
+    case = KVCase(layers_total=4, num_layers=4, start_layer=0, kv=2, ng=64, nh=64, tokens=16,
+                  heads=4, dim=128).fill(seed=21 + num_cus)
+    dc = DeviceCase(case)
+    g, c = inputs.distinct_ids(7, 40, 64), inputs.distinct_ids(8, 40, 64)
+    st = c_ext.transfer_stream(num_cus)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(st):
+        hnd = _abi_layerwise(dc, g.copy(), c.copy(), False, 1, stream=st)
+    hnd.release()
+    assert np.array_equal(dc.host_np(), case.expect_d2h(g, c))
+    import ctypes
+    out = ctypes.c_void_p()
+    assert _lib.load().fkv_stream_create(100000, ctypes.byref(out)) == 1
+    assert "num_cus" in _lib.last_error()
