@@ -278,6 +278,53 @@ def layerwise_h2d(wl: Workload, steps: int):
     }
 
 
+def engine_layerwise(wl: Workload, steps: int):
+    """A layer-wise read graph (one H2D op per layer, each after the previous,
+    convert_read_graph_to_layer_wise_graph) through TransferEngine with a
+    thread worker; submit-to-graph-complete time, with and without eager
+    dispatch of same-worker chains."""
+    from flexkv_amd.cache.transfer_pattern import (convert_read_graph_to_layer_wise_graph,
+                                                   create_read_graph_cpu_storage)
+    from flexkv_amd.common.config import CacheConfig, ModelConfig
+    from flexkv_amd.common.storage import KVCacheLayout, KVCacheLayoutType
+    from flexkv_amd.storage.allocator import AccessHandleType, StorageHandle
+    from flexkv_amd.transfer.transfer_engine import TransferEngine
+    w = wl.w
+    L = w["layers"]
+    gl = KVCacheLayout(KVCacheLayoutType.LAYERWISE, L, w["ng"], w["tokens"], w["heads"],
+                       w["dim"], is_mla=wl.mla)
+    cl = KVCacheLayout(KVCacheLayoutType.BLOCKWISE, L, w["nh"], w["tokens"], w["heads"],
+                       w["dim"], is_mla=wl.mla)
+    gpu_h = StorageHandle(AccessHandleType.TENSOR, wl.layers, gl, wl.dtype, gpu_device_id=0)
+    cpu_h = StorageHandle(AccessHandleType.TENSOR, wl.host, cl, wl.dtype)
+    mc = ModelConfig(num_layers=L, num_kv_heads=w["heads"], head_size=w["dim"],
+                     use_mla=wl.mla, dtype=wl.dtype)
+    out = {}
+    for eager in (False, True):
+        eng = TransferEngine([gpu_h], mc, CacheConfig(), cpu_handle=cpu_h, eager_dispatch=eager)
+        eng.start()
+        times = []
+        try:
+            for _ in range(steps + 1):
+                rg, ends = create_read_graph_cpu_storage(wl.gids, wl.cids,
+                                                         torch.empty(0, dtype=torch.int64),
+                                                         layer_num=L)
+                lw, _ = convert_read_graph_to_layer_wise_graph(rg, ends, L, 1)
+                t0 = time.perf_counter()
+                eng.submit_transfer_graph(lw)
+                seen = []
+                while (lw.graph_id, -1) not in seen:
+                    seen += eng.get_completed_graphs_and_ops(timeout=0.05)
+                times.append(time.perf_counter() - t0)
+        finally:
+            eng.shutdown()
+        med = statistics.median(times[1:])
+        out["eager" if eager else "reference_scheduling"] = {
+            "ms": round(med * 1e3, 2), "gbps": round(wl.bytes_per_op / med / 1e9, 2)}
+    out["what"] = f"{L} one-layer H2D ops chained layer by layer, thread worker, zero-copy path"
+    return out
+
+
 def call_latency(wl: Workload, reps: int = 200):
     """Wall time of small synchronous calls (1 block x 1 layer, 16 blocks x 1
     layer, 16 blocks x all layers), zero-copy path, median of `reps`."""
@@ -523,6 +570,8 @@ def main() -> int:
         log(f"CE per-chunk loop: {gb / el:.2f} GB/s")
         result["layerwise_h2d"] = layerwise_h2d(wl, args.steps)
         log(f"layer-wise H2D: {result['layerwise_h2d']}")
+        result["engine_layerwise_read"] = engine_layerwise(wl, args.steps)
+        log(f"engine layer-wise read: {result['engine_layerwise_read']}")
         result["call_latency"] = call_latency(wl)
         log(f"call latency: {result['call_latency']}")
         threads, cpu = cpu_baseline(wl, args.cpu_budget)

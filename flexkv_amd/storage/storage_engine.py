@@ -1,0 +1,67 @@
+"""Storage handles for the GPU and host caches (role of
+flexkv/storage/storage_engine.py:15-90, CPU and GPU tiers).
+
+The host cache is allocated pinned (CacheConfig.use_pinned_memory, default
+True here; pageable memory cannot be used by the device path)."""
+from __future__ import annotations
+
+from typing import Any, Dict, List, Optional, Tuple, Union
+
+import torch
+
+from ..common.config import CacheConfig, ModelConfig
+from ..common.memory_handle import TensorSharedHandle
+from ..common.storage import KVCacheLayout, KVCacheLayoutType
+from ..common.transfer import DeviceType
+from .allocator import CPUAllocator, GPUAllocator, StorageHandle
+
+
+class StorageEngine:
+    def __init__(self, model_config: ModelConfig, cache_config: CacheConfig) -> None:
+        self._storage_handles: Dict[Tuple[DeviceType, int], StorageHandle] = {}
+        self._model_config = model_config
+        self._cache_config = cache_config
+        if cache_config.gpu_kv_layout_type != KVCacheLayoutType.LAYERWISE:
+            raise ValueError("Only layerwise layout is supported for GPU")
+        self._cpu_layout: Optional[KVCacheLayout] = None
+        if cache_config.enable_cpu:
+            self._cpu_layout = KVCacheLayout(
+                type=cache_config.cpu_kv_layout_type, num_layer=model_config.num_layers,
+                num_block=cache_config.num_cpu_blocks,
+                tokens_per_block=cache_config.tokens_per_block,
+                num_head=model_config.num_kv_heads, head_size=model_config.head_size,
+                is_mla=model_config.use_mla)
+            self.allocate(DeviceType.CPU, self._cpu_layout, model_config.dtype,
+                          pin_memory=cache_config.use_pinned_memory)
+
+    def register_gpu_blocks(self, gpu_blocks: List[Union[TensorSharedHandle, torch.Tensor]],
+                            gpu_layout: KVCacheLayout, device_id: int = 0,
+                            dtype: torch.dtype = torch.float16) -> None:
+        self.allocate(DeviceType.GPU, gpu_layout, dtype, device_id=device_id, raw_data=gpu_blocks)
+
+    def allocate(self, device_type: DeviceType, layout: KVCacheLayout, dtype: torch.dtype,
+                 device_id: int = 0, raw_data: Optional[Any] = None, **kwargs: Any) -> bool:
+        key = (device_type, device_id)
+        if key in self._storage_handles:
+            return False
+        if device_type == DeviceType.CPU:
+            handle = CPUAllocator.from_raw_data(raw_data, layout, dtype) if raw_data is not None \
+                else CPUAllocator.allocate(layout, dtype, pin_memory=kwargs.get("pin_memory", True))
+        elif device_type == DeviceType.GPU:
+            handle = GPUAllocator.from_raw_data(raw_data, layout, dtype, device_id=device_id) \
+                if raw_data is not None else \
+                GPUAllocator.allocate(layout, dtype, device_id=device_id,
+                                      num_chunks=kwargs.get("num_chunks", layout.num_layer))
+        else:
+            raise ValueError(f"storage tier {device_type.name} is not provided by this package")
+        self._storage_handles[key] = handle
+        return True
+
+    def get_storage_handle(self, device_type: DeviceType, device_id: int = 0) -> StorageHandle:
+        key = (device_type, device_id)
+        if key not in self._storage_handles:
+            raise ValueError(f"no storage handle for {device_type.name}:{device_id}")
+        return self._storage_handles[key]
+
+    def has_storage(self, device_type: DeviceType, device_id: int = 0) -> bool:
+        return (device_type, device_id) in self._storage_handles

@@ -1,0 +1,211 @@
+"""Transfer engine: runs transfer graphs on workers (role of
+flexkv/transfer/transfer_engine.py:42-307, GPU<->CPU tier).
+
+Same interface as the reference: TransferEngine(gpu_handles, model_config,
+cache_config, cpu_handle, ...), start(), submit_transfer_graph(graph),
+get_completed_graphs_and_ops(timeout) -> [(graph_id, op_id)] with op_id -1
+for a finished graph, shutdown().  One GPU<->CPU worker per data-parallel
+group takes the H2D and D2H ops of that group (op.dp_id).
+
+Differences:
+  * workers run on threads of this process by default (worker_mode="thread"):
+    the transfer releases the GIL, and the pinned host cache needs no
+    inter-process sharing; worker_mode="process" spawns them as the
+    reference does, each allocating its own pinned host cache;
+  * the scheduler thread blocks on one event queue (new graphs and finished
+    ops) instead of polling every millisecond;
+  * eager_dispatch: an op whose unfinished predecessors are all already
+    queued on the same worker is handed to that worker at once; the worker
+    runs its ops in submission order on one stream, so the dependency holds
+    without a scheduler round trip between layer groups.
+"""
+from __future__ import annotations
+
+import queue
+import threading
+from typing import Dict, List, Optional, Tuple
+
+import torch
+
+from ..common.config import CacheConfig, ModelConfig
+from ..common.debug import flexkv_logger
+from ..common.transfer import TransferOp, TransferOpGraph, TransferType
+from ..storage.allocator import HostCacheSpec, StorageHandle
+from .scheduler import TransferScheduler
+from .worker import GPUCPUTransferWorker
+
+_GPU_CPU = (TransferType.H2D, TransferType.D2H)
+
+
+class TransferEngine:
+    def __init__(self, gpu_handles: List[StorageHandle], model_config: ModelConfig,
+                 cache_config: CacheConfig, cpu_handle: Optional[StorageHandle] = None,
+                 ssd_handle: Optional[StorageHandle] = None,
+                 remote_handle: Optional[StorageHandle] = None,
+                 worker_mode: str = "thread", eager_dispatch: bool = True) -> None:
+        if worker_mode not in ("thread", "process"):
+            raise ValueError(f"worker_mode must be 'thread' or 'process', got {worker_mode!r}")
+        if model_config.tp_size != 1:
+            raise NotImplementedError("tensor-parallel groups need one worker per GPU group; "
+                                      "this engine drives one GPU per data-parallel group")
+        if ssd_handle is not None or remote_handle is not None:
+            raise NotImplementedError("only the GPU<->CPU tier is provided")
+        assert len(gpu_handles) == model_config.dp_size * model_config.tp_size
+        self.model_config = model_config
+        self.cache_config = cache_config
+        self.gpu_handles = gpu_handles
+        self._cpu_handle = cpu_handle
+        self.worker_mode = worker_mode
+        self.eager_dispatch = eager_dispatch
+        self.scheduler = TransferScheduler(self._same_worker if eager_dispatch else None)
+        self._events: "queue.Queue" = queue.Queue()
+        self.completed_queue: "queue.Queue[Tuple[int, int]]" = queue.Queue()
+        self.op_id_to_op: Dict[int, TransferOp] = {}
+        self._running = False
+        self._workers: List = []
+        self._mp_finished = None
+        self._forwarder: Optional[threading.Thread] = None
+
+    # -- worker routing ---------------------------------------------------
+    @staticmethod
+    def _worker_key(op: TransferOp):
+        return ("gpucpu", op.dp_id) if op.transfer_type in _GPU_CPU else (op.transfer_type, 0)
+
+    def _same_worker(self, op: TransferOp, pending_predecessors: List[TransferOp]) -> bool:
+        if op.transfer_type == TransferType.VIRTUAL:
+            return False
+        key = self._worker_key(op)
+        return all(p.transfer_type != TransferType.VIRTUAL and self._worker_key(p) == key
+                   for p in pending_predecessors)
+
+    # -- lifecycle ----------------------------------------------------------
+    def _init_workers(self) -> None:
+        if self._running:
+            return
+        if self._cpu_handle is None:
+            raise ValueError("a CPU storage handle is required")
+        cfg = self.cache_config
+        for i in range(self.model_config.dp_size):
+            g = self.gpu_handles[i]
+            common = dict(gpu_kv_layout=g.kv_layout, cpu_kv_layout=self._cpu_handle.kv_layout,
+                          dtype=g.dtype, gpu_device_id=g.gpu_device_id if g.gpu_device_id is not None else i,
+                          use_ce_transfer_h2d=cfg.use_ce_transfer_h2d,
+                          use_ce_transfer_d2h=cfg.use_ce_transfer_d2h,
+                          transfer_sms_h2d=cfg.transfer_sms_h2d,
+                          transfer_sms_d2h=cfg.transfer_sms_d2h)
+            if self.worker_mode == "thread":
+                w = GPUCPUTransferWorker.create_worker_thread(
+                    i, self._events, gpu_blocks=g.get_tensor_list(),
+                    cpu_blocks=self._cpu_handle.get_tensor(), **common)
+                w.wait_ready(60)
+            else:
+                import multiprocessing as mp
+                if self._mp_finished is None:
+                    self._mp_finished = mp.get_context("spawn").Queue()
+                w = GPUCPUTransferWorker.create_worker(
+                    i, self._mp_finished, gpu_blocks=g.get_tensor_handle_list(),
+                    cpu_blocks=HostCacheSpec(self._cpu_handle.kv_layout, self._cpu_handle.dtype),
+                    **common)
+                if not w.ready_event.wait(120):
+                    raise TimeoutError(f"worker {i} did not start")
+            self._workers.append(w)
+        self._running = True
+        if self._mp_finished is not None:
+            self._forwarder = threading.Thread(target=self._forward_finished, daemon=True)
+            self._forwarder.start()
+        self._scheduler_thread = threading.Thread(target=self._scheduler_loop, daemon=True,
+                                                  name="flexkv-scheduler")
+        self._scheduler_thread.start()
+        flexkv_logger.info(f"TransferEngine running with {len(self._workers)} "
+                           f"{self.worker_mode} worker(s)")
+
+    def start(self) -> None:
+        self._init_workers()
+
+    def _forward_finished(self) -> None:
+        while self._running:
+            try:
+                op_id = self._mp_finished.get(timeout=0.05)
+            except queue.Empty:
+                continue
+            self._events.put(op_id)
+
+    def _scheduler_loop(self) -> None:
+        while self._running:
+            try:
+                self._schedule_once()
+            except Exception as e:  # keep scheduling other graphs
+                flexkv_logger.error(f"Error in scheduler loop: {e}")
+
+    def _schedule_once(self) -> None:
+        """Take every pending event (new graphs, finished op ids), schedule, dispatch."""
+        try:
+            first = self._events.get(timeout=0.05)
+        except queue.Empty:
+            return
+        items = [first]
+        while True:
+            try:
+                items.append(self._events.get_nowait())
+            except queue.Empty:
+                break
+        finished: List[TransferOp] = []
+        for item in items:
+            if isinstance(item, TransferOpGraph):
+                self.scheduler.add_transfer_graph(item)
+            elif item is None:
+                continue
+            else:
+                op = self.op_id_to_op.pop(item)
+                self.completed_queue.put((op.graph_id, op.op_id))
+                finished.append(op)
+        done_graphs, next_ops = self.scheduler.schedule(finished)
+        for op in next_ops:
+            if op.transfer_type == TransferType.VIRTUAL:
+                self.completed_queue.put((op.graph_id, op.op_id))
+            else:
+                self.op_id_to_op[op.op_id] = op
+                self._assign_op_to_worker(op)
+        for gid in done_graphs:
+            self.completed_queue.put((gid, -1))
+
+    def _assign_op_to_worker(self, op: TransferOp) -> None:
+        if op.transfer_type not in _GPU_CPU:
+            raise ValueError(f"Unsupported transfer type: {op.transfer_type}")
+        self._workers[op.dp_id].submit_transfer(op)
+
+    # -- public API ------------------------------------------------------------
+    def submit_transfer_graph(self, transfer_graph: TransferOpGraph) -> None:
+        self._events.put(transfer_graph)
+
+    def get_completed_graphs_and_ops(self, timeout: Optional[float] = None
+                                     ) -> List[Tuple[int, int]]:
+        """Every (graph_id, op_id) completed so far; op_id -1 marks a finished
+        graph.  Waits up to `timeout` for the first one."""
+        out: List[Tuple[int, int]] = []
+        try:
+            out.append(self.completed_queue.get(timeout=timeout) if timeout
+                       else self.completed_queue.get_nowait())
+        except queue.Empty:
+            return out
+        while True:
+            try:
+                out.append(self.completed_queue.get_nowait())
+            except queue.Empty:
+                return out
+
+    def shutdown(self) -> None:
+        self._running = False
+        self._events.put(None)
+        if hasattr(self, "_scheduler_thread"):
+            self._scheduler_thread.join(timeout=5)
+        for w in self._workers:
+            try:
+                w.shutdown()
+            except Exception as e:
+                flexkv_logger.error(f"Error during worker shutdown: {e}")
+        self._workers = []
+        if self._forwarder is not None:
+            self._forwarder.join(timeout=5)
+        if torch.cuda.is_available():
+            torch.cuda.synchronize()

@@ -18,7 +18,9 @@ Differences from the reference:
 """
 from __future__ import annotations
 
+import collections
 import multiprocessing as mp
+import threading
 import time
 from abc import ABC, abstractmethod
 from multiprocessing.connection import Connection
@@ -68,6 +70,35 @@ class WorkerTransferOp:
                 f"layer_id={self.layer_id}, granularity={self.layer_granularity})")
 
 
+class LocalChannel:
+    """In-process stand-in for a multiprocessing Connection pair: send() from
+    the engine, poll()/recv() in the worker thread."""
+
+    def __init__(self) -> None:
+        self._items: "collections.deque" = collections.deque()
+        self._cv = threading.Condition()
+
+    def send(self, obj: Any) -> None:
+        with self._cv:
+            self._items.append(obj)
+            self._cv.notify()
+
+    def poll(self, timeout: float = 0.0) -> bool:
+        with self._cv:
+            if not self._items and timeout:
+                self._cv.wait(timeout)
+            return bool(self._items)
+
+    def recv(self) -> Any:
+        with self._cv:
+            while not self._items:
+                self._cv.wait()
+            return self._items.popleft()
+
+    def close(self) -> None:
+        pass
+
+
 class TransferWorkerBase(ABC):
     def __init__(self, worker_id: int, transfer_conn: Optional[Connection],
                  finished_ops_queue: Optional[Any]) -> None:
@@ -96,6 +127,30 @@ class TransferWorkerBase(ABC):
                               kwargs=kwargs, daemon=True)
         process.start()
         return WorkerHandle(worker_id, parent_conn, process, ready_event)
+
+    @classmethod
+    def create_worker_thread(cls, worker_id: int, finished_ops_queue: Any, *args: Any,
+                             **kwargs: Any) -> "ThreadWorkerHandle":
+        """Start the worker on a thread of this process.  The transfer call
+        releases the GIL (ctypes), and the worker shares this process's pinned
+        host cache and device tensors directly, with no IPC."""
+        conn = LocalChannel()
+        ready_event = threading.Event()
+        errors: List[BaseException] = []
+
+        def body() -> None:
+            try:
+                worker = cls(worker_id, conn, finished_ops_queue, *args, **kwargs)
+            except BaseException as e:  # surfaced by ThreadWorkerHandle.wait_ready
+                errors.append(e)
+                ready_event.set()
+                return
+            ready_event.set()
+            worker.run()
+
+        thread = threading.Thread(target=body, name=f"flexkv-worker-{worker_id}", daemon=True)
+        thread.start()
+        return ThreadWorkerHandle(worker_id, conn, thread, ready_event, errors)
 
     @classmethod
     def _worker_process(cls, worker_id: int, transfer_conn: Connection, finished_ops_queue: Any,
@@ -190,6 +245,32 @@ class WorkerHandle:
                 self.shutdown()
         except Exception:
             pass
+
+
+class ThreadWorkerHandle:
+    """Handle of a worker running on a thread (same interface as WorkerHandle)."""
+
+    def __init__(self, worker_id: int, conn: LocalChannel, thread: threading.Thread,
+                 ready_event: threading.Event, errors: List[BaseException]) -> None:
+        self.worker_id = worker_id
+        self.transfer_conn = conn
+        self.thread = thread
+        self.ready_event = ready_event
+        self._errors = errors
+
+    def wait_ready(self, timeout: float = 60.0) -> None:
+        if not self.ready_event.wait(timeout):
+            raise TimeoutError(f"worker {self.worker_id} did not start in {timeout}s")
+        if self._errors:
+            raise RuntimeError(f"worker {self.worker_id} failed to start: {self._errors[0]}") \
+                from self._errors[0]
+
+    def submit_transfer(self, op: TransferOp) -> None:
+        self.transfer_conn.send(WorkerTransferOp(op))
+
+    def shutdown(self) -> None:
+        self.transfer_conn.send(None)
+        self.thread.join(timeout=5)
 
 
 class GPUCPUTransferWorker(TransferWorkerBase):
