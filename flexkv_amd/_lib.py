@@ -38,6 +38,9 @@ EXPORTED_SYMBOLS = (
     "fkv_handle_release",
     "fkv_stream_create",
     "fkv_stream_destroy",
+    "fkv_ssd_open",
+    "fkv_ssd_close",
+    "fkv_transfer_kv_blocks_ssd",
     "fkv_last_error",
     "fkv_host_alloc",
     "fkv_host_free",
@@ -94,6 +97,15 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.fkv_stream_create.argtypes = [c_int, ctypes.POINTER(c_vp)]
     lib.fkv_stream_destroy.restype = c_int
     lib.fkv_stream_destroy.argtypes = [c_vp]
+    lib.fkv_ssd_open.restype = c_int
+    lib.fkv_ssd_open.argtypes = [ctypes.POINTER(ctypes.c_char_p), c_int, c_int,
+                                 ctypes.POINTER(c_vp)]
+    lib.fkv_ssd_close.restype = c_int
+    lib.fkv_ssd_close.argtypes = [c_vp]
+    f = lib.fkv_transfer_kv_blocks_ssd
+    f.restype = c_int
+    f.argtypes = [c_vp, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_i64, c_i64, c_i64, c_i64,
+                  c_i64, c_i64, c_int, c_int, c_int, c_int]
     lib.fkv_last_error.restype = ctypes.c_char_p
     lib.fkv_last_error.argtypes = []
     lib.fkv_host_alloc.restype = c_int

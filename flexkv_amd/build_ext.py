@@ -11,7 +11,7 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SOURCES = [os.path.join(HERE, "csrc", "kv_transfer.hip")]
+SOURCES = [os.path.join(HERE, "csrc", "kv_transfer.hip"), os.path.join(HERE, "csrc", "kv_ssd.cpp")]
 OUT = os.path.join(HERE, "libflexkv_hip.so")
 ARCH = "gfx950"
 

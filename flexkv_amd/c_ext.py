@@ -14,7 +14,8 @@ import torch
 from . import _lib
 
 __all__ = ["transfer_kv_blocks", "gather_kv_blocks", "scatter_kv_blocks",
-           "transfer_kv_blocks_layerwise", "LayerwiseTransfer", "transfer_stream"]
+           "transfer_kv_blocks_layerwise", "LayerwiseTransfer", "transfer_stream",
+           "SSDIOCTX", "transfer_kv_blocks_ssd"]
 
 
 def _require_int64_host(t: torch.Tensor, name: str) -> None:
@@ -229,3 +230,83 @@ def transfer_stream(num_cus: int = 0) -> torch.cuda.ExternalStream:
     out = ctypes.c_void_p()
     _lib.check(lib.fkv_stream_create(int(num_cus), ctypes.byref(out)), "fkv_stream_create")
     return torch.cuda.ExternalStream(out.value)
+
+
+class SSDIOCTX:
+    """Open SSD cache files (csrc/transfer_ssd.h:174-204, bound at
+    csrc/bindings.cpp:141-142): ``ssd_files`` maps device index -> file paths,
+    every device holding the same number of files.  Each file is opened for
+    buffered I/O and, where the file system allows it, O_DIRECT reads.  The
+    io_uring arguments are accepted for interface parity; I/O is done with
+    pread/pwrite on worker threads."""
+
+    def __init__(self, ssd_files, num_devices: int, iouring_entries: int = 0,
+                 iouring_flags: int = 0) -> None:
+        import ctypes
+
+        self._h = None
+        if num_devices <= 0:
+            raise ValueError("num_devices must be positive")
+        lists = [list(ssd_files[d]) for d in range(num_devices)]
+        per = len(lists[0])
+        if per == 0 or any(len(x) != per for x in lists):
+            raise ValueError("every SSD device needs the same, non-zero number of files")
+        paths = [p.encode() for x in lists for p in x]
+        arr = (ctypes.c_char_p * len(paths))(*paths)
+        out = ctypes.c_void_p()
+        lib = _lib.load()
+        rc = lib.fkv_ssd_open(arr, int(num_devices), int(per), ctypes.byref(out))
+        if rc != 0:
+            raise RuntimeError(_lib.last_error() or "Failed to open file")
+        self._h = out.value
+        self.num_devices = num_devices
+        self.num_files_per_device = per
+
+    def close(self) -> None:
+        h, self._h = self._h, None
+        if h:
+            _lib.load().fkv_ssd_close(h)
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def transfer_kv_blocks_ssd(ioctx: SSDIOCTX, cpu_layer_id_list: torch.Tensor, cpu_tensor_ptr: int,
+                           ssd_block_ids: torch.Tensor, cpu_block_ids: torch.Tensor,
+                           cpu_layer_stride_in_bytes: int, cpu_kv_stride_in_bytes: int,
+                           ssd_layer_stride_in_bytes: int, ssd_kv_stride_in_bytes: int,
+                           chunk_size_in_bytes: int, block_stride_in_bytes: int, is_read: bool,
+                           num_blocks_per_file: int, round_robin: int = 1,
+                           num_threads_per_device: int = 16, is_mla: bool = False) -> None:
+    """Host cache <-> SSD files (csrc/bindings.cpp:57-76 and :110-117,
+    csrc/transfer_ssd.cpp:182-285): the layers of ``cpu_layer_id_list`` (a
+    contiguous int32 range) of each block pair move between the host cache at
+    ``cpu_tensor_ptr`` and the files of ``ioctx``.  Blocking; raises
+    RuntimeError on an I/O failure."""
+    if ssd_block_ids.dtype != torch.int64:
+        raise TypeError("ssd_block_ids must be int64")
+    if cpu_block_ids.dtype != torch.int64:
+        raise TypeError("cpu_block_ids must be int64")
+    if ssd_block_ids.numel() != cpu_block_ids.numel():
+        raise RuntimeError("ssd and cpu block id tensors differ in length")
+    if ioctx._h is None:
+        raise RuntimeError("SSD context is closed")
+    layers = cpu_layer_id_list.to(torch.int64).tolist()
+    if not layers:
+        return
+    start = int(layers[0])
+    if layers != list(range(start, start + len(layers))):
+        raise ValueError("cpu_layer_id_list must be a contiguous ascending range")
+    sids = ssd_block_ids.contiguous().cpu()
+    cids = cpu_block_ids.contiguous().cpu()
+    rc = _lib.load().fkv_transfer_kv_blocks_ssd(
+        ioctx._h, start, len(layers), int(cpu_tensor_ptr), sids.data_ptr(), cids.data_ptr(),
+        int(sids.numel()), int(cpu_layer_stride_in_bytes), int(cpu_kv_stride_in_bytes),
+        int(ssd_layer_stride_in_bytes), int(ssd_kv_stride_in_bytes), int(chunk_size_in_bytes),
+        int(block_stride_in_bytes), 1 if is_read else 0, int(round_robin),
+        int(num_threads_per_device), 1 if is_mla else 0)
+    if rc != 0:
+        raise RuntimeError(_lib.last_error() or "Failed to transfer data")

@@ -1,14 +1,18 @@
 """Model and cache configuration for the GPU<->CPU transfer path.
 
 ModelConfig matches the reference (flexkv/common/config.py:10-25).  CacheConfig
-keeps the fields that shape this path (config.py:27-51): block size, host
-layout and pinning, host block count, and the per-direction transfer knobs.
-The SSD, remote and trace fields belong to tiers this package does not
-implement and are not present.
+keeps the fields that shape this path and its SSD tier (config.py:27-57):
+block size, host layout and pinning, host block count, the per-direction
+transfer knobs, and the SSD cache (enable_ssd, layout, block count, files).
+The remote and trace fields belong to parts this package does not implement
+and are not present.  Defaults that differ from the reference: the host and
+SSD layouts are BLOCKWISE (one block's layers contiguous, which the device
+path and the SSD path both move as single runs) and the host cache is pinned.
 """
 from __future__ import annotations
 
 from dataclasses import dataclass
+from typing import List, Optional, Union
 
 import torch
 
@@ -35,13 +39,24 @@ class ModelConfig:
 class CacheConfig:
     tokens_per_block: int = 16
     enable_cpu: bool = True
+    enable_ssd: bool = False
     use_pinned_memory: bool = True
     gpu_kv_layout_type: KVCacheLayoutType = KVCacheLayoutType.LAYERWISE
     cpu_kv_layout_type: KVCacheLayoutType = KVCacheLayoutType.BLOCKWISE
+    ssd_kv_layout_type: KVCacheLayoutType = KVCacheLayoutType.BLOCKWISE
     num_cpu_blocks: int = 1000000
+    num_ssd_blocks: int = 10000000
     # False = zero-copy kernel, True = copy engines via on-device staging
     use_ce_transfer_h2d: bool = False
     use_ce_transfer_d2h: bool = False
     # compute units the zero-copy kernel may occupy (-1 = automatic)
     transfer_sms_h2d: int = 8
     transfer_sms_d2h: int = 8
+    # SSD cache: one directory per device; -1 = no per-file block limit
+    max_blocks_per_file: int = 32000
+    ssd_cache_dir: Optional[Union[str, List[str]]] = None
+    # accepted for interface parity (I/O uses pread/pwrite threads)
+    ssd_cache_iouring_entries: int = 0
+    ssd_cache_iouring_flags: int = 0
+    # threads per SSD device for one transfer (worker.py:573 uses 32)
+    ssd_threads_per_device: int = 32

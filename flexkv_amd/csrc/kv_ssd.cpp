@@ -1,0 +1,212 @@
+// kv_ssd.cpp - host cache <-> SSD files for KV blocks (host code only).
+//
+// File layout and block mapping follow the reference SSD tier
+// (csrc/transfer_ssd.cpp:17-285, flexkv/storage/allocator.py:132-193,
+// flexkv/transfer/worker.py:482-602):
+//   * SSD block b lives on device d = (b / rr) % D at device block
+//     ((b / rr) / D) * rr + b % rr  (rr = round-robin width);
+//   * a device block x lives in file x % F of that device, at in-file block
+//     x / F;
+//   * chunk (layer l, K|V k) of a block is at
+//       file:  x_in_file * block_stride + l * ssd_layer_stride + k * ssd_kv_stride
+//       host:  cpu_id    * block_stride + l * cpu_layer_stride + k * cpu_kv_stride
+//     and is chunk_size bytes;
+//   * each device's blocks are split into contiguous ranges over
+//     num_threads_per_device threads.
+// Reads use O_DIRECT descriptors when chunk_size is a multiple of 4096
+// (transfer_ssd.cpp:201), like the reference.  Where a block's layers are
+// contiguous on both sides (block-wise layouts), the layer window of a block
+// moves as one I/O instead of one per chunk.
+
+#include <fcntl.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cerrno>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "flexkv_hip.h"
+#include "fkv_error.h"
+
+namespace {
+
+int ssd_fail(const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  fkv_detail::last_error() = buf;
+  return 1;
+}
+
+// Full-length pread/pwrite, retrying short transfers and EINTR.
+bool io_all(int fd, char* buf, int64_t bytes, int64_t off, bool is_read) {
+  while (bytes > 0) {
+    const ssize_t r = is_read ? pread(fd, buf, static_cast<size_t>(bytes), off)
+                              : pwrite(fd, buf, static_cast<size_t>(bytes), off);
+    if (r < 0) {
+      if (errno == EINTR) continue;
+      return false;
+    }
+    if (r == 0) return false;  // past end of file
+    buf += r;
+    off += r;
+    bytes -= r;
+  }
+  return true;
+}
+
+}  // namespace
+
+struct fkv_ssd_s {
+  int num_devices = 0;
+  int files_per_device = 0;
+  std::vector<std::vector<int>> fd_buffered;  // [device][file]
+  std::vector<std::vector<int>> fd_direct;    // [device][file], -1 if unavailable
+};
+
+extern "C" {
+
+int fkv_ssd_open(const char* const* paths, int num_devices, int files_per_device,
+                 fkv_ssd_t* out) {
+  fkv_detail::last_error().clear();
+  if (!out || !paths || num_devices <= 0 || files_per_device <= 0)
+    return ssd_fail("bad arguments to fkv_ssd_open");
+  *out = nullptr;
+  auto* h = new fkv_ssd_s();
+  h->num_devices = num_devices;
+  h->files_per_device = files_per_device;
+  h->fd_buffered.assign(num_devices, std::vector<int>(files_per_device, -1));
+  h->fd_direct.assign(num_devices, std::vector<int>(files_per_device, -1));
+  for (int d = 0; d < num_devices; ++d) {
+    for (int f = 0; f < files_per_device; ++f) {
+      const char* p = paths[d * files_per_device + f];
+      const int fd = open(p, O_RDWR);
+      if (fd < 0) {
+        const int e = errno;
+        fkv_ssd_close(h);
+        return ssd_fail("open(%s) failed: %s", p, strerror(e));
+      }
+      posix_fadvise(fd, 0, 0, POSIX_FADV_SEQUENTIAL);
+      h->fd_buffered[d][f] = fd;
+      h->fd_direct[d][f] = open(p, O_RDWR | O_DIRECT);  // may fail (e.g. tmpfs): fall back
+    }
+  }
+  *out = h;
+  return 0;
+}
+
+int fkv_ssd_close(fkv_ssd_t h) {
+  if (!h) return 0;
+  for (auto* v : {&h->fd_buffered, &h->fd_direct})
+    for (auto& row : *v)
+      for (int fd : row)
+        if (fd >= 0) close(fd);
+  delete h;
+  return 0;
+}
+
+int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, void* cpu_ptr,
+                               const int64_t* ssd_block_ids, const int64_t* cpu_block_ids,
+                               int num_blocks, int64_t cpu_layer_stride_bytes,
+                               int64_t cpu_kv_stride_bytes, int64_t ssd_layer_stride_bytes,
+                               int64_t ssd_kv_stride_bytes, int64_t chunk_size_bytes,
+                               int64_t block_stride_bytes, int is_read, int round_robin,
+                               int num_threads_per_device, int is_mla) {
+  fkv_detail::last_error().clear();
+  if (!h) return ssd_fail("null SSD context");
+  if (num_blocks <= 0 || num_layers <= 0) return 0;
+  if (!cpu_ptr || !ssd_block_ids || !cpu_block_ids || chunk_size_bytes <= 0 || round_robin <= 0 ||
+      start_layer < 0 || num_threads_per_device <= 0)
+    return ssd_fail("bad arguments to fkv_transfer_kv_blocks_ssd");
+  const int D = h->num_devices, F = h->files_per_device, kv = is_mla ? 1 : 2;
+  // partition by device, keeping the id-list order within a device
+  std::vector<std::vector<int64_t>> dev_ssd(D), dev_cpu(D);
+  for (int i = 0; i < num_blocks; ++i) {
+    const int64_t b = ssd_block_ids[i], c = cpu_block_ids[i];
+    if (b < 0 || c < 0) return ssd_fail("negative block id at position %d", i);
+    const int64_t q = b / round_robin;
+    const int d = static_cast<int>(q % D);
+    dev_ssd[d].push_back((q / D) * round_robin + b % round_robin);
+    dev_cpu[d].push_back(c);
+  }
+  const bool direct = is_read && chunk_size_bytes % 4096 == 0;
+  // one I/O per block when the layer window is contiguous on both sides
+  const bool row_io = (kv == 1 || (cpu_kv_stride_bytes == chunk_size_bytes &&
+                                   ssd_kv_stride_bytes == chunk_size_bytes)) &&
+                      (num_layers == 1 || (cpu_layer_stride_bytes == kv * chunk_size_bytes &&
+                                           ssd_layer_stride_bytes == kv * chunk_size_bytes));
+  std::atomic<int> failed{0};
+  std::string first_err;
+  std::atomic<bool> have_err{false};
+  auto record = [&](const char* what, int d, int64_t blk) {
+    failed = 1;
+    bool expect = false;
+    if (have_err.compare_exchange_strong(expect, true)) {
+      char buf[256];
+      snprintf(buf, sizeof(buf), "%s failed on device %d block %lld: %s", what, d,
+               static_cast<long long>(blk), strerror(errno));
+      first_err = buf;
+    }
+  };
+  auto work = [&](int d, size_t lo, size_t hi) {
+    char* base = static_cast<char*>(cpu_ptr);
+    for (size_t j = lo; j < hi && !failed; ++j) {
+      const int64_t x = dev_ssd[d][j];
+      const int f = static_cast<int>(x % F);
+      const int64_t in_file = x / F;
+      int fd = h->fd_buffered[d][f];
+      const int dfd = direct ? h->fd_direct[d][f] : -1;
+      // O_DIRECT needs an aligned buffer; fall back to the page cache if not
+      auto io = [&](char* buf, int64_t bytes, int64_t off) {
+        if (dfd >= 0 && reinterpret_cast<uintptr_t>(buf) % 4096 == 0 && bytes % 4096 == 0 &&
+            off % 4096 == 0 && io_all(dfd, buf, bytes, off, true))
+          return true;
+        return io_all(fd, buf, bytes, off, is_read != 0);
+      };
+      char* cbase = base + dev_cpu[d][j] * block_stride_bytes;
+      const int64_t sbase = in_file * block_stride_bytes;
+      if (row_io) {
+        const int64_t off_c = static_cast<int64_t>(start_layer) * cpu_layer_stride_bytes;
+        const int64_t off_s = static_cast<int64_t>(start_layer) * ssd_layer_stride_bytes;
+        if (!io(cbase + off_c, static_cast<int64_t>(num_layers) * kv * chunk_size_bytes,
+                sbase + off_s))
+          record(is_read ? "read" : "write", d, x);
+        continue;
+      }
+      for (int l = start_layer; l < start_layer + num_layers && !failed; ++l) {
+        for (int k = 0; k < kv; ++k) {
+          char* c = cbase + static_cast<int64_t>(l) * cpu_layer_stride_bytes +
+                    k * cpu_kv_stride_bytes;
+          const int64_t s = sbase + static_cast<int64_t>(l) * ssd_layer_stride_bytes +
+                            k * ssd_kv_stride_bytes;
+          if (!io(c, chunk_size_bytes, s)) {
+            record(is_read ? "read" : "write", d, x);
+            break;
+          }
+        }
+      }
+    }
+  };
+  std::vector<std::thread> threads;
+  for (int d = 0; d < D; ++d) {
+    const size_t n = dev_ssd[d].size();
+    if (n == 0) continue;
+    const size_t per = (n + num_threads_per_device - 1) / num_threads_per_device;
+    for (size_t lo = 0; lo < n; lo += per) threads.emplace_back(work, d, lo, std::min(n, lo + per));
+  }
+  for (auto& t : threads) t.join();
+  if (failed) return ssd_fail("%s", first_err.c_str());
+  return 0;
+}
+
+}  // extern "C"

@@ -31,6 +31,7 @@
 #include <vector>
 
 #include "flexkv_hip.h"
+#include "fkv_error.h"
 
 namespace {
 
@@ -223,7 +224,18 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
 // ---------------------------------------------------------------------------
 // Errors
 
-thread_local std::string t_err;
+}  // namespace
+
+namespace fkv_detail {
+std::string& last_error() {
+  static thread_local std::string msg;
+  return msg;
+}
+}  // namespace fkv_detail
+
+namespace {
+
+#define t_err (::fkv_detail::last_error())
 
 int fail(int code, const char* fmt, ...) {
   char buf[1024];

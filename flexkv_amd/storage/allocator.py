@@ -1,6 +1,6 @@
-"""Host and GPU cache allocation for the transfer path.
+"""Host, GPU and SSD cache allocation for the transfer path.
 
-Role of flexkv/storage/allocator.py:41-130.  The host cache is one flat 1-D
+Role of flexkv/storage/allocator.py:41-206.  The host cache is one flat 1-D
 tensor of layout.get_total_elements() elements (allocator.py:99-107).  Pinned
 host caches come from fkv_host_alloc (hipHostMalloc, mapped into the device
 address space) rather than torch's caching host allocator, which rounds
@@ -10,9 +10,10 @@ owns its allocation: the memory is freed when the last view of it dies.
 from __future__ import annotations
 
 import ctypes
+import os
 from dataclasses import dataclass
 from enum import Enum, auto
-from typing import Any, List, Optional, Union
+from typing import Any, BinaryIO, Dict, List, Optional, Union
 
 import numpy as np
 import torch
@@ -51,6 +52,11 @@ class StorageHandle:
         if self.handle_type == AccessHandleType.TENSOR_HANDLE:
             return [h.get_tensor() for h in self.data]
         raise ValueError(f"Invalid handle type: {self.handle_type}, expected TENSOR or TENSOR_HANDLE")
+
+    def get_file_list(self) -> Union[List[str], Dict[int, List[str]]]:
+        if self.handle_type != AccessHandleType.FILE:
+            raise ValueError(f"Invalid handle type: {self.handle_type}, expected FILE")
+        return self.data
 
     def get_tensor_handle_list(self) -> List[TensorSharedHandle]:
         if self.handle_type == AccessHandleType.TENSOR_HANDLE:
@@ -160,3 +166,77 @@ class CPUAllocator:
     def from_raw_data(cls, data: torch.Tensor, layout: KVCacheLayout, dtype: torch.dtype,
                       **kwargs: Any) -> StorageHandle:
         return StorageHandle(AccessHandleType.TENSOR, data, layout, dtype)
+
+
+class SSDAllocator:
+    """SSD cache files (allocator.py:132-206).  The blocks of `layout` are
+    split evenly over the directories of `cache_dir` (one per device); each
+    device holds ceil(blocks_per_device / num_blocks_per_file) files named
+    ``{file_prefix}_{device}_{file}.bin``, each truncated to
+    num_blocks_per_file * block bytes, where num_blocks_per_file is the
+    smaller of max_blocks_per_file and what the first directory's free space
+    holds.  The handle's data is {device: [paths]}."""
+
+    @classmethod
+    def allocate(cls, layout: KVCacheLayout, dtype: torch.dtype, **kwargs: Any) -> StorageHandle:
+        cache_dir = kwargs.get("cache_dir")
+        file_prefix = kwargs.get("file_prefix", "flexkv_ssd_cache")
+        cfg_max = kwargs.get("max_blocks_per_file", -1)
+        if cfg_max == -1:
+            cfg_max = int(1e9)
+        if cache_dir is None:
+            raise ValueError("cache_dir is required for SSD allocator")
+        if isinstance(cache_dir, str):
+            cache_dir = [cache_dir]
+        for d in cache_dir:
+            os.makedirs(d, exist_ok=True)
+            if not os.path.isdir(d):
+                raise ValueError("cache_dir must be a directory")
+        if not isinstance(file_prefix, str):
+            raise ValueError("file_prefix must be a string")
+        num_devices = len(cache_dir)
+        if layout.num_block % num_devices != 0:
+            raise ValueError(f"num_ssd_blocks ({layout.num_block}) must be a multiple of "
+                             f"num_ssd_devices ({num_devices})")
+        per_device = layout.num_block // num_devices
+        block_size = layout.get_elements_per_block() * dtype.itemsize
+        num_blocks_per_file = min(cls.get_file_size_limit(cache_dir[0]) // block_size, cfg_max)
+        if num_blocks_per_file <= 0:
+            raise ValueError(f"no room for one {block_size}-byte block in {cache_dir[0]}")
+        files_per_device = (per_device + num_blocks_per_file - 1) // num_blocks_per_file
+        file_size = num_blocks_per_file * block_size
+        ssd_files: Dict[int, List[str]] = {}
+        for i, d in enumerate(cache_dir):
+            ssd_files[i] = []
+            for j in range(files_per_device):
+                path = os.path.join(d, f"{file_prefix}_{i}_{j}.bin")
+                with open(path, "wb+", buffering=0) as f:
+                    cls._create_file(f, file_size)
+                ssd_files[i].append(path)
+        flexkv_logger.info(f"SSD allocate {num_devices} device(s) x {files_per_device} file(s) "
+                           f"of {file_size / 2**30:.3f} GiB")
+        return StorageHandle(AccessHandleType.FILE, ssd_files, layout, dtype,
+                             num_blocks_per_file=num_blocks_per_file)
+
+    @classmethod
+    def _create_file(cls, file: BinaryIO, size: int) -> None:
+        try:
+            os.truncate(file.fileno(), size)
+        except OSError as e:
+            raise RuntimeError(f"Failed to initialize file: {e}") from e
+        file.flush()
+        os.fsync(file.fileno())
+
+    @classmethod
+    def from_raw_data(cls, data: Union[str, List[str]], layout: KVCacheLayout,
+                      dtype: torch.dtype, **kwargs: Any) -> StorageHandle:
+        raise NotImplementedError
+
+    @classmethod
+    def free(cls, handle: StorageHandle) -> None:
+        pass
+
+    @staticmethod
+    def get_file_size_limit(path: str) -> int:
+        st = os.statvfs(path)
+        return st.f_frsize * st.f_bavail

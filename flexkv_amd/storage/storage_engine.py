@@ -1,5 +1,5 @@
-"""Storage handles for the GPU and host caches (role of
-flexkv/storage/storage_engine.py:15-90, CPU and GPU tiers).
+"""Storage handles for the GPU, host and SSD caches (role of
+flexkv/storage/storage_engine.py:15-190, CPU, GPU and SSD tiers).
 
 The host cache is allocated pinned (CacheConfig.use_pinned_memory, default
 True here; pageable memory cannot be used by the device path)."""
@@ -13,7 +13,7 @@ from ..common.config import CacheConfig, ModelConfig
 from ..common.memory_handle import TensorSharedHandle
 from ..common.storage import KVCacheLayout, KVCacheLayoutType
 from ..common.transfer import DeviceType
-from .allocator import CPUAllocator, GPUAllocator, StorageHandle
+from .allocator import CPUAllocator, GPUAllocator, SSDAllocator, StorageHandle
 
 
 class StorageEngine:
@@ -33,6 +33,20 @@ class StorageEngine:
                 is_mla=model_config.use_mla)
             self.allocate(DeviceType.CPU, self._cpu_layout, model_config.dtype,
                           pin_memory=cache_config.use_pinned_memory)
+        self._ssd_layout: Optional[KVCacheLayout] = None
+        if cache_config.enable_ssd:
+            if self._cpu_layout is None or cache_config.ssd_kv_layout_type != self._cpu_layout.type:
+                raise ValueError("SSD layout type must be the same as CPU layout type: "
+                                 f"{None if self._cpu_layout is None else self._cpu_layout.type}")
+            self._ssd_layout = KVCacheLayout(
+                type=cache_config.ssd_kv_layout_type, num_layer=model_config.num_layers,
+                num_block=cache_config.num_ssd_blocks,
+                tokens_per_block=cache_config.tokens_per_block,
+                num_head=model_config.num_kv_heads, head_size=model_config.head_size,
+                is_mla=model_config.use_mla)
+            self.allocate(DeviceType.SSD, self._ssd_layout, model_config.dtype,
+                          cache_dir=cache_config.ssd_cache_dir,
+                          max_blocks_per_file=cache_config.max_blocks_per_file)
 
     def register_gpu_blocks(self, gpu_blocks: List[Union[TensorSharedHandle, torch.Tensor]],
                             gpu_layout: KVCacheLayout, device_id: int = 0,
@@ -52,6 +66,16 @@ class StorageEngine:
                 if raw_data is not None else \
                 GPUAllocator.allocate(layout, dtype, device_id=device_id,
                                       num_chunks=kwargs.get("num_chunks", layout.num_layer))
+        elif device_type == DeviceType.SSD:
+            if raw_data is not None:
+                handle = SSDAllocator.from_raw_data(raw_data, layout, dtype)
+            else:
+                if not kwargs.get("cache_dir"):
+                    raise ValueError("cache_dir is required for SSD allocator")
+                handle = SSDAllocator.allocate(layout, dtype, cache_dir=kwargs["cache_dir"],
+                                               file_prefix="flexkv_ssd_cache",
+                                               max_blocks_per_file=kwargs.get(
+                                                   "max_blocks_per_file", -1))
         else:
             raise ValueError(f"storage tier {device_type.name} is not provided by this package")
         self._storage_handles[key] = handle

@@ -1,11 +1,13 @@
 """Transfer engine: runs transfer graphs on workers (role of
-flexkv/transfer/transfer_engine.py:42-307, GPU<->CPU tier).
+flexkv/transfer/transfer_engine.py:42-307, GPU<->CPU and CPU<->SSD tiers).
 
 Same interface as the reference: TransferEngine(gpu_handles, model_config,
-cache_config, cpu_handle, ...), start(), submit_transfer_graph(graph),
-get_completed_graphs_and_ops(timeout) -> [(graph_id, op_id)] with op_id -1
-for a finished graph, shutdown().  One GPU<->CPU worker per data-parallel
-group takes the H2D and D2H ops of that group (op.dp_id).
+cache_config, cpu_handle, ssd_handle, ...), start(),
+submit_transfer_graph(graph), get_completed_graphs_and_ops(timeout) ->
+[(graph_id, op_id)] with op_id -1 for a finished graph, shutdown().  One
+GPU<->CPU worker per data-parallel group takes the H2D and D2H ops of that
+group (op.dp_id); with an SSD handle, one CPU<->SSD worker takes the DISK2H
+ops and another the H2DISK ops (transfer_engine.py:129-153).
 
 Differences:
   * workers run on threads of this process by default (worker_mode="thread"):
@@ -17,7 +19,9 @@ Differences:
   * eager_dispatch: an op whose unfinished predecessors are all already
     queued on the same worker is handed to that worker at once; the worker
     runs its ops in submission order on one stream, so the dependency holds
-    without a scheduler round trip between layer groups.
+    without a scheduler round trip between layer groups;
+  * the SSD workers share the engine process's host cache, so an SSD tier
+    needs worker_mode="thread".
 """
 from __future__ import annotations
 
@@ -32,9 +36,10 @@ from ..common.debug import flexkv_logger
 from ..common.transfer import TransferOp, TransferOpGraph, TransferType
 from ..storage.allocator import HostCacheSpec, StorageHandle
 from .scheduler import TransferScheduler
-from .worker import GPUCPUTransferWorker
+from .worker import CPUSSDDiskTransferWorker, GPUCPUTransferWorker
 
 _GPU_CPU = (TransferType.H2D, TransferType.D2H)
+_CPU_SSD = (TransferType.DISK2H, TransferType.H2DISK)
 
 
 class TransferEngine:
@@ -48,13 +53,18 @@ class TransferEngine:
         if model_config.tp_size != 1:
             raise NotImplementedError("tensor-parallel groups need one worker per GPU group; "
                                       "this engine drives one GPU per data-parallel group")
-        if ssd_handle is not None or remote_handle is not None:
-            raise NotImplementedError("only the GPU<->CPU tier is provided")
+        if remote_handle is not None:
+            raise NotImplementedError("the remote tier is not provided")
+        if ssd_handle is not None and worker_mode != "thread":
+            raise NotImplementedError("the SSD tier shares the engine's host cache and needs "
+                                      "worker_mode='thread'")
         assert len(gpu_handles) == model_config.dp_size * model_config.tp_size
         self.model_config = model_config
         self.cache_config = cache_config
         self.gpu_handles = gpu_handles
         self._cpu_handle = cpu_handle
+        self._ssd_handle = ssd_handle
+        self._ssd_workers: Dict[TransferType, object] = {}
         self.worker_mode = worker_mode
         self.eager_dispatch = eager_dispatch
         self.scheduler = TransferScheduler(self._same_worker if eager_dispatch else None)
@@ -109,6 +119,18 @@ class TransferEngine:
                 if not w.ready_event.wait(120):
                     raise TimeoutError(f"worker {i} did not start")
             self._workers.append(w)
+        if self._ssd_handle is not None:
+            common = dict(cpu_blocks=self._cpu_handle.get_tensor(),
+                          ssd_files=self._ssd_handle.get_file_list(),
+                          cpu_kv_layout=self._cpu_handle.kv_layout,
+                          ssd_kv_layout=self._ssd_handle.kv_layout,
+                          dtype=self._cpu_handle.dtype,
+                          num_blocks_per_file=self._ssd_handle.num_blocks_per_file,
+                          cache_config=cfg)
+            for wid, kind in ((10, TransferType.DISK2H), (11, TransferType.H2DISK)):
+                w = CPUSSDDiskTransferWorker.create_worker_thread(wid, self._events, **common)
+                w.wait_ready(60)
+                self._ssd_workers[kind] = w
         self._running = True
         if self._mp_finished is not None:
             self._forwarder = threading.Thread(target=self._forward_finished, daemon=True)
@@ -170,9 +192,12 @@ class TransferEngine:
             self.completed_queue.put((gid, -1))
 
     def _assign_op_to_worker(self, op: TransferOp) -> None:
-        if op.transfer_type not in _GPU_CPU:
+        if op.transfer_type in _GPU_CPU:
+            self._workers[op.dp_id].submit_transfer(op)
+        elif op.transfer_type in _CPU_SSD and op.transfer_type in self._ssd_workers:
+            self._ssd_workers[op.transfer_type].submit_transfer(op)
+        else:
             raise ValueError(f"Unsupported transfer type: {op.transfer_type}")
-        self._workers[op.dp_id].submit_transfer(op)
 
     # -- public API ------------------------------------------------------------
     def submit_transfer_graph(self, transfer_graph: TransferOpGraph) -> None:
@@ -199,12 +224,13 @@ class TransferEngine:
         self._events.put(None)
         if hasattr(self, "_scheduler_thread"):
             self._scheduler_thread.join(timeout=5)
-        for w in self._workers:
+        for w in self._workers + list(self._ssd_workers.values()):
             try:
                 w.shutdown()
             except Exception as e:
                 flexkv_logger.error(f"Error during worker shutdown: {e}")
         self._workers = []
+        self._ssd_workers = {}
         if self._forwarder is not None:
             self._forwarder.join(timeout=5)
         if torch.cuda.is_available():

@@ -1,11 +1,12 @@
-"""Transfer workers for the GPU<->CPU path.
+"""Transfer workers for the GPU<->CPU path and the CPU<->SSD tier.
 
 Same API as the reference's worker module for the single-GPU case
-(flexkv/transfer/worker.py:49-342): WorkerTransferOp, TransferWorkerBase
-(create_worker spawns a process fed through a Pipe, run() polls and batches
-ops, finished op ids go to a queue), WorkerHandle (submit_transfer, shutdown)
-and GPUCPUTransferWorker (_transfer_impl, launch_transfer).  The transfer
-itself is flexkv_amd.c_ext.transfer_kv_blocks.
+(flexkv/transfer/worker.py:49-342 and :482-602): WorkerTransferOp,
+TransferWorkerBase (create_worker spawns a process fed through a Pipe, run()
+polls and batches ops, finished op ids go to a queue), WorkerHandle
+(submit_transfer, shutdown), GPUCPUTransferWorker and CPUSSDDiskTransferWorker
+(_transfer_impl, launch_transfer).  The transfers themselves are
+flexkv_amd.c_ext.transfer_kv_blocks and transfer_kv_blocks_ssd.
 
 Differences from the reference:
   * the host cache must already be pinned (CPUAllocator pin_memory=True);
@@ -24,14 +25,14 @@ import threading
 import time
 from abc import ABC, abstractmethod
 from multiprocessing.connection import Connection
-from typing import Any, List, Optional, Sequence, Union
+from typing import Any, Dict, List, Optional, Sequence, Union
 
 import ctypes
 import numpy as np
 import torch
 
 from .. import _lib
-from ..c_ext import transfer_kv_blocks
+from ..c_ext import SSDIOCTX, transfer_kv_blocks, transfer_kv_blocks_ssd
 from ..common.debug import flexkv_logger
 from ..common.memory_handle import TensorSharedHandle
 from ..common.storage import KVCacheLayout, KVCacheLayoutType
@@ -353,3 +354,104 @@ class GPUCPUTransferWorker(TransferWorkerBase):
         kv_dim = 1 if self.is_mla else 2
         size = self.chunk_size_in_bytes * granularity * len(transfer_op.src_block_ids) * kv_dim
         self._log_transfer_performance(transfer_op, size, start, end)
+
+
+class CPUSSDDiskTransferWorker(TransferWorkerBase):
+    """Moves KV blocks between the host cache and the SSD cache files
+    (worker.py:482-602): H2DISK writes host blocks to SSD blocks, DISK2H
+    reads them back.  The SSD layout is split over all files
+    (div_block(num_files, padding=True)) for its layer and K/V strides; the
+    block stride is the host layout's, so both layouts must be the same
+    type.  Host code only: it needs no device."""
+
+    def __init__(self, worker_id: int, transfer_conn: Optional[Connection],
+                 finished_ops_queue: Optional[Any], cpu_blocks: torch.Tensor,
+                 ssd_files: Dict[int, List[str]], cpu_kv_layout: KVCacheLayout,
+                 ssd_kv_layout: KVCacheLayout, dtype: torch.dtype, num_blocks_per_file: int,
+                 cache_config: Any = None) -> None:
+        super().__init__(worker_id, transfer_conn, finished_ops_queue)
+        if cpu_kv_layout.type != ssd_kv_layout.type:
+            raise ValueError("no support for different CPU and SSD KV cache layout type")
+        self.ssd_files = ssd_files
+        self.num_blocks_per_file = num_blocks_per_file
+        self.num_files = sum(len(v) for v in ssd_files.values())
+        self.num_layers = cpu_kv_layout.num_layer
+        self.num_cpu_blocks = cpu_kv_layout.num_block
+        self.num_ssd_blocks = ssd_kv_layout.num_block
+        self.round_robin = 1
+        self.dtype = dtype
+        self.cpu_tensor = cpu_blocks
+        self.is_mla = cpu_kv_layout.is_mla
+        per_file = ssd_kv_layout.div_block(self.num_files, padding=True)
+        es = dtype.itemsize
+        self.chunk_size_in_bytes = cpu_kv_layout.get_chunk_size() * es
+        self.block_stride_in_bytes = cpu_kv_layout.get_block_stride() * es
+        self.cpu_kv_stride_in_bytes = cpu_kv_layout.get_kv_stride() * es
+        self.cpu_layer_stride_in_bytes = cpu_kv_layout.get_layer_stride() * es
+        self.ssd_kv_stride_in_bytes = per_file.get_kv_stride() * es
+        self.ssd_layer_stride_in_bytes = per_file.get_layer_stride() * es
+        self.num_threads_per_device = getattr(cache_config, "ssd_threads_per_device", 32)
+        try:
+            self.ioctx = SSDIOCTX(ssd_files, len(ssd_files),
+                                  getattr(cache_config, "ssd_cache_iouring_entries", 0),
+                                  getattr(cache_config, "ssd_cache_iouring_flags", 0))
+        except Exception as e:
+            flexkv_logger.error(f"Error setting ssd ioctx: {e}")
+            raise RuntimeError("SSD Worker init failed") from e
+
+    def _transfer_impl(self, src_block_ids: np.ndarray, dst_block_ids: np.ndarray,
+                       transfer_type: TransferType, layer_id: int, layer_granularity: int,
+                       **kwargs: Any) -> None:
+        assert src_block_ids.dtype == np.int64
+        assert dst_block_ids.dtype == np.int64
+        assert len(src_block_ids) == len(dst_block_ids)
+        if transfer_type == TransferType.H2DISK:
+            ssd_ids, cpu_ids = dst_block_ids, src_block_ids
+        elif transfer_type == TransferType.DISK2H:
+            ssd_ids, cpu_ids = src_block_ids, dst_block_ids
+        else:
+            raise ValueError(f"Invalid transfer type: {transfer_type} for CPUSSDDiskTransferWorker")
+        if len(ssd_ids) == 0:
+            return
+        if layer_id < 0 or layer_granularity < 1 or layer_id + layer_granularity > self.num_layers:
+            raise ValueError(f"layer range [{layer_id}, {layer_id + layer_granularity}) is outside "
+                             f"[0, {self.num_layers})")
+        # a write past a file's end would grow the file, a read past it fails:
+        # reject ids outside either cache up front
+        for name, ids, limit in (("ssd", ssd_ids, self.num_ssd_blocks),
+                                 ("cpu", cpu_ids, self.num_cpu_blocks)):
+            if ids.min() < 0 or ids.max() >= limit:
+                raise ValueError(f"{name} block id out of range [0, {limit})")
+        transfer_kv_blocks_ssd(
+            ioctx=self.ioctx,
+            cpu_layer_id_list=torch.arange(layer_id, layer_id + layer_granularity,
+                                           dtype=torch.int32),
+            cpu_tensor_ptr=self.cpu_tensor.data_ptr(),
+            ssd_block_ids=torch.from_numpy(np.ascontiguousarray(ssd_ids)),
+            cpu_block_ids=torch.from_numpy(np.ascontiguousarray(cpu_ids)),
+            cpu_layer_stride_in_bytes=self.cpu_layer_stride_in_bytes,
+            cpu_kv_stride_in_bytes=self.cpu_kv_stride_in_bytes,
+            ssd_layer_stride_in_bytes=self.ssd_layer_stride_in_bytes,
+            ssd_kv_stride_in_bytes=self.ssd_kv_stride_in_bytes,
+            chunk_size_in_bytes=self.chunk_size_in_bytes,
+            block_stride_in_bytes=self.block_stride_in_bytes,
+            is_read=transfer_type == TransferType.DISK2H,
+            num_blocks_per_file=self.num_blocks_per_file,
+            round_robin=self.round_robin,
+            num_threads_per_device=self.num_threads_per_device,
+            is_mla=self.is_mla)
+
+    def launch_transfer(self, transfer_op: WorkerTransferOp) -> None:
+        layer_id = 0 if transfer_op.layer_id == -1 else transfer_op.layer_id
+        granularity = self.num_layers if transfer_op.layer_granularity == -1 \
+            else transfer_op.layer_granularity
+        start = time.time()
+        self._transfer_impl(transfer_op.src_block_ids, transfer_op.dst_block_ids,
+                            transfer_op.transfer_type, layer_id, granularity)
+        end = time.time()
+        kv_dim = 1 if self.is_mla else 2
+        size = self.chunk_size_in_bytes * granularity * len(transfer_op.src_block_ids) * kv_dim
+        self._log_transfer_performance(transfer_op, size, start, end)
+
+    def close(self) -> None:
+        self.ioctx.close()

@@ -153,6 +153,30 @@ int fkv_handle_release(fkv_transfer_handle h);
 int fkv_stream_create(int num_cus, fkv_stream_t* out);
 int fkv_stream_destroy(fkv_stream_t s);
 
+/* Host cache <-> SSD files (host code, no device work).  Same file layout,
+ * block mapping and thread fan-out as the reference SSD tier
+ * (csrc/transfer_ssd.cpp:17-285 transfer_kv_blocks_ssd, SSDIOCTX at
+ * csrc/transfer_ssd.h:174-242): `paths` lists num_devices * files_per_device
+ * files, device-major.  SSD block b maps to device (b/rr) % D, device block
+ * ((b/rr)/D)*rr + b%rr, file (device block) % F, in-file block
+ * (device block) / F; chunk (l, k) of a block sits at
+ * in_file*block_stride + l*ssd_layer_stride + k*ssd_kv_stride in the file and
+ * at cpu_id*block_stride + l*cpu_layer_stride + k*cpu_kv_stride in host
+ * memory.  Layers [start_layer, start_layer + num_layers) move.  Reads use
+ * O_DIRECT when chunk_size is a multiple of 4096 and the buffer is aligned.
+ * Synchronous; returns 0 or 1 with fkv_last_error() set. */
+typedef struct fkv_ssd_s* fkv_ssd_t;
+int fkv_ssd_open(const char* const* paths, int num_devices, int files_per_device,
+                 fkv_ssd_t* out);
+int fkv_ssd_close(fkv_ssd_t h);
+int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, void* cpu_ptr,
+                               const int64_t* ssd_block_ids, const int64_t* cpu_block_ids,
+                               int num_blocks, int64_t cpu_layer_stride_bytes,
+                               int64_t cpu_kv_stride_bytes, int64_t ssd_layer_stride_bytes,
+                               int64_t ssd_kv_stride_bytes, int64_t chunk_size_bytes,
+                               int64_t block_stride_bytes, int is_read, int round_robin,
+                               int num_threads_per_device, int is_mla);
+
 /* Message of the last failed call made by this thread ("" if none). */
 const char* fkv_last_error(void);
 

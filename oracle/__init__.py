@@ -47,6 +47,12 @@ def _load():
             ctypes.c_int64, ctypes.c_int64,
             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
         ]
+        g = lib.oracle_transfer_kv_blocks_ssd
+        g.restype = ctypes.c_int
+        g.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                      ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                      ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         _lib = lib
     return _lib
 
@@ -98,5 +104,30 @@ def transfer_kv_blocks(gpu_block_ids, gpu_layers: Sequence, gpu_kv_stride_in_byt
         int(cpu_block_stride_in_bytes), int(cpu_startoff_inside_chunks),
         int(chunk_size_in_bytes), int(bool(is_host_to_device)), int(use_ce_transfer),
         int(bool(is_mla)), int(num_threads))
+    if rc != 0:
+        raise ValueError(f"oracle rejected arguments (rc={rc})")
+
+
+def transfer_kv_blocks_ssd(files: Sequence, num_devices: int, files_per_device: int,
+                           start_layer: int, num_layers: int, cpu_buffer, ssd_block_ids,
+                           cpu_block_ids, cpu_layer_stride: int, cpu_kv_stride: int,
+                           ssd_layer_stride: int, ssd_kv_stride: int, chunk_size: int,
+                           block_stride: int, is_read: bool, round_robin: int = 1,
+                           is_mla: bool = False) -> None:
+    """Oracle SSD transfer over in-memory file images (`files`, device-major,
+    num_devices * files_per_device writable byte arrays), in place."""
+    sids = _ids(ssd_block_ids)
+    cids = _ids(cpu_block_ids)
+    if sids.shape != cids.shape:
+        raise ValueError("ssd and cpu block id lists differ in length")
+    if len(files) != num_devices * files_per_device:
+        raise ValueError("need num_devices * files_per_device file images")
+    ptrs = np.array([_addr(f) for f in files], dtype=np.uint64)
+    rc = _load().oracle_transfer_kv_blocks_ssd(
+        ptrs.ctypes.data, int(num_devices), int(files_per_device), int(start_layer),
+        int(num_layers), _addr(cpu_buffer), sids.ctypes.data, cids.ctypes.data, int(sids.size),
+        int(cpu_layer_stride), int(cpu_kv_stride), int(ssd_layer_stride), int(ssd_kv_stride),
+        int(chunk_size), int(block_stride), int(bool(is_read)), int(round_robin),
+        int(bool(is_mla)))
     if rc != 0:
         raise ValueError(f"oracle rejected arguments (rc={rc})")

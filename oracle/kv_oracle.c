@@ -19,7 +19,9 @@
  *   - the multi-threaded variant partitions blocks into contiguous ranges of
  *     ceil(n / threads) and each thread loops block -> layer -> K then V, the
  *     structure of the reference's CPU fan-out, csrc/transfer_ssd.cpp:120-179
- *     and :215-284, with memcpy in place of pread/pwrite.
+ *     and :215-284, with memcpy in place of pread/pwrite;
+ *   - oracle_transfer_kv_blocks_ssd restates the SSD tier's block mapping and
+ *     offsets over in-memory file images (end of this file).
  */
 #include <pthread.h>
 #include <stdint.h>
@@ -146,5 +148,46 @@ int oracle_transfer_kv_blocks(int num_blocks, int start_layer_id, int num_layers
   free(tids);
   free(jobs);
   free(started);
+  return 0;
+}
+
+/*
+ * SSD tier restated (csrc/transfer_ssd.cpp:17-32 partition_and_remap,
+ * :120-179 single-thread loop): `files` holds num_devices * files_per_device
+ * in-memory file images, device-major.  For each block i in list order:
+ * device d = (b / rr) % D, device block x = ((b / rr) / D) * rr + b % rr,
+ * file x % F, in-file block x / F; then for each layer of the window, K then
+ * V: chunk_size bytes between
+ *   file + in_file*block_stride + l*ssd_layer_stride (+ ssd_kv_stride for V)
+ *   cpu  + cpu_id*block_stride + l*cpu_layer_stride (+ cpu_kv_stride for V).
+ * is_read: file -> cpu.  Returns 0, or -1 on bad arguments.
+ */
+int oracle_transfer_kv_blocks_ssd(void *const *files, int num_devices, int files_per_device,
+                                  int start_layer, int num_layers, void *cpu_ptr,
+                                  const int64_t *ssd_block_ids, const int64_t *cpu_block_ids,
+                                  int num_blocks, int64_t cpu_layer_stride, int64_t cpu_kv_stride,
+                                  int64_t ssd_layer_stride, int64_t ssd_kv_stride,
+                                  int64_t chunk_size, int64_t block_stride, int is_read,
+                                  int round_robin, int is_mla) {
+  if (num_devices <= 0 || files_per_device <= 0 || round_robin <= 0 || num_blocks < 0)
+    return -1;
+  for (int i = 0; i < num_blocks; ++i) {
+    int64_t b = ssd_block_ids[i];
+    int64_t d = (b / round_robin) % num_devices;
+    int64_t x = ((b / round_robin) / num_devices) * round_robin + (b % round_robin);
+    char *file = (char *)files[d * files_per_device + (x % files_per_device)];
+    int64_t in_file = x / files_per_device;
+    for (int l = start_layer; l < start_layer + num_layers; ++l) {
+      for (int k = 0; k < (is_mla ? 1 : 2); ++k) {
+        char *s = file + in_file * block_stride + l * ssd_layer_stride + k * ssd_kv_stride;
+        char *c = (char *)cpu_ptr + cpu_block_ids[i] * block_stride + l * cpu_layer_stride +
+                  k * cpu_kv_stride;
+        if (is_read)
+          memcpy(c, s, (size_t)chunk_size);
+        else
+          memcpy(s, c, (size_t)chunk_size);
+      }
+    }
+  }
   return 0;
 }

@@ -1,7 +1,9 @@
-"""The reference's GPU<->CPU round trip through the engine stack
-(tests/test_transfer_engine.py:55-161 with tests/test_utils.py:15-204):
-StorageEngine + TransferEngine, a write graph (GPU->CPU), zeroed GPU blocks,
-a read graph (CPU->GPU), then every layer compared with the ground truth."""
+"""The reference's round trips through the engine stack
+(tests/test_transfer_engine.py:55-410 with tests/test_utils.py:15-204):
+StorageEngine + TransferEngine, a write graph (GPU->CPU[->SSD]), zeroed GPU
+blocks (and, with an SSD tier, a zeroed host cache, so the data must come
+back from the files), a read graph ([SSD->]CPU->GPU), then every layer
+compared with the ground truth."""
 import time
 
 import pytest
@@ -22,6 +24,7 @@ pytestmark = pytest.mark.gpu
 MODEL = dict(num_layers=4, num_kv_heads=32, head_size=128, dtype=torch.float16)
 CACHE = dict(tokens_per_block=16, num_cpu_blocks=128, use_ce_transfer_h2d=False,
              use_ce_transfer_d2h=True, transfer_sms_h2d=4, transfer_sms_d2h=4)
+SSD_BLOCKS = 512     # over two SSD directories, as tests/test_utils.py:31,40
 
 
 def _wait(engine, gid, limit=30.0):
@@ -34,9 +37,16 @@ def _wait(engine, gid, limit=30.0):
     raise AssertionError(f"graph {gid} did not complete")
 
 
-def _setup(use_mla, layout, worker_mode="thread", eager=True, num_gpu_blocks=128):
+def _setup(use_mla, layout, worker_mode="thread", eager=True, num_gpu_blocks=128,
+           ssd_dirs=None, num_blocks=None):
     mc = ModelConfig(use_mla=use_mla, **MODEL)
-    cc = CacheConfig(cpu_kv_layout_type=layout, **CACHE)
+    extra = dict(CACHE)
+    if num_blocks is not None:
+        extra["num_cpu_blocks"] = num_blocks
+    if ssd_dirs is not None:
+        extra.update(enable_ssd=True, ssd_kv_layout_type=layout, ssd_cache_dir=ssd_dirs,
+                     num_ssd_blocks=SSD_BLOCKS if num_blocks is None else num_blocks)
+    cc = CacheConfig(cpu_kv_layout_type=layout, **extra)
     gl = KVCacheLayout(KVCacheLayoutType.LAYERWISE, mc.num_layers, num_gpu_blocks,
                        cc.tokens_per_block, mc.num_kv_heads, mc.head_size, is_mla=use_mla)
     gen = torch.Generator().manual_seed(17)
@@ -47,8 +57,11 @@ def _setup(use_mla, layout, worker_mode="thread", eager=True, num_gpu_blocks=128
     se.register_gpu_blocks(gpu, gl, device_id=0, dtype=mc.dtype)
     te = TransferEngine([se.get_storage_handle(DeviceType.GPU, 0)], mc, cc,
                         cpu_handle=se.get_storage_handle(DeviceType.CPU),
+                        ssd_handle=se.get_storage_handle(DeviceType.SSD)
+                        if ssd_dirs is not None else None,
                         worker_mode=worker_mode, eager_dispatch=eager)
     te.start()
+    te._test_host = se.get_storage_handle(DeviceType.CPU).get_tensor()
     return mc, gt, gpu, te
 
 
@@ -125,5 +138,88 @@ def test_process_workers_round_trip():
         _wait(te, rg.graph_id, limit=120)
         for l in range(mc.num_layers):
             assert torch.equal(gpu[l].cpu(), gt[l]), f"layer {l}"
+    finally:
+        te.shutdown()
+
+
+def _ssd_dirs(tmp_path):
+    return [str(tmp_path / "ssd_cache"), str(tmp_path / "ssd_cache2")]
+
+
+@pytest.mark.parametrize("transfer_block_num", [8, 16])
+@pytest.mark.parametrize("use_mla", [True, False])
+@pytest.mark.parametrize("layout", [KVCacheLayoutType.LAYERWISE, KVCacheLayoutType.BLOCKWISE])
+def test_ssd_round_trip(tmp_path, transfer_block_num, use_mla, layout):
+    """GPU -> CPU -> SSD, then SSD -> CPU -> GPU (test_transfer_engine.py:165-265)."""
+    mc, gt, gpu, te = _setup(use_mla, layout, ssd_dirs=_ssd_dirs(tmp_path))
+    try:
+        ids = torch.arange(0, transfer_block_num, dtype=torch.int64)
+        wg, _ = create_write_graph_cpu_storage(ids, ids, ids, gpu_device_id=0,
+                                               layer_num=mc.num_layers)
+        wg.bind_to_dp_group(0)
+        te.submit_transfer_graph(wg)
+        _wait(te, wg.graph_id)
+        for t in gpu:
+            t[:, ids].zero_()
+        torch.cuda.synchronize()
+        te._test_host.zero_()
+        rg, _ = create_read_graph_cpu_storage(ids, ids, ids, gpu_device_id=0,
+                                              layer_num=mc.num_layers)
+        rg.bind_to_dp_group(0)
+        te.submit_transfer_graph(rg)
+        _wait(te, rg.graph_id)
+        for l in range(mc.num_layers):
+            assert torch.equal(gpu[l].cpu(), gt[l]), f"layer {l}"
+    finally:
+        te.shutdown()
+
+
+@pytest.mark.parametrize("include_ssd", [True, False])
+@pytest.mark.parametrize("use_mla", [True, False])
+def test_concurrent_mixed_transfers(tmp_path, include_ssd, use_mla):
+    """Four write graphs, then four read graphs, all in flight at once
+    (test_transfer_engine.py:268-410; 16 blocks per transfer)."""
+    n, per = 4, 16
+    blocks = max(128, n * per * 2)
+    mc, gt, gpu, te = _setup(use_mla, KVCacheLayoutType.BLOCKWISE, num_gpu_blocks=blocks,
+                             ssd_dirs=_ssd_dirs(tmp_path) if include_ssd else None,
+                             num_blocks=blocks)
+    empty = torch.tensor([], dtype=torch.int64)
+    try:
+        graphs = []
+        for i in range(n):
+            ids = torch.arange(i * per, (i + 1) * per, dtype=torch.int64)
+            g, _ = create_write_graph_cpu_storage(ids, ids, ids if include_ssd else empty,
+                                                  gpu_device_id=0, layer_num=mc.num_layers)
+            graphs.append(g)
+        for g in graphs:
+            te.submit_transfer_graph(g)
+        seen = []
+        for g in graphs:
+            if (g.graph_id, -1) not in seen:
+                seen += _wait(te, g.graph_id)
+        cleared = torch.arange(0, (n + 1) * per, dtype=torch.int64)
+        for t in gpu:
+            t[:, cleared].zero_()
+        torch.cuda.synchronize()
+        if include_ssd:
+            te._test_host.zero_()
+        graphs = []
+        for i in range(n):
+            ids = torch.arange(i * per, (i + 1) * per, dtype=torch.int64)
+            g, _ = create_read_graph_cpu_storage(ids, ids, ids if include_ssd else empty,
+                                                 gpu_device_id=0, layer_num=mc.num_layers)
+            graphs.append(g)
+        for g in graphs:
+            te.submit_transfer_graph(g)
+        seen = []
+        for g in graphs:
+            if (g.graph_id, -1) not in seen:
+                seen += _wait(te, g.graph_id)
+        for l in range(mc.num_layers):
+            assert torch.equal(gpu[l][:, :(n + 1) * per].cpu(),
+                               torch.cat([gt[l][:, :n * per],
+                                          torch.zeros_like(gt[l][:, n * per:(n + 1) * per])],
+                                         dim=1)), f"layer {l}"
     finally:
         te.shutdown()
