@@ -11,7 +11,8 @@ chunk * layers * blocks * kv (flexkv/transfer/worker.py:334-335).
 
 Also reported, in the same run: every transfer path, the measured host-link
 peak (1 GiB contiguous pinned copies) and device-to-device copy rate, the
-reference's one-DMA-per-chunk copy-engine loop, the CPU baseline (the oracle's
+reference's one-DMA-per-chunk copy-engine loop, the host cache <-> SSD file
+tier (write, fsync, O_DIRECT read, bit-exact), the CPU baseline (the oracle's
 block-partitioned memcpy on this host's cores), a per-kernel roofline from
 HIP events recorded by the library around each launch, and a bit-exact check
 of every moved block.
@@ -345,6 +346,77 @@ def call_latency(wl: Workload, reps: int = 200):
     return out
 
 
+def ssd_tier(wl: Workload, max_bytes: int = 1 << 30):
+    """Host cache <-> SSD files for blocks the last D2H left in the host cache:
+    H2DISK of the step's first blocks (buffered writes, then fsync), DISK2H
+    into other host blocks (O_DIRECT reads: page-sized chunks, page-aligned
+    pinned cache), then a bit-exact compare of the host rows.  Files go to a
+    temporary directory on this host's file system and are removed after."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+
+    from flexkv_amd.common.config import CacheConfig
+    from flexkv_amd.common.storage import KVCacheLayout, KVCacheLayoutType
+    from flexkv_amd.common.transfer import TransferType
+    from flexkv_amd.storage.allocator import SSDAllocator
+    from flexkv_amd.transfer.worker import CPUSSDDiskTransferWorker
+
+    w = wl.w
+    L = w["layers"]
+    row = L * w["kv"] * wl.chunk
+    n = int(min(len(wl.cids), max(1, max_bytes // row)))
+    d = tempfile.mkdtemp(prefix="flexkv_ssd_bench_")
+    try:
+        free = SSDAllocator.get_file_size_limit(d)
+        if free < 4 * n * row:
+            return {"skipped": f"{free / 2**30:.1f} GiB free under {d}"}
+        fs = "?"
+        with open("/proc/mounts") as f:
+            best = ""
+            for line in f:
+                parts = line.split()
+                if len(parts) > 2 and d.startswith(parts[1]) and len(parts[1]) >= len(best):
+                    best, fs = parts[1], parts[2]
+        mk = lambda nb: KVCacheLayout(KVCacheLayoutType.BLOCKWISE, L, nb, w["tokens"],
+                                      w["heads"], w["dim"], is_mla=wl.mla)
+        ssd_lay = mk(n)
+        h = SSDAllocator.allocate(ssd_lay, wl.dtype, cache_dir=[d], max_blocks_per_file=n)
+        worker = CPUSSDDiskTransferWorker(0, None, None, wl.host, h.get_file_list(),
+                                          mk(w["nh"]), ssd_lay, wl.dtype, h.num_blocks_per_file,
+                                          CacheConfig())
+        src = wl.cids[:n].numpy().astype(np.int64)
+        sids = np.arange(n, dtype=np.int64)
+        taken = set(wl.cids.tolist())
+        dst = np.array([c for c in range(w["nh"]) if c not in taken][:n], dtype=np.int64)
+        t0 = time.perf_counter()
+        worker._transfer_impl(src, sids, TransferType.H2DISK, 0, L)
+        t_write = time.perf_counter() - t0
+        for paths in h.get_file_list().values():
+            for pth in paths:
+                fd = os.open(pth, os.O_RDONLY)
+                os.fsync(fd)
+                os.close(fd)
+        t_sync = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        worker._transfer_impl(sids, dst, TransferType.DISK2H, 0, L)
+        t_read = time.perf_counter() - t0
+        worker.close()
+        hv = wl.host.view(w["nh"], row // 2).view(torch.int16)
+        ok = bool(torch.equal(hv[torch.from_numpy(dst)], hv[torch.from_numpy(src)]))
+        gb = n * row / 1e9
+        return {"blocks": n, "bytes": n * row, "fs": fs,
+                "write_gbps_buffered": round(gb / t_write, 3),
+                "write_gbps_with_fsync": round(gb / t_sync, 3),
+                "read_gbps": round(gb / t_read, 3),
+                "read_io": "O_DIRECT" if wl.chunk % 4096 == 0 else "buffered",
+                "bit_exact": ok,
+                "threads_per_device": CacheConfig().ssd_threads_per_device}
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
 def cpu_baseline(wl: Workload, budget_s: float):
     """The oracle's block-partitioned memcpy (oracle/kv_oracle.c) on this host's
     cores: D2H from host-resident copies of the selected GPU blocks into the
@@ -574,6 +646,9 @@ def main() -> int:
         log(f"engine layer-wise read: {result['engine_layerwise_read']}")
         result["call_latency"] = call_latency(wl)
         log(f"call latency: {result['call_latency']}")
+        wl.transfer(False, default_ce)     # host rows of the step's ids hold the GPU blocks
+        result["ssd_tier"] = ssd_tier(wl)
+        log(f"SSD tier: {result['ssd_tier']}")
         threads, cpu = cpu_baseline(wl, args.cpu_budget)
         v, reps, el = cpu[threads]
         v1, reps1, el1 = cpu[1]

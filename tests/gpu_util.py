@@ -65,3 +65,12 @@ def abi_transfer(dc: DeviceCase, gids, cids, h2d: bool, mode: int, transfer_cus:
         s["startoff"], s["chunk"], st.cuda_stream, transfer_cus, 1 if h2d else 0, mode,
         1 if case.kv == 1 else 0)
     _lib.check(rc, "fkv_transfer_kv_blocks")
+
+
+def zero_blocks(t: torch.Tensor, ids: torch.Tensor) -> None:
+    """Zero blocks `ids` (axis 1) of a per-layer [kv, blocks, ...] tensor in
+    place and check that they are zero (``t[:, ids].zero_()`` would only
+    zero a gathered copy)."""
+    idx = ids.to(t.device)
+    t.index_fill_(1, idx, 0)
+    assert not t.index_select(1, idx).any(), "blocks were not cleared"

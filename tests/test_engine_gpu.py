@@ -9,6 +9,7 @@ import time
 import pytest
 import torch
 
+from gpu_util import zero_blocks
 from flexkv_amd.cache.transfer_pattern import (convert_read_graph_to_layer_wise_graph,
                                                create_read_graph_cpu_storage,
                                                create_write_graph_cpu_storage)
@@ -77,7 +78,7 @@ def test_gpu_cpu_round_trip(use_mla, layout):
         te.submit_transfer_graph(wg)
         _wait(te, wg.graph_id)
         for t in gpu:
-            t[:, gids].zero_()
+            zero_blocks(t, gids)
         torch.cuda.synchronize()
         rg, _ = create_read_graph_cpu_storage(gids, cids, torch.tensor([], dtype=torch.int64),
                                               gpu_device_id=0, layer_num=mc.num_layers)
@@ -103,7 +104,7 @@ def test_layer_wise_read_graph(eager):
         te.submit_transfer_graph(wg)
         _wait(te, wg.graph_id)
         for t in gpu:
-            t[:, gids].zero_()
+            zero_blocks(t, gids)
         torch.cuda.synchronize()
         rg, ends = create_read_graph_cpu_storage(gids, cids, torch.tensor([], dtype=torch.int64),
                                                  layer_num=mc.num_layers)
@@ -130,7 +131,7 @@ def test_process_workers_round_trip():
         te.submit_transfer_graph(wg)
         _wait(te, wg.graph_id, limit=120)
         for t in gpu:
-            t[:, gids].zero_()
+            zero_blocks(t, gids)
         torch.cuda.synchronize()
         rg, _ = create_read_graph_cpu_storage(gids, cids, torch.tensor([], dtype=torch.int64),
                                               layer_num=mc.num_layers)
@@ -160,7 +161,7 @@ def test_ssd_round_trip(tmp_path, transfer_block_num, use_mla, layout):
         te.submit_transfer_graph(wg)
         _wait(te, wg.graph_id)
         for t in gpu:
-            t[:, ids].zero_()
+            zero_blocks(t, ids)
         torch.cuda.synchronize()
         te._test_host.zero_()
         rg, _ = create_read_graph_cpu_storage(ids, ids, ids, gpu_device_id=0,
@@ -200,7 +201,7 @@ def test_concurrent_mixed_transfers(tmp_path, include_ssd, use_mla):
                 seen += _wait(te, g.graph_id)
         cleared = torch.arange(0, (n + 1) * per, dtype=torch.int64)
         for t in gpu:
-            t[:, cleared].zero_()
+            zero_blocks(t, cleared)
         torch.cuda.synchronize()
         if include_ssd:
             te._test_host.zero_()

@@ -7,6 +7,7 @@ import numpy as np
 import pytest
 import torch
 
+from gpu_util import zero_blocks
 from flexkv_amd.common.storage import KVCacheLayout, KVCacheLayoutType
 from flexkv_amd.common.transfer import DeviceType, TransferDescriptor, TransferOp, TransferType
 from flexkv_amd.storage.allocator import CPUAllocator
@@ -46,7 +47,7 @@ def test_in_process_round_trip(mla, layout, ce):
     cids = torch.arange(40, 56, dtype=torch.int64)
     w.launch_transfer(WorkerTransferOp(_op(TransferType.D2H, gids, cids)))
     for t in gpu:
-        t[:, gids].zero_()
+        zero_blocks(t, gids)
     torch.cuda.synchronize()
     w.launch_transfer(WorkerTransferOp(_op(TransferType.H2D, cids, gids)))
     for l in range(L):
@@ -125,7 +126,7 @@ def test_spawned_worker_with_shared_gpu_tensors():
         handle.submit_transfer(op)
         assert q.get(timeout=120) == op.op_id
         for t in gpu:
-            t[:, gids].zero_()
+            zero_blocks(t, gids)
         torch.cuda.synchronize()
         op2 = _op(TransferType.H2D, cids, gids)
         handle.submit_transfer(op2)
