@@ -18,6 +18,23 @@ __all__ = ["transfer_kv_blocks", "gather_kv_blocks", "scatter_kv_blocks",
            "SSDIOCTX", "transfer_kv_blocks_ssd"]
 
 
+_device_visible = None
+
+
+def _stream_handle(fn_name: str) -> int:
+    """Raw handle of the current torch stream of the current device.  Raises
+    when no HIP device is visible (checked once per process)."""
+    global _device_visible
+    if _device_visible is None:
+        _device_visible = torch.cuda.is_available()
+    if not _device_visible:
+        raise RuntimeError(f"{fn_name} needs a HIP device; none is visible")
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:      # avoids building a Stream object per call
+        return raw(torch._C._cuda_getDevice())
+    return torch.cuda.current_stream().cuda_stream
+
+
 def _require_int64_host(t: torch.Tensor, name: str) -> None:
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
@@ -67,10 +84,8 @@ def transfer_kv_blocks(gpu_block_id_tensor: torch.Tensor,
         mode = _lib.FKV_XFER_CE if use_ce_transfer else _lib.FKV_XFER_KERNEL
     else:
         mode = int(use_ce_transfer)
-    if not torch.cuda.is_available():
-        raise RuntimeError("transfer_kv_blocks needs a HIP device; none is visible")
+    stream = _stream_handle("transfer_kv_blocks")
     lib = _lib.load()
-    stream = torch.cuda.current_stream().cuda_stream
     rc = lib.fkv_transfer_kv_blocks(
         int(num_blocks), int(start_layer_id), int(num_layers),
         gpu_block_id_tensor.data_ptr(), gpu_layer_ptrs_tensor.data_ptr(),
@@ -90,10 +105,8 @@ def _contiguous(fn_name: str, gpu_block_id_tensor, gpu_layer_ptrs_tensor, gpu_kv
     _require_int64_host(gpu_layer_ptrs_tensor, "gpu_layer_ptrs_tensor")
     if not isinstance(buffer, torch.Tensor) or not buffer.is_contiguous():
         raise TypeError("buffer must be a contiguous torch.Tensor")
-    if not torch.cuda.is_available():
-        raise RuntimeError(f"{fn_name} needs a HIP device; none is visible")
+    stream = _stream_handle(fn_name)
     lib = _lib.load()
-    stream = torch.cuda.current_stream().cuda_stream
     rc = getattr(lib, fn_name)(
         int(gpu_block_id_tensor.numel()), int(gpu_layer_ptrs_tensor.numel()),
         gpu_block_id_tensor.data_ptr(), gpu_layer_ptrs_tensor.data_ptr(),
@@ -202,8 +215,7 @@ def transfer_kv_blocks_layerwise(gpu_block_id_tensor: torch.Tensor,
     _require_int64_host(gpu_layer_ptrs_tensor, "gpu_layer_ptrs_tensor")
     if cpu_block_id_tensor.numel() != gpu_block_id_tensor.numel():
         raise RuntimeError("gpu and cpu block id tensors differ in length")
-    if not torch.cuda.is_available():
-        raise RuntimeError("transfer_kv_blocks_layerwise needs a HIP device; none is visible")
+    stream = _stream_handle("transfer_kv_blocks_layerwise")
     lib = _lib.load()
     out = ctypes.c_void_p()
     rc = lib.fkv_transfer_kv_blocks_layerwise(
@@ -213,7 +225,7 @@ def transfer_kv_blocks_layerwise(gpu_block_id_tensor: torch.Tensor,
         int(gpu_kv_stride_in_bytes), int(gpu_block_stride_in_bytes),
         cpu_block_id_tensor.data_ptr(), cpu_tensor.data_ptr(), int(cpu_kv_stride_in_bytes),
         int(cpu_layer_stride_in_bytes), int(cpu_block_stride_in_bytes), 0,
-        int(chunk_size_in_bytes), torch.cuda.current_stream().cuda_stream, int(transfer_sms),
+        int(chunk_size_in_bytes), stream, int(transfer_sms),
         1 if is_host_to_device else 0, 1 if is_mla else 0, ctypes.byref(out))
     if rc != 0:
         raise RuntimeError(_lib.last_error() or f"fkv_transfer_kv_blocks_layerwise failed ({rc})")
