@@ -119,7 +119,10 @@ int fkv_scatter_kv_blocks(int num_blocks, int num_layers, const int64_t* gpu_blo
  * on per group: on the host (fkv_handle_query / fkv_handle_wait) or on the
  * device (fkv_handle_stream_wait makes another stream, e.g. the one running
  * layer l of the model, wait for group g without a host round trip).
- * Arguments and checks as in fkv_transfer_kv_blocks; the id lists are copied
+ * Arguments and checks as in fkv_transfer_kv_blocks, except that
+ * transfer_cus = -1 selects 2 compute units for host-to-device transfers
+ * (enough for the link, and the rest of the chip stays with the compute the
+ * transfer overlaps) and 8 for device-to-host; the id lists are copied
  * before the call returns.  The caller keeps the GPU cache and host cache
  * alive until the handle is released; fkv_handle_release waits for all groups
  * and frees the handle.
