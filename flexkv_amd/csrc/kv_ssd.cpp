@@ -48,21 +48,22 @@ int ssd_fail(const char* fmt, ...) {
   return 1;
 }
 
-// Full-length pread/pwrite, retrying short transfers and EINTR.
-bool io_all(int fd, char* buf, int64_t bytes, int64_t off, bool is_read) {
+// Full-length pread/pwrite, retrying short transfers and EINTR.  Returns 0,
+// the errno of the failed call, or -1 when a read hits the end of the file.
+int io_all(int fd, char* buf, int64_t bytes, int64_t off, bool is_read) {
   while (bytes > 0) {
     const ssize_t r = is_read ? pread(fd, buf, static_cast<size_t>(bytes), off)
                               : pwrite(fd, buf, static_cast<size_t>(bytes), off);
     if (r < 0) {
       if (errno == EINTR) continue;
-      return false;
+      return errno ? errno : EIO;
     }
-    if (r == 0) return false;  // past end of file
+    if (r == 0) return -1;
     buf += r;
     off += r;
     bytes -= r;
   }
-  return true;
+  return 0;
 }
 
 }  // namespace
@@ -77,7 +78,7 @@ struct fkv_ssd_s {
 extern "C" {
 
 int fkv_ssd_open(const char* const* paths, int num_devices, int files_per_device,
-                 fkv_ssd_t* out) {
+                 fkv_ssd_t* out) try {
   fkv_detail::last_error().clear();
   if (!out || !paths || num_devices <= 0 || files_per_device <= 0)
     return ssd_fail("bad arguments to fkv_ssd_open");
@@ -103,6 +104,8 @@ int fkv_ssd_open(const char* const* paths, int num_devices, int files_per_device
   }
   *out = h;
   return 0;
+} catch (const std::exception& e) {
+  return ssd_fail("fkv_ssd_open: %s", e.what());
 }
 
 int fkv_ssd_close(fkv_ssd_t h) {
@@ -121,7 +124,7 @@ int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, voi
                                int64_t cpu_kv_stride_bytes, int64_t ssd_layer_stride_bytes,
                                int64_t ssd_kv_stride_bytes, int64_t chunk_size_bytes,
                                int64_t block_stride_bytes, int is_read, int round_robin,
-                               int num_threads_per_device, int is_mla) {
+                               int num_threads_per_device, int is_mla) try {
   fkv_detail::last_error().clear();
   if (!h) return ssd_fail("null SSD context");
   if (num_blocks <= 0 || num_layers <= 0) return 0;
@@ -148,13 +151,13 @@ int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, voi
   std::atomic<int> failed{0};
   std::string first_err;
   std::atomic<bool> have_err{false};
-  auto record = [&](const char* what, int d, int64_t blk) {
+  auto record = [&](const char* what, int d, int64_t blk, int err) {
     failed = 1;
     bool expect = false;
     if (have_err.compare_exchange_strong(expect, true)) {
       char buf[256];
       snprintf(buf, sizeof(buf), "%s failed on device %d block %lld: %s", what, d,
-               static_cast<long long>(blk), strerror(errno));
+               static_cast<long long>(blk), err > 0 ? strerror(err) : "unexpected end of file");
       first_err = buf;
     }
   };
@@ -169,8 +172,8 @@ int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, voi
       // O_DIRECT needs an aligned buffer; fall back to the page cache if not
       auto io = [&](char* buf, int64_t bytes, int64_t off) {
         if (dfd >= 0 && reinterpret_cast<uintptr_t>(buf) % 4096 == 0 && bytes % 4096 == 0 &&
-            off % 4096 == 0 && io_all(dfd, buf, bytes, off, true))
-          return true;
+            off % 4096 == 0 && io_all(dfd, buf, bytes, off, true) == 0)
+          return 0;
         return io_all(fd, buf, bytes, off, is_read != 0);
       };
       char* cbase = base + dev_cpu[d][j] * block_stride_bytes;
@@ -178,9 +181,9 @@ int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, voi
       if (row_io) {
         const int64_t off_c = static_cast<int64_t>(start_layer) * cpu_layer_stride_bytes;
         const int64_t off_s = static_cast<int64_t>(start_layer) * ssd_layer_stride_bytes;
-        if (!io(cbase + off_c, static_cast<int64_t>(num_layers) * kv * chunk_size_bytes,
-                sbase + off_s))
-          record(is_read ? "read" : "write", d, x);
+        const int err = io(cbase + off_c, static_cast<int64_t>(num_layers) * kv * chunk_size_bytes,
+                           sbase + off_s);
+        if (err) record(is_read ? "read" : "write", d, x, err);
         continue;
       }
       for (int l = start_layer; l < start_layer + num_layers && !failed; ++l) {
@@ -189,8 +192,9 @@ int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, voi
                     k * cpu_kv_stride_bytes;
           const int64_t s = sbase + static_cast<int64_t>(l) * ssd_layer_stride_bytes +
                             k * ssd_kv_stride_bytes;
-          if (!io(c, chunk_size_bytes, s)) {
-            record(is_read ? "read" : "write", d, x);
+          const int err = io(c, chunk_size_bytes, s);
+          if (err) {
+            record(is_read ? "read" : "write", d, x, err);
             break;
           }
         }
@@ -198,15 +202,24 @@ int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, voi
     }
   };
   std::vector<std::thread> threads;
-  for (int d = 0; d < D; ++d) {
+  threads.reserve(static_cast<size_t>(D) * num_threads_per_device);
+  for (int d = 0; d < D && !failed; ++d) {
     const size_t n = dev_ssd[d].size();
     if (n == 0) continue;
     const size_t per = (n + num_threads_per_device - 1) / num_threads_per_device;
-    for (size_t lo = 0; lo < n; lo += per) threads.emplace_back(work, d, lo, std::min(n, lo + per));
+    for (size_t lo = 0; lo < n && !failed; lo += per) {
+      try {
+        threads.emplace_back(work, d, lo, std::min(n, lo + per));
+      } catch (const std::exception&) {
+        work(d, lo, std::min(n, lo + per));  // no thread available: do this range here
+      }
+    }
   }
   for (auto& t : threads) t.join();
   if (failed) return ssd_fail("%s", first_err.c_str());
   return 0;
+} catch (const std::exception& e) {
+  return ssd_fail("fkv_transfer_kv_blocks_ssd: %s", e.what());
 }
 
 }  // extern "C"

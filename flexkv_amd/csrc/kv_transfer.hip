@@ -653,12 +653,29 @@ int stream_device(hipStream_t s, int* dev) {
   return 0;
 }
 
+// When a transfer fails after enqueueing work, wait for that work before the
+// call returns: a copy must not land in the caller's buffers, or read the
+// reused id and staging buffers, after the error has been reported.
+struct DrainOnError {
+  hipStream_t stream;
+  const DeviceState* dev_state;
+  bool armed = true;
+  ~DrainOnError() {
+    if (!armed) return;
+    (void)hipStreamSynchronize(stream);
+    if (dev_state)
+      for (int s = 0; s < dev_state->num_dma; ++s) (void)hipStreamSynchronize(dev_state->dma[s]);
+    (void)hipGetLastError();
+  }
+};
+
 int transfer_zero_copy(const Geometry& g, hipStream_t stream, int dev, int transfer_cus,
                        bool h2d) {
   DeviceState& d = g_dev[dev];
   char* ids_dev = nullptr;
   int rc = pack_ids(g, &ids_dev);
   if (rc) return rc;
+  DrainOnError drain{stream, nullptr};
   int cus = transfer_cus <= 0 ? std::min(kAutoZeroCopyCus, d.num_cus)
                               : std::min(transfer_cus, d.num_cus);
   const int grid_cap = cus * (h2d ? d.occ_zero_copy[1] : d.occ_zero_copy[0]);
@@ -675,6 +692,7 @@ int transfer_zero_copy(const Geometry& g, hipStream_t stream, int dev, int trans
     if (rc) return rc;
   }
   FKV_HIP(hipStreamSynchronize(stream));
+  drain.armed = false;
   prof.flush();
   return 0;
 }
@@ -794,6 +812,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   char* ids_dev = nullptr;
   rc = pack_ids(g, &ids_dev);
   if (rc) return rc;
+  DrainOnError drain{stream, &d};
 
   // A piece is a run of whole blocks over a layer window; the window covers
   // all layers unless one block row would not fit a staging half.
@@ -872,6 +891,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
       if (dma_used[h][s]) FKV_HIP(hipStreamWaitEvent(stream, d.ev_dma[h][s], 0));
   FKV_HIP(hipStreamSynchronize(stream));
   for (int s = 0; s < nd; ++s) FKV_HIP(hipStreamSynchronize(d.dma[s]));
+  drain.armed = false;
   prof.flush();
   return 0;
 }
@@ -885,6 +905,7 @@ int transfer_contiguous(const Geometry& g, hipStream_t stream, int dev, bool to_
   int rc = pack_ids(g, &ids_dev);
   if (rc) return rc;
   const int grid_cap = d.num_cus * (to_gpu ? d.occ_staged[1] : d.occ_staged[0]);
+  DrainOnError drain{stream, nullptr};
   ProfRecorder prof;
   for (int l0 = 0; l0 < g.num_layers; l0 += kMaxLayersPerLaunch) {
     const int nl = std::min(kMaxLayersPerLaunch, g.num_layers - l0);
@@ -896,6 +917,7 @@ int transfer_contiguous(const Geometry& g, hipStream_t stream, int dev, bool to_
     if (rc) return rc;
   }
   FKV_HIP(hipStreamSynchronize(stream));
+  drain.armed = false;
   prof.flush();
   return 0;
 }
@@ -948,6 +970,7 @@ int contiguous_entry(int num_blocks, int num_layers, const int64_t* gpu_block_id
 // The reference copy-engine loop, csrc/transfer.cu:97-121: one async copy per
 // (layer, K|V, block) chunk, issued layer-major then K|V then block.
 int transfer_ce_per_chunk(const Geometry& g, hipStream_t stream, bool h2d) {
+  DrainOnError drain{stream, nullptr};
   ProfRecorder prof;
   hipEvent_t ev = nullptr;
   int rc = prof.begin(stream, &ev);
@@ -970,6 +993,7 @@ int transfer_ce_per_chunk(const Geometry& g, hipStream_t stream, bool h2d) {
   const int64_t copies = static_cast<int64_t>(g.num_layers) * g.kv * g.num_blocks;
   if ((rc = prof.end(stream, ev, copies * g.chunk, copies, true))) return rc;
   FKV_HIP(hipStreamSynchronize(stream));
+  drain.armed = false;
   prof.flush();
   return 0;
 }
@@ -1028,6 +1052,7 @@ struct fkv_transfer_handle_s {
   std::vector<hipEvent_t> done;   // one per layer group, in order
   PoolBuf ids;
   ProfRecorder prof;
+  bool enqueued = false;          // every group was enqueued
 };
 
 namespace {
@@ -1059,6 +1084,7 @@ int layerwise_enqueue(const Geometry& g, hipStream_t stream, int dev, int transf
     h->done.push_back(ev);
     FKV_HIP(hipEventRecord(ev, stream));
   }
+  h->enqueued = true;
   return 0;
 }
 
@@ -1066,7 +1092,7 @@ int layerwise_enqueue(const Geometry& g, hipStream_t stream, int dev, int transf
 // whose enqueue failed part-way.
 int handle_destroy(fkv_transfer_handle_s* h) {
   int rc = 0;
-  if (!h->done.empty()) {
+  if (h->enqueued && !h->done.empty()) {
     hipError_t e = hipEventSynchronize(h->done.back());
     if (e != hipSuccess) rc = fail(static_cast<int>(e), "hipEventSynchronize: %s", hipGetErrorString(e));
   } else if (h->ids.host) {  // enqueue failed after taking ids: drain what was issued
