@@ -470,8 +470,10 @@ def measured_traffic(workload: str, run: int, alg_bytes: int):
 
 def counters_pass(args) -> int:
     """Kernels for `rocprofv3 --pmc` passes: the calibration copy first, so the
-    per-dispatch counter of a copy of known size scales the others."""
-    wl = Workload(args.workload, args.seed, args.run, host=False)
+    per-dispatch counter of a copy of known size scales the others; then 3
+    gathers, 3 scatters, 3 zero-copy D2H and 3 zero-copy H2D transfers of the
+    step's blocks."""
+    wl = Workload(args.workload, args.seed, args.run, host=True)
     cal = torch.empty(1 << 30, dtype=torch.uint8, device=wl.dev)
     cal_dst = torch.empty_like(cal)
     torch.cuda.synchronize()
@@ -482,10 +484,14 @@ def counters_pass(args) -> int:
         wl.gather(buf)
     for _ in range(3):
         wl.gather(buf, scatter=True)
+    del buf
+    for h2d in (False, True):
+        for _ in range(3):
+            wl.transfer(h2d, False)
     torch.cuda.synchronize()
     print(json.dumps({"calibration_copy_bytes": cal.numel(), "gather_launches": 3,
-                      "scatter_launches": 3, "moved_bytes_per_launch": wl.bytes_per_op}),
-          flush=True)
+                      "scatter_launches": 3, "d2h_launches": 3, "h2d_launches": 3,
+                      "moved_bytes_per_launch": wl.bytes_per_op}), flush=True)
     return 0
 
 
@@ -503,7 +509,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=1001)
     ap.add_argument("--counters", action="store_true",
                     help="run only the kernels a PMC pass needs: a 1 GiB plain device copy "
-                         "(calibration), then 3 gathers and 3 scatters of the step's blocks")
+                         "(calibration), then 3 gathers, 3 scatters, 3 zero-copy D2H and 3 "
+                         "zero-copy H2D transfers of the step's blocks")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

@@ -330,12 +330,15 @@ class GPUCPUTransferWorker(TransferWorkerBase):
             raise ValueError(f"Invalid transfer type: {transfer_type} for GPUCPUTransferWorker")
         if len(gpu_ids) == 0:
             return
-        gpu_id_t = torch.from_numpy(np.ascontiguousarray(gpu_ids)).pin_memory()
-        cpu_id_t = torch.from_numpy(np.ascontiguousarray(cpu_ids)).pin_memory()
         if layer_id < 0 or layer_granularity < 1 or layer_id + layer_granularity > self.num_layers:
             raise ValueError(f"layer range [{layer_id}, {layer_id + layer_granularity}) is outside "
                              f"[0, {self.num_layers})")
-        layer_ptrs = self.gpu_layer_ptrs[layer_id:layer_id + layer_granularity].contiguous().pin_memory()
+        # The library reads ids and layer pointers on the host and stages them
+        # itself, so ordinary host tensors do (the reference pins them because
+        # its kernel reads them, worker.py:285-295).
+        gpu_id_t = torch.from_numpy(np.ascontiguousarray(gpu_ids))
+        cpu_id_t = torch.from_numpy(np.ascontiguousarray(cpu_ids))
+        layer_ptrs = self.gpu_layer_ptrs[layer_id:layer_id + layer_granularity]
         transfer_kv_blocks(gpu_id_t, layer_ptrs, self.gpu_kv_stride_in_bytes,
                            self.gpu_block_stride_in_bytes, cpu_id_t, self.cpu_tensor,
                            self.cpu_kv_stride_in_bytes, self.cpu_layer_stride_in_bytes,
