@@ -28,6 +28,7 @@ FKV_HOST_NONCOHERENT = 2
 # Names declared in include/flexkv_hip.h; tests check the library exports all.
 EXPORTED_SYMBOLS = (
     "fkv_transfer_kv_blocks",
+    "fkv_transfer_kv_blocks_kv_ptrs",
     "fkv_gather_kv_blocks",
     "fkv_scatter_kv_blocks",
     "fkv_transfer_kv_blocks_layerwise",
@@ -79,6 +80,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     f.restype = c_int
     f.argtypes = [c_int, c_int, c_int, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64,
                   c_i64, c_i64, c_i64, c_vp, c_int, c_int, c_int, c_int]
+    f = lib.fkv_transfer_kv_blocks_kv_ptrs
+    f.restype = c_int
+    f.argtypes = [c_int, c_int, c_int, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64,
+                  c_i64, c_i64, c_vp, c_int, c_int, c_int, c_int]
     for name in ("fkv_gather_kv_blocks", "fkv_scatter_kv_blocks"):
         g = getattr(lib, name)
         g.restype = c_int

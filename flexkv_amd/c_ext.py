@@ -13,7 +13,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["transfer_kv_blocks", "gather_kv_blocks", "scatter_kv_blocks",
+__all__ = ["transfer_kv_blocks", "transfer_kv_blocks_kv_ptrs", "gather_kv_blocks",
+           "scatter_kv_blocks",
            "transfer_kv_blocks_layerwise", "LayerwiseTransfer", "transfer_stream",
            "SSDIOCTX", "transfer_kv_blocks_ssd"]
 
@@ -97,6 +98,53 @@ def transfer_kv_blocks(gpu_block_id_tensor: torch.Tensor,
         1 if is_mla else 0)
     if rc != 0:
         raise RuntimeError(_lib.last_error() or f"fkv_transfer_kv_blocks failed ({rc})")
+
+
+def transfer_kv_blocks_kv_ptrs(gpu_block_id_tensor: torch.Tensor,
+                               gpu_kv_ptrs_tensor: torch.Tensor,
+                               gpu_block_stride_in_bytes: int,
+                               cpu_block_id_tensor: torch.Tensor,
+                               cpu_tensor: torch.Tensor,
+                               cpu_kv_stride_in_bytes: int,
+                               cpu_layer_stride_in_bytes: int,
+                               cpu_block_stride_in_bytes: int,
+                               chunk_size_in_bytes: int,
+                               start_layer_id: int,
+                               transfer_sms: int = -1,
+                               is_host_to_device: bool = True,
+                               use_ce_transfer=False,
+                               is_mla: bool = False) -> None:
+    """transfer_kv_blocks for K and V held in separate allocations
+    (extension): ``gpu_kv_ptrs_tensor`` is an int64 host tensor of
+    ``layers * kv`` base pointers ordered [layer][K|V] (kv = 1 for MLA)."""
+    _require_int64_host(gpu_block_id_tensor, "gpu_block_id_tensor")
+    _require_int64_host(cpu_block_id_tensor, "cpu_block_id_tensor")
+    _require_int64_host(gpu_kv_ptrs_tensor, "gpu_kv_ptrs_tensor")
+    if not isinstance(cpu_tensor, torch.Tensor):
+        raise TypeError(f"cpu_tensor must be a torch.Tensor, got {type(cpu_tensor).__name__}")
+    kv = 1 if is_mla else 2
+    if gpu_kv_ptrs_tensor.numel() % kv:
+        raise RuntimeError(f"gpu_kv_ptrs_tensor holds {gpu_kv_ptrs_tensor.numel()} pointers, "
+                           f"not a multiple of {kv}")
+    num_blocks = gpu_block_id_tensor.numel()
+    if cpu_block_id_tensor.numel() != num_blocks:
+        raise RuntimeError(
+            f"gpu_block_id_tensor has {num_blocks} ids but cpu_block_id_tensor has "
+            f"{cpu_block_id_tensor.numel()}")
+    if isinstance(use_ce_transfer, bool):
+        mode = _lib.FKV_XFER_CE if use_ce_transfer else _lib.FKV_XFER_KERNEL
+    else:
+        mode = int(use_ce_transfer)
+    stream = _stream_handle("transfer_kv_blocks_kv_ptrs")
+    rc = _lib.load().fkv_transfer_kv_blocks_kv_ptrs(
+        int(num_blocks), int(start_layer_id), int(gpu_kv_ptrs_tensor.numel() // kv),
+        gpu_block_id_tensor.data_ptr(), gpu_kv_ptrs_tensor.data_ptr(),
+        int(gpu_block_stride_in_bytes), cpu_block_id_tensor.data_ptr(), cpu_tensor.data_ptr(),
+        int(cpu_kv_stride_in_bytes), int(cpu_layer_stride_in_bytes),
+        int(cpu_block_stride_in_bytes), 0, int(chunk_size_in_bytes), stream,
+        int(transfer_sms), 1 if is_host_to_device else 0, mode, 1 if is_mla else 0)
+    if rc != 0:
+        raise RuntimeError(_lib.last_error() or f"fkv_transfer_kv_blocks_kv_ptrs failed ({rc})")
 
 
 def _contiguous(fn_name: str, gpu_block_id_tensor, gpu_layer_ptrs_tensor, gpu_kv_stride_in_bytes,

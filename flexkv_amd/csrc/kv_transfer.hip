@@ -118,6 +118,7 @@ struct CopyArgs {
   int32_t tile_layers;
   int32_t tiles_b;           // tiles along the block axis
   int32_t num_tiles;
+  int32_t ptrs_per_layer;    // 1: layer_ptr[l] + k*gpu_kv_stride; kv: layer_ptr[l*kv + k]
   uint64_t layer_ptr[kMaxLayersPerLaunch];
 };
 
@@ -146,6 +147,7 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t kv = static_cast<uint32_t>(a.kv_dim);
   const uint32_t rpc = static_cast<uint32_t>(a.rows_per_chunk);
+  const uint32_t ppl = static_cast<uint32_t>(a.ptrs_per_layer);
   // true when every row of a chunk is a full 64-lane row
   const bool full_rows = (a.chunk_vec & 63) == 0;
 
@@ -187,7 +189,7 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
         const int64_t gid = wave_uniform(s_gid[bsafe]);
         const int64_t cid = wave_uniform(s_cid[bsafe]);
         const int64_t row_off = static_cast<int64_t>(rr) * (64 * 16);
-        char* gpu = reinterpret_cast<char*>(a.layer_ptr[layer]) +
+        char* gpu = reinterpret_cast<char*>(a.layer_ptr[layer * ppl + k * (ppl - 1)]) +
                     static_cast<int64_t>(k) * a.gpu_kv_stride + gid * a.gpu_block_stride + row_off;
         char* cpu = a.cpu_base + static_cast<int64_t>(layer) * a.cpu_layer_stride +
                     static_cast<int64_t>(k) * a.cpu_kv_stride + cid * a.cpu_block_stride + row_off;
@@ -429,11 +431,20 @@ struct Geometry {
   int num_blocks, start_layer, num_layers, kv;
   const int64_t* gids;
   const int64_t* cids;
-  void* const* layer_ptrs;
+  void* const* layer_ptrs;   // num_layers * ptrs_per_layer entries
+  int ptrs_per_layer = 1;    // kv when K and V are separate allocations (gks = 0)
   int64_t gks, gbs, cks, cls, cbs, startoff, chunk;
   char* cpu_ptr;
   PtrInfo cpu_info;
   int64_t min_gid, max_gid, min_cid, max_cid;
+
+  // Base address of half k of call layer l (block 0).
+  char* gpu_base(int l, int k) const {
+    const int64_t i = static_cast<int64_t>(l) * ptrs_per_layer + (ptrs_per_layer > 1 ? k : 0);
+    return static_cast<char*>(layer_ptrs[i]) + k * gks;
+  }
+  // Layers whose pointers fit one launch's kernel arguments.
+  int layers_per_launch() const { return kMaxLayersPerLaunch / ptrs_per_layer; }
 };
 
 int validate(Geometry& g, int mode) {
@@ -489,20 +500,23 @@ int validate(Geometry& g, int mode) {
   const __int128 glo = static_cast<__int128>(g.min_gid) * g.gbs;
   const __int128 ghi = static_cast<__int128>(g.kv - 1) * g.gks +
                        static_cast<__int128>(g.max_gid) * g.gbs + g.chunk;
-  // Layer tables usually repeat one allocation per layer; query each pointer.
-  for (int l = 0; l < g.num_layers; ++l) {
-    const char* p = static_cast<const char*>(g.layer_ptrs[l]);
-    if (!p) return fail(kInval, "gpu layer pointer %d is null", l);
+  // Every layer (or K/V) pointer is its own allocation as a rule; query each.
+  if (g.ptrs_per_layer != 1 && (g.ptrs_per_layer != g.kv || g.gks != 0))
+    return fail(kInval, "separate K/V pointers need kv pointers per layer and no kv stride");
+  const int64_t nptr = static_cast<int64_t>(g.num_layers) * g.ptrs_per_layer;
+  for (int64_t i = 0; i < nptr; ++i) {
+    const char* p = static_cast<const char*>(g.layer_ptrs[i]);
+    if (!p) return fail(kInval, "gpu layer pointer %lld is null", (long long)i);
     if (vec_mode && reinterpret_cast<uintptr_t>(p) % 16 != 0)
-      return fail(kInval, "gpu layer pointer %d is not 16-byte aligned", l);
+      return fail(kInval, "gpu layer pointer %lld is not 16-byte aligned", (long long)i);
     PtrInfo pi;
     if (query_ptr(p, &pi) != 0 || !pi.device)
-      return fail(kInval, "gpu layer pointer %d (%p) is not device memory", l, p);
+      return fail(kInval, "gpu layer pointer %lld (%p) is not device memory", (long long)i, p);
     if (!range_inside(p, glo, ghi, pi))
       return fail(kInval,
                   "gpu block ids [%lld, %lld] address bytes outside the allocation of "
-                  "layer %d (%zu bytes)",
-                  (long long)g.min_gid, (long long)g.max_gid, l, pi.size);
+                  "layer pointer %lld (%zu bytes)",
+                  (long long)g.min_gid, (long long)g.max_gid, (long long)i, pi.size);
   }
   return 0;
 }
@@ -614,7 +628,9 @@ int launch_copy(const Geometry& g, char* ids_dev, char* cpu_base, int64_t cks, i
   a.num_blocks = nb;
   a.num_layers = nl;
   a.kv_dim = g.kv;
-  for (int l = 0; l < nl; ++l) a.layer_ptr[l] = reinterpret_cast<uint64_t>(g.layer_ptrs[l0 + l]);
+  a.ptrs_per_layer = g.ptrs_per_layer;
+  for (int i = 0; i < nl * g.ptrs_per_layer; ++i)
+    a.layer_ptr[i] = reinterpret_cast<uint64_t>(g.layer_ptrs[l0 * g.ptrs_per_layer + i]);
   choose_tiles(nb, nl, g.kv, a.rows_per_chunk, grid_cap,
                kIota ? FKV_TILE_FACTOR_HBM : FKV_TILE_FACTOR, &a);
   int grid = std::max(1, std::min(grid_cap, a.num_tiles));
@@ -682,8 +698,9 @@ int transfer_zero_copy(const Geometry& g, hipStream_t stream, int dev, int trans
   char* cpu_dev = g.cpu_info.dev_ptr + g.startoff +
                   static_cast<int64_t>(g.start_layer) * g.cls;
   ProfRecorder prof;
-  for (int l0 = 0; l0 < g.num_layers; l0 += kMaxLayersPerLaunch) {
-    const int nl = std::min(kMaxLayersPerLaunch, g.num_layers - l0);
+  const int per_launch = g.layers_per_launch();
+  for (int l0 = 0; l0 < g.num_layers; l0 += per_launch) {
+    const int nl = std::min(per_launch, g.num_layers - l0);
     char* base = cpu_dev + static_cast<int64_t>(l0) * g.cls;
     rc = h2d ? launch_copy<true, false>(g, ids_dev, base, g.cks, g.cls, g.cbs, 0,
                                         g.num_blocks, l0, nl, grid_cap, stream, prof)
@@ -818,7 +835,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   // all layers unless one block row would not fit a staging half.
   const size_t req = g_staging_request.load();
   const size_t half_default = (req ? req : kDefaultStagingBytes) / 2;
-  int nl_piece = std::min(g.num_layers, kMaxLayersPerLaunch);
+  int nl_piece = std::min(g.num_layers, g.layers_per_launch());
   while (nl_piece > 1 && static_cast<size_t>(nl_piece) * g.kv * g.chunk > half_default) nl_piece /= 2;
   const size_t row_bytes = static_cast<size_t>(nl_piece) * g.kv * g.chunk;
   rc = ensure_staging(d, row_bytes);
@@ -907,8 +924,9 @@ int transfer_contiguous(const Geometry& g, hipStream_t stream, int dev, bool to_
   const int grid_cap = d.num_cus * (to_gpu ? d.occ_staged[1] : d.occ_staged[0]);
   DrainOnError drain{stream, nullptr};
   ProfRecorder prof;
-  for (int l0 = 0; l0 < g.num_layers; l0 += kMaxLayersPerLaunch) {
-    const int nl = std::min(kMaxLayersPerLaunch, g.num_layers - l0);
+  const int per_launch = g.layers_per_launch();
+  for (int l0 = 0; l0 < g.num_layers; l0 += per_launch) {
+    const int nl = std::min(per_launch, g.num_layers - l0);
     char* base = g.cpu_info.dev_ptr + static_cast<int64_t>(l0) * g.cls;
     rc = to_gpu ? launch_copy<true, true>(g, ids_dev, base, g.cks, g.cls, g.cbs, 0, g.num_blocks,
                                           l0, nl, grid_cap, stream, prof)
@@ -976,12 +994,12 @@ int transfer_ce_per_chunk(const Geometry& g, hipStream_t stream, bool h2d) {
   int rc = prof.begin(stream, &ev);
   if (rc) return rc;
   for (int l = 0; l < g.num_layers; ++l) {
-    char* gl = static_cast<char*>(g.layer_ptrs[l]);
     for (int k = 0; k < g.kv; ++k) {
+      char* gk = g.gpu_base(l, k);
       for (int i = 0; i < g.num_blocks; ++i) {
         char* cpu = g.cpu_ptr + static_cast<int64_t>(l + g.start_layer) * g.cls + k * g.cks +
                     g.cids[i] * g.cbs + g.startoff;
-        char* gpu = gl + k * g.gks + g.gids[i] * g.gbs;
+        char* gpu = gk + g.gids[i] * g.gbs;
         if (h2d) {
           FKV_HIP(hipMemcpyAsync(gpu, cpu, g.chunk, hipMemcpyHostToDevice, stream));
         } else {
@@ -1070,8 +1088,8 @@ int layerwise_enqueue(const Geometry& g, hipStream_t stream, int dev, int transf
   char* cpu_dev = g.cpu_info.dev_ptr + g.startoff + static_cast<int64_t>(g.start_layer) * g.cls;
   for (int g0 = 0; g0 < g.num_layers; g0 += granularity) {
     const int gend = std::min(g.num_layers, g0 + granularity);
-    for (int l0 = g0; l0 < gend; l0 += kMaxLayersPerLaunch) {
-      const int nl = std::min(kMaxLayersPerLaunch, gend - l0);
+    for (int l0 = g0; l0 < gend; l0 += g.layers_per_launch()) {
+      const int nl = std::min(g.layers_per_launch(), gend - l0);
       char* base = cpu_dev + static_cast<int64_t>(l0) * g.cls;
       rc = h2d ? launch_copy<true, false>(g, h->ids.dev, base, g.cks, g.cls, g.cbs, 0,
                                           g.num_blocks, l0, nl, grid_cap, stream, h->prof)
@@ -1130,6 +1148,23 @@ Geometry make_geometry(int num_blocks, int start_layer_id, int num_layers,
   g.cpu_ptr = static_cast<char*>(cpu_ptr);
   return g;
 }
+
+// Validate, then run one synchronous transfer in the requested mode.
+int transfer_entry(Geometry& g, hipStream_t s, int transfer_cus, bool h2d, int mode) {
+  int rc = validate(g, mode);
+  if (rc) return rc;
+  int dev = 0;
+  if ((rc = stream_device(s, &dev))) return rc;
+  if ((rc = ensure_device_basics(dev))) return rc;
+  switch (mode) {
+    case FKV_XFER_KERNEL:
+      return transfer_zero_copy(g, s, dev, transfer_cus, h2d);
+    case FKV_XFER_CE:
+      return transfer_staged(g, s, dev, h2d);
+    default:
+      return transfer_ce_per_chunk(g, s, h2d);
+  }
+}
 }  // namespace
 
 extern "C" {
@@ -1153,21 +1188,36 @@ int fkv_transfer_kv_blocks(int num_blocks, int start_layer_id, int num_layers,
                                cpu_block_ids, cpu_ptr, cpu_kv_stride_bytes,
                                cpu_layer_stride_bytes, cpu_block_stride_bytes,
                                cpu_startoff_inside_chunks, chunk_size_bytes, is_mla);
-    int rc = validate(g, use_ce_transfer);
-    if (rc) return rc;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    int dev = 0;
-    if ((rc = stream_device(s, &dev))) return rc;
-    if ((rc = ensure_device_basics(dev))) return rc;
-    const bool h2d = is_host_to_device != 0;
-    switch (use_ce_transfer) {
-      case FKV_XFER_KERNEL:
-        return transfer_zero_copy(g, s, dev, transfer_cus, h2d);
-      case FKV_XFER_CE:
-        return transfer_staged(g, s, dev, h2d);
-      default:
-        return transfer_ce_per_chunk(g, s, h2d);
-    }
+    return transfer_entry(g, static_cast<hipStream_t>(stream), transfer_cus,
+                          is_host_to_device != 0, use_ce_transfer);
+  } catch (const std::exception& e) {
+    return fail(static_cast<int>(hipErrorUnknown), "exception: %s", e.what());
+  } catch (...) {
+    return fail(static_cast<int>(hipErrorUnknown), "unknown exception");
+  }
+}
+
+int fkv_transfer_kv_blocks_kv_ptrs(int num_blocks, int start_layer_id, int num_layers,
+                                   const int64_t* gpu_block_ids, void* const* gpu_kv_ptrs,
+                                   int64_t gpu_block_stride_bytes, const int64_t* cpu_block_ids,
+                                   void* cpu_ptr, int64_t cpu_kv_stride_bytes,
+                                   int64_t cpu_layer_stride_bytes, int64_t cpu_block_stride_bytes,
+                                   int64_t cpu_startoff_inside_chunks, int64_t chunk_size_bytes,
+                                   fkv_stream_t stream, int transfer_cus, int is_host_to_device,
+                                   int use_ce_transfer, int is_mla) {
+  try {
+    t_err.clear();
+    if (use_ce_transfer < FKV_XFER_KERNEL || use_ce_transfer > FKV_XFER_CE_PER_CHUNK)
+      return fail(kInval, "use_ce_transfer must be 0 (kernel), 1 (CE) or 2 (CE per chunk), got %d",
+                  use_ce_transfer);
+    if (num_blocks == 0 || num_layers == 0) return 0;
+    Geometry g = make_geometry(num_blocks, start_layer_id, num_layers, gpu_block_ids, gpu_kv_ptrs,
+                               0, gpu_block_stride_bytes, cpu_block_ids, cpu_ptr,
+                               cpu_kv_stride_bytes, cpu_layer_stride_bytes, cpu_block_stride_bytes,
+                               cpu_startoff_inside_chunks, chunk_size_bytes, is_mla);
+    g.ptrs_per_layer = g.kv;
+    return transfer_entry(g, static_cast<hipStream_t>(stream), transfer_cus,
+                          is_host_to_device != 0, use_ce_transfer);
   } catch (const std::exception& e) {
     return fail(static_cast<int>(hipErrorUnknown), "exception: %s", e.what());
   } catch (...) {

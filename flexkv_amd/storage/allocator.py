@@ -47,10 +47,12 @@ class StorageHandle:
         return self.data
 
     def get_tensor_list(self) -> List[torch.Tensor]:
+        """Per-layer tensors; a layer whose K and V are separate allocations
+        is a [K, V] list."""
         if self.handle_type == AccessHandleType.TENSOR:
             return list(self.data)
         if self.handle_type == AccessHandleType.TENSOR_HANDLE:
-            return [h.get_tensor() for h in self.data]
+            return [_map_layer(h, lambda x: x.get_tensor()) for h in self.data]
         raise ValueError(f"Invalid handle type: {self.handle_type}, expected TENSOR or TENSOR_HANDLE")
 
     def get_file_list(self) -> Union[List[str], Dict[int, List[str]]]:
@@ -62,8 +64,20 @@ class StorageHandle:
         if self.handle_type == AccessHandleType.TENSOR_HANDLE:
             return list(self.data)
         if self.handle_type == AccessHandleType.TENSOR:
-            return [TensorSharedHandle(t) for t in self.data]
+            return [_map_layer(t, TensorSharedHandle) for t in self.data]
         raise ValueError(f"Invalid handle type: {self.handle_type}, expected TENSOR_HANDLE or TENSOR")
+
+
+def _map_layer(layer, fn):
+    """Apply fn to a layer entry: one tensor/handle, or a [K, V] sequence."""
+    if isinstance(layer, (list, tuple)):
+        return [fn(x) for x in layer]
+    return fn(layer)
+
+
+def _first_leaf(layers):
+    x = layers[0]
+    return x[0] if isinstance(x, (list, tuple)) else x
 
 
 def _owned_host_array(ptr: int, nbytes: int):
@@ -141,7 +155,8 @@ class GPUAllocator:
         device_id = kwargs.get("device_id")
         if device_id is None:
             raise ValueError("device_id is required for GPU allocator")
-        kind = AccessHandleType.TENSOR if isinstance(data[0], torch.Tensor) else AccessHandleType.TENSOR_HANDLE
+        kind = AccessHandleType.TENSOR if isinstance(_first_leaf(data), torch.Tensor) \
+            else AccessHandleType.TENSOR_HANDLE
         return StorageHandle(kind, data, layout, dtype, gpu_device_id=device_id)
 
 

@@ -32,7 +32,8 @@ import numpy as np
 import torch
 
 from .. import _lib
-from ..c_ext import SSDIOCTX, transfer_kv_blocks, transfer_kv_blocks_ssd
+from ..c_ext import (SSDIOCTX, transfer_kv_blocks, transfer_kv_blocks_kv_ptrs,
+                     transfer_kv_blocks_ssd)
 from ..common.debug import flexkv_logger
 from ..common.memory_handle import TensorSharedHandle
 from ..common.storage import KVCacheLayout, KVCacheLayoutType
@@ -293,9 +294,23 @@ class GPUCPUTransferWorker(TransferWorkerBase):
         if isinstance(cpu_blocks, HostCacheSpec):
             cpu_blocks = cpu_blocks.allocate()
         host_register(cpu_blocks)
-        self.gpu_blocks = [h.get_tensor() if isinstance(h, TensorSharedHandle) else h
-                           for h in gpu_blocks]
-        self.gpu_layer_ptrs = self._get_layer_ptrs(self.gpu_blocks)
+
+        def tensor(h):
+            return h.get_tensor() if isinstance(h, TensorSharedHandle) else h
+
+        # A layer given as a [K, V] pair (K and V separate allocations, each
+        # [blocks, tokens, heads, dim]) uses the separate-pointer entry point.
+        self.separate_kv = isinstance(gpu_blocks[0], (list, tuple))
+        kv = 1 if gpu_kv_layout.is_mla else 2
+        if self.separate_kv:
+            self.gpu_blocks = [[tensor(h) for h in pair] for pair in gpu_blocks]
+            if any(len(pair) != kv for pair in self.gpu_blocks):
+                raise ValueError(f"separate K/V layers need {kv} tensor(s) per layer")
+            self.gpu_layer_ptrs = self._get_layer_ptrs(
+                [t for pair in self.gpu_blocks for t in pair])
+        else:
+            self.gpu_blocks = [tensor(h) for h in gpu_blocks]
+            self.gpu_layer_ptrs = self._get_layer_ptrs(self.gpu_blocks)
         self.cpu_tensor = cpu_blocks
         self.dtype = dtype
         self.is_mla = gpu_kv_layout.is_mla
@@ -338,6 +353,15 @@ class GPUCPUTransferWorker(TransferWorkerBase):
         # its kernel reads them, worker.py:285-295).
         gpu_id_t = torch.from_numpy(np.ascontiguousarray(gpu_ids))
         cpu_id_t = torch.from_numpy(np.ascontiguousarray(cpu_ids))
+        if self.separate_kv:
+            kv = 1 if self.is_mla else 2
+            ptrs = self.gpu_layer_ptrs[layer_id * kv:(layer_id + layer_granularity) * kv]
+            transfer_kv_blocks_kv_ptrs(
+                gpu_id_t, ptrs, self.gpu_block_stride_in_bytes, cpu_id_t, self.cpu_tensor,
+                self.cpu_kv_stride_in_bytes, self.cpu_layer_stride_in_bytes,
+                self.cpu_block_stride_in_bytes, self.chunk_size_in_bytes, layer_id, sms,
+                transfer_type == TransferType.H2D, use_ce, self.is_mla)
+            return
         layer_ptrs = self.gpu_layer_ptrs[layer_id:layer_id + layer_granularity]
         transfer_kv_blocks(gpu_id_t, layer_ptrs, self.gpu_kv_stride_in_bytes,
                            self.gpu_block_stride_in_bytes, cpu_id_t, self.cpu_tensor,

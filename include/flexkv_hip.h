@@ -94,6 +94,22 @@ int fkv_transfer_kv_blocks(int num_blocks, int start_layer_id, int num_layers,
                            int transfer_cus, int is_host_to_device,
                            int use_ce_transfer, int is_mla);
 
+/* As fkv_transfer_kv_blocks, for engines that allocate K and V of a layer
+ * separately (e.g. one [N, tokens, heads, dim] tensor each): gpu_kv_ptrs
+ * holds num_layers * kv base pointers, [layer][K|V] (kv = 1 for MLA), and the
+ * chunk of block b is at ptr + b * gpu_block_stride_bytes.  Same modes,
+ * checks and semantics.  No counterpart in the reference, whose kernel needs
+ * V = K + gpu_kv_stride within one allocation (csrc/transfer.cu:48-50). */
+int fkv_transfer_kv_blocks_kv_ptrs(int num_blocks, int start_layer_id, int num_layers,
+                                   const int64_t* gpu_block_ids, void* const* gpu_kv_ptrs,
+                                   int64_t gpu_block_stride_bytes,
+                                   const int64_t* cpu_block_ids, void* cpu_ptr,
+                                   int64_t cpu_kv_stride_bytes, int64_t cpu_layer_stride_bytes,
+                                   int64_t cpu_block_stride_bytes,
+                                   int64_t cpu_startoff_inside_chunks, int64_t chunk_size_bytes,
+                                   fkv_stream_t stream, int transfer_cus,
+                                   int is_host_to_device, int use_ce_transfer, int is_mla);
+
 /* Device-side gather / scatter between the per-layer GPU cache and one
  * contiguous buffer laid out [num_blocks][num_layers][K|V][chunk] (block i of
  * the id list at byte offset i * num_layers * kv * chunk).  This is the

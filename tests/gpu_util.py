@@ -74,3 +74,28 @@ def zero_blocks(t: torch.Tensor, ids: torch.Tensor) -> None:
     idx = ids.to(t.device)
     t.index_fill_(1, idx, 0)
     assert not t.index_select(1, idx).any(), "blocks were not cleared"
+
+
+def split_kv_layers(dc: DeviceCase):
+    """The case's device layers as separate allocations, [layer][K|V], each
+    [ng, tokens, heads, dim] (one per layer for MLA)."""
+    return [[dc.gpu[l][k].clone() for k in range(dc.case.kv)] for l in range(len(dc.gpu))]
+
+
+def abi_transfer_kv_ptrs(dc: DeviceCase, kv_tensors, gids, cids, h2d: bool, mode: int,
+                         transfer_cus: int = -1) -> None:
+    """fkv_transfer_kv_blocks_kv_ptrs over the case's host geometry with the
+    device side given as separate K/V tensors; raises RuntimeError."""
+    case = dc.case
+    s = case.strides()
+    flat = [t for pair in kv_tensors for t in pair]
+    gids = np.ascontiguousarray(gids, dtype=np.int64)
+    cids = np.ascontiguousarray(cids, dtype=np.int64)
+    ptrs = (ctypes.c_void_p * max(1, len(flat)))(*[t.data_ptr() for t in flat])
+    lib = _lib.load()
+    rc = lib.fkv_transfer_kv_blocks_kv_ptrs(
+        len(gids), case.start_layer, len(kv_tensors), gids.ctypes.data, ptrs, s["gpu_block"],
+        cids.ctypes.data, dc.host.data_ptr(), s["cpu_kv"], s["cpu_layer"], s["cpu_block"],
+        s["startoff"], s["chunk"], torch.cuda.current_stream().cuda_stream, transfer_cus,
+        1 if h2d else 0, mode, 1 if case.kv == 1 else 0)
+    _lib.check(rc, "fkv_transfer_kv_blocks_kv_ptrs")

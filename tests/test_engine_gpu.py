@@ -224,3 +224,43 @@ def test_concurrent_mixed_transfers(tmp_path, include_ssd, use_mla):
                                          dim=1)), f"layer {l}"
     finally:
         te.shutdown()
+
+
+@pytest.mark.parametrize("use_mla", [False, True])
+def test_separate_kv_layers_round_trip(use_mla):
+    """An engine whose layers are [K, V] pairs of separate [N, tokens, heads,
+    dim] tensors (as SGLang allocates them) round-trips through the host cache."""
+    mc = ModelConfig(use_mla=use_mla, **MODEL)
+    cc = CacheConfig(cpu_kv_layout_type=KVCacheLayoutType.BLOCKWISE, **CACHE)
+    gl = KVCacheLayout(KVCacheLayoutType.LAYERWISE, mc.num_layers, 128, cc.tokens_per_block,
+                       mc.num_kv_heads, mc.head_size, is_mla=use_mla)
+    gen = torch.Generator().manual_seed(23)
+    gt = [torch.randn(tuple(gl.kv_shape[1:]), generator=gen).to(mc.dtype)
+          for _ in range(mc.num_layers)]
+    pairs = [[gt[l][k].cuda() for k in range(gl.kv_shape[1])] for l in range(mc.num_layers)]
+    se = StorageEngine(mc, cc)
+    se.register_gpu_blocks(pairs, gl, device_id=0, dtype=mc.dtype)
+    te = TransferEngine([se.get_storage_handle(DeviceType.GPU, 0)], mc, cc,
+                        cpu_handle=se.get_storage_handle(DeviceType.CPU))
+    te.start()
+    try:
+        gids = torch.tensor([0, 7, 99, 127, 64], dtype=torch.int64)
+        cids = torch.tensor([3, 1, 126, 40, 77], dtype=torch.int64)
+        wg, _ = create_write_graph_cpu_storage(gids, cids, torch.tensor([], dtype=torch.int64),
+                                               layer_num=mc.num_layers)
+        te.submit_transfer_graph(wg)
+        _wait(te, wg.graph_id)
+        for pair in pairs:
+            for t in pair:
+                t.index_fill_(0, gids.cuda(), 0)
+                assert not t.index_select(0, gids.cuda()).any()
+        torch.cuda.synchronize()
+        rg, _ = create_read_graph_cpu_storage(gids, cids, torch.tensor([], dtype=torch.int64),
+                                              layer_num=mc.num_layers)
+        te.submit_transfer_graph(rg)
+        _wait(te, rg.graph_id)
+        for l in range(mc.num_layers):
+            for k, t in enumerate(pairs[l]):
+                assert torch.equal(t.cpu(), gt[l][k]), f"layer {l} half {k}"
+    finally:
+        te.shutdown()

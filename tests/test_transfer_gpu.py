@@ -142,6 +142,65 @@ def test_geometries_match_oracle(dev, geo, mode):
     check_case(case, gids, cids, mode)
 
 
+# Separate K and V allocations (fkv_transfer_kv_blocks_kv_ptrs): the same
+# bytes must move as with K and V halves of one allocation, so the oracle of
+# the combined layout is the expectation.  Geometry 7 (130 layers) needs three
+# launches at 64 layers of K/V pointer pairs each.
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("geo", [GEOMETRIES[i] for i in (0, 1, 2, 3, 5, 6, 7)],
+                         ids=[f"g{i}" for i in (0, 1, 2, 3, 5, 6, 7)])
+def test_separate_kv_allocations_match_oracle(dev, geo, mode):
+    from gpu_util import DeviceCase, abi_transfer_kv_ptrs, split_kv_layers
+    lt, nl, st, kv, ng, nh, t, h, d, dt, layout, tp, rank, n = geo
+    print(f"kv_ptrs L={nl} kv={kv} n={n} layout={layout} mode={mode}", flush=True)
+    case = KVCase(layers_total=lt, num_layers=nl, start_layer=st, kv=kv, ng=ng, nh=nh, tokens=t,
+                  heads=h, dim=d, dtype=dt, layout=layout, tp=tp, rank=rank).fill(seed=lt * 5 + n)
+    gids = inputs.distinct_ids(n + 3, n, ng)
+    cids = inputs.distinct_ids(n + 4, n, nh)
+    dc = DeviceCase(case)
+    kvt = split_kv_layers(dc)
+    abi_transfer_kv_ptrs(dc, kvt, gids, cids, h2d=False, mode=mode)
+    torch.cuda.synchronize()
+    assert np.array_equal(dc.host_np(), _oracle_d2h(case, gids, cids, mode)), "D2H"
+    # H2D of fresh host values into sentinel-filled separate tensors
+    fresh = KVCase(**{k: getattr(case, k) for k in (
+        "layers_total", "num_layers", "start_layer", "kv", "ng", "nh", "tokens", "heads", "dim",
+        "dtype", "layout", "tp", "rank")}).fill(seed=77)
+    dc.set_host(fresh.host)
+    for l, pair in enumerate(kvt):
+        for k, tk in enumerate(pair):
+            tk.copy_(to_torch_layer(fresh.gpu[l][k]))
+    abi_transfer_kv_ptrs(dc, kvt, gids, cids, h2d=True, mode=mode)
+    torch.cuda.synchronize()
+    want = _oracle_h2d(fresh, gids, cids, fresh.gpu, mode)
+    for l, pair in enumerate(kvt):
+        for k, tk in enumerate(pair):
+            got = tk.cpu().numpy().view(case.dtype)
+            assert np.array_equal(got, want[l][k]), f"H2D layer {l} half {k}"
+
+
+def to_torch_layer(a):
+    from gpu_util import to_torch
+    return to_torch(a)
+
+
+def test_separate_kv_rejects_bad_pointers(dev):
+    """A K/V pointer outside device memory, or ids past a separate tensor's
+    end, are refused before any launch."""
+    import ctypes
+    from flexkv_amd import _lib
+    from gpu_util import DeviceCase, abi_transfer_kv_ptrs, split_kv_layers
+    case = KVCase(layers_total=2, num_layers=2, start_layer=0, kv=2, ng=8, nh=8, tokens=16,
+                  heads=1, dim=64).fill(seed=5)
+    dc = DeviceCase(case)
+    kvt = split_kv_layers(dc)
+    with pytest.raises(RuntimeError, match="outside the allocation"):
+        abi_transfer_kv_ptrs(dc, kvt, np.array([1 << 22]), np.array([0]), h2d=False, mode=0)
+    kvt[1][1] = torch.empty_like(kvt[1][1], device="cpu")     # host memory as a V pointer
+    with pytest.raises(RuntimeError, match="not device memory"):
+        abi_transfer_kv_ptrs(dc, kvt, np.array([0]), np.array([0]), h2d=False, mode=0)
+
+
 @pytest.mark.parametrize("cus", [1, 3, 256])
 def test_zero_copy_cu_limits(dev, cus):
     case = KVCase(layers_total=4, num_layers=4, start_layer=0, kv=2, ng=80, nh=80, tokens=16,

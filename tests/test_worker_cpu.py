@@ -89,6 +89,7 @@ def _bare_gpu_worker(monkeypatch, mla=False):
     w = object.__new__(W.GPUCPUTransferWorker)
     W.TransferWorkerBase.__init__(w, 0, None, None)
     w.gpu_layer_ptrs = torch.arange(100, 108, dtype=torch.int64)
+    w.separate_kv = False
     w.num_layers = 8
     w.cpu_tensor = torch.zeros(4)
     w.is_mla = mla
@@ -113,6 +114,23 @@ def test_direction_mapping(monkeypatch):
     assert list(a[0]) == [30, 40] and list(a[4]) == [1, 2]      # gpu = dst for H2D
     assert list(a[1]) == [102, 103, 104] and a[10] == 2           # layer window, start layer
     assert a[11] == 16 and a[12] is True and a[13] is True
+
+
+def test_separate_kv_pointer_window(monkeypatch):
+    """Layers given as [K, V] pairs: the pointer table is [layer][K|V] and a
+    layer window takes 2 entries per layer (1 for MLA)."""
+    for mla, kv in ((False, 2), (True, 1)):
+        w, rec = _bare_gpu_worker(monkeypatch, mla=mla)
+        kvrec = _Recorder()
+        monkeypatch.setattr(W, "transfer_kv_blocks_kv_ptrs", kvrec)
+        w.separate_kv = True
+        w.gpu_layer_ptrs = torch.arange(200, 200 + 8 * kv, dtype=torch.int64)
+        src, dst = np.array([5], np.int64), np.array([6], np.int64)
+        w._transfer_impl(src, dst, TransferType.H2D, 3, 2)
+        a = kvrec.calls[-1]
+        assert list(a[1]) == list(range(200 + 3 * kv, 200 + 5 * kv))
+        assert list(a[0]) == [6] and list(a[3]) == [5] and a[9] == 3 and a[11] is True
+        assert not rec.calls
 
 
 def test_bad_type_empty_ids_and_layer_window(monkeypatch):
