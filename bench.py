@@ -346,6 +346,41 @@ def call_latency(wl: Workload, reps: int = 200):
     return out
 
 
+def request_batch(wl: Workload, steps: int, num_requests: int = 32, max_blocks: int = 128):
+    """Requests of U{1..max_blocks} blocks with distinct random ids (seeded),
+    moved one synchronous call per request and as one batched call, both
+    directions, zero-copy path; the batched D2H result is checked bit-exact."""
+    from flexkv_amd import c_ext
+    L, kv = wl.w["layers"], wl.w["kv"]
+    g = torch.Generator().manual_seed(1006)
+    sizes = torch.randint(1, max_blocks + 1, (num_requests,), generator=g)
+    total = int(sizes.sum())
+    gids = torch.randperm(wl.w["ng"], generator=g)[:total].to(torch.int64)
+    cids = torch.randperm(wl.w["nh"], generator=g)[:total].to(torch.int64)
+    bounds = [0] + torch.cumsum(sizes, 0).tolist()
+    reqs = [(gids[bounds[i]:bounds[i + 1]].clone(), cids[bounds[i]:bounds[i + 1]].clone())
+            for i in range(num_requests)]
+    nbytes = total * L * kv * wl.chunk
+
+    def call(gi, ci, h2d):
+        c_ext.transfer_kv_blocks(gi, wl.ptrs, wl.gkv, wl.gblk, ci, wl.host, wl.ckv, wl.clay,
+                                 wl.cblk, wl.chunk, 0, -1, h2d, False, wl.mla)
+
+    out = {"requests": num_requests, "blocks": total, "bytes": nbytes}
+    for h2d in (False, True):
+        name = "h2d" if h2d else "d2h"
+        per, _, _ = time_steps(lambda: [call(gi, ci, h2d) for gi, ci in reqs], steps, 1)
+        bat, _, _ = time_steps(lambda: call(gids, cids, h2d), steps, 1)
+        out[f"{name}_per_request_gbps"] = round(nbytes / per / 1e9, 2)
+        out[f"{name}_batched_gbps"] = round(nbytes / bat / 1e9, 2)
+    call(gids, cids, False)
+    saved = wl.gids, wl.cids
+    wl.gids, wl.cids = gids, cids
+    out["bit_exact"] = wl.check()
+    wl.gids, wl.cids = saved
+    return out
+
+
 def ssd_tier(wl: Workload, max_bytes: int = 1 << 30):
     """Host cache <-> SSD files for blocks the last D2H left in the host cache:
     H2DISK of the step's first blocks (buffered writes, then fsync), DISK2H
@@ -653,6 +688,9 @@ def main() -> int:
         log(f"engine layer-wise read: {result['engine_layerwise_read']}")
         result["call_latency"] = call_latency(wl)
         log(f"call latency: {result['call_latency']}")
+        if wl.mla:
+            result["request_batch"] = request_batch(wl, args.steps)
+            log(f"request batch: {result['request_batch']}")
         wl.transfer(False, default_ce)     # host rows of the step's ids hold the GPU blocks
         result["ssd_tier"] = ssd_tier(wl)
         log(f"SSD tier: {result['ssd_tier']}")
