@@ -75,6 +75,19 @@ namespace {
 #ifndef FKV_NT_STORE_HOST
 #define FKV_NT_STORE_HOST 0
 #endif
+// The staging scatter (packed HBM -> scattered chunks) has its own knobs.
+#ifndef FKV_UNROLL_SCATTER
+#define FKV_UNROLL_SCATTER FKV_UNROLL_HBM
+#endif
+#ifndef FKV_TILE_FACTOR_SCATTER
+#define FKV_TILE_FACTOR_SCATTER FKV_TILE_FACTOR_HBM
+#endif
+#ifndef FKV_NT_LOAD_SCATTER
+#define FKV_NT_LOAD_SCATTER FKV_NT_LOAD
+#endif
+#ifndef FKV_NT_STORE_SCATTER
+#define FKV_NT_STORE_SCATTER FKV_NT_STORE_HBM
+#endif
 
 constexpr int kThreads = 256;               // 4 wavefronts of 64 lanes
 constexpr int kWaves = kThreads / 64;
@@ -135,9 +148,13 @@ __device__ inline int64_t wave_uniform(int64_t x) {
 // 16-byte slot, so one 32-bit lane offset serves every access.
 template <bool kH2D, bool kIotaCpu>
 __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
-  constexpr int kUnroll = kIotaCpu ? kUnrollHbm : (kH2D ? FKV_UNROLL_ZC_H2D : FKV_UNROLL_ZC_D2H);
+  constexpr bool kScatter = kIotaCpu && kH2D;
+  constexpr int kUnroll = kIotaCpu ? (kScatter ? FKV_UNROLL_SCATTER : kUnrollHbm)
+                                   : (kH2D ? FKV_UNROLL_ZC_H2D : FKV_UNROLL_ZC_D2H);
   // only the zero-copy D2H instantiation stores into host memory
-  constexpr bool kNtStore = (kIotaCpu || kH2D) ? FKV_NT_STORE_HBM : FKV_NT_STORE_HOST;
+  constexpr bool kNtStore = kScatter ? FKV_NT_STORE_SCATTER
+                                     : ((kIotaCpu || kH2D) ? FKV_NT_STORE_HBM : FKV_NT_STORE_HOST);
+  constexpr bool kNtLoad = kScatter ? FKV_NT_LOAD_SCATTER : FKV_NT_LOAD;
   __shared__ int64_t s_gid[kMaxTileBlocks];
   __shared__ int64_t s_cid[kMaxTileBlocks];
 
@@ -214,11 +231,10 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
       for (int u = 0; u < kUnroll; ++u) {
         if (live[u]) {
           const gvec* p = (const gvec*)(src[u] + lane_off);
-#if FKV_NT_LOAD
-          v[u] = __builtin_nontemporal_load(p);
-#else
-          v[u] = *p;
-#endif
+          if (kNtLoad)
+            v[u] = __builtin_nontemporal_load(p);
+          else
+            v[u] = *p;
         }
       }
 #pragma unroll
@@ -632,7 +648,8 @@ int launch_copy(const Geometry& g, char* ids_dev, char* cpu_base, int64_t cks, i
   for (int i = 0; i < nl * g.ptrs_per_layer; ++i)
     a.layer_ptr[i] = reinterpret_cast<uint64_t>(g.layer_ptrs[l0 * g.ptrs_per_layer + i]);
   choose_tiles(nb, nl, g.kv, a.rows_per_chunk, grid_cap,
-               kIota ? FKV_TILE_FACTOR_HBM : FKV_TILE_FACTOR, &a);
+               kIota ? (kH2D ? FKV_TILE_FACTOR_SCATTER : FKV_TILE_FACTOR_HBM) : FKV_TILE_FACTOR,
+               &a);
   int grid = std::max(1, std::min(grid_cap, a.num_tiles));
   if (kIota && FKV_HBM_ONEPASS) grid = a.num_tiles;
   hipEvent_t ev = nullptr;
