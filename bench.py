@@ -382,11 +382,14 @@ def request_batch(wl: Workload, steps: int, num_requests: int = 32, max_blocks: 
 
 
 def ssd_tier(wl: Workload, max_bytes: int = 1 << 30):
-    """Host cache <-> SSD files for blocks the last D2H left in the host cache:
-    H2DISK of the step's first blocks (buffered writes, then fsync), DISK2H
-    into other host blocks (O_DIRECT reads: page-sized chunks, page-aligned
-    pinned cache), then a bit-exact compare of the host rows.  Files go to a
-    temporary directory on this host's file system and are removed after."""
+    """Host cache <-> SSD files for about 1 GiB of blocks: the rows the last
+    D2H left in the host cache are copied to host blocks [0, n), written to
+    SSD slots [0, n) (buffered writes, then fsync), read back into n random
+    host blocks (one request per block) and into host blocks [n, 2n)
+    (consecutive blocks merge into large requests); both reads are compared
+    with the written rows bit for bit.  O_DIRECT reads when the chunk is a
+    multiple of 4 KiB.  Files go to a temporary directory on this host's file
+    system and are removed after."""
     import shutil
     import tempfile
 
@@ -401,7 +404,7 @@ def ssd_tier(wl: Workload, max_bytes: int = 1 << 30):
     w = wl.w
     L = w["layers"]
     row = L * w["kv"] * wl.chunk
-    n = int(min(len(wl.cids), max(1, max_bytes // row)))
+    n = int(min(len(wl.cids), max(1, max_bytes // row), w["nh"] // 4))
     d = tempfile.mkdtemp(prefix="flexkv_ssd_bench_")
     try:
         free = SSDAllocator.get_file_size_limit(d)
@@ -421,10 +424,14 @@ def ssd_tier(wl: Workload, max_bytes: int = 1 << 30):
         worker = CPUSSDDiskTransferWorker(0, None, None, wl.host, h.get_file_list(),
                                           mk(w["nh"]), ssd_lay, wl.dtype, h.num_blocks_per_file,
                                           CacheConfig())
-        src = wl.cids[:n].numpy().astype(np.int64)
+        hv = wl.host.view(w["nh"], row // 2).view(torch.int16)
+        hv[:n] = hv[wl.cids[:n]]
+        src = np.arange(n, dtype=np.int64)
         sids = np.arange(n, dtype=np.int64)
-        taken = set(wl.cids.tolist())
-        dst = np.array([c for c in range(w["nh"]) if c not in taken][:n], dtype=np.int64)
+        rnd = (2 * n + torch.randperm(w["nh"] - 2 * n,
+                                      generator=torch.Generator().manual_seed(7))[:n]).numpy()
+        rnd = rnd.astype(np.int64)
+        run = np.arange(n, 2 * n, dtype=np.int64)
         t0 = time.perf_counter()
         worker._transfer_impl(src, sids, TransferType.H2DISK, 0, L)
         t_write = time.perf_counter() - t0
@@ -435,16 +442,20 @@ def ssd_tier(wl: Workload, max_bytes: int = 1 << 30):
                 os.close(fd)
         t_sync = time.perf_counter() - t0
         t0 = time.perf_counter()
-        worker._transfer_impl(sids, dst, TransferType.DISK2H, 0, L)
-        t_read = time.perf_counter() - t0
+        worker._transfer_impl(sids, rnd, TransferType.DISK2H, 0, L)
+        t_rnd = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        worker._transfer_impl(sids, run, TransferType.DISK2H, 0, L)
+        t_run = time.perf_counter() - t0
         worker.close()
-        hv = wl.host.view(w["nh"], row // 2).view(torch.int16)
-        ok = bool(torch.equal(hv[torch.from_numpy(dst)], hv[torch.from_numpy(src)]))
+        ok = bool(torch.equal(hv[torch.from_numpy(rnd)], hv[:n]) and
+                  torch.equal(hv[n:2 * n], hv[:n]))
         gb = n * row / 1e9
         return {"blocks": n, "bytes": n * row, "fs": fs,
                 "write_gbps_buffered": round(gb / t_write, 3),
                 "write_gbps_with_fsync": round(gb / t_sync, 3),
-                "read_gbps": round(gb / t_read, 3),
+                "read_gbps_random_host_blocks": round(gb / t_rnd, 3),
+                "read_gbps_consecutive_host_blocks": round(gb / t_run, 3),
                 "read_io": "O_DIRECT" if wl.chunk % 4096 == 0 else "buffered",
                 "bit_exact": ok,
                 "threads_per_device": CacheConfig().ssd_threads_per_device}
@@ -692,7 +703,7 @@ def main() -> int:
             result["request_batch"] = request_batch(wl, args.steps)
             log(f"request batch: {result['request_batch']}")
         wl.transfer(False, default_ce)     # host rows of the step's ids hold the GPU blocks
-        result["ssd_tier"] = ssd_tier(wl)
+        result["ssd_tier"] = ssd_tier(wl)   # overwrites host blocks it stages through
         log(f"SSD tier: {result['ssd_tier']}")
         threads, cpu = cpu_baseline(wl, args.cpu_budget)
         v, reps, el = cpu[threads]

@@ -14,9 +14,10 @@
 //   * each device's blocks are split into contiguous ranges over
 //     num_threads_per_device threads.
 // Reads use O_DIRECT descriptors when chunk_size is a multiple of 4096
-// (transfer_ssd.cpp:201), like the reference.  Where a block's layers are
-// contiguous on both sides (block-wise layouts), the layer window of a block
-// moves as one I/O instead of one per chunk.
+// (transfer_ssd.cpp:201), like the reference.  Unlike the reference's one
+// request per chunk, chunks adjacent in both the file and the host cache are
+// merged into one request: a block's layer window in block-wise layouts, and
+// runs of consecutive blocks in either layout.
 
 #include <fcntl.h>
 #include <sys/stat.h>
@@ -143,11 +144,15 @@ int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, voi
     dev_cpu[d].push_back(c);
   }
   const bool direct = is_read && chunk_size_bytes % 4096 == 0;
-  // one I/O per block when the layer window is contiguous on both sides
-  const bool row_io = (kv == 1 || (cpu_kv_stride_bytes == chunk_size_bytes &&
-                                   ssd_kv_stride_bytes == chunk_size_bytes)) &&
-                      (num_layers == 1 || (cpu_layer_stride_bytes == kv * chunk_size_bytes &&
-                                           ssd_layer_stride_bytes == kv * chunk_size_bytes));
+  // Chunks are visited in the order that makes neighbours adjacent in both
+  // the file and the host cache: block by block when a block's layer window
+  // is contiguous on both sides (block-wise layouts, MLA), else layer by
+  // layer and K|V by K|V over the blocks (layer-wise layouts).  Adjacent
+  // chunks of one file merge into one request.
+  const bool block_major = (kv == 1 || (cpu_kv_stride_bytes == chunk_size_bytes &&
+                                        ssd_kv_stride_bytes == chunk_size_bytes)) &&
+                           (num_layers == 1 || (cpu_layer_stride_bytes == kv * chunk_size_bytes &&
+                                                ssd_layer_stride_bytes == kv * chunk_size_bytes));
   std::atomic<int> failed{0};
   std::string first_err;
   std::atomic<bool> have_err{false};
@@ -163,43 +168,57 @@ int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, voi
   };
   auto work = [&](int d, size_t lo, size_t hi) {
     char* base = static_cast<char*>(cpu_ptr);
-    for (size_t j = lo; j < hi && !failed; ++j) {
-      const int64_t x = dev_ssd[d][j];
+    // the request being built: `bytes` at host `buf`, file `file` offset `off`
+    struct Pending {
+      int file = -1;
+      char* buf = nullptr;
+      int64_t off = 0, bytes = 0, first_block = 0;
+    } p;
+    auto flush = [&]() {
+      if (p.bytes == 0 || failed) return;
+      const int fd = h->fd_buffered[d][p.file];
+      const int dfd = direct ? h->fd_direct[d][p.file] : -1;
+      int err = -2;
+      // O_DIRECT needs an aligned buffer, size and offset; else the page cache
+      if (dfd >= 0 && reinterpret_cast<uintptr_t>(p.buf) % 4096 == 0 && p.bytes % 4096 == 0 &&
+          p.off % 4096 == 0)
+        err = io_all(dfd, p.buf, p.bytes, p.off, true);
+      if (err != 0) err = io_all(fd, p.buf, p.bytes, p.off, is_read != 0);
+      if (err) record(is_read ? "read" : "write", d, p.first_block, err);
+      p.bytes = 0;
+    };
+    auto add = [&](int64_t x, char* buf, int64_t off, int64_t bytes) {
       const int f = static_cast<int>(x % F);
-      const int64_t in_file = x / F;
-      int fd = h->fd_buffered[d][f];
-      const int dfd = direct ? h->fd_direct[d][f] : -1;
-      // O_DIRECT needs an aligned buffer; fall back to the page cache if not
-      auto io = [&](char* buf, int64_t bytes, int64_t off) {
-        if (dfd >= 0 && reinterpret_cast<uintptr_t>(buf) % 4096 == 0 && bytes % 4096 == 0 &&
-            off % 4096 == 0 && io_all(dfd, buf, bytes, off, true) == 0)
-          return 0;
-        return io_all(fd, buf, bytes, off, is_read != 0);
-      };
-      char* cbase = base + dev_cpu[d][j] * block_stride_bytes;
-      const int64_t sbase = in_file * block_stride_bytes;
-      if (row_io) {
-        const int64_t off_c = static_cast<int64_t>(start_layer) * cpu_layer_stride_bytes;
-        const int64_t off_s = static_cast<int64_t>(start_layer) * ssd_layer_stride_bytes;
-        const int err = io(cbase + off_c, static_cast<int64_t>(num_layers) * kv * chunk_size_bytes,
-                           sbase + off_s);
-        if (err) record(is_read ? "read" : "write", d, x, err);
-        continue;
+      if (p.bytes > 0 && f == p.file && buf == p.buf + p.bytes && off == p.off + p.bytes) {
+        p.bytes += bytes;
+        return;
       }
-      for (int l = start_layer; l < start_layer + num_layers && !failed; ++l) {
-        for (int k = 0; k < kv; ++k) {
-          char* c = cbase + static_cast<int64_t>(l) * cpu_layer_stride_bytes +
-                    k * cpu_kv_stride_bytes;
-          const int64_t s = sbase + static_cast<int64_t>(l) * ssd_layer_stride_bytes +
-                            k * ssd_kv_stride_bytes;
-          const int err = io(c, chunk_size_bytes, s);
-          if (err) {
-            record(is_read ? "read" : "write", d, x, err);
-            break;
-          }
-        }
-      }
+      flush();
+      p.file = f;
+      p.buf = buf;
+      p.off = off;
+      p.bytes = bytes;
+      p.first_block = x;
+    };
+    auto host_chunk = [&](size_t j, int l, int k) {
+      return base + dev_cpu[d][j] * block_stride_bytes +
+             static_cast<int64_t>(l) * cpu_layer_stride_bytes + k * cpu_kv_stride_bytes;
+    };
+    auto file_chunk = [&](size_t j, int l, int k) {
+      return (dev_ssd[d][j] / F) * block_stride_bytes +
+             static_cast<int64_t>(l) * ssd_layer_stride_bytes + k * ssd_kv_stride_bytes;
+    };
+    if (block_major) {
+      const int64_t row = static_cast<int64_t>(num_layers) * kv * chunk_size_bytes;
+      for (size_t j = lo; j < hi && !failed; ++j)
+        add(dev_ssd[d][j], host_chunk(j, start_layer, 0), file_chunk(j, start_layer, 0), row);
+    } else {
+      for (int l = start_layer; l < start_layer + num_layers && !failed; ++l)
+        for (int k = 0; k < kv && !failed; ++k)
+          for (size_t j = lo; j < hi && !failed; ++j)
+            add(dev_ssd[d][j], host_chunk(j, l, k), file_chunk(j, l, k), chunk_size_bytes);
     }
+    flush();
   };
   std::vector<std::thread> threads;
   threads.reserve(static_cast<size_t>(D) * num_threads_per_device);

@@ -247,6 +247,29 @@ def test_product_matches_oracle(tmp_path, geom, window):
     c["worker"].close()
 
 
+@pytest.mark.parametrize("geom", GEOMS, ids=lambda g: f"{g[0].name}-mla{int(g[1])}-d{g[2]}"
+                         f"-f{g[3]}-{g[4]}x{g[5]}x{g[6]}")
+def test_contiguous_runs_match_oracle(tmp_path, geom):
+    """Runs of consecutive SSD and host ids, where neighbouring chunks merge
+    into single requests: two runs plus a stray block, written then read."""
+    layout, mla, n_dev, mbpf, tpb, H, Dh = geom
+    c = _product_case(tmp_path, layout, mla, n_dev, mbpf, tpb, H, Dh, seed=7)
+    sids = np.concatenate([np.arange(3, 19), np.arange(30, 41), [1]]).astype(np.int64)
+    cids = np.concatenate([np.arange(10, 26), np.arange(27, 38), [39]]).astype(np.int64)
+    for start, nl in ((0, c["cpu"].num_layer), (1, 2)):
+        images = _file_images(c["files"], c["used"])
+        _oracle_mirror(c, images, c["host"], sids, cids, start, nl, is_read=False)
+        c["worker"]._transfer_impl(cids, sids, TransferType.H2DISK, start, nl)
+        assert all(np.array_equal(a, b) for a, b in zip(_file_images(c["files"], c["used"]),
+                                                        images))
+        dst = np.roll(cids, 5)
+        expect = c["host"].copy()
+        _oracle_mirror(c, images, expect, sids, dst, start, nl, is_read=True)
+        c["worker"]._transfer_impl(sids, dst, TransferType.DISK2H, start, nl)
+        assert np.array_equal(c["host"], expect)
+    c["worker"].close()
+
+
 def test_reference_worker_geometry(tmp_path):
     """The reference test's SSD setup (tests/test_utils.py:15-53): two
     devices, 512 SSD blocks, LAYERWISE, 16 tokens x head_size 128 fp16, 4
