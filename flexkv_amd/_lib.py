@@ -133,14 +133,14 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.fkv_version.argtypes = []
 
 
-def hip_runtimes_loaded() -> list:
-    """Distinct libamdhip64 files mapped into this process."""
+def hip_runtimes_loaded(name: str = "libamdhip64.so") -> list:
+    """Distinct files of runtime `name` (HIP by default) mapped into this process."""
     paths = set()
     try:
         with open("/proc/self/maps") as fh:
             for line in fh:
                 parts = line.split()
-                if len(parts) >= 6 and "libamdhip64.so" in parts[-1]:
+                if len(parts) >= 6 and name in parts[-1]:
                     paths.add(os.path.realpath(parts[-1]))
     except OSError:
         pass
@@ -160,9 +160,11 @@ def load() -> ctypes.CDLL:
                     "g.build()'` from the repository root")
             lib = ctypes.CDLL(LIB_PATH)
             _declare(lib)
-            runtimes = hip_runtimes_loaded()
-            if len(runtimes) > 1:
-                raise ImportError(f"two HIP runtimes are mapped into this process: {runtimes}")
+            for name in ("libamdhip64.so", "libhsa-runtime64.so"):
+                runtimes = hip_runtimes_loaded(name)
+                if len(runtimes) > 1:
+                    raise ImportError(f"two copies of {name} are mapped into this process: "
+                                      f"{runtimes}")
             _lib = lib
     return _lib
 
