@@ -6,8 +6,9 @@
 //   * zero-copy mode: the "CPU side" is the pinned host cache itself and the
 //     kernel's 16-byte loads/stores travel over PCIe;
 //   * copy-engine mode: the "CPU side" is a contiguous HBM staging buffer laid
-//     out [block][layer][K|V][chunk]; the DMA engines then move maximal
-//     contiguous host runs between staging and the host cache.
+//     out [block][layer][K|V][chunk]; the SDMA engines (queued through HSA)
+//     then move maximal contiguous host runs between staging and the host
+//     cache.
 //
 // Work decomposition: a workgroup (4 wavefronts) owns a tile of consecutive
 // blocks; it stages the tile's (gpu_id, cpu_id) pairs in LDS, then its
