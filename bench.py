@@ -302,7 +302,7 @@ def engine_layerwise(wl: Workload, steps: int):
                      use_mla=wl.mla, dtype=wl.dtype)
     out = {}
     for eager in (False, True):
-        eng = TransferEngine([gpu_h], mc, CacheConfig(), cpu_handle=cpu_h, eager_dispatch=eager)
+        eng = TransferEngine([gpu_h], mc, CacheConfig(use_ce_transfer_h2d=False), cpu_handle=cpu_h, eager_dispatch=eager)
         eng.start()
         times = []
         try:
@@ -328,21 +328,76 @@ def engine_layerwise(wl: Workload, steps: int):
 
 def call_latency(wl: Workload, reps: int = 200):
     """Wall time of small synchronous calls (1 block x 1 layer, 16 blocks x 1
-    layer, 16 blocks x all layers), zero-copy path, median of `reps`."""
+    layer, 16 blocks x all layers), zero-copy and copy-engine paths,
+    alternating direction, median of `reps`."""
     from flexkv_amd import c_ext
     out = {}
     L = wl.w["layers"]
-    for nb, nl in ((1, 1), (16, 1), (16, L)):
-        g = wl.gids_p[:nb].clone().pin_memory()
-        c = wl.cids_p[:nb].clone().pin_memory()
-        p = wl.ptrs[:nl].clone().pin_memory()
-        ts = []
-        for i in range(reps + 5):
-            t0 = time.perf_counter()
-            c_ext.transfer_kv_blocks(g, p, wl.gkv, wl.gblk, c, wl.host, wl.ckv, wl.clay, wl.cblk,
-                                     wl.chunk, 0, -1, i % 2 == 0, False, wl.mla)
-            ts.append(time.perf_counter() - t0)
-        out[f"{nb}blk_{nl}layer_us"] = round(statistics.median(ts[5:]) * 1e6, 1)
+    for path, ce in (("zc", False), ("ce", True)):
+        for nb, nl in ((1, 1), (16, 1), (16, L)):
+            g = wl.gids_p[:nb].clone().pin_memory()
+            c = wl.cids_p[:nb].clone().pin_memory()
+            p = wl.ptrs[:nl].clone().pin_memory()
+            ts = []
+            for i in range(reps + 5):
+                t0 = time.perf_counter()
+                c_ext.transfer_kv_blocks(g, p, wl.gkv, wl.gblk, c, wl.host, wl.ckv, wl.clay,
+                                         wl.cblk, wl.chunk, 0, -1, i % 2 == 0, ce, wl.mla)
+                ts.append(time.perf_counter() - t0)
+            out[f"{path}_{nb}blk_{nl}layer_us"] = round(statistics.median(ts[5:]) * 1e6, 1)
+    return out
+
+
+def overlap_with_compute(wl: Workload, steps: int = 3, gemms: int = 160):
+    """One full transfer op on its own stream (from a second host thread)
+    while the main thread runs bf16 GEMMs [8192x4096]x[4096x4096] on a compute
+    stream: GEMM time alone and beside each path and direction.  The
+    zero-copy kernel shares compute units with the GEMMs; the copy-engine
+    path leaves the PCIe copies to the SDMA engines."""
+    import threading
+
+    from flexkv_amd import c_ext
+    xfer = c_ext.transfer_stream()
+    comp = torch.cuda.Stream()
+    a = torch.randn(8192, 4096, device=wl.dev, dtype=torch.bfloat16)
+    b = torch.randn(4096, 4096, device=wl.dev, dtype=torch.bfloat16)
+    c = torch.empty(8192, 4096, device=wl.dev, dtype=torch.bfloat16)
+
+    def once(h2d, ce, with_xfer=True):
+        torch.cuda.synchronize()
+        res = {}
+
+        def move():
+            with torch.cuda.stream(xfer):
+                t0 = time.perf_counter()
+                wl.transfer(h2d, ce)
+                res["xfer"] = time.perf_counter() - t0
+        th = threading.Thread(target=move) if with_xfer else None
+        if th:
+            th.start()
+        with torch.cuda.stream(comp):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(gemms):
+                torch.mm(a, b, out=c)
+            e1.record()
+        if th:
+            th.join()
+        torch.cuda.synchronize()
+        res["gemm"] = e0.elapsed_time(e1) / 1e3
+        return res
+
+    once(True, False)
+    out = {"gemm_alone_ms": round(statistics.median(
+        once(True, False, with_xfer=False)["gemm"] for _ in range(steps)) * 1e3, 2)}
+    for h2d in (False, True):
+        for ce in (False, True):
+            rs = [once(h2d, ce) for _ in range(steps)]
+            key = ("h2d" if h2d else "d2h") + ("_ce" if ce else "_kernel")
+            out[key] = {"gemm_ms": round(statistics.median(r["gemm"] for r in rs) * 1e3, 2),
+                        "transfer_ms": round(statistics.median(r["xfer"] for r in rs) * 1e3, 2)}
+    out["what"] = (f"{gemms} GEMMs on a compute stream beside one {wl.bytes_per_op / 2**30:.0f} "
+                   "GiB transfer on a transfer stream")
     return out
 
 
@@ -699,6 +754,8 @@ def main() -> int:
         log(f"engine layer-wise read: {result['engine_layerwise_read']}")
         result["call_latency"] = call_latency(wl)
         log(f"call latency: {result['call_latency']}")
+        result["overlap_with_compute"] = overlap_with_compute(wl)
+        log(f"overlap with compute: {result['overlap_with_compute']}")
         if wl.mla:
             result["request_batch"] = request_batch(wl, args.steps)
             log(f"request batch: {result['request_batch']}")

@@ -7,7 +7,12 @@ transfer knobs, and the SSD cache (enable_ssd, layout, block count, files).
 The remote and trace fields belong to parts this package does not implement
 and are not present.  Defaults that differ from the reference: the host and
 SSD layouts are BLOCKWISE (one block's layers contiguous, which the device
-path and the SSD path both move as single runs) and the host cache is pinned.
+path and the SSD path both move as single runs), the host cache is pinned, and
+both directions use the copy-engine path: on MI355X it moves whole-block
+transfers as fast as the zero-copy kernel (56.3 / 56.6 GB/s against 56.5 /
+57.2) while leaving the compute units to the model (GEMMs beside a 2 GiB D2H
+slow down 7% instead of 120%), and it hands small or fine-grained transfers to
+the zero-copy kernel by itself.
 """
 from __future__ import annotations
 
@@ -46,9 +51,9 @@ class CacheConfig:
     ssd_kv_layout_type: KVCacheLayoutType = KVCacheLayoutType.BLOCKWISE
     num_cpu_blocks: int = 1000000
     num_ssd_blocks: int = 10000000
-    # False = zero-copy kernel, True = copy engines via on-device staging
-    use_ce_transfer_h2d: bool = False
-    use_ce_transfer_d2h: bool = False
+    # False = zero-copy kernel, True = SDMA engines via on-device staging
+    use_ce_transfer_h2d: bool = True
+    use_ce_transfer_d2h: bool = True
     # compute units the zero-copy kernel may occupy (-1 = automatic)
     transfer_sms_h2d: int = 8
     transfer_sms_d2h: int = 8

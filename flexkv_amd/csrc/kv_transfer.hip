@@ -165,9 +165,6 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
   __shared__ int64_t s_cid[kMaxTileBlocks];
 
   if (!kIotaCpu && FKV_ZC_PRIO > 0) __builtin_amdgcn_s_setprio(FKV_ZC_PRIO);
-  // The scatter reads staging that copy engines wrote, outside any HIP
-  // stream: acquire at system scope so no stale cache line is read.
-  if (kScatter) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
   const int lane = threadIdx.x & 63;
   const uint32_t lane_off = static_cast<uint32_t>(lane) * 16;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -258,6 +255,13 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
       }
     }
   }
+}
+
+// A system-scope acquire in every workgroup.  Launched with a workgroup per
+// compute unit (so every XCD's L2 takes part) before a kernel reads memory
+// the copy engines wrote outside any HIP stream: no stale line survives it.
+__global__ __launch_bounds__(64) void acquire_system_kernel() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
 }
 
 // ---------------------------------------------------------------------------
@@ -930,8 +934,8 @@ int issue_sdma(DeviceState& d, const std::vector<Run>& runs, char* staging, bool
 //  D2H, per piece: wait for the half's previous copies -> gather kernel ->
 //  wait for it -> queue the half's copies.
 //  H2D: queue the copies of the first two pieces; per piece: wait for its
-//  copies -> scatter kernel; once that has read the half, queue the copies of
-//  the piece two ahead into it.
+//  copies -> system-scope acquire -> scatter kernel; once that has read the
+//  half, queue the copies of the piece two ahead into it.
 int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   DeviceState& d = g_dev[dev];
   std::lock_guard<std::mutex> lk(d.mu);
@@ -1015,6 +1019,8 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
       const int h = pi & 1;
       sdma_wait(d.sig[h]);
       pending[h] = false;
+      hipLaunchKernelGGL(acquire_system_kernel, dim3(d.num_cus), dim3(64), 0, stream);
+      FKV_HIP(hipGetLastError());
       if ((rc = launch(pi))) return rc;
       if (pi + 2 < np) {
         FKV_HIP(hipEventRecord(d.ev_compute[h], stream));
@@ -1272,6 +1278,26 @@ Geometry make_geometry(int num_blocks, int start_layer_id, int num_layers,
   return g;
 }
 
+// Copy-engine mode hands a transfer to the SDMA engines only when the
+// engines pay off: the op moves at least FLEXKV_CE_MIN_BYTES (default 8 MiB)
+// and its contiguous host runs are at least 128 KiB.  Each engine copy costs
+// about 6 us and the host-side ordering about 40 us per call (MI355X: a
+// 1 MiB op of 64 KiB runs takes 77 us on the engines, 39 us in the zero-copy
+// kernel); smaller or finer-grained transfers go to the zero-copy kernel,
+// with identical results.
+constexpr int64_t kCeMinBytesDefault = int64_t(8) << 20;
+constexpr int64_t kCeMinRunBytes = int64_t(128) << 10;
+
+bool ce_pays_off(const Geometry& g) {
+  const char* e = getenv("FLEXKV_CE_MIN_BYTES");
+  const int64_t min_bytes = e ? std::max<int64_t>(0, atoll(e)) : kCeMinBytesDefault;
+  const int64_t total = static_cast<int64_t>(g.num_blocks) * g.num_layers * g.kv * g.chunk;
+  const bool row_contig = (g.kv == 1 || g.cks == g.chunk) &&
+                          (g.num_layers == 1 || g.cls == g.kv * g.chunk);
+  const int64_t run = row_contig ? static_cast<int64_t>(g.num_layers) * g.kv * g.chunk : g.chunk;
+  return total >= min_bytes && (min_bytes == 0 || run >= kCeMinRunBytes);
+}
+
 // Validate, then run one synchronous transfer in the requested mode.
 int transfer_entry(Geometry& g, hipStream_t s, int transfer_cus, bool h2d, int mode) {
   int rc = validate(g, mode);
@@ -1283,6 +1309,7 @@ int transfer_entry(Geometry& g, hipStream_t s, int transfer_cus, bool h2d, int m
     case FKV_XFER_KERNEL:
       return transfer_zero_copy(g, s, dev, transfer_cus, h2d);
     case FKV_XFER_CE:
+      if (!ce_pays_off(g)) return transfer_zero_copy(g, s, dev, transfer_cus, h2d);
       return transfer_staged(g, s, dev, h2d);
     default:
       return transfer_ce_per_chunk(g, s, h2d);

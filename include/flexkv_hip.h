@@ -38,10 +38,13 @@ enum {
    * csrc/transfer.cu:123-129. */
   FKV_XFER_KERNEL = 0,
   /* Copy-engine path: a gather kernel packs the selected chunks into a
-   * contiguous HBM staging buffer and the DMA engines move maximal contiguous
-   * host runs (D2H); H2D is DMA into staging followed by a scatter kernel.
-   * Staging pieces are double-buffered across the caller's stream and a side
-   * stream.  Same role as the reference CE mode, csrc/transfer.cu:97-121. */
+   * contiguous HBM staging buffer and the SDMA engines move maximal
+   * contiguous host runs (D2H); H2D is SDMA into staging followed by a
+   * scatter kernel.  Staging is double-buffered; the PCIe copies take no
+   * compute units.  Transfers under FLEXKV_CE_MIN_BYTES (default 8 MiB) or
+   * with host runs under 128 KiB move with the zero-copy kernel instead,
+   * where the engines' per-copy cost would dominate.  Same role as the
+   * reference CE mode, csrc/transfer.cu:97-121. */
   FKV_XFER_CE = 1,
   /* The reference's copy-engine algorithm restated literally: one
    * hipMemcpyAsync per (layer, K|V, block) chunk, csrc/transfer.cu:97-121.

@@ -7,6 +7,10 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
+# Copy-engine mode hands transfers under 8 MiB to the zero-copy kernel; the
+# parity tests use small shapes and must reach the SDMA path itself.
+os.environ["FLEXKV_CE_MIN_BYTES"] = "0"
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a HIP device (MI355X)")

@@ -142,6 +142,48 @@ def test_geometries_match_oracle(dev, geo, mode):
     check_case(case, gids, cids, mode)
 
 
+@pytest.mark.parametrize("h2d", [False, True])
+@pytest.mark.parametrize("layout", ["BLOCKWISE", "LAYERWISE"])
+def test_copy_engine_size_policy(dev, h2d, layout, monkeypatch):
+    """Copy-engine mode sends transfers under FLEXKV_CE_MIN_BYTES, or with
+    host runs under 128 KiB (layer-wise host layout: one 32 KiB chunk per
+    run), to the zero-copy kernel and the rest to the SDMA engines; 0 forces
+    the engines.  The bytes are the same either way.  The library's profile
+    counts SDMA batches."""
+    from flexkv_amd import _lib
+    from gpu_util import DeviceCase, abi_transfer
+    case = KVCase(layers_total=4, num_layers=4, start_layer=0, kv=2, ng=64, nh=96, tokens=16,
+                  heads=8, dim=128, layout=layout).fill(seed=31)   # 32 KiB chunks
+    n = 20                                                          # 5 MiB moved
+    gids = inputs.distinct_ids(3, n, 64)
+    cids = inputs.distinct_ids(4, n, 96)
+    want = _oracle_d2h(case, gids, cids, 1)
+    total = n * 4 * 2 * 32768
+    rows = layout == "BLOCKWISE"
+    for env, engines in (("0", True), (None, False), (str(total), rows), (str(total + 1), False)):
+        if env is None:
+            monkeypatch.delenv("FLEXKV_CE_MIN_BYTES", raising=False)
+        else:
+            monkeypatch.setenv("FLEXKV_CE_MIN_BYTES", env)
+        print(f"policy layout={layout} h2d={h2d} env={env}", flush=True)
+        dc = DeviceCase(case)
+        _lib.profile_enable(True)
+        abi_transfer(dc, gids, cids, h2d=False, mode=1)
+        if h2d:
+            dc.set_gpu([np.zeros_like(g) for g in case.gpu])
+            abi_transfer(dc, gids, cids, h2d=True, mode=1)
+        prof = _lib.profile_read()
+        _lib.profile_enable(False)
+        torch.cuda.synchronize()
+        assert (prof["dma_batches"] > 0) == engines, (env, prof)
+        assert np.array_equal(dc.host_np(), want)
+        if h2d:
+            for l, g in enumerate(dc.gpu_np()):
+                expect = np.zeros_like(case.gpu[l])
+                expect[:, gids] = case.gpu[l][:, gids]
+                assert np.array_equal(g, expect), f"layer {l}"
+
+
 # Separate K and V allocations (fkv_transfer_kv_blocks_kv_ptrs): the same
 # bytes must move as with K and V halves of one allocation, so the oracle of
 # the combined layout is the expectation.  Geometry 7 (130 layers) needs three
