@@ -160,11 +160,11 @@ def load() -> ctypes.CDLL:
                     "g.build()'` from the repository root")
             lib = ctypes.CDLL(LIB_PATH)
             _declare(lib)
-            for name in ("libamdhip64.so", "libhsa-runtime64.so"):
-                runtimes = hip_runtimes_loaded(name)
-                if len(runtimes) > 1:
-                    raise ImportError(f"two copies of {name} are mapped into this process: "
-                                      f"{runtimes}")
+            # (A profiler may map a second HSA runtime for itself; the library
+            # resolves its HSA calls from the one next to the HIP runtime.)
+            runtimes = hip_runtimes_loaded()
+            if len(runtimes) > 1:
+                raise ImportError(f"two HIP runtimes are mapped into this process: {runtimes}")
             _lib = lib
     return _lib
 

@@ -29,10 +29,7 @@ def command() -> list:
         # no packed fp32 instructions anywhere in device code
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-I", os.path.join(ROOT, "include"),
-        *SOURCES, "-o", OUT + ".tmp",
-        # the copy engines are driven through HSA; in a PyTorch process this
-        # binds to the runtime torch already loaded (same soname)
-        "-lhsa-runtime64",
+        *SOURCES, "-o", OUT + ".tmp", "-ldl",
     ]
 
 

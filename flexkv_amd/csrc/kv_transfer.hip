@@ -21,6 +21,7 @@
 #include <hip/hip_runtime.h>
 #include <hsa/hsa.h>
 #include <hsa/hsa_ext_amd.h>
+#include <dlfcn.h>
 
 #include <algorithm>
 #include <atomic>
@@ -32,6 +33,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "flexkv_hip.h"
@@ -368,13 +370,15 @@ struct DeviceState {
   char* staging = nullptr;
   size_t staging_bytes = 0;
   // Copy engines: the HSA agents of this GPU and of the host, the SDMA
-  // engines usable in each direction, and per staging half one completion
-  // signal (counts the half's outstanding copies) and one event (the
-  // gather/scatter kernel that last used the half, on the caller's stream).
+  // engines usable in each direction, and per staging half a pool of
+  // completion signals (one per queued copy, `in_flight` of them in use) and
+  // one event (the gather/scatter kernel that last used the half, on the
+  // caller's stream).
   bool sdma_init = false;
   hsa_agent_t gpu_agent{}, cpu_agent{};
   std::vector<hsa_amd_sdma_engine_id_t> engines[2];   // [D2H, H2D]
-  hsa_signal_t sig[2] = {{0}, {0}};
+  std::vector<hsa_signal_t> sigs[2];
+  size_t in_flight[2] = {0, 0};
   hipEvent_t ev_compute[2] = {nullptr, nullptr};
 };
 
@@ -702,11 +706,31 @@ int stream_device(hipStream_t s, int* dev) {
   return 0;
 }
 
+// The HSA entry points the copy-engine path needs, resolved from the HSA
+// runtime that the process's HIP runtime uses.  Binding by name could reach a
+// second HSA runtime mapped into the process, which knows nothing of HIP's
+// allocations.
+struct HsaApi {
+  decltype(&::hsa_iterate_agents) iterate_agents = nullptr;
+  decltype(&::hsa_agent_get_info) agent_get_info = nullptr;
+  decltype(&::hsa_status_string) status_string = nullptr;
+  decltype(&::hsa_signal_create) signal_create = nullptr;
+  decltype(&::hsa_signal_store_screlease) signal_store_screlease = nullptr;
+  decltype(&::hsa_signal_wait_scacquire) signal_wait_scacquire = nullptr;
+  decltype(&::hsa_amd_memory_copy_engine_status) copy_engine_status = nullptr;
+  decltype(&::hsa_amd_memory_async_copy_on_engine) async_copy_on_engine = nullptr;
+};
+HsaApi g_hsa;
 // Wait until a half's copies have finished (its signal counts down to 0).
-void sdma_wait(hsa_signal_t s) {
-  while (hsa_signal_wait_scacquire(s, HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX,
-                                   HSA_WAIT_STATE_BLOCKED) >= 1) {
-  }
+// Wait until every copy queued on a staging half has finished.  Each copy
+// has its own signal: a counted signal shared by many copies would depend on
+// every layer between here and the engines decrementing it by exactly one.
+void sdma_wait(DeviceState& d, int half) {
+  for (size_t i = 0; i < d.in_flight[half]; ++i)
+    while (g_hsa.signal_wait_scacquire(d.sigs[half][i], HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX,
+                                       HSA_WAIT_STATE_BLOCKED) >= 1) {
+    }
+  d.in_flight[half] = 0;
 }
 
 // When a transfer fails after enqueueing work, wait for that work before the
@@ -714,13 +738,13 @@ void sdma_wait(hsa_signal_t s) {
 // reused id and staging buffers, after the error has been reported.
 struct DrainOnError {
   hipStream_t stream;
-  const DeviceState* dev_state;
+  DeviceState* dev_state;
   bool armed = true;
   ~DrainOnError() {
     if (!armed) return;
     (void)hipStreamSynchronize(stream);
     if (dev_state && dev_state->sdma_init)
-      for (int h = 0; h < 2; ++h) sdma_wait(dev_state->sig[h]);
+      for (int h = 0; h < 2; ++h) sdma_wait(*dev_state, h);
     (void)hipGetLastError();
   }
 };
@@ -795,6 +819,66 @@ int sdma_engines_wanted() {
   return std::max(1, std::min(n, 32));
 }
 
+std::mutex g_hsa_mu;
+bool g_hsa_loaded = false;
+
+hsa_status_t count_agent(hsa_agent_t, void* n) {
+  ++*static_cast<int*>(n);
+  return HSA_STATUS_SUCCESS;
+}
+
+// The HSA runtime behind HIP is the mapped copy that is initialised: a
+// process can map a second, idle copy (a wheel's bundled runtime next to the
+// system one a profiling tool preloaded), and which one HIP bound to depends
+// on load order.
+int load_hsa() {
+  std::lock_guard<std::mutex> lk(g_hsa_mu);
+  if (g_hsa_loaded) return 0;
+  std::vector<std::string> paths;
+  if (FILE* f = fopen("/proc/self/maps", "r")) {
+    char line[4096];
+    while (fgets(line, sizeof(line), f)) {
+      const char* p = strchr(line, '/');
+      if (!p || !strstr(p, "libhsa-runtime64.so")) continue;
+      std::string path(p);
+      while (!path.empty() && (path.back() == '\n' || path.back() == ' ')) path.pop_back();
+      if (std::find(paths.begin(), paths.end(), path) == paths.end()) paths.push_back(path);
+    }
+    fclose(f);
+  }
+  void* lib = nullptr;
+  for (const std::string& path : paths) {
+    void* h = dlopen(path.c_str(), RTLD_NOW | RTLD_NOLOAD);
+    if (!h) continue;
+    auto iterate = reinterpret_cast<decltype(&::hsa_iterate_agents)>(dlsym(h, "hsa_iterate_agents"));
+    int n = 0;
+    if (iterate && iterate(count_agent, &n) == HSA_STATUS_SUCCESS && n > 0) {
+      lib = h;
+      break;
+    }
+    dlclose(h);
+  }
+  if (!lib) return fail(kInval, "no initialised HSA runtime is mapped into the process");
+  HsaApi a;
+  int missing = 0;
+  auto sym = [&](auto& fn, const char* name) {
+    fn = reinterpret_cast<std::remove_reference_t<decltype(fn)>>(dlsym(lib, name));
+    if (!fn) ++missing;
+  };
+  sym(a.iterate_agents, "hsa_iterate_agents");
+  sym(a.agent_get_info, "hsa_agent_get_info");
+  sym(a.status_string, "hsa_status_string");
+  sym(a.signal_create, "hsa_signal_create");
+  sym(a.signal_store_screlease, "hsa_signal_store_screlease");
+  sym(a.signal_wait_scacquire, "hsa_signal_wait_scacquire");
+  sym(a.copy_engine_status, "hsa_amd_memory_copy_engine_status");
+  sym(a.async_copy_on_engine, "hsa_amd_memory_async_copy_on_engine");
+  if (missing) return fail(kInval, "the HSA runtime lacks %d entry points", missing);
+  g_hsa = a;
+  g_hsa_loaded = true;
+  return 0;
+}
+
 struct AgentSearch {
   uint32_t bus = 0, device = 0, domain = 0;
   bool found_gpu = false, found_cpu = false;
@@ -804,17 +888,17 @@ struct AgentSearch {
 hsa_status_t find_agents(hsa_agent_t a, void* arg) {
   auto* q = static_cast<AgentSearch*>(arg);
   hsa_device_type_t t;
-  if (hsa_agent_get_info(a, HSA_AGENT_INFO_DEVICE, &t) != HSA_STATUS_SUCCESS)
+  if (g_hsa.agent_get_info(a, HSA_AGENT_INFO_DEVICE, &t) != HSA_STATUS_SUCCESS)
     return HSA_STATUS_SUCCESS;
   if (t == HSA_DEVICE_TYPE_CPU && !q->found_cpu) {
     q->cpu = a;
     q->found_cpu = true;
   } else if (t == HSA_DEVICE_TYPE_GPU && !q->found_gpu) {
     uint32_t bdf = 0, domain = 0;
-    if (hsa_agent_get_info(a, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_BDFID), &bdf) !=
+    if (g_hsa.agent_get_info(a, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_BDFID), &bdf) !=
         HSA_STATUS_SUCCESS)
       return HSA_STATUS_SUCCESS;
-    (void)hsa_agent_get_info(a, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_DOMAIN), &domain);
+    (void)g_hsa.agent_get_info(a, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_DOMAIN), &domain);
     if ((bdf >> 8) == q->bus && ((bdf >> 3) & 31) == q->device && domain == q->domain) {
       q->gpu = a;
       q->found_gpu = true;
@@ -828,7 +912,7 @@ hsa_status_t find_agents(hsa_agent_t a, void* arg) {
     hsa_status_t st_ = (expr);                                                          \
     if (st_ != HSA_STATUS_SUCCESS) {                                                    \
       const char* m_ = nullptr;                                                         \
-      (void)hsa_status_string(st_, &m_);                                                \
+      (void)g_hsa.status_string(st_, &m_);                                                \
       return fail(static_cast<int>(hipErrorUnknown), "%s failed: %s", #expr, m_ ? m_ : "?"); \
     }                                                                                   \
   } while (0)
@@ -838,7 +922,7 @@ hsa_status_t find_agents(hsa_agent_t a, void* arg) {
 // the host side uses the GPU's nearest CPU agent when the runtime reports one.
 int ensure_sdma(DeviceState& d, int dev) {
   if (d.sdma_init) return 0;
-  FKV_HSA(hsa_init());
+  if (int rc = load_hsa()) return rc;
   AgentSearch q;
   int bus = 0, device = 0, domain = 0;
   FKV_HIP(hipDeviceGetAttribute(&bus, hipDeviceAttributePciBusId, dev));
@@ -847,19 +931,20 @@ int ensure_sdma(DeviceState& d, int dev) {
   q.bus = static_cast<uint32_t>(bus);
   q.device = static_cast<uint32_t>(device);
   q.domain = static_cast<uint32_t>(domain);
-  FKV_HSA(hsa_iterate_agents(find_agents, &q));
+  // load_hsa picked the runtime HIP initialised; no reference of our own.
+  FKV_HSA(g_hsa.iterate_agents(find_agents, &q));
   if (!q.found_gpu || !q.found_cpu)
     return fail(kInval, "no HSA agent matches HIP device %d (pci %04x:%02x:%02x)", dev, domain,
                 bus, device);
   hsa_agent_t nearest{};
-  if (hsa_agent_get_info(q.gpu, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_NEAREST_CPU),
+  if (g_hsa.agent_get_info(q.gpu, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_NEAREST_CPU),
                          &nearest) == HSA_STATUS_SUCCESS && nearest.handle != 0)
     q.cpu = nearest;
   const int want = sdma_engines_wanted();
   for (int dir = 0; dir < 2; ++dir) {
     uint32_t mask = 0;
-    FKV_HSA(dir == 0 ? hsa_amd_memory_copy_engine_status(q.cpu, q.gpu, &mask)
-                     : hsa_amd_memory_copy_engine_status(q.gpu, q.cpu, &mask));
+    FKV_HSA(dir == 0 ? g_hsa.copy_engine_status(q.cpu, q.gpu, &mask)
+                     : g_hsa.copy_engine_status(q.gpu, q.cpu, &mask));
     d.engines[dir].clear();
     for (int b = 0; b < 32 && static_cast<int>(d.engines[dir].size()) < want; ++b)
       if (mask & (1u << b))
@@ -868,10 +953,8 @@ int ensure_sdma(DeviceState& d, int dev) {
       return fail(kInval, "device %d reports no SDMA engine for %s copies", dev,
                   dir == 0 ? "device-to-host" : "host-to-device");
   }
-  for (int h = 0; h < 2; ++h) {
-    FKV_HSA(hsa_signal_create(0, 0, nullptr, &d.sig[h]));
+  for (int h = 0; h < 2; ++h)
     FKV_HIP(hipEventCreateWithFlags(&d.ev_compute[h], hipEventDisableTiming));
-  }
   d.gpu_agent = q.gpu;
   d.cpu_agent = q.cpu;
   d.sdma_init = true;
@@ -897,31 +980,36 @@ int ensure_staging(DeviceState& d, size_t need_half) {
 }
 
 // Queue the copies of `runs` between the host cache and staging half `half`
-// on the device's SDMA engines, round robin; each copy counts the half's
-// signal down by one.
+// on the device's SDMA engines, round robin, each with its own completion
+// signal.
 int issue_sdma(DeviceState& d, const std::vector<Run>& runs, char* staging, bool h2d, int half,
                hsa_agent_t host_agent) {
   const std::vector<hsa_amd_sdma_engine_id_t>& eng = d.engines[h2d ? 1 : 0];
-  hsa_signal_store_screlease(d.sig[half], static_cast<hsa_signal_value_t>(runs.size()));
+  std::vector<hsa_signal_t>& sigs = d.sigs[half];
+  while (sigs.size() < runs.size()) {
+    hsa_signal_t sg;
+    FKV_HSA(g_hsa.signal_create(1, 0, nullptr, &sg));
+    sigs.push_back(sg);
+  }
   for (size_t i = 0; i < runs.size(); ++i) {
     const Run& r = runs[i];
     char* dev_p = staging + r.staging_off;
     const hsa_amd_sdma_engine_id_t e = eng[i % eng.size()];
+    g_hsa.signal_store_screlease(sigs[i], 1);
     const hsa_status_t st =
-        h2d ? hsa_amd_memory_async_copy_on_engine(dev_p, d.gpu_agent, r.host, host_agent,
-                                                  static_cast<size_t>(r.bytes), 0, nullptr,
-                                                  d.sig[half], e, false)
-            : hsa_amd_memory_async_copy_on_engine(r.host, host_agent, dev_p, d.gpu_agent,
-                                                  static_cast<size_t>(r.bytes), 0, nullptr,
-                                                  d.sig[half], e, false);
+        h2d ? g_hsa.async_copy_on_engine(dev_p, d.gpu_agent, r.host, host_agent,
+                                         static_cast<size_t>(r.bytes), 0, nullptr, sigs[i], e,
+                                         false)
+            : g_hsa.async_copy_on_engine(r.host, host_agent, dev_p, d.gpu_agent,
+                                         static_cast<size_t>(r.bytes), 0, nullptr, sigs[i], e,
+                                         false);
     if (st != HSA_STATUS_SUCCESS) {
-      // copies never queued will never count down
-      hsa_signal_subtract_screlease(d.sig[half], static_cast<hsa_signal_value_t>(runs.size() - i));
       const char* m = nullptr;
-      (void)hsa_status_string(st, &m);
+      (void)g_hsa.status_string(st, &m);
       return fail(static_cast<int>(hipErrorUnknown), "SDMA copy of %lld bytes failed: %s",
                   static_cast<long long>(r.bytes), m ? m : "?");
     }
+    d.in_flight[half] = i + 1;
   }
   return 0;
 }
@@ -1004,7 +1092,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
     for (int pi = 0; pi < np; ++pi) {
       const int h = pi & 1;
       if (pending[h]) {
-        sdma_wait(d.sig[h]);
+        sdma_wait(d, h);
         pending[h] = false;
       }
       if ((rc = launch(pi))) return rc;
@@ -1017,7 +1105,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
       if ((rc = queue_copies(pi))) return rc;
     for (int pi = 0; pi < np; ++pi) {
       const int h = pi & 1;
-      sdma_wait(d.sig[h]);
+      sdma_wait(d, h);
       pending[h] = false;
       hipLaunchKernelGGL(acquire_system_kernel, dim3(d.num_cus), dim3(64), 0, stream);
       FKV_HIP(hipGetLastError());
@@ -1030,7 +1118,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
     }
   }
   for (int h = 0; h < 2; ++h)
-    if (pending[h]) sdma_wait(d.sig[h]);
+    if (pending[h]) sdma_wait(d, h);
   FKV_HIP(hipStreamSynchronize(stream));
   drain.armed = false;
   if (prof.on) {
