@@ -698,7 +698,9 @@ def main() -> int:
                    "bytes_per_step": wl.bytes_per_op},
         "d2h": {"gbps": round(gb / d2h_s, 3), "median_ms": round(d2h_med * 1e3, 3),
                 "best_ms": round(d2h_best * 1e3, 3),
-                "kernel_avg_ms": round(z_ms, 4)},
+                **({"gather_piece_avg_ms": round(z_ms, 4),
+                    "sdma_copies": prof_d2h["dma_copies"], "sdma_bytes": prof_d2h["dma_bytes"]}
+                   if default_ce else {"kernel_avg_ms": round(z_ms, 4)})},
         "h2d": {"gbps": round(gb / h2d_s, 3), "ms_per_step": round(h2d_s * 1e3, 3),
                 "median_ms": round(h2d_med * 1e3, 3), "best_ms": round(h2d_best * 1e3, 3)},
         "bit_exact": parity and gather_ok,
@@ -726,7 +728,8 @@ def main() -> int:
             "h2d_peak_gbps_measured": round(peaks["h2d"], 2),
             "d2h_frac": round((gb / d2h_s) / peaks["d2h"], 4),
             "h2d_frac": round((gb / h2d_s) / peaks["h2d"], 4),
-            "d2h_kernel_frac": round((gb / (z_ms * 1e-3)) / peaks["d2h"], 4),
+            **({} if default_ce else
+               {"d2h_kernel_frac": round((gb / (z_ms * 1e-3)) / peaks["d2h"], 4)}),
             "d2d_copy_gbps_measured": round(peaks["d2d_copy_read_plus_write"], 1),
             "how": "best of 8 hipMemcpyAsync over 1 GiB contiguous pinned host memory per "
                    "direction; D2D = 4 GiB device copy counted read+write",
