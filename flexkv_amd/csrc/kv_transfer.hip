@@ -1047,7 +1047,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   const size_t half = d.staging_bytes / 2;
   const int blocks_per_piece = static_cast<int>(std::max<size_t>(1, half / row_bytes));
   const int grid_cap = d.num_cus * (h2d ? d.occ_staged[1] : d.occ_staged[0]);
-  const hsa_agent_t host_agent = g.cpu_info.device ? d.gpu_agent : d.cpu_agent;
+  const hsa_agent_t host_agent = d.cpu_agent;   // device-resident caches never get here
 
   struct Piece {
     int l0, nl, b0, nb;
@@ -1371,12 +1371,14 @@ Geometry make_geometry(int num_blocks, int start_layer_id, int num_layers,
 // and its contiguous host runs are at least 128 KiB.  Each engine copy costs
 // about 6 us and the host-side ordering about 40 us per call (MI355X: a
 // 1 MiB op of 64 KiB runs takes 77 us on the engines, 39 us in the zero-copy
-// kernel); smaller or finer-grained transfers go to the zero-copy kernel,
-// with identical results.
+// kernel); smaller or finer-grained transfers, and caches in device memory,
+// go to the zero-copy kernel, with identical results.
 constexpr int64_t kCeMinBytesDefault = int64_t(8) << 20;
 constexpr int64_t kCeMinRunBytes = int64_t(128) << 10;
 
 bool ce_pays_off(const Geometry& g) {
+  // a "host" cache that is device memory has no PCIe copy to offload
+  if (g.cpu_info.device) return false;
   const char* e = getenv("FLEXKV_CE_MIN_BYTES");
   const int64_t min_bytes = e ? std::max<int64_t>(0, atoll(e)) : kCeMinBytesDefault;
   const int64_t total = static_cast<int64_t>(g.num_blocks) * g.num_layers * g.kv * g.chunk;
