@@ -56,7 +56,8 @@ def log(msg: str) -> None:
 
 
 class Workload:
-    def __init__(self, name: str, seed: int, run: int = 0, host: bool = True):
+    def __init__(self, name: str, seed: int, run: int = 0, host: bool = True,
+                 host_layout: str = "BLOCKWISE"):
         from flexkv_amd.common.storage import KVCacheLayout, KVCacheLayoutType
         from flexkv_amd.storage.allocator import CPUAllocator
 
@@ -68,8 +69,9 @@ class Workload:
         self.dtype = torch.bfloat16
         gl = KVCacheLayout(KVCacheLayoutType.LAYERWISE, L, w["ng"], w["tokens"], w["heads"],
                            w["dim"], is_mla=mla)
-        cl = KVCacheLayout(KVCacheLayoutType.BLOCKWISE, L, w["nh"], w["tokens"], w["heads"],
+        cl = KVCacheLayout(KVCacheLayoutType[host_layout], L, w["nh"], w["tokens"], w["heads"],
                            w["dim"], is_mla=mla)
+        self.cl = cl
         self.chunk, self.gkv, _, self.gblk = gl.div_layer(L).byte_strides(self.dtype)
         _, self.ckv, self.clay, self.cblk = cl.byte_strides(self.dtype)
         self.mla = mla
@@ -119,20 +121,36 @@ class Workload:
         want = torch.stack([t[:, g] for t in self.layers], dim=1)
         return want.permute(2, 1, 0, *range(3, want.dim())).reshape(-1).contiguous()
 
+    def host_rows(self, ids: torch.Tensor) -> torch.Tensor:
+        """Host blocks `ids` as int16 rows [n, layers, kv, chunk], any layout."""
+        L, kv, nh = self.w["layers"], self.w["kv"], self.w["nh"]
+        ce = self.chunk // 2
+        h = self.host.view(torch.int16)
+        if self.cl.type.name == "BLOCKWISE":
+            return h.view(nh, L, kv, ce)[ids]
+        return h.view(L, kv, nh, ce)[:, :, ids].permute(2, 0, 1, 3)
+
+    def set_host_rows(self, ids: torch.Tensor, rows: torch.Tensor) -> None:
+        L, kv, nh = self.w["layers"], self.w["kv"], self.w["nh"]
+        ce = self.chunk // 2
+        h = self.host.view(torch.int16)
+        if self.cl.type.name == "BLOCKWISE":
+            h.view(nh, L, kv, ce)[ids] = rows
+        else:
+            h.view(L, kv, nh, ce)[:, :, ids] = rows.permute(1, 2, 0, 3)
+
     def check(self) -> bool:
-        """Every moved block: host block row == the GPU blocks, bit for bit."""
+        """Every moved block: host block == the GPU blocks, bit for bit."""
         L, kv = self.w["layers"], self.w["kv"]
-        row = L * kv * self.chunk // 2
-        hv = self.host.view(self.w["nh"], row)
         ok = True
         step = 128
         for s in range(0, len(self.gids), step):
             g = self.gids[s:s + step].to(self.dev)
             c = self.cids[s:s + step]
-            want = torch.stack([t[:, g] for t in self.layers], dim=1)  # [kv, b, ...] per layer
-            want = want.permute(2, 1, 0, *range(3, want.dim())).reshape(len(c), row)
-            got = hv[c].to(self.dev)
-            ok &= bool(torch.equal(got.view(torch.int16), want.view(torch.int16)))
+            want = torch.stack([t[:, g] for t in self.layers], dim=1)  # [kv, L, b, ...]
+            want = want.permute(2, 1, 0, *range(3, want.dim())).reshape(len(c), L, kv, -1)
+            got = self.host_rows(c).to(self.dev)
+            ok &= bool(torch.equal(got, want.view(torch.int16)))
         return ok
 
 
@@ -294,8 +312,7 @@ def engine_layerwise(wl: Workload, steps: int):
     L = w["layers"]
     gl = KVCacheLayout(KVCacheLayoutType.LAYERWISE, L, w["ng"], w["tokens"], w["heads"],
                        w["dim"], is_mla=wl.mla)
-    cl = KVCacheLayout(KVCacheLayoutType.BLOCKWISE, L, w["nh"], w["tokens"], w["heads"],
-                       w["dim"], is_mla=wl.mla)
+    cl = wl.cl
     gpu_h = StorageHandle(AccessHandleType.TENSOR, wl.layers, gl, wl.dtype, gpu_device_id=0)
     cpu_h = StorageHandle(AccessHandleType.TENSOR, wl.host, cl, wl.dtype)
     mc = ModelConfig(num_layers=L, num_kv_heads=w["heads"], head_size=w["dim"],
@@ -472,15 +489,15 @@ def ssd_tier(wl: Workload, max_bytes: int = 1 << 30):
                 parts = line.split()
                 if len(parts) > 2 and d.startswith(parts[1]) and len(parts[1]) >= len(best):
                     best, fs = parts[1], parts[2]
-        mk = lambda nb: KVCacheLayout(KVCacheLayoutType.BLOCKWISE, L, nb, w["tokens"],
+        mk = lambda nb: KVCacheLayout(wl.cl.type, L, nb, w["tokens"],
                                       w["heads"], w["dim"], is_mla=wl.mla)
         ssd_lay = mk(n)
         h = SSDAllocator.allocate(ssd_lay, wl.dtype, cache_dir=[d], max_blocks_per_file=n)
         worker = CPUSSDDiskTransferWorker(0, None, None, wl.host, h.get_file_list(),
                                           mk(w["nh"]), ssd_lay, wl.dtype, h.num_blocks_per_file,
                                           CacheConfig())
-        hv = wl.host.view(w["nh"], row // 2).view(torch.int16)
-        hv[:n] = hv[wl.cids[:n]]
+        first = torch.arange(n)
+        wl.set_host_rows(first, wl.host_rows(wl.cids[:n]))
         src = np.arange(n, dtype=np.int64)
         sids = np.arange(n, dtype=np.int64)
         rnd = (2 * n + torch.randperm(w["nh"] - 2 * n,
@@ -503,8 +520,9 @@ def ssd_tier(wl: Workload, max_bytes: int = 1 << 30):
         worker._transfer_impl(sids, run, TransferType.DISK2H, 0, L)
         t_run = time.perf_counter() - t0
         worker.close()
-        ok = bool(torch.equal(hv[torch.from_numpy(rnd)], hv[:n]) and
-                  torch.equal(hv[n:2 * n], hv[:n]))
+        written = wl.host_rows(first)
+        ok = bool(torch.equal(wl.host_rows(torch.from_numpy(rnd)), written) and
+                  torch.equal(wl.host_rows(torch.arange(n, 2 * n)), written))
         gb = n * row / 1e9
         return {"blocks": n, "bytes": n * row, "fs": fs,
                 "write_gbps_buffered": round(gb / t_write, 3),
@@ -603,6 +621,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="llama3-8b", choices=sorted(WORKLOADS))
     ap.add_argument("--run", type=int, default=0, help="contiguous id runs of this length")
+    ap.add_argument("--host-layout", default="BLOCKWISE", choices=["BLOCKWISE", "LAYERWISE"],
+                    help="host cache layout (the reference's CacheConfig default is LAYERWISE)")
     ap.add_argument("--path", default=None, choices=["kernel", "ce"],
                     help="D2H/H2D path reported as value (default: the product default)")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
@@ -630,7 +650,7 @@ def main() -> int:
         return counters_pass(args)
     cfg = CacheConfig()
     default_ce = {"kernel": False, "ce": True}[args.path] if args.path else cfg.use_ce_transfer_d2h
-    wl = Workload(args.workload, args.seed, args.run)
+    wl = Workload(args.workload, args.seed, args.run, host_layout=args.host_layout)
     gb = wl.bytes_per_op / 1e9
 
     # primary: D2H on the default path, library kernel timing on
@@ -693,7 +713,11 @@ def main() -> int:
         "data": "synthetic: KV values ~N(0,1) bf16 from torch's seeded device generator; "
                 "block ids from a seeded permutation",
         "config": {"workload": WORKLOADS[args.workload]["desc"] +
-                   (f"; ids in contiguous runs of {args.run}" if args.run else ""),
+                   (f"; ids in contiguous runs of {args.run}" if args.run else "") +
+                   ("; layer-wise host cache [32,2,16384,16,8,128]"
+                    if args.host_layout == "LAYERWISE" and args.workload == "llama3-8b" else
+                    f"; {args.host_layout.lower()} host cache"
+                    if args.host_layout != "BLOCKWISE" else ""),
                    "direction": "D2H", "path": "ce" if default_ce else "kernel",
                    "bytes_per_step": wl.bytes_per_op},
         "d2h": {"gbps": round(gb / d2h_s, 3), "median_ms": round(d2h_med * 1e3, 3),
