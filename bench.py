@@ -709,7 +709,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "u8",   # a byte copy: no arithmetic on the values, which are bf16
         "data": "synthetic: KV values ~N(0,1) bf16 from torch's seeded device generator; "
                 "block ids from a seeded permutation",
         "config": {"workload": WORKLOADS[args.workload]["desc"] +
@@ -719,6 +719,7 @@ def main() -> int:
                     f"; {args.host_layout.lower()} host cache"
                     if args.host_layout != "BLOCKWISE" else ""),
                    "direction": "D2H", "path": "ce" if default_ce else "kernel",
+                   "element_dtype": "bf16",
                    "bytes_per_step": wl.bytes_per_op},
         "d2h": {"gbps": round(gb / d2h_s, 3), "median_ms": round(d2h_med * 1e3, 3),
                 "best_ms": round(d2h_best * 1e3, 3),
