@@ -456,3 +456,38 @@ def test_engine_rejects_ssd_in_process_mode(tmp_path):
     with pytest.raises(NotImplementedError):
         TransferEngine([h], ModelConfig(1, 1, 8), CacheConfig(), cpu_handle=h, ssd_handle=h,
                        worker_mode="process")
+
+
+# ------------------------------------------------------------ randomized
+
+from hypothesis import HealthCheck, given, settings, strategies as st  # noqa: E402
+
+
+@settings(max_examples=25, deadline=None, suppress_health_check=[HealthCheck.function_scoped_fixture])
+@given(layout=st.sampled_from([LW, BW]), mla=st.booleans(), n_dev=st.integers(1, 3),
+       mbpf=st.sampled_from([-1, 3, 5, 16]), tpb=st.sampled_from([1, 4, 16]),
+       dh=st.sampled_from([8, 64, 72]), start=st.integers(0, 2), seed=st.integers(0, 10**6))
+def test_random_geometries_match_oracle(tmp_path_factory, layout, mla, n_dev, mbpf, tpb, dh,
+                                        start, seed):
+    """Random layouts, devices, files per device, chunk sizes (some not
+    page multiples), layer windows and id lists: files and host cache equal
+    the oracle's after a write and a read."""
+    tmp = tmp_path_factory.mktemp("ssd")
+    L = 3
+    c = _product_case(tmp, layout, mla, n_dev, mbpf, tpb, 1, dh, L=L, N_cpu=24,
+                      n_ssd=12 * n_dev, seed=seed % 997)
+    g = np.random.default_rng(seed)
+    n = int(g.integers(1, 12))
+    sids = g.permutation(c["ssd"].num_block)[:n].astype(np.int64)
+    cids = g.permutation(c["cpu"].num_block)[:n].astype(np.int64)
+    nl = int(g.integers(1, L - start + 1))
+    images = _file_images(c["files"], c["used"])
+    _oracle_mirror(c, images, c["host"], sids, cids, start, nl, is_read=False)
+    c["worker"]._transfer_impl(cids, sids, TransferType.H2DISK, start, nl)
+    assert all(np.array_equal(a, b) for a, b in zip(_file_images(c["files"], c["used"]), images))
+    dst = g.permutation(c["cpu"].num_block)[:n].astype(np.int64)
+    expect = c["host"].copy()
+    _oracle_mirror(c, images, expect, sids, dst, start, nl, is_read=True)
+    c["worker"]._transfer_impl(sids, dst, TransferType.DISK2H, start, nl)
+    assert np.array_equal(c["host"], expect)
+    c["worker"].close()

@@ -528,3 +528,28 @@ def test_gather_scatter_match_oracle(dev, geo, buffer_on_host):
                               use_ce_transfer=True, is_mla=kv == 1)
     for x, e in zip(layers, exp):
         assert np.array_equal(to_numpy(x, np.uint16), e)
+
+
+from hypothesis import HealthCheck, given, settings, strategies as st  # noqa: E402
+
+
+@settings(max_examples=30, deadline=None, derandomize=True,
+          suppress_health_check=[HealthCheck.function_scoped_fixture])
+@given(layout=st.sampled_from(["BLOCKWISE", "LAYERWISE"]), kv=st.sampled_from([1, 2]),
+       lt=st.integers(1, 6), tokens=st.sampled_from([1, 2, 16]), heads=st.sampled_from([1, 3]),
+       dim=st.sampled_from([8, 64, 72, 128]), tp=st.sampled_from([1, 2]), mode=st.sampled_from(MODES),
+       seed=st.integers(0, 10**6))
+def test_random_geometries_match_oracle(dev, layout, kv, lt, tokens, heads, dim, tp, mode, seed):
+    """Seeded random geometries (layouts, MLA, layer windows, TP host chunks,
+    chunk sizes from 16 B up, block counts) in every mode, against the oracle."""
+    g = np.random.default_rng(seed)
+    nl = int(g.integers(1, lt + 1))
+    st_l = int(g.integers(0, lt - nl + 1))
+    ng, nh = int(g.integers(4, 60)), int(g.integers(4, 60))
+    n = int(g.integers(1, min(ng, nh) + 1))
+    case = KVCase(layers_total=lt, num_layers=nl, start_layer=st_l, kv=kv, ng=ng, nh=nh,
+                  tokens=tokens, heads=heads, dim=dim, layout=layout, tp=tp,
+                  rank=int(g.integers(0, tp))).fill(seed=seed % 9973)
+    gids = inputs.distinct_ids(seed % 7919 + 1, n, ng)
+    cids = inputs.distinct_ids(seed % 7907 + 2, n, nh)
+    check_case(case, gids, cids, mode)
