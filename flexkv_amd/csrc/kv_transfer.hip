@@ -712,6 +712,7 @@ int stream_device(hipStream_t s, int* dev) {
 // allocations.
 struct HsaApi {
   decltype(&::hsa_iterate_agents) iterate_agents = nullptr;
+  decltype(&::hsa_amd_pointer_info) pointer_info = nullptr;
   decltype(&::hsa_agent_get_info) agent_get_info = nullptr;
   decltype(&::hsa_status_string) status_string = nullptr;
   decltype(&::hsa_signal_create) signal_create = nullptr;
@@ -822,16 +823,11 @@ int sdma_engines_wanted() {
 std::mutex g_hsa_mu;
 bool g_hsa_loaded = false;
 
-hsa_status_t count_agent(hsa_agent_t, void* n) {
-  ++*static_cast<int*>(n);
-  return HSA_STATUS_SUCCESS;
-}
-
-// The HSA runtime behind HIP is the mapped copy that is initialised: a
-// process can map a second, idle copy (a wheel's bundled runtime next to the
-// system one a profiling tool preloaded), and which one HIP bound to depends
-// on load order.
-int load_hsa() {
+// The HSA runtime behind HIP is the mapped copy that knows `hip_ptr`, a
+// device allocation HIP made: a process can map a second copy (a wheel's
+// bundled runtime next to the system one a profiling tool preloaded), and
+// which one HIP bound to depends on load order.
+int load_hsa(const void* hip_ptr) {
   std::lock_guard<std::mutex> lk(g_hsa_mu);
   if (g_hsa_loaded) return 0;
   std::vector<std::string> paths;
@@ -850,15 +846,18 @@ int load_hsa() {
   for (const std::string& path : paths) {
     void* h = dlopen(path.c_str(), RTLD_NOW | RTLD_NOLOAD);
     if (!h) continue;
-    auto iterate = reinterpret_cast<decltype(&::hsa_iterate_agents)>(dlsym(h, "hsa_iterate_agents"));
-    int n = 0;
-    if (iterate && iterate(count_agent, &n) == HSA_STATUS_SUCCESS && n > 0) {
+    auto info = reinterpret_cast<decltype(&::hsa_amd_pointer_info)>(dlsym(h, "hsa_amd_pointer_info"));
+    hsa_amd_pointer_info_t pi;
+    memset(&pi, 0, sizeof(pi));
+    pi.size = sizeof(pi);
+    if (info && info(hip_ptr, &pi, nullptr, nullptr, nullptr) == HSA_STATUS_SUCCESS &&
+        pi.type != HSA_EXT_POINTER_TYPE_UNKNOWN) {
       lib = h;
       break;
     }
     dlclose(h);
   }
-  if (!lib) return fail(kInval, "no initialised HSA runtime is mapped into the process");
+  if (!lib) return fail(kInval, "no HSA runtime mapped into the process knows HIP's allocations");
   HsaApi a;
   int missing = 0;
   auto sym = [&](auto& fn, const char* name) {
@@ -866,6 +865,7 @@ int load_hsa() {
     if (!fn) ++missing;
   };
   sym(a.iterate_agents, "hsa_iterate_agents");
+  sym(a.pointer_info, "hsa_amd_pointer_info");
   sym(a.agent_get_info, "hsa_agent_get_info");
   sym(a.status_string, "hsa_status_string");
   sym(a.signal_create, "hsa_signal_create");
@@ -879,30 +879,12 @@ int load_hsa() {
   return 0;
 }
 
-struct AgentSearch {
-  uint32_t bus = 0, device = 0, domain = 0;
-  bool found_gpu = false, found_cpu = false;
-  hsa_agent_t gpu{}, cpu{};
-};
-
-hsa_status_t find_agents(hsa_agent_t a, void* arg) {
-  auto* q = static_cast<AgentSearch*>(arg);
+hsa_status_t first_cpu_agent(hsa_agent_t a, void* out) {
   hsa_device_type_t t;
-  if (g_hsa.agent_get_info(a, HSA_AGENT_INFO_DEVICE, &t) != HSA_STATUS_SUCCESS)
-    return HSA_STATUS_SUCCESS;
-  if (t == HSA_DEVICE_TYPE_CPU && !q->found_cpu) {
-    q->cpu = a;
-    q->found_cpu = true;
-  } else if (t == HSA_DEVICE_TYPE_GPU && !q->found_gpu) {
-    uint32_t bdf = 0, domain = 0;
-    if (g_hsa.agent_get_info(a, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_BDFID), &bdf) !=
-        HSA_STATUS_SUCCESS)
-      return HSA_STATUS_SUCCESS;
-    (void)g_hsa.agent_get_info(a, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_DOMAIN), &domain);
-    if ((bdf >> 8) == q->bus && ((bdf >> 3) & 31) == q->device && domain == q->domain) {
-      q->gpu = a;
-      q->found_gpu = true;
-    }
+  if (g_hsa.agent_get_info(a, HSA_AGENT_INFO_DEVICE, &t) == HSA_STATUS_SUCCESS &&
+      t == HSA_DEVICE_TYPE_CPU) {
+    *static_cast<hsa_agent_t*>(out) = a;
+    return HSA_STATUS_INFO_BREAK;
   }
   return HSA_STATUS_SUCCESS;
 }
@@ -918,27 +900,30 @@ hsa_status_t find_agents(hsa_agent_t a, void* arg) {
   } while (0)
 
 // HSA agents and SDMA engines for the copy-engine path on device `dev`: the
-// GPU agent is the one on the same PCI bus/device/domain as the HIP device,
-// the host side uses the GPU's nearest CPU agent when the runtime reports one.
-int ensure_sdma(DeviceState& d, int dev) {
+// GPU agent is the owner of `hip_ptr` (a device allocation HIP made on
+// `dev`), the host side is the GPU's nearest CPU agent when the runtime
+// reports one, else the first CPU agent.
+int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr) {
   if (d.sdma_init) return 0;
-  if (int rc = load_hsa()) return rc;
-  AgentSearch q;
-  int bus = 0, device = 0, domain = 0;
-  FKV_HIP(hipDeviceGetAttribute(&bus, hipDeviceAttributePciBusId, dev));
-  FKV_HIP(hipDeviceGetAttribute(&device, hipDeviceAttributePciDeviceId, dev));
-  FKV_HIP(hipDeviceGetAttribute(&domain, hipDeviceAttributePciDomainID, dev));
-  q.bus = static_cast<uint32_t>(bus);
-  q.device = static_cast<uint32_t>(device);
-  q.domain = static_cast<uint32_t>(domain);
-  // load_hsa picked the runtime HIP initialised; no reference of our own.
-  FKV_HSA(g_hsa.iterate_agents(find_agents, &q));
-  if (!q.found_gpu || !q.found_cpu)
-    return fail(kInval, "no HSA agent matches HIP device %d (pci %04x:%02x:%02x)", dev, domain,
-                bus, device);
+  if (int rc = load_hsa(hip_ptr)) return rc;
+  hsa_amd_pointer_info_t pi;
+  memset(&pi, 0, sizeof(pi));
+  pi.size = sizeof(pi);
+  FKV_HSA(g_hsa.pointer_info(hip_ptr, &pi, nullptr, nullptr, nullptr));
+  hsa_device_type_t t;
+  if (pi.agentOwner.handle == 0 ||
+      g_hsa.agent_get_info(pi.agentOwner, HSA_AGENT_INFO_DEVICE, &t) != HSA_STATUS_SUCCESS ||
+      t != HSA_DEVICE_TYPE_GPU)
+    return fail(kInval, "no GPU agent owns the staging buffer of device %d", dev);
+  struct {
+    hsa_agent_t gpu, cpu;
+  } q{pi.agentOwner, {0}};
+  const hsa_status_t it = g_hsa.iterate_agents(first_cpu_agent, &q.cpu);
+  if ((it != HSA_STATUS_SUCCESS && it != HSA_STATUS_INFO_BREAK) || q.cpu.handle == 0)
+    return fail(kInval, "no CPU agent found for device %d", dev);
   hsa_agent_t nearest{};
   if (g_hsa.agent_get_info(q.gpu, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_NEAREST_CPU),
-                         &nearest) == HSA_STATUS_SUCCESS && nearest.handle != 0)
+                           &nearest) == HSA_STATUS_SUCCESS && nearest.handle != 0)
     q.cpu = nearest;
   const int want = sdma_engines_wanted();
   for (int dir = 0; dir < 2; ++dir) {
@@ -1030,7 +1015,6 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   DeviceGuard guard;
   int rc = guard.set(dev);
   if (rc) return rc;
-  if ((rc = ensure_sdma(d, dev))) return rc;
   char* ids_dev = nullptr;
   rc = pack_ids(g, &ids_dev);
   if (rc) return rc;
@@ -1044,6 +1028,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   const size_t row_bytes = static_cast<size_t>(nl_piece) * g.kv * g.chunk;
   rc = ensure_staging(d, row_bytes);
   if (rc) return rc;
+  if ((rc = ensure_sdma(d, dev, d.staging))) return rc;
   const size_t half = d.staging_bytes / 2;
   const int blocks_per_piece = static_cast<int>(std::max<size_t>(1, half / row_bytes));
   const int grid_cap = d.num_cus * (h2d ? d.occ_staged[1] : d.occ_staged[0]);
