@@ -30,6 +30,9 @@ import time
 
 import torch
 
+# per-op transfer logs of the workers would drown the bench's own lines
+os.environ.setdefault("FLEXKV_LOG_LEVEL", "WARNING")
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
