@@ -25,6 +25,7 @@ import argparse
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -175,6 +176,29 @@ def time_steps(fn, steps: int, warmup: int):
     torch.cuda.synchronize()
     total = time.perf_counter() - t_all
     return total / steps, statistics.median(times), min(times)
+
+
+def device_ceilings(timeout_s: float = 180.0):
+    """The device's plain HBM stream rates (read only, write only, copy) from
+    the hbm_ceiling program built beside the library, run as a child process
+    before this process touches the GPU.  None when the program is missing or
+    fails."""
+    exe = os.path.join(ROOT, "flexkv_amd", "hbm_ceiling")
+    if not os.path.exists(exe):
+        log("hbm_ceiling not built; device ceilings not measured")
+        return None
+    try:
+        res = subprocess.run([exe], capture_output=True, text=True, timeout=timeout_s)
+    except subprocess.TimeoutExpired:
+        log("hbm_ceiling timed out")
+        return None
+    if res.returncode != 0:
+        log(f"hbm_ceiling failed ({res.returncode}): {res.stderr.strip()[-300:]}")
+        return None
+    out = json.loads(res.stdout.strip().splitlines()[-1])
+    log(f"device ceilings: read {out['read_gbps']:.0f}, write {out['write_gbps']:.0f}, "
+        f"copy {out['copy_gbps']:.0f} GB/s")
+    return out
 
 
 def link_peaks(wl: Workload, reps: int = 8):
@@ -641,6 +665,7 @@ def main() -> int:
         print("bench.py measures one GPU: the transfer path is per-GPU (one PCIe link, one HBM); "
               "multi-GPU runs are out of scope for this build", file=sys.stderr)
         return 2
+    ceilings = None if (args.quick or args.counters) else device_ceilings()
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 2
@@ -743,7 +768,16 @@ def main() -> int:
                      "bytes_rule": "2 x moved bytes (scattered 32 KiB reads + packed writes)",
                      "traffic_source": "profiles/kv_gather_<workload>_counters.json",
                      "scatter": {"achieved": round(s_rate, 1), "frac": round(s_rate / HBM_PEAK_GBS, 4),
-                                 "avg_launch_ms": round(s_ms, 4)}},
+                                 "avg_launch_ms": round(s_ms, 4)},
+                     **({"device_ceilings": {
+                         "read_gbps": ceilings["read_gbps"], "write_gbps": ceilings["write_gbps"],
+                         "copy_gbps": ceilings["copy_gbps"],
+                         "gather_frac_of_copy": round(g_rate / ceilings["copy_gbps"], 4),
+                         "scatter_frac_of_copy": round(s_rate / ceilings["copy_gbps"], 4),
+                         "how": "flexkv_amd/hbm_ceiling: plain 16 B/lane read-only, write-only "
+                                "and copy kernels over 4 GiB, launch shapes swept, best of 10 "
+                                "launches each; rates count bytes read + bytes written"}}
+                        if ceilings else {})},
         "library_profile": {"d2h": prof_d2h, "h2d": prof_h2d, "gather": prof_g,
                             "scatter": prof_s},
     }

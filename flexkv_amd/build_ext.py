@@ -1,4 +1,6 @@
-"""Compile libflexkv_hip.so in-tree with hipcc for gfx950.
+"""Compile libflexkv_hip.so in-tree with hipcc for gfx950, and the
+hbm_ceiling program that measures the device's plain read / write / copy
+rates (bench.py reports them beside the gather's roofline).
 
     python -m flexkv_amd.build_ext
 """
@@ -13,6 +15,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SOURCES = [os.path.join(HERE, "csrc", "kv_transfer.hip"), os.path.join(HERE, "csrc", "kv_ssd.cpp")]
 OUT = os.path.join(HERE, "libflexkv_hip.so")
+CEILING_SOURCE = os.path.join(HERE, "csrc", "hbm_ceiling.hip")
+CEILING_OUT = os.path.join(HERE, "hbm_ceiling")
 ARCH = "gfx950"
 
 
@@ -23,24 +27,34 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
+# no packed fp32 instructions anywhere in device code
+COMMON = ["-O3", "-std=c++17", "-Wall", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
 def command() -> list:
     return [
-        hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared", "-Wall",
-        # no packed fp32 instructions anywhere in device code
-        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        hipcc(), f"--offload-arch={ARCH}", *COMMON, "-fPIC", "-shared",
         "-I", os.path.join(ROOT, "include"),
         *SOURCES, "-o", OUT + ".tmp", "-ldl",
     ]
 
 
-def build(verbose: bool = False) -> str:
-    cmd = command()
+def ceiling_command() -> list:
+    return [hipcc(), f"--offload-arch={ARCH}", *COMMON, CEILING_SOURCE, "-o", CEILING_OUT + ".tmp"]
+
+
+def _run(cmd: list, out: str, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
-    os.replace(OUT + ".tmp", OUT)
+    os.replace(out + ".tmp", out)
+
+
+def build(verbose: bool = False) -> str:
+    _run(command(), OUT, verbose)
+    _run(ceiling_command(), CEILING_OUT, verbose)
     return OUT
 
 

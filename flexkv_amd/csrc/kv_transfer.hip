@@ -722,7 +722,6 @@ struct HsaApi {
   decltype(&::hsa_amd_memory_async_copy_on_engine) async_copy_on_engine = nullptr;
 };
 HsaApi g_hsa;
-// Wait until a half's copies have finished (its signal counts down to 0).
 // Wait until every copy queued on a staging half has finished.  Each copy
 // has its own signal: a counted signal shared by many copies would depend on
 // every layer between here and the engines decrementing it by exactly one.
