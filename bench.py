@@ -480,15 +480,70 @@ def request_batch(wl: Workload, steps: int, num_requests: int = 32, max_blocks: 
     return out
 
 
+def disk_ceilings(d: str, nbytes: int):
+    """Sequential O_DIRECT rates of the file system under `d`: `nbytes` written
+    to one preallocated file (timed to the end of an fsync), then read back,
+    for a few (threads, request size) shapes; the best of each is the
+    ceiling the SSD tier is measured against."""
+    import mmap
+    from concurrent.futures import ThreadPoolExecutor
+
+    path = os.path.join(d, "ceiling.bin")
+    shapes = ((16, 8 << 20), (32, 1 << 20), (64, 1 << 20))
+    runs = []
+    try:
+        fd = os.open(path, os.O_RDWR | os.O_CREAT | os.O_DIRECT, 0o600)
+    except OSError as e:
+        return {"skipped": f"O_DIRECT open failed: {e}"}
+    try:
+        for threads, io in shapes:
+            nio = max(1, nbytes // io)
+            bufs = []
+            for _ in range(threads):
+                b = mmap.mmap(-1, io)          # page aligned, as O_DIRECT needs
+                b.write(os.urandom(io))
+                bufs.append(b)
+            try:
+                os.posix_fallocate(fd, 0, nio * io)
+                with ThreadPoolExecutor(max_workers=threads) as ex:
+                    t0 = time.perf_counter()
+                    list(ex.map(lambda i: os.pwritev(fd, [bufs[i % threads]], i * io),
+                                range(nio)))
+                    os.fsync(fd)
+                    t_w = time.perf_counter() - t0
+                    t0 = time.perf_counter()
+                    list(ex.map(lambda i: os.preadv(fd, [bufs[i % threads]], i * io),
+                                range(nio)))
+                    t_r = time.perf_counter() - t0
+            finally:
+                for b in bufs:
+                    b.close()
+            gb = nio * io / 1e9
+            runs.append({"threads": threads, "request_mib": io >> 20,
+                         "write_gbps_with_fsync": round(gb / t_w, 3),
+                         "read_gbps": round(gb / t_r, 3)})
+    except OSError as e:
+        return {"skipped": f"O_DIRECT I/O failed: {e}"}
+    finally:
+        os.close(fd)
+        os.unlink(path)
+    return {"seq_write_gbps_with_fsync": max(r["write_gbps_with_fsync"] for r in runs),
+            "seq_read_gbps": max(r["read_gbps"] for r in runs),
+            "how": f"O_DIRECT over {nbytes / 1e9:.2f} GB, best of the shapes in runs",
+            "runs": runs}
+
+
 def ssd_tier(wl: Workload, max_bytes: int = 1 << 30):
     """Host cache <-> SSD files for about 1 GiB of blocks: the rows the last
     D2H left in the host cache are copied to host blocks [0, n), written to
     SSD slots [0, n) (buffered writes, then fsync), read back into n random
     host blocks (one request per block) and into host blocks [n, 2n)
     (consecutive blocks merge into large requests); both reads are compared
-    with the written rows bit for bit.  O_DIRECT reads when the chunk is a
+    with the written rows bit for bit.  Run once with the threads engine and
+    once with a 256-deep io_uring ring.  O_DIRECT reads when the chunk is a
     multiple of 4 KiB.  Files go to a temporary directory on this host's file
-    system and are removed after."""
+    system and are removed after; the file system's sequential O_DIRECT
+    rates are measured in the same directory."""
     import shutil
     import tempfile
 
@@ -520,45 +575,73 @@ def ssd_tier(wl: Workload, max_bytes: int = 1 << 30):
                                       w["heads"], w["dim"], is_mla=wl.mla)
         ssd_lay = mk(n)
         h = SSDAllocator.allocate(ssd_lay, wl.dtype, cache_dir=[d], max_blocks_per_file=n)
-        worker = CPUSSDDiskTransferWorker(0, None, None, wl.host, h.get_file_list(),
-                                          mk(w["nh"]), ssd_lay, wl.dtype, h.num_blocks_per_file,
-                                          CacheConfig())
         first = torch.arange(n)
-        wl.set_host_rows(first, wl.host_rows(wl.cids[:n]))
+        base = wl.host_rows(wl.cids[:n])
         src = np.arange(n, dtype=np.int64)
         sids = np.arange(n, dtype=np.int64)
         rnd = (2 * n + torch.randperm(w["nh"] - 2 * n,
                                       generator=torch.Generator().manual_seed(7))[:n]).numpy()
         rnd = rnd.astype(np.int64)
         run = np.arange(n, 2 * n, dtype=np.int64)
-        t0 = time.perf_counter()
-        worker._transfer_impl(src, sids, TransferType.H2DISK, 0, L)
-        t_write = time.perf_counter() - t0
-        for paths in h.get_file_list().values():
-            for pth in paths:
-                fd = os.open(pth, os.O_RDONLY)
-                os.fsync(fd)
-                os.close(fd)
-        t_sync = time.perf_counter() - t0
-        t0 = time.perf_counter()
-        worker._transfer_impl(sids, rnd, TransferType.DISK2H, 0, L)
-        t_rnd = time.perf_counter() - t0
-        t0 = time.perf_counter()
-        worker._transfer_impl(sids, run, TransferType.DISK2H, 0, L)
-        t_run = time.perf_counter() - t0
-        worker.close()
-        written = wl.host_rows(first)
-        ok = bool(torch.equal(wl.host_rows(torch.from_numpy(rnd)), written) and
-                  torch.equal(wl.host_rows(torch.arange(n, 2 * n)), written))
         gb = n * row / 1e9
-        return {"blocks": n, "bytes": n * row, "fs": fs,
-                "write_gbps_buffered": round(gb / t_write, 3),
-                "write_gbps_with_fsync": round(gb / t_sync, 3),
-                "read_gbps_random_host_blocks": round(gb / t_rnd, 3),
-                "read_gbps_consecutive_host_blocks": round(gb / t_run, 3),
-                "read_io": "O_DIRECT" if wl.chunk % 4096 == 0 else "buffered",
-                "bit_exact": ok,
-                "threads_per_device": CacheConfig().ssd_threads_per_device}
+
+        def engine(entries: int, salt: int):
+            # each engine writes rows of its own and reads into cleared blocks,
+            # so one engine's result cannot pass for another's
+            written = base ^ salt
+            wl.set_host_rows(first, written)
+            wl.set_host_rows(torch.from_numpy(rnd), torch.zeros_like(written))
+            wl.set_host_rows(torch.arange(n, 2 * n), torch.zeros_like(written))
+            cfg = CacheConfig(ssd_cache_iouring_entries=entries)
+            worker = CPUSSDDiskTransferWorker(0, None, None, wl.host, h.get_file_list(),
+                                              mk(w["nh"]), ssd_lay, wl.dtype,
+                                              h.num_blocks_per_file, cfg)
+            depth = worker.ioctx.iouring_depth
+            if entries and not depth:
+                worker.close()
+                return {"skipped": "the kernel refused an io_uring ring"}
+            t0 = time.perf_counter()
+            worker._transfer_impl(src, sids, TransferType.H2DISK, 0, L)
+            t_write = time.perf_counter() - t0
+            for paths in h.get_file_list().values():
+                for pth in paths:
+                    fd = os.open(pth, os.O_RDONLY)
+                    os.fsync(fd)
+                    os.close(fd)
+            t_sync = time.perf_counter() - t0
+            t0 = time.perf_counter()
+            worker._transfer_impl(sids, rnd, TransferType.DISK2H, 0, L)
+            t_rnd = time.perf_counter() - t0
+            t0 = time.perf_counter()
+            worker._transfer_impl(sids, run, TransferType.DISK2H, 0, L)
+            t_run = time.perf_counter() - t0
+            stats = worker.ioctx.stats()
+            worker.close()
+            ok = bool(torch.equal(wl.host_rows(torch.from_numpy(rnd)), written) and
+                      torch.equal(wl.host_rows(torch.arange(n, 2 * n)), written))
+            return {"write_gbps_buffered": round(gb / t_write, 3),
+                    "write_gbps_with_fsync": round(gb / t_sync, 3),
+                    "read_gbps_random_host_blocks": round(gb / t_rnd, 3),
+                    "read_gbps_consecutive_host_blocks": round(gb / t_run, 3),
+                    "bit_exact": ok,
+                    "io_counters": stats,
+                    **({"iouring_depth": depth} if depth else
+                       {"threads_per_device": cfg.ssd_threads_per_device})}
+
+        threads = engine(0, 0x1111)
+        uring = engine(256, 0x2222)
+        disk = disk_ceilings(d, n * row)
+        out = {"blocks": n, "bytes": n * row, "fs": fs,
+               "read_io": ("O_DIRECT into page-aligned bounce buffers, then copied to the "
+                           "pinned host cache" if wl.chunk % 4096 == 0 else "buffered"),
+               "threads": threads, "io_uring": uring, "disk": disk,
+               "bit_exact": threads["bit_exact"] and uring.get("bit_exact", True)}
+        if "seq_read_gbps" in disk:
+            out["read_frac_of_disk_seq"] = {
+                name: {k: round(r[f"read_gbps_{k}_host_blocks"] / disk["seq_read_gbps"], 4)
+                       for k in ("random", "consecutive")}
+                for name, r in (("threads", threads), ("io_uring", uring)) if "bit_exact" in r}
+        return out
     finally:
         shutil.rmtree(d, ignore_errors=True)
 

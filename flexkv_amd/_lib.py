@@ -40,6 +40,8 @@ EXPORTED_SYMBOLS = (
     "fkv_stream_create",
     "fkv_stream_destroy",
     "fkv_ssd_open",
+    "fkv_ssd_iouring_depth",
+    "fkv_ssd_stats_read",
     "fkv_ssd_close",
     "fkv_transfer_kv_blocks_ssd",
     "fkv_last_error",
@@ -64,6 +66,21 @@ class FkvProfile(ctypes.Structure):
         ("dma_copies", ctypes.c_int64),
         ("dma_ms", ctypes.c_double),
         ("dma_bytes", ctypes.c_int64),
+    ]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+class SsdStats(ctypes.Structure):
+    """fkv_ssd_stats: cumulative I/O counters of an SSD handle."""
+    _fields_ = [
+        ("direct_read_bytes", ctypes.c_int64),
+        ("buffered_read_bytes", ctypes.c_int64),
+        ("write_bytes", ctypes.c_int64),
+        ("requests", ctypes.c_int64),
+        ("ring_entries", ctypes.c_int64),
+        ("fallbacks", ctypes.c_int64),
     ]
 
     def as_dict(self) -> dict:
@@ -103,8 +120,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.fkv_stream_destroy.restype = c_int
     lib.fkv_stream_destroy.argtypes = [c_vp]
     lib.fkv_ssd_open.restype = c_int
-    lib.fkv_ssd_open.argtypes = [ctypes.POINTER(ctypes.c_char_p), c_int, c_int,
+    lib.fkv_ssd_open.argtypes = [ctypes.POINTER(ctypes.c_char_p), c_int, c_int, c_int, c_int,
                                  ctypes.POINTER(c_vp)]
+    lib.fkv_ssd_iouring_depth.restype = c_int
+    lib.fkv_ssd_iouring_depth.argtypes = [c_vp]
+    lib.fkv_ssd_stats_read.restype = c_int
+    lib.fkv_ssd_stats_read.argtypes = [c_vp, ctypes.POINTER(SsdStats)]
     lib.fkv_ssd_close.restype = c_int
     lib.fkv_ssd_close.argtypes = [c_vp]
     f = lib.fkv_transfer_kv_blocks_ssd

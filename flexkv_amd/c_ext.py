@@ -296,9 +296,12 @@ class SSDIOCTX:
     """Open SSD cache files (csrc/transfer_ssd.h:174-204, bound at
     csrc/bindings.cpp:141-142): ``ssd_files`` maps device index -> file paths,
     every device holding the same number of files.  Each file is opened for
-    buffered I/O and, where the file system allows it, O_DIRECT reads.  The
-    io_uring arguments are accepted for interface parity; I/O is done with
-    pread/pwrite on worker threads."""
+    buffered I/O and, where the file system allows it, O_DIRECT reads.
+    ``iouring_entries > 0`` asks for an io_uring ring of that depth (created
+    with ``iouring_flags``) that then carries every transfer on this context;
+    when the kernel refuses the ring, transfers run pread/pwrite on threads,
+    as in the reference (csrc/transfer_ssd.h:19-28).  ``iouring_depth`` is the
+    ring's depth, 0 on threads."""
 
     def __init__(self, ssd_files, num_devices: int, iouring_entries: int = 0,
                  iouring_flags: int = 0) -> None:
@@ -315,12 +318,29 @@ class SSDIOCTX:
         arr = (ctypes.c_char_p * len(paths))(*paths)
         out = ctypes.c_void_p()
         lib = _lib.load()
-        rc = lib.fkv_ssd_open(arr, int(num_devices), int(per), ctypes.byref(out))
+        if iouring_entries < 0:
+            raise ValueError("iouring_entries must be >= 0")
+        rc = lib.fkv_ssd_open(arr, int(num_devices), int(per), int(iouring_entries),
+                              int(iouring_flags), ctypes.byref(out))
         if rc != 0:
             raise RuntimeError(_lib.last_error() or "Failed to open file")
         self._h = out.value
         self.num_devices = num_devices
         self.num_files_per_device = per
+        self.iouring_depth = int(lib.fkv_ssd_iouring_depth(self._h))
+
+    def stats(self) -> dict:
+        """Cumulative I/O counters since the context was opened: bytes read
+        with O_DIRECT, bytes read through the page cache, bytes written, file
+        requests, io_uring entries and blocking retries."""
+        import ctypes
+
+        if self._h is None:
+            raise RuntimeError("SSD context is closed")
+        out = _lib.SsdStats()
+        if _lib.load().fkv_ssd_stats_read(self._h, ctypes.byref(out)) != 0:
+            raise RuntimeError(_lib.last_error())
+        return out.as_dict()
 
     def close(self) -> None:
         h, self._h = self._h, None

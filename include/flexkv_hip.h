@@ -185,11 +185,42 @@ int fkv_stream_destroy(fkv_stream_t s);
  * in_file*block_stride + l*ssd_layer_stride + k*ssd_kv_stride in the file and
  * at cpu_id*block_stride + l*cpu_layer_stride + k*cpu_kv_stride in host
  * memory.  Layers [start_layer, start_layer + num_layers) move.  Reads use
- * O_DIRECT when chunk_size is a multiple of 4096 and the buffer is aligned.
+ * O_DIRECT when chunk_size is a multiple of 4096, into page-aligned bounce
+ * buffers that are then copied to host memory.
+ * Chunks adjacent in both the file and host memory merge into one request of
+ * at most FLEXKV_SSD_MAX_REQUEST_BYTES (default and maximum 1 GiB).
  * Synchronous; returns 0 or 1 with fkv_last_error() set. */
 typedef struct fkv_ssd_s* fkv_ssd_t;
+/* iouring_entries / iouring_flags are the reference's SSDIOCTX arguments
+ * (csrc/transfer_ssd.h:177-178, CacheConfig.ssd_cache_iouring_entries/_flags):
+ * entries > 0 asks for an io_uring submission ring of that depth, created
+ * with io_uring_setup(entries, flags); every transfer on the handle then
+ * queues its requests on the ring from the calling thread (one caller at a
+ * time per handle) instead of fanning out over threads.  A ring the kernel
+ * refuses leaves the handle on threads, with a warning on stderr, as in the
+ * reference (transfer_ssd.h:19-28). */
 int fkv_ssd_open(const char* const* paths, int num_devices, int files_per_device,
-                 fkv_ssd_t* out);
+                 int iouring_entries, int iouring_flags, fkv_ssd_t* out);
+/* Depth of the handle's io_uring ring, 0 when transfers use threads (no ring
+ * asked for, or the kernel refused it), -1 for a null handle
+ * (IOUring::enabled, csrc/transfer_ssd.h:40). */
+int fkv_ssd_iouring_depth(fkv_ssd_t h);
+/* Cumulative I/O counters of a handle since it was opened, in the spirit of
+ * the reference's IOUring::dump (csrc/transfer_ssd.h:124-134): bytes read
+ * with O_DIRECT (through the library's page-aligned bounce buffers; O_DIRECT
+ * cannot target HIP-pinned host memory), bytes read through the page cache,
+ * bytes written, file requests after merging, io_uring entries completed,
+ * and requests or ring entries redone with blocking page-cache I/O after
+ * O_DIRECT or the ring could not complete them. */
+typedef struct {
+  int64_t direct_read_bytes;
+  int64_t buffered_read_bytes;
+  int64_t write_bytes;
+  int64_t requests;
+  int64_t ring_entries;
+  int64_t fallbacks;
+} fkv_ssd_stats;
+int fkv_ssd_stats_read(fkv_ssd_t h, fkv_ssd_stats* out);
 int fkv_ssd_close(fkv_ssd_t h);
 int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, void* cpu_ptr,
                                const int64_t* ssd_block_ids, const int64_t* cpu_block_ids,

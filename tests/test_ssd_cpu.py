@@ -30,6 +30,24 @@ from flexkv_amd.transfer.worker import CPUSSDDiskTransferWorker
 LW, BW = KVCacheLayoutType.LAYERWISE, KVCacheLayoutType.BLOCKWISE
 
 
+def _uring_available():
+    """Whether this kernel gives an unprivileged process an io_uring ring."""
+    import ctypes
+    import platform
+    if platform.machine() != "x86_64":
+        return False
+    libc = ctypes.CDLL(None, use_errno=True)
+    params = (ctypes.c_uint32 * 30)()          # struct io_uring_params is 120 bytes
+    fd = libc.syscall(425, 4, ctypes.byref(params))   # __NR_io_uring_setup
+    if fd < 0:
+        return False
+    os.close(fd)
+    return True
+
+
+URING = _uring_available()
+
+
 def _rng_bytes(n, seed):
     return np.random.default_rng(seed).integers(0, 256, size=n, dtype=np.uint8)
 
@@ -163,8 +181,12 @@ def test_oracle_write_read_round_trip(layout_type, mla):
 
 # ----------------------------------------------------------- product vs oracle
 
+ENGINES = {"threads": 0, "uring64": 64, "uring2": 2}
+
+
 def _product_case(tmp_path, layout_type, mla, n_dev, max_blocks_per_file, tpb, H, Dh,
-                  L=4, N_cpu=40, n_ssd=48, dtype=torch.float16, seed=0):
+                  L=4, N_cpu=40, n_ssd=48, dtype=torch.float16, seed=0, engine="threads",
+                  iouring_flags=0):
     dirs = [str(tmp_path / f"dev{d}") for d in range(n_dev)]
     cpu_lay = KVCacheLayout(layout_type, L, N_cpu, tpb, H, Dh, is_mla=mla)
     ssd_lay = KVCacheLayout(layout_type, L, n_ssd, tpb, H, Dh, is_mla=mla)
@@ -187,9 +209,13 @@ def _product_case(tmp_path, layout_type, mla, n_dev, max_blocks_per_file, tpb, H
         for j, p in enumerate(paths):
             with open(p, "r+b") as f:
                 f.write(_rng_bytes(min(used, os.path.getsize(p)), 1000 + 10 * d + j).tobytes())
+    cfg = CacheConfig(ssd_threads_per_device=4, ssd_cache_iouring_entries=ENGINES[engine],
+                      ssd_cache_iouring_flags=iouring_flags)
     worker = CPUSSDDiskTransferWorker(0, None, None, torch.from_numpy(host), files, cpu_lay,
-                                      ssd_lay, dtype, h.num_blocks_per_file,
-                                      CacheConfig(ssd_threads_per_device=4))
+                                      ssd_lay, dtype, h.num_blocks_per_file, cfg)
+    if ENGINES[engine] and iouring_flags == 0 and URING:
+        # the ring this test asked for is the one that carries the transfers
+        assert worker.ioctx.iouring_depth >= ENGINES[engine]
     return dict(host=host, files=files, worker=worker, cpu=cpu_lay, ssd=ssd_lay, es=es,
                 n_dev=n_dev, F=len(files[0]), raw=raw, used=used)
 
@@ -222,9 +248,11 @@ GEOMS = [
 @pytest.mark.parametrize("geom", GEOMS, ids=lambda g: f"{g[0].name}-mla{int(g[1])}-d{g[2]}"
                          f"-f{g[3]}-{g[4]}x{g[5]}x{g[6]}")
 @pytest.mark.parametrize("window", [(0, -1), (1, 2)], ids=["all", "l1+2"])
-def test_product_matches_oracle(tmp_path, geom, window):
+@pytest.mark.parametrize("engine", list(ENGINES))
+def test_product_matches_oracle(tmp_path, geom, window, engine):
     layout, mla, n_dev, mbpf, tpb, H, Dh = geom
-    c = _product_case(tmp_path, layout, mla, n_dev, mbpf, tpb, H, Dh, seed=hash(geom) & 0xffff)
+    c = _product_case(tmp_path, layout, mla, n_dev, mbpf, tpb, H, Dh, seed=hash(geom) & 0xffff,
+                      engine=engine)
     start, nl = window
     nl = c["cpu"].num_layer if nl == -1 else nl
     g = np.random.default_rng(11)
@@ -249,11 +277,17 @@ def test_product_matches_oracle(tmp_path, geom, window):
 
 @pytest.mark.parametrize("geom", GEOMS, ids=lambda g: f"{g[0].name}-mla{int(g[1])}-d{g[2]}"
                          f"-f{g[3]}-{g[4]}x{g[5]}x{g[6]}")
-def test_contiguous_runs_match_oracle(tmp_path, geom):
+@pytest.mark.parametrize("engine,max_request", [("threads", None), ("uring64", None),
+                                                ("threads", 4096), ("uring2", 8192)])
+def test_contiguous_runs_match_oracle(tmp_path, monkeypatch, geom, engine, max_request):
     """Runs of consecutive SSD and host ids, where neighbouring chunks merge
-    into single requests: two runs plus a stray block, written then read."""
+    into single requests: two runs plus a stray block, written then read.
+    With a small FLEXKV_SSD_MAX_REQUEST_BYTES the merged runs (and chunks
+    larger than the cap) are cut into several requests."""
+    if max_request:
+        monkeypatch.setenv("FLEXKV_SSD_MAX_REQUEST_BYTES", str(max_request))
     layout, mla, n_dev, mbpf, tpb, H, Dh = geom
-    c = _product_case(tmp_path, layout, mla, n_dev, mbpf, tpb, H, Dh, seed=7)
+    c = _product_case(tmp_path, layout, mla, n_dev, mbpf, tpb, H, Dh, seed=7, engine=engine)
     sids = np.concatenate([np.arange(3, 19), np.arange(30, 41), [1]]).astype(np.int64)
     cids = np.concatenate([np.arange(10, 26), np.arange(27, 38), [39]]).astype(np.int64)
     for start, nl in ((0, c["cpu"].num_layer), (1, 2)):
@@ -298,8 +332,11 @@ def test_reference_worker_geometry(tmp_path):
     w.close()
 
 
-def test_unaligned_host_buffer_falls_back_to_buffered_io(tmp_path):
-    c = _product_case(tmp_path, BW, False, 1, -1, 16, 2, 64)
+@pytest.mark.parametrize("engine", ["threads", "uring64"])
+def test_unaligned_host_buffer_reads_exact(tmp_path, engine):
+    """Direct reads land in page-aligned bounce buffers, so a host cache that
+    is not page aligned reads the same bytes."""
+    c = _product_case(tmp_path, BW, False, 1, -1, 16, 2, 64, engine=engine)
     w = c["worker"]
     sids = np.array([1, 2, 3], np.int64)
     cids = np.array([4, 5, 6], np.int64)
@@ -320,6 +357,119 @@ def test_unaligned_host_buffer_falls_back_to_buffered_io(tmp_path):
     for s, ci in zip(sids, cids):
         assert np.array_equal(got[ci], f[s])
     w.close()
+
+
+# ------------------------------------------------------------ io_uring engine
+
+def test_iouring_depth_reported(tmp_path):
+    """iouring_entries = 0 keeps threads; a ring the kernel grants reports its
+    depth (setup rounds entries up to a power of two)."""
+    p = tmp_path / "f.bin"
+    p.write_bytes(b"\0" * 8192)
+    assert c_ext.SSDIOCTX({0: [str(p)]}, 1).iouring_depth == 0
+    ctx = c_ext.SSDIOCTX({0: [str(p)]}, 1, iouring_entries=24)
+    if URING:
+        assert ctx.iouring_depth == 32
+    else:
+        assert ctx.iouring_depth == 0
+    with pytest.raises(ValueError):
+        c_ext.SSDIOCTX({0: [str(p)]}, 1, iouring_entries=-1)
+
+
+def _o_direct_supported(path):
+    try:
+        fd = os.open(path, os.O_RDONLY | os.O_DIRECT)
+    except OSError:
+        return False
+    os.close(fd)
+    return True
+
+
+@pytest.mark.parametrize("engine", ["threads", "uring64", "uring2"])
+def test_stats_count_direct_reads(tmp_path, engine):
+    """Page-multiple chunks are read with O_DIRECT (through the bounce
+    buffers) wherever the file system allows it, with no page-cache retries;
+    the counters account for every byte moved."""
+    c = _product_case(tmp_path, BW, False, 2, -1, 16, 2, 64, engine=engine)
+    w = c["worker"]
+    # SSD ids 2, 4, 6 are consecutive slots of device 0's file (two devices,
+    # round robin 1) and go to consecutive host blocks: one request each way
+    # on the ring; the threads engine gives each of those blocks a thread of
+    # its own (4 threads per device), one request each
+    per_op = 2 if engine != "threads" and URING else 4
+    sids = np.array([2, 4, 6, 3], np.int64)
+    cids = np.array([10, 11, 12, 0], np.int64)
+    w._transfer_impl(cids, sids, TransferType.H2DISK, 0, 4)
+    moved = len(sids) * w.block_stride_in_bytes
+    st = w.ioctx.stats()
+    assert st["write_bytes"] == moved and st["fallbacks"] == 0
+    assert st["requests"] == per_op
+    w._transfer_impl(sids, cids + 13, TransferType.DISK2H, 0, 4)
+    st = w.ioctx.stats()
+    if _o_direct_supported(c["files"][0][0]):
+        assert st["direct_read_bytes"] == moved and st["buffered_read_bytes"] == 0
+    else:
+        assert st["buffered_read_bytes"] == moved
+    assert st["fallbacks"] == 0 and st["requests"] == 2 * per_op
+    if engine != "threads" and URING:
+        assert st["ring_entries"] >= st["requests"]
+    w.close()
+
+
+def test_iouring_refused_ring_falls_back_to_threads(tmp_path, capfd):
+    """A ring the kernel refuses (here: an undefined setup flag) leaves the
+    context on threads, with a warning, and transfers stay exact."""
+    c = _product_case(tmp_path, BW, False, 2, -1, 16, 2, 64, engine="uring64",
+                      iouring_flags=1 << 30)
+    assert c["worker"].ioctx.iouring_depth == 0
+    assert "io_uring setup" in capfd.readouterr().err
+    sids = np.array([5, 0, 9, 2], np.int64)
+    cids = np.array([1, 7, 3, 30], np.int64)
+    images = _file_images(c["files"], c["used"])
+    _oracle_mirror(c, images, c["host"], sids, cids, 0, 4, is_read=False)
+    c["worker"]._transfer_impl(cids, sids, TransferType.H2DISK, 0, 4)
+    assert all(np.array_equal(a, b) for a, b in zip(_file_images(c["files"], c["used"]), images))
+    c["worker"].close()
+
+
+@pytest.mark.skipif(not URING, reason="the kernel gives this process no io_uring ring")
+@pytest.mark.parametrize("flags", [1, 2], ids=["IOPOLL", "SQPOLL"])
+def test_iouring_setup_flags_match_oracle(tmp_path, flags):
+    """Rings set up for polled completions (IORING_SETUP_IOPOLL: page-cache
+    requests are refused by the kernel and redone with blocking I/O) and with
+    a kernel submission thread (IORING_SETUP_SQPOLL) move the same bytes as
+    the oracle, through writes and O_DIRECT-sized reads."""
+    c = _product_case(tmp_path, BW, False, 2, -1, 16, 2, 64, engine="uring64",
+                      iouring_flags=flags)
+    g = np.random.default_rng(flags)
+    sids = g.permutation(c["ssd"].num_block)[:13].astype(np.int64)
+    cids = g.permutation(c["cpu"].num_block)[:13].astype(np.int64)
+    images = _file_images(c["files"], c["used"])
+    _oracle_mirror(c, images, c["host"], sids, cids, 0, 4, is_read=False)
+    c["worker"]._transfer_impl(cids, sids, TransferType.H2DISK, 0, 4)
+    after = _file_images(c["files"], c["used"])
+    assert all(np.array_equal(a, b) for a, b in zip(after, images))
+    dst = g.permutation(c["cpu"].num_block)[:13].astype(np.int64)
+    expect = c["host"].copy()
+    _oracle_mirror(c, after, expect, sids, dst, 0, 4, is_read=True)
+    c["worker"]._transfer_impl(sids, dst, TransferType.DISK2H, 0, 4)
+    assert np.array_equal(c["host"], expect)
+    c["worker"].close()
+
+
+def test_iouring_read_past_end_of_file_reports_error(tmp_path):
+    """A ring read that meets the end of a file fails the call like the
+    threaded read does."""
+    p = tmp_path / "short.bin"
+    p.write_bytes(b"\1" * 4096)
+    ctx = c_ext.SSDIOCTX({0: [str(p)]}, 1, iouring_entries=8)
+    host = np.zeros(4 * 4096 + 4096, np.uint8)
+    with pytest.raises(RuntimeError, match="read failed|end of file"):
+        c_ext.transfer_kv_blocks_ssd(
+            ctx, torch.arange(0, 1, dtype=torch.int32), host.ctypes.data,
+            torch.tensor([3], dtype=torch.int64), torch.tensor([0], dtype=torch.int64),
+            4096, 4096, 4096, 4096, 4096, 4096, True, 4)
+    ctx.close()
 
 
 # ------------------------------------------------------------ error behaviour
@@ -466,16 +616,17 @@ from hypothesis import HealthCheck, given, settings, strategies as st  # noqa: E
 @settings(max_examples=25, deadline=None, suppress_health_check=[HealthCheck.function_scoped_fixture])
 @given(layout=st.sampled_from([LW, BW]), mla=st.booleans(), n_dev=st.integers(1, 3),
        mbpf=st.sampled_from([-1, 3, 5, 16]), tpb=st.sampled_from([1, 4, 16]),
-       dh=st.sampled_from([8, 64, 72]), start=st.integers(0, 2), seed=st.integers(0, 10**6))
+       dh=st.sampled_from([8, 64, 72]), start=st.integers(0, 2), seed=st.integers(0, 10**6),
+       engine=st.sampled_from(list(ENGINES)))
 def test_random_geometries_match_oracle(tmp_path_factory, layout, mla, n_dev, mbpf, tpb, dh,
-                                        start, seed):
+                                        start, seed, engine):
     """Random layouts, devices, files per device, chunk sizes (some not
     page multiples), layer windows and id lists: files and host cache equal
     the oracle's after a write and a read."""
     tmp = tmp_path_factory.mktemp("ssd")
     L = 3
     c = _product_case(tmp, layout, mla, n_dev, mbpf, tpb, 1, dh, L=L, N_cpu=24,
-                      n_ssd=12 * n_dev, seed=seed % 997)
+                      n_ssd=12 * n_dev, seed=seed % 997, engine=engine)
     g = np.random.default_rng(seed)
     n = int(g.integers(1, 12))
     sids = g.permutation(c["ssd"].num_block)[:n].astype(np.int64)
