@@ -60,7 +60,8 @@ class CacheConfig:
     # SSD cache: one directory per device; -1 = no per-file block limit
     max_blocks_per_file: int = 32000
     ssd_cache_dir: Optional[Union[str, List[str]]] = None
-    # accepted for interface parity (I/O uses pread/pwrite threads)
+    # io_uring ring depth for SSD transfers (0 = pread/pwrite threads) and
+    # the ring's io_uring_setup flags
     ssd_cache_iouring_entries: int = 0
     ssd_cache_iouring_flags: int = 0
     # threads per SSD device for one transfer (worker.py:573 uses 32)

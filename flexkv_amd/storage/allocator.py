@@ -129,8 +129,12 @@ class HostCacheSpec:
     layout: KVCacheLayout
     dtype: torch.dtype
     coherence: int = _lib.FKV_HOST_DEFAULT
+    # False: ordinary pageable memory (enough for a worker that only does file I/O)
+    pinned: bool = True
 
     def allocate(self) -> torch.Tensor:
+        if not self.pinned:
+            return torch.empty(self.layout.get_total_elements(), dtype=self.dtype)
         return pinned_empty(self.layout.get_total_elements(), self.dtype, self.coherence)
 
 

@@ -392,13 +392,16 @@ class CPUSSDDiskTransferWorker(TransferWorkerBase):
     type.  Host code only: it needs no device."""
 
     def __init__(self, worker_id: int, transfer_conn: Optional[Connection],
-                 finished_ops_queue: Optional[Any], cpu_blocks: torch.Tensor,
+                 finished_ops_queue: Optional[Any],
+                 cpu_blocks: Union[torch.Tensor, HostCacheSpec],
                  ssd_files: Dict[int, List[str]], cpu_kv_layout: KVCacheLayout,
                  ssd_kv_layout: KVCacheLayout, dtype: torch.dtype, num_blocks_per_file: int,
                  cache_config: Any = None) -> None:
         super().__init__(worker_id, transfer_conn, finished_ops_queue)
         if cpu_kv_layout.type != ssd_kv_layout.type:
             raise ValueError("no support for different CPU and SSD KV cache layout type")
+        if isinstance(cpu_blocks, HostCacheSpec):   # a worker in its own process
+            cpu_blocks = cpu_blocks.allocate()
         self.ssd_files = ssd_files
         self.num_blocks_per_file = num_blocks_per_file
         self.num_files = sum(len(v) for v in ssd_files.values())

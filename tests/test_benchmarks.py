@@ -1,0 +1,90 @@
+"""The worker benchmark with the reference's command line
+(flexkv_amd/benchmarks/benchmark_workers.py): config parsing, the SSD
+transfer types end to end through a spawned worker process (host code only),
+and, on a GPU, H2D / D2H through a spawned GPU worker on both paths."""
+import json
+
+import pytest
+import torch
+
+from flexkv_amd.benchmarks import benchmark_workers as bw
+from flexkv_amd.common.storage import KVCacheLayoutType
+from flexkv_amd.common.transfer import TransferType
+
+
+def _config(tmp_path, **cache):
+    cfg = {
+        "ModelConfig": {"num_layers": 4, "num_kv_heads": 2, "head_size": 64,
+                        "dtype": "float16", "use_mla": False, "tp_size": 1, "dp_size": 1},
+        "CacheConfig": {"tokens_per_block": 16, "cpu_kv_layout_type": "LAYERWISE",
+                        "ssd_kv_layout_type": "LAYERWISE", "num_cpu_blocks": 64,
+                        "num_ssd_blocks": 128, "use_pinned_memory": False,
+                        "ssd_cache_dir": str(tmp_path / "ssd"),
+                        # keys of parts this package does not have
+                        "enable_remote": False, "remote_cache_path": None,
+                        "enable_trace": False, "use_gds": False, **cache},
+    }
+    (tmp_path / "ssd").mkdir(exist_ok=True)
+    p = tmp_path / "cfg.json"
+    p.write_text(json.dumps(cfg))
+    return str(p)
+
+
+def test_example_config_parses():
+    args = bw.parse_args(["--transfer-type", "D2H", "--num-blocks", "64"])
+    model, cache, bench = bw.make_configs(args)
+    assert model.dtype == torch.bfloat16 and model.num_layers == 32
+    assert cache.cpu_kv_layout_type == KVCacheLayoutType.LAYERWISE
+    assert not cache.use_ce_transfer_d2h and cache.transfer_sms_d2h == 8
+    assert bench.transfer_type == TransferType.D2H and bench.num_blocks_to_transfer == 64
+
+
+def test_reference_style_keys_are_ignored_and_tp_refused(tmp_path):
+    args = bw.parse_args(["--config", _config(tmp_path)])
+    model, cache, _ = bw.make_configs(args)
+    assert model.dtype == torch.float16 and cache.num_ssd_blocks == 128
+    p = tmp_path / "tp.json"
+    cfg = json.loads(open(_config(tmp_path)).read())
+    cfg["ModelConfig"]["tp_size"] = 2
+    p.write_text(json.dumps(cfg))
+    with pytest.raises(ValueError, match="tp_size"):
+        bw.make_configs(bw.parse_args(["--config", str(p)]))
+
+
+@pytest.mark.parametrize("kind,shuffle,entries", [("H2DISK", False, 0), ("DISK2H", True, 0),
+                                                  ("DISK2H", False, 16)])
+def test_ssd_benchmark_runs(tmp_path, kind, shuffle, entries):
+    args = bw.parse_args(["--config", _config(tmp_path, ssd_cache_iouring_entries=entries),
+                          "--transfer-type", kind, "--num-blocks", "24",
+                          "--benchmark-round", "2"] + (["--shuffle-ids"] if shuffle else []))
+    res = bw.bench_worker(args)
+    # 24 blocks x 16 tokens x (4 layers x 2 heads x 64 x 2 (K,V) x 2 bytes)
+    assert res["bytes"] == 24 * 16 * 4 * 2 * 64 * 2 * 2
+    assert res["gb_per_s"] > 0 and res["path"] == "ssd"
+
+
+def test_unsupported_transfer_type(tmp_path):
+    with pytest.raises(ValueError, match="Unsupported transfer type"):
+        bw.bench_worker(bw.parse_args(["--config", _config(tmp_path),
+                                       "--transfer-type", "REMOTE2H"]))
+
+
+def test_more_blocks_than_the_cache_holds(tmp_path):
+    with pytest.raises(ValueError, match="exceeds"):
+        bw.bench_worker(bw.parse_args(["--config", _config(tmp_path), "--transfer-type",
+                                       "H2DISK", "--num-blocks", "65"]))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind,ce", [("D2H", False), ("H2D", False), ("D2H", True),
+                                     ("H2D", True)])
+def test_gpu_benchmark_runs(tmp_path, kind, ce):
+    """H2D / D2H through a spawned GPUCPUTransferWorker fed TensorSharedHandles,
+    on the zero-copy kernel and the copy-engine path."""
+    cfg = _config(tmp_path, use_pinned_memory=True, use_ce_transfer_h2d=ce,
+                  use_ce_transfer_d2h=ce)
+    res = bw.bench_worker(bw.parse_args(["--config", cfg, "--transfer-type", kind,
+                                         "--num-blocks", "48", "--shuffle-ids",
+                                         "--benchmark-round", "3"]))
+    assert res["bytes"] == 48 * 16 * 4 * 2 * 64 * 2 * 2
+    assert res["path"] == ("ce" if ce else "kernel") and res["gb_per_s"] > 0
