@@ -1,0 +1,239 @@
+// kv_internal.h - declarations shared by the library's translation units:
+// kv_transfer.hip (kernels and transfer paths), kv_host.cpp (errors, pointer
+// checks, validation, id staging, host-only entry points) and kv_sdma.cpp
+// (copy engines through HSA).  Not installed; not part of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <hsa/hsa.h>
+#include <hsa/hsa_ext_amd.h>
+
+#include <atomic>
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "flexkv_hip.h"
+#include "fkv_error.h"
+
+namespace fkv_detail {
+#pragma GCC visibility push(hidden)
+
+constexpr int kMaxLayersPerLaunch = 128;    // layer pointers in kernel args
+constexpr int kMaxDevices = 64;
+constexpr size_t kDefaultStagingBytes = size_t(256) << 20;
+constexpr int kInval = static_cast<int>(hipErrorInvalidValue);
+
+// Set the calling thread's error message; returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+#define FKV_HIP(call)                                                          \
+  do {                                                                         \
+    hipError_t e_ = (call);                                                    \
+    if (e_ != hipSuccess) {                                                    \
+      return ::fkv_detail::fail(static_cast<int>(e_), "%s failed: %s (%s:%d)", \
+                                #call, hipGetErrorString(e_), __FILE__,        \
+                                __LINE__);                                     \
+    }                                                                          \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Pointer classification and bounds
+
+struct PtrInfo {
+  bool host = false;     // pinned host memory
+  bool device = false;   // device memory
+  char* dev_ptr = nullptr;  // device-visible address of the queried pointer
+  char* base = nullptr;     // allocation start (host address space)
+  size_t size = 0;          // allocation size
+};
+
+// Returns 0 and fills `out` if p lies in memory known to the HIP runtime.
+int query_ptr(const void* p, PtrInfo* out);
+// [p + lo, p + hi) must lie inside the allocation described by info.
+bool range_inside(const char* p, __int128 lo, __int128 hi, const PtrInfo& info);
+
+// ---------------------------------------------------------------------------
+// Per-device state: staging buffer, copy engines, events, occupancy.
+
+struct DeviceState {
+  std::mutex mu;            // serialises copy-engine transfers on the device
+  bool init = false;
+  int num_cus = 0;
+  int occ_zero_copy[2] = {0, 0};
+  int occ_staged[2] = {0, 0};
+  char* staging = nullptr;
+  size_t staging_bytes = 0;
+  // Copy engines: the HSA agents of this GPU and of the host, the SDMA
+  // engines usable in each direction, and per staging half a pool of
+  // completion signals (one per queued copy, `in_flight` of them in use) and
+  // one event (the gather/scatter kernel that last used the half, on the
+  // caller's stream).
+  bool sdma_init = false;
+  hsa_agent_t gpu_agent{}, cpu_agent{};
+  std::vector<hsa_amd_sdma_engine_id_t> engines[2];   // [D2H, H2D]
+  std::vector<hsa_signal_t> sigs[2];
+  size_t in_flight[2] = {0, 0};
+  hipEvent_t ev_compute[2] = {nullptr, nullptr};
+};
+
+extern DeviceState g_dev[kMaxDevices];
+// staging bytes per device asked for with fkv_set_staging_bytes (0: default)
+extern std::atomic<size_t> g_staging_request;
+
+// Makes a device current for the guard's lifetime.
+struct DeviceGuard {
+  int prev = -1;
+  bool changed = false;
+  int set(int dev) {
+    FKV_HIP(hipGetDevice(&prev));
+    if (prev != dev) {
+      FKV_HIP(hipSetDevice(dev));
+      changed = true;
+    }
+    return 0;
+  }
+  ~DeviceGuard() {
+    if (changed) (void)hipSetDevice(prev);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Geometry validated on the host before anything is launched.
+
+struct Geometry {
+  int num_blocks, start_layer, num_layers, kv;
+  const int64_t* gids;
+  const int64_t* cids;
+  void* const* layer_ptrs;   // num_layers * ptrs_per_layer entries
+  int ptrs_per_layer = 1;    // kv when K and V are separate allocations (gks = 0)
+  int64_t gks, gbs, cks, cls, cbs, startoff, chunk;
+  char* cpu_ptr;
+  PtrInfo cpu_info;
+  int64_t min_gid, max_gid, min_cid, max_cid;
+
+  // Base address of half k of call layer l (block 0).
+  char* gpu_base(int l, int k) const {
+    const int64_t i = static_cast<int64_t>(l) * ptrs_per_layer + (ptrs_per_layer > 1 ? k : 0);
+    return static_cast<char*>(layer_ptrs[i]) + k * gks;
+  }
+  // Layers whose pointers fit one launch's kernel arguments.
+  int layers_per_launch() const { return kMaxLayersPerLaunch / ptrs_per_layer; }
+};
+
+// Check ids, strides, alignment and that every byte the transfer touches lies
+// inside the host and device allocations; fills the id ranges and cpu_info.
+int validate(Geometry& g, int mode);
+
+// Profiling (fkv_profile_enable / fkv_profile_read)
+extern std::atomic<bool> g_prof_on;
+void prof_add_kernel(double ms, int64_t bytes);
+void prof_add_dma(double ms, int64_t copies, int64_t bytes);
+
+// Event pairs recorded around launches when profiling is on; read after the
+// final synchronisation.
+struct ProfSpan {
+  hipEvent_t a, b;
+  int64_t bytes;
+  int64_t copies;
+  bool dma;
+};
+
+struct ProfRecorder {
+  bool on = g_prof_on.load(std::memory_order_relaxed);
+  std::vector<ProfSpan> spans;
+  int begin(hipStream_t s, hipEvent_t* a) {
+    if (!on) return 0;
+    FKV_HIP(hipEventCreate(a));
+    FKV_HIP(hipEventRecord(*a, s));
+    return 0;
+  }
+  int end(hipStream_t s, hipEvent_t a, int64_t bytes, int64_t copies, bool dma) {
+    if (!on) return 0;
+    hipEvent_t b;
+    FKV_HIP(hipEventCreate(&b));
+    FKV_HIP(hipEventRecord(b, s));
+    spans.push_back({a, b, bytes, copies, dma});
+    return 0;
+  }
+  void flush() {
+    for (auto& sp : spans) {
+      float ms = 0.f;
+      if (hipEventElapsedTime(&ms, sp.a, sp.b) == hipSuccess) {
+        if (sp.dma)
+          prof_add_dma(ms, sp.copies, sp.bytes);
+        else
+          prof_add_kernel(ms, sp.bytes);
+      }
+      (void)hipEventDestroy(sp.a);
+      (void)hipEventDestroy(sp.b);
+    }
+    spans.clear();
+  }
+  ~ProfRecorder() {
+    for (auto& sp : spans) {
+      (void)hipEventDestroy(sp.a);
+      (void)hipEventDestroy(sp.b);
+    }
+  }
+};
+
+// The calling thread's pinned, device-mapped buffer of at least `bytes`.
+// Calls are synchronous, so the previous call's kernels have finished
+// before the buffer is rewritten or regrown.
+int pinned_ids(size_t bytes, int64_t** host, char** dev);
+// The ids as (gpu_id, cpu_id) pairs.
+void pack_ids_into(const Geometry& g, int64_t* h);
+// Pack ids into the thread's pinned buffer as (gpu_id, cpu_id) pairs.
+int pack_ids(const Geometry& g, char** ids_dev);
+// The device a stream belongs to (the current device for the null stream).
+int stream_device(hipStream_t s, int* dev);
+
+// ---------------------------------------------------------------------------
+// Copy engines (kv_sdma.cpp)
+
+// One contiguous DMA between staging and the host cache.
+struct Run {
+  int64_t staging_off;
+  char* host;
+  int64_t bytes;
+};
+
+// Host runs for blocks [b0, b0+nb) of a piece whose staging layout is
+// [block][layer][kv][chunk] over `nl` layers starting at `l0`.
+void build_runs(const Geometry& g, int b0, int nb, int l0, int nl, std::vector<Run>& runs);
+// HSA agents and SDMA engines for the copy-engine path on device `dev`, found
+// through `hip_ptr`, a device allocation HIP made on `dev`.
+int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr);
+// A staging buffer of at least two halves of `need_half` bytes.
+int ensure_staging(DeviceState& d, size_t need_half);
+// Queue the copies of `runs` between the host cache and staging half `half`
+// on the device's SDMA engines, round robin, each with its own completion
+// signal.
+int issue_sdma(DeviceState& d, const std::vector<Run>& runs, char* staging, bool h2d, int half,
+               hsa_agent_t host_agent);
+// Wait until every copy queued on a staging half has finished.  Each copy
+// has its own signal: a counted signal shared by many copies would depend on
+// every layer between here and the engines decrementing it by exactly one.
+void sdma_wait(DeviceState& d, int half);
+
+// When a transfer fails after enqueueing work, wait for that work before the
+// call returns: a copy must not land in the caller's buffers, or read the
+// reused id and staging buffers, after the error has been reported.
+struct DrainOnError {
+  hipStream_t stream;
+  DeviceState* dev_state;
+  bool armed = true;
+  ~DrainOnError() {
+    if (!armed) return;
+    (void)hipStreamSynchronize(stream);
+    if (dev_state && dev_state->sdma_init)
+      for (int h = 0; h < 2; ++h) sdma_wait(*dev_state, h);
+    (void)hipGetLastError();
+  }
+};
+
+#pragma GCC visibility pop
+}  // namespace fkv_detail

@@ -1,0 +1,261 @@
+// kv_sdma.cpp - the copy engines of the copy-engine transfer path: the HSA
+// entry points resolved from the runtime HIP uses, the GPU and host agents and
+// SDMA engines of a device, its staging buffer, and the queueing of and
+// waiting for whole-block copies between staging and the host cache.
+
+#include <dlfcn.h>
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <type_traits>
+#include <vector>
+
+#include "kv_internal.h"
+
+namespace fkv_detail {
+
+namespace {
+
+// SDMA engines the copy-engine path spreads its copies over: measured on
+// MI355X with 2 MiB copies, one engine moves 45 GB/s, four 56 GB/s in either
+// direction, all sixteen 46 GB/s device-to-host.
+constexpr int kDefaultSdmaEngines = 4;
+
+// The HSA entry points the copy-engine path needs, resolved from the HSA
+// runtime that the process's HIP runtime uses.  Binding by name could reach a
+// second HSA runtime mapped into the process, which knows nothing of HIP's
+// allocations.
+struct HsaApi {
+  decltype(&::hsa_iterate_agents) iterate_agents = nullptr;
+  decltype(&::hsa_amd_pointer_info) pointer_info = nullptr;
+  decltype(&::hsa_agent_get_info) agent_get_info = nullptr;
+  decltype(&::hsa_status_string) status_string = nullptr;
+  decltype(&::hsa_signal_create) signal_create = nullptr;
+  decltype(&::hsa_signal_store_screlease) signal_store_screlease = nullptr;
+  decltype(&::hsa_signal_wait_scacquire) signal_wait_scacquire = nullptr;
+  decltype(&::hsa_amd_memory_copy_engine_status) copy_engine_status = nullptr;
+  decltype(&::hsa_amd_memory_async_copy_on_engine) async_copy_on_engine = nullptr;
+};
+HsaApi g_hsa;
+
+int sdma_engines_wanted() {
+  const char* e = getenv("FLEXKV_SDMA_ENGINES");
+  const int n = e ? atoi(e) : kDefaultSdmaEngines;
+  return std::max(1, std::min(n, 32));
+}
+
+std::mutex g_hsa_mu;
+bool g_hsa_loaded = false;
+
+// The HSA runtime behind HIP is the mapped copy that knows `hip_ptr`, a
+// device allocation HIP made: a process can map a second copy (a wheel's
+// bundled runtime next to the system one a profiling tool preloaded), and
+// which one HIP bound to depends on load order.
+int load_hsa(const void* hip_ptr) {
+  std::lock_guard<std::mutex> lk(g_hsa_mu);
+  if (g_hsa_loaded) return 0;
+  std::vector<std::string> paths;
+  if (FILE* f = fopen("/proc/self/maps", "r")) {
+    char line[4096];
+    while (fgets(line, sizeof(line), f)) {
+      const char* p = strchr(line, '/');
+      if (!p || !strstr(p, "libhsa-runtime64.so")) continue;
+      std::string path(p);
+      while (!path.empty() && (path.back() == '\n' || path.back() == ' ')) path.pop_back();
+      if (std::find(paths.begin(), paths.end(), path) == paths.end()) paths.push_back(path);
+    }
+    fclose(f);
+  }
+  void* lib = nullptr;
+  for (const std::string& path : paths) {
+    void* h = dlopen(path.c_str(), RTLD_NOW | RTLD_NOLOAD);
+    if (!h) continue;
+    auto info = reinterpret_cast<decltype(&::hsa_amd_pointer_info)>(dlsym(h, "hsa_amd_pointer_info"));
+    hsa_amd_pointer_info_t pi;
+    memset(&pi, 0, sizeof(pi));
+    pi.size = sizeof(pi);
+    if (info && info(hip_ptr, &pi, nullptr, nullptr, nullptr) == HSA_STATUS_SUCCESS &&
+        pi.type != HSA_EXT_POINTER_TYPE_UNKNOWN) {
+      lib = h;
+      break;
+    }
+    dlclose(h);
+  }
+  if (!lib) return fail(kInval, "no HSA runtime mapped into the process knows HIP's allocations");
+  HsaApi a;
+  int missing = 0;
+  auto sym = [&](auto& fn, const char* name) {
+    fn = reinterpret_cast<std::remove_reference_t<decltype(fn)>>(dlsym(lib, name));
+    if (!fn) ++missing;
+  };
+  sym(a.iterate_agents, "hsa_iterate_agents");
+  sym(a.pointer_info, "hsa_amd_pointer_info");
+  sym(a.agent_get_info, "hsa_agent_get_info");
+  sym(a.status_string, "hsa_status_string");
+  sym(a.signal_create, "hsa_signal_create");
+  sym(a.signal_store_screlease, "hsa_signal_store_screlease");
+  sym(a.signal_wait_scacquire, "hsa_signal_wait_scacquire");
+  sym(a.copy_engine_status, "hsa_amd_memory_copy_engine_status");
+  sym(a.async_copy_on_engine, "hsa_amd_memory_async_copy_on_engine");
+  if (missing) return fail(kInval, "the HSA runtime lacks %d entry points", missing);
+  g_hsa = a;
+  g_hsa_loaded = true;
+  return 0;
+}
+
+hsa_status_t first_cpu_agent(hsa_agent_t a, void* out) {
+  hsa_device_type_t t;
+  if (g_hsa.agent_get_info(a, HSA_AGENT_INFO_DEVICE, &t) == HSA_STATUS_SUCCESS &&
+      t == HSA_DEVICE_TYPE_CPU) {
+    *static_cast<hsa_agent_t*>(out) = a;
+    return HSA_STATUS_INFO_BREAK;
+  }
+  return HSA_STATUS_SUCCESS;
+}
+
+#define FKV_HSA(expr)                                                                   \
+  do {                                                                                  \
+    hsa_status_t st_ = (expr);                                                          \
+    if (st_ != HSA_STATUS_SUCCESS) {                                                    \
+      const char* m_ = nullptr;                                                         \
+      (void)g_hsa.status_string(st_, &m_);                                                \
+      return fail(static_cast<int>(hipErrorUnknown), "%s failed: %s", #expr, m_ ? m_ : "?"); \
+    }                                                                                   \
+  } while (0)
+
+}  // namespace
+
+void sdma_wait(DeviceState& d, int half) {
+  for (size_t i = 0; i < d.in_flight[half]; ++i)
+    while (g_hsa.signal_wait_scacquire(d.sigs[half][i], HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX,
+                                       HSA_WAIT_STATE_BLOCKED) >= 1) {
+    }
+  d.in_flight[half] = 0;
+}
+
+void build_runs(const Geometry& g, int b0, int nb, int l0, int nl, std::vector<Run>& runs) {
+  runs.clear();
+  const int64_t row_chunks = static_cast<int64_t>(nl) * g.kv;
+  const bool row_contig = (g.kv == 1 || g.cks == g.chunk) && (nl == 1 || g.cls == g.kv * g.chunk);
+  char* host0 = g.cpu_ptr + g.startoff + static_cast<int64_t>(g.start_layer + l0) * g.cls;
+  int64_t soff = 0;
+  auto push = [&](char* h, int64_t bytes) {
+    if (!runs.empty() && runs.back().host + runs.back().bytes == h &&
+        runs.back().staging_off + runs.back().bytes == soff) {
+      runs.back().bytes += bytes;
+    } else {
+      runs.push_back({soff, h, bytes});
+    }
+    soff += bytes;
+  };
+  for (int i = b0; i < b0 + nb; ++i) {
+    char* hb = host0 + g.cids[i] * g.cbs;
+    if (row_contig) {
+      push(hb, row_chunks * g.chunk);
+    } else {
+      for (int l = 0; l < nl; ++l)
+        for (int k = 0; k < g.kv; ++k) push(hb + l * g.cls + k * g.cks, g.chunk);
+    }
+  }
+}
+
+int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr) {
+  if (d.sdma_init) return 0;
+  if (int rc = load_hsa(hip_ptr)) return rc;
+  hsa_amd_pointer_info_t pi;
+  memset(&pi, 0, sizeof(pi));
+  pi.size = sizeof(pi);
+  FKV_HSA(g_hsa.pointer_info(hip_ptr, &pi, nullptr, nullptr, nullptr));
+  hsa_device_type_t t;
+  if (pi.agentOwner.handle == 0 ||
+      g_hsa.agent_get_info(pi.agentOwner, HSA_AGENT_INFO_DEVICE, &t) != HSA_STATUS_SUCCESS ||
+      t != HSA_DEVICE_TYPE_GPU)
+    return fail(kInval, "no GPU agent owns the staging buffer of device %d", dev);
+  struct {
+    hsa_agent_t gpu, cpu;
+  } q{pi.agentOwner, {0}};
+  const hsa_status_t it = g_hsa.iterate_agents(first_cpu_agent, &q.cpu);
+  if ((it != HSA_STATUS_SUCCESS && it != HSA_STATUS_INFO_BREAK) || q.cpu.handle == 0)
+    return fail(kInval, "no CPU agent found for device %d", dev);
+  hsa_agent_t nearest{};
+  if (g_hsa.agent_get_info(q.gpu, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_NEAREST_CPU),
+                           &nearest) == HSA_STATUS_SUCCESS && nearest.handle != 0)
+    q.cpu = nearest;
+  const int want = sdma_engines_wanted();
+  for (int dir = 0; dir < 2; ++dir) {
+    uint32_t mask = 0;
+    FKV_HSA(dir == 0 ? g_hsa.copy_engine_status(q.cpu, q.gpu, &mask)
+                     : g_hsa.copy_engine_status(q.gpu, q.cpu, &mask));
+    d.engines[dir].clear();
+    for (int b = 0; b < 32 && static_cast<int>(d.engines[dir].size()) < want; ++b)
+      if (mask & (1u << b))
+        d.engines[dir].push_back(static_cast<hsa_amd_sdma_engine_id_t>(1u << b));
+    if (d.engines[dir].empty())
+      return fail(kInval, "device %d reports no SDMA engine for %s copies", dev,
+                  dir == 0 ? "device-to-host" : "host-to-device");
+  }
+  for (int h = 0; h < 2; ++h)
+    FKV_HIP(hipEventCreateWithFlags(&d.ev_compute[h], hipEventDisableTiming));
+  d.gpu_agent = q.gpu;
+  d.cpu_agent = q.cpu;
+  d.sdma_init = true;
+  return 0;
+}
+
+int ensure_staging(DeviceState& d, size_t need_half) {
+  size_t want = g_staging_request.load();
+  if (want == 0) want = kDefaultStagingBytes;
+  want = std::max(want, 2 * need_half);
+  want = (want + 4095) & ~size_t(4095);
+  if (d.staging && d.staging_bytes == want) return 0;
+  if (d.staging) {
+    FKV_HIP(hipFree(d.staging));
+    d.staging = nullptr;
+    d.staging_bytes = 0;
+  }
+  void* p = nullptr;
+  FKV_HIP(hipMalloc(&p, want));
+  d.staging = static_cast<char*>(p);
+  d.staging_bytes = want;
+  return 0;
+}
+
+int issue_sdma(DeviceState& d, const std::vector<Run>& runs, char* staging, bool h2d, int half,
+               hsa_agent_t host_agent) {
+  const std::vector<hsa_amd_sdma_engine_id_t>& eng = d.engines[h2d ? 1 : 0];
+  std::vector<hsa_signal_t>& sigs = d.sigs[half];
+  while (sigs.size() < runs.size()) {
+    hsa_signal_t sg;
+    FKV_HSA(g_hsa.signal_create(1, 0, nullptr, &sg));
+    sigs.push_back(sg);
+  }
+  for (size_t i = 0; i < runs.size(); ++i) {
+    const Run& r = runs[i];
+    char* dev_p = staging + r.staging_off;
+    const hsa_amd_sdma_engine_id_t e = eng[i % eng.size()];
+    g_hsa.signal_store_screlease(sigs[i], 1);
+    const hsa_status_t st =
+        h2d ? g_hsa.async_copy_on_engine(dev_p, d.gpu_agent, r.host, host_agent,
+                                         static_cast<size_t>(r.bytes), 0, nullptr, sigs[i], e,
+                                         false)
+            : g_hsa.async_copy_on_engine(r.host, host_agent, dev_p, d.gpu_agent,
+                                         static_cast<size_t>(r.bytes), 0, nullptr, sigs[i], e,
+                                         false);
+    if (st != HSA_STATUS_SUCCESS) {
+      const char* m = nullptr;
+      (void)g_hsa.status_string(st, &m);
+      return fail(static_cast<int>(hipErrorUnknown), "SDMA copy of %lld bytes failed: %s",
+                  static_cast<long long>(r.bytes), m ? m : "?");
+    }
+    d.in_flight[half] = i + 1;
+  }
+  return 0;
+}
+
+}  // namespace fkv_detail

@@ -17,27 +17,27 @@
 // ordered block -> layer -> K|V -> offset, which is host-address order for the
 // block-wise host layout.  Layer base pointers travel in the kernel argument
 // block (scalar loads, no PCIe round trip per chunk).
+//
+// This file holds the kernels, the transfer paths that launch them and the
+// transfer entry points of the C ABI; kv_host.cpp holds validation, id staging
+// and the host-only entry points, kv_sdma.cpp the copy engines.
 
 #include <hip/hip_runtime.h>
-#include <hsa/hsa.h>
-#include <hsa/hsa_ext_amd.h>
-#include <dlfcn.h>
 
 #include <algorithm>
 #include <atomic>
 #include <chrono>
-#include <cstdarg>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
-#include <type_traits>
 #include <vector>
 
-#include "flexkv_hip.h"
-#include "fkv_error.h"
+#include "kv_internal.h"
+
+using namespace fkv_detail;
 
 namespace {
 
@@ -98,13 +98,7 @@ namespace {
 constexpr int kThreads = 256;               // 4 wavefronts of 64 lanes
 constexpr int kWaves = kThreads / 64;
 constexpr int kUnrollHbm = FKV_UNROLL_HBM;
-constexpr int kMaxLayersPerLaunch = 128;    // layer pointers in kernel args
 constexpr int kMaxTileBlocks = 64;
-constexpr int kMaxDevices = 64;
-// SDMA engines the copy-engine path spreads its copies over: measured on
-// MI355X with 2 MiB copies, one engine moves 45 GB/s, four 56 GB/s in either
-// direction, all sixteen 46 GB/s device-to-host.
-constexpr int kDefaultSdmaEngines = 4;
 // Compute units of the zero-copy kernel when the caller passes -1: enough
 // loads/stores in flight to saturate the PCIe Gen5 x16 link (measured on
 // MI355X: 8 CUs reach the link's copy rate; more add contention).
@@ -115,7 +109,6 @@ constexpr int kAutoZeroCopyCus = 8;
 // Llama-3-8B load overlapped with per-layer GEMMs finishes in 42.8 ms on 2
 // CUs against 46.1 ms on 8.
 constexpr int kAutoLayerwiseH2DCus = 2;
-constexpr size_t kDefaultStagingBytes = size_t(256) << 20;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // Every address the kernel touches is global memory (HBM or mapped pinned
@@ -266,130 +259,7 @@ __global__ __launch_bounds__(64) void acquire_system_kernel() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
 }
 
-// ---------------------------------------------------------------------------
-// Errors
-
-}  // namespace
-
-namespace fkv_detail {
-std::string& last_error() {
-  static thread_local std::string msg;
-  return msg;
-}
-}  // namespace fkv_detail
-
-namespace {
-
-#define t_err (::fkv_detail::last_error())
-
-int fail(int code, const char* fmt, ...) {
-  char buf[1024];
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(buf, sizeof(buf), fmt, ap);
-  va_end(ap);
-  t_err = buf;
-  return code;
-}
-
-#define FKV_HIP(call)                                                          \
-  do {                                                                         \
-    hipError_t e_ = (call);                                                    \
-    if (e_ != hipSuccess) {                                                    \
-      return fail(static_cast<int>(e_), "%s failed: %s (%s:%d)", #call,        \
-                  hipGetErrorString(e_), __FILE__, __LINE__);                  \
-    }                                                                          \
-  } while (0)
-
-constexpr int kInval = static_cast<int>(hipErrorInvalidValue);
-
-// ---------------------------------------------------------------------------
-// Pointer classification and bounds
-
-struct PtrInfo {
-  bool host = false;     // pinned host memory
-  bool device = false;   // device memory
-  char* dev_ptr = nullptr;  // device-visible address of the queried pointer
-  char* base = nullptr;     // allocation start (host address space)
-  size_t size = 0;          // allocation size
-};
-
-// Returns 0 and fills `out` if p lies in memory known to the HIP runtime.
-int query_ptr(const void* p, PtrInfo* out) {
-  hipPointerAttribute_t at;
-  memset(&at, 0, sizeof(at));
-  hipError_t e = hipPointerGetAttributes(&at, p);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    return kInval;
-  }
-  if (at.type == hipMemoryTypeHost) {
-    out->host = true;
-    void* dp = nullptr;
-    if (hipHostGetDevicePointer(&dp, const_cast<void*>(p), 0) != hipSuccess || dp == nullptr) {
-      (void)hipGetLastError();
-      return kInval;
-    }
-    out->dev_ptr = static_cast<char*>(dp);
-  } else if (at.type == hipMemoryTypeDevice) {
-    out->device = true;
-    out->dev_ptr = static_cast<char*>(const_cast<void*>(p));
-  } else {
-    return kInval;
-  }
-  hipDeviceptr_t base = nullptr;
-  size_t size = 0;
-  e = hipMemGetAddressRange(&base, &size, const_cast<void*>(p));
-  if (e != hipSuccess || base == nullptr) {
-    (void)hipGetLastError();
-    return kInval;
-  }
-  out->base = static_cast<char*>(base);
-  out->size = size;
-  return 0;
-}
-
-// [p + lo, p + hi) must lie inside the allocation described by info.
-bool range_inside(const char* p, __int128 lo, __int128 hi, const PtrInfo& info) {
-  const __int128 start = static_cast<__int128>(reinterpret_cast<uintptr_t>(p)) + lo;
-  const __int128 end = static_cast<__int128>(reinterpret_cast<uintptr_t>(p)) + hi;
-  const __int128 a0 = static_cast<__int128>(reinterpret_cast<uintptr_t>(info.base));
-  const __int128 a1 = a0 + static_cast<__int128>(info.size);
-  return lo <= hi && start >= a0 && end <= a1;
-}
-
-// ---------------------------------------------------------------------------
-// Per-device state: staging buffer, side stream, events, occupancy.
-
-struct DeviceState {
-  std::mutex mu;            // serialises copy-engine transfers on the device
-  bool init = false;
-  int num_cus = 0;
-  int occ_zero_copy[2] = {0, 0};
-  int occ_staged[2] = {0, 0};
-  char* staging = nullptr;
-  size_t staging_bytes = 0;
-  // Copy engines: the HSA agents of this GPU and of the host, the SDMA
-  // engines usable in each direction, and per staging half a pool of
-  // completion signals (one per queued copy, `in_flight` of them in use) and
-  // one event (the gather/scatter kernel that last used the half, on the
-  // caller's stream).
-  bool sdma_init = false;
-  hsa_agent_t gpu_agent{}, cpu_agent{};
-  std::vector<hsa_amd_sdma_engine_id_t> engines[2];   // [D2H, H2D]
-  std::vector<hsa_signal_t> sigs[2];
-  size_t in_flight[2] = {0, 0};
-  hipEvent_t ev_compute[2] = {nullptr, nullptr};
-};
-
-DeviceState g_dev[kMaxDevices];
 std::mutex g_init_mu;
-std::atomic<size_t> g_staging_request{0};
-
-// Profiling
-std::atomic<bool> g_prof_on{false};
-std::mutex g_prof_mu;
-fkv_profile g_prof{};
 
 template <bool H, bool I>
 void* kernel_ptr() {
@@ -413,212 +283,6 @@ int ensure_device_basics(int dev) {
   d.init = true;
   return 0;
 }
-
-struct DeviceGuard {
-  int prev = -1;
-  bool changed = false;
-  int set(int dev) {
-    FKV_HIP(hipGetDevice(&prev));
-    if (prev != dev) {
-      FKV_HIP(hipSetDevice(dev));
-      changed = true;
-    }
-    return 0;
-  }
-  ~DeviceGuard() {
-    if (changed) (void)hipSetDevice(prev);
-  }
-};
-
-// Thread-local pinned buffer holding the packed (gpu_id, cpu_id) pairs the
-// kernels read.  Calls are synchronous, so the previous call's kernels have
-// finished before the buffer is rewritten or regrown.  Buffers are not freed
-// at thread exit (the runtime may already be gone at process exit).
-struct PinnedIds {
-  int64_t* p = nullptr;
-  char* dev = nullptr;
-  size_t cap = 0;  // bytes
-};
-thread_local PinnedIds t_ids;
-
-int pinned_ids(size_t bytes, int64_t** host, char** dev) {
-  if (bytes > t_ids.cap) {
-    if (t_ids.p) FKV_HIP(hipHostFree(t_ids.p));
-    t_ids.p = nullptr;
-    t_ids.cap = 0;
-    size_t cap = std::max<size_t>(bytes, 64 << 10);
-    void* p = nullptr;
-    FKV_HIP(hipHostMalloc(&p, cap, hipHostMallocPortable | hipHostMallocMapped | hipHostMallocCoherent));
-    void* dp = nullptr;
-    FKV_HIP(hipHostGetDevicePointer(&dp, p, 0));
-    t_ids.p = static_cast<int64_t*>(p);
-    t_ids.dev = static_cast<char*>(dp);
-    t_ids.cap = cap;
-  }
-  *host = t_ids.p;
-  *dev = t_ids.dev;
-  return 0;
-}
-
-// ---------------------------------------------------------------------------
-// Geometry validated on the host before anything is launched.
-
-struct Geometry {
-  int num_blocks, start_layer, num_layers, kv;
-  const int64_t* gids;
-  const int64_t* cids;
-  void* const* layer_ptrs;   // num_layers * ptrs_per_layer entries
-  int ptrs_per_layer = 1;    // kv when K and V are separate allocations (gks = 0)
-  int64_t gks, gbs, cks, cls, cbs, startoff, chunk;
-  char* cpu_ptr;
-  PtrInfo cpu_info;
-  int64_t min_gid, max_gid, min_cid, max_cid;
-
-  // Base address of half k of call layer l (block 0).
-  char* gpu_base(int l, int k) const {
-    const int64_t i = static_cast<int64_t>(l) * ptrs_per_layer + (ptrs_per_layer > 1 ? k : 0);
-    return static_cast<char*>(layer_ptrs[i]) + k * gks;
-  }
-  // Layers whose pointers fit one launch's kernel arguments.
-  int layers_per_launch() const { return kMaxLayersPerLaunch / ptrs_per_layer; }
-};
-
-int validate(Geometry& g, int mode) {
-  if (g.num_blocks < 0 || g.num_layers < 0 || g.start_layer < 0)
-    return fail(kInval, "negative count: num_blocks=%d num_layers=%d start_layer_id=%d",
-                g.num_blocks, g.num_layers, g.start_layer);
-  if (!g.gids || !g.cids || !g.layer_ptrs || !g.cpu_ptr)
-    return fail(kInval, "null pointer argument");
-  if (g.chunk <= 0) return fail(kInval, "chunk_size_in_bytes must be positive, got %lld", (long long)g.chunk);
-  if (g.gks < 0 || g.gbs < 0 || g.cks < 0 || g.cls < 0 || g.cbs < 0 || g.startoff < 0)
-    return fail(kInval, "strides and cpu_startoff_inside_chunks must be non-negative");
-  const bool vec_mode = (mode == FKV_XFER_KERNEL || mode == FKV_XFER_CE);
-  if (vec_mode) {
-    const int64_t vals[] = {g.chunk, g.gks, g.gbs, g.cks, g.cls, g.cbs, g.startoff};
-    for (int64_t v : vals)
-      if (v % 16 != 0)
-        return fail(kInval,
-                    "kernel/CE transfer needs chunk size, strides and start offset in "
-                    "multiples of 16 bytes (chunk=%lld gkv=%lld gblk=%lld ckv=%lld "
-                    "clayer=%lld cblk=%lld startoff=%lld)",
-                    (long long)g.chunk, (long long)g.gks, (long long)g.gbs, (long long)g.cks,
-                    (long long)g.cls, (long long)g.cbs, (long long)g.startoff);
-    if (reinterpret_cast<uintptr_t>(g.cpu_ptr) % 16 != 0)
-      return fail(kInval, "cpu_ptr is not 16-byte aligned");
-  }
-  // Host must be able to read ids and the layer table.
-  g.min_gid = g.min_cid = INT64_MAX;
-  g.max_gid = g.max_cid = -1;
-  for (int i = 0; i < g.num_blocks; ++i) {
-    const int64_t a = g.gids[i], b = g.cids[i];
-    if (a < 0 || b < 0)
-      return fail(kInval, "negative block id at position %d (gpu %lld, cpu %lld)", i,
-                  (long long)a, (long long)b);
-    g.min_gid = std::min(g.min_gid, a);
-    g.max_gid = std::max(g.max_gid, a);
-    g.min_cid = std::min(g.min_cid, b);
-    g.max_cid = std::max(g.max_cid, b);
-  }
-  if (query_ptr(g.cpu_ptr, &g.cpu_info) != 0)
-    return fail(kInval, "cpu_ptr %p is not pinned host or device memory known to HIP "
-                "(allocate the host cache with fkv_host_alloc / pin_memory=True)", g.cpu_ptr);
-  const __int128 lo = static_cast<__int128>(g.start_layer) * g.cls +
-                      static_cast<__int128>(g.min_cid) * g.cbs + g.startoff;
-  const __int128 hi = static_cast<__int128>(g.start_layer + g.num_layers - 1) * g.cls +
-                      static_cast<__int128>(g.kv - 1) * g.cks +
-                      static_cast<__int128>(g.max_cid) * g.cbs + g.startoff + g.chunk;
-  if (!range_inside(g.cpu_ptr, lo, hi, g.cpu_info))
-    return fail(kInval,
-                "cpu block ids [%lld, %lld] with layers [%d, %d) address bytes outside the "
-                "host cache allocation (%zu bytes)",
-                (long long)g.min_cid, (long long)g.max_cid, g.start_layer,
-                g.start_layer + g.num_layers, g.cpu_info.size);
-  const __int128 glo = static_cast<__int128>(g.min_gid) * g.gbs;
-  const __int128 ghi = static_cast<__int128>(g.kv - 1) * g.gks +
-                       static_cast<__int128>(g.max_gid) * g.gbs + g.chunk;
-  // Every layer (or K/V) pointer is its own allocation as a rule; query each.
-  if (g.ptrs_per_layer != 1 && (g.ptrs_per_layer != g.kv || g.gks != 0))
-    return fail(kInval, "separate K/V pointers need kv pointers per layer and no kv stride");
-  const int64_t nptr = static_cast<int64_t>(g.num_layers) * g.ptrs_per_layer;
-  for (int64_t i = 0; i < nptr; ++i) {
-    const char* p = static_cast<const char*>(g.layer_ptrs[i]);
-    if (!p) return fail(kInval, "gpu layer pointer %lld is null", (long long)i);
-    if (vec_mode && reinterpret_cast<uintptr_t>(p) % 16 != 0)
-      return fail(kInval, "gpu layer pointer %lld is not 16-byte aligned", (long long)i);
-    PtrInfo pi;
-    if (query_ptr(p, &pi) != 0 || !pi.device)
-      return fail(kInval, "gpu layer pointer %lld (%p) is not device memory", (long long)i, p);
-    if (!range_inside(p, glo, ghi, pi))
-      return fail(kInval,
-                  "gpu block ids [%lld, %lld] address bytes outside the allocation of "
-                  "layer pointer %lld (%zu bytes)",
-                  (long long)g.min_gid, (long long)g.max_gid, (long long)i, pi.size);
-  }
-  return 0;
-}
-
-void prof_add_kernel(double ms, int64_t bytes) {
-  std::lock_guard<std::mutex> lk(g_prof_mu);
-  g_prof.kernel_launches += 1;
-  g_prof.kernel_ms += ms;
-  g_prof.kernel_bytes += bytes;
-}
-
-void prof_add_dma(double ms, int64_t copies, int64_t bytes) {
-  std::lock_guard<std::mutex> lk(g_prof_mu);
-  g_prof.dma_batches += 1;
-  g_prof.dma_copies += copies;
-  g_prof.dma_ms += ms;
-  g_prof.dma_bytes += bytes;
-}
-
-// Event pairs recorded around launches when profiling is on; read after the
-// final synchronisation.
-struct ProfSpan {
-  hipEvent_t a, b;
-  int64_t bytes;
-  int64_t copies;
-  bool dma;
-};
-
-struct ProfRecorder {
-  bool on = g_prof_on.load(std::memory_order_relaxed);
-  std::vector<ProfSpan> spans;
-  int begin(hipStream_t s, hipEvent_t* a) {
-    if (!on) return 0;
-    FKV_HIP(hipEventCreate(a));
-    FKV_HIP(hipEventRecord(*a, s));
-    return 0;
-  }
-  int end(hipStream_t s, hipEvent_t a, int64_t bytes, int64_t copies, bool dma) {
-    if (!on) return 0;
-    hipEvent_t b;
-    FKV_HIP(hipEventCreate(&b));
-    FKV_HIP(hipEventRecord(b, s));
-    spans.push_back({a, b, bytes, copies, dma});
-    return 0;
-  }
-  void flush() {
-    for (auto& sp : spans) {
-      float ms = 0.f;
-      if (hipEventElapsedTime(&ms, sp.a, sp.b) == hipSuccess) {
-        if (sp.dma)
-          prof_add_dma(ms, sp.copies, sp.bytes);
-        else
-          prof_add_kernel(ms, sp.bytes);
-      }
-      (void)hipEventDestroy(sp.a);
-      (void)hipEventDestroy(sp.b);
-    }
-    spans.clear();
-  }
-  ~ProfRecorder() {
-    for (auto& sp : spans) {
-      (void)hipEventDestroy(sp.a);
-      (void)hipEventDestroy(sp.b);
-    }
-  }
-};
 
 // Tiles are tb blocks x tl layers.  Start from whole block rows (one block,
 // every layer) and halve the layer window until there are about `factor`
@@ -680,75 +344,6 @@ int launch_copy(const Geometry& g, char* ids_dev, char* cpu_base, int64_t cks, i
   return prof.end(stream, ev, static_cast<int64_t>(nb) * nl * g.kv * g.chunk, 0, false);
 }
 
-void pack_ids_into(const Geometry& g, int64_t* h) {
-  for (int i = 0; i < g.num_blocks; ++i) {
-    h[2 * i] = g.gids[i];
-    h[2 * i + 1] = g.cids[i];
-  }
-}
-
-// Pack ids into the thread's pinned buffer as (gpu_id, cpu_id) pairs.
-int pack_ids(const Geometry& g, char** ids_dev) {
-  int64_t* h = nullptr;
-  int rc = pinned_ids(static_cast<size_t>(g.num_blocks) * 16, &h, ids_dev);
-  if (rc) return rc;
-  pack_ids_into(g, h);
-  return 0;
-}
-
-int stream_device(hipStream_t s, int* dev) {
-  if (s == nullptr) {
-    FKV_HIP(hipGetDevice(dev));
-  } else {
-    FKV_HIP(hipStreamGetDevice(s, dev));
-  }
-  if (*dev < 0 || *dev >= kMaxDevices) return fail(kInval, "device %d out of range", *dev);
-  return 0;
-}
-
-// The HSA entry points the copy-engine path needs, resolved from the HSA
-// runtime that the process's HIP runtime uses.  Binding by name could reach a
-// second HSA runtime mapped into the process, which knows nothing of HIP's
-// allocations.
-struct HsaApi {
-  decltype(&::hsa_iterate_agents) iterate_agents = nullptr;
-  decltype(&::hsa_amd_pointer_info) pointer_info = nullptr;
-  decltype(&::hsa_agent_get_info) agent_get_info = nullptr;
-  decltype(&::hsa_status_string) status_string = nullptr;
-  decltype(&::hsa_signal_create) signal_create = nullptr;
-  decltype(&::hsa_signal_store_screlease) signal_store_screlease = nullptr;
-  decltype(&::hsa_signal_wait_scacquire) signal_wait_scacquire = nullptr;
-  decltype(&::hsa_amd_memory_copy_engine_status) copy_engine_status = nullptr;
-  decltype(&::hsa_amd_memory_async_copy_on_engine) async_copy_on_engine = nullptr;
-};
-HsaApi g_hsa;
-// Wait until every copy queued on a staging half has finished.  Each copy
-// has its own signal: a counted signal shared by many copies would depend on
-// every layer between here and the engines decrementing it by exactly one.
-void sdma_wait(DeviceState& d, int half) {
-  for (size_t i = 0; i < d.in_flight[half]; ++i)
-    while (g_hsa.signal_wait_scacquire(d.sigs[half][i], HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX,
-                                       HSA_WAIT_STATE_BLOCKED) >= 1) {
-    }
-  d.in_flight[half] = 0;
-}
-
-// When a transfer fails after enqueueing work, wait for that work before the
-// call returns: a copy must not land in the caller's buffers, or read the
-// reused id and staging buffers, after the error has been reported.
-struct DrainOnError {
-  hipStream_t stream;
-  DeviceState* dev_state;
-  bool armed = true;
-  ~DrainOnError() {
-    if (!armed) return;
-    (void)hipStreamSynchronize(stream);
-    if (dev_state && dev_state->sdma_init)
-      for (int h = 0; h < 2; ++h) sdma_wait(*dev_state, h);
-    (void)hipGetLastError();
-  }
-};
-
 int transfer_zero_copy(const Geometry& g, hipStream_t stream, int dev, int transfer_cus,
                        bool h2d) {
   DeviceState& d = g_dev[dev];
@@ -775,226 +370,6 @@ int transfer_zero_copy(const Geometry& g, hipStream_t stream, int dev, int trans
   FKV_HIP(hipStreamSynchronize(stream));
   drain.armed = false;
   prof.flush();
-  return 0;
-}
-
-// One contiguous DMA between staging and the host cache.
-struct Run {
-  int64_t staging_off;
-  char* host;
-  int64_t bytes;
-};
-
-// Host runs for blocks [b0, b0+nb) of a piece whose staging layout is
-// [block][layer][kv][chunk] over `nl` layers starting at `l0`.
-void build_runs(const Geometry& g, int b0, int nb, int l0, int nl, std::vector<Run>& runs) {
-  runs.clear();
-  const int64_t row_chunks = static_cast<int64_t>(nl) * g.kv;
-  const bool row_contig = (g.kv == 1 || g.cks == g.chunk) && (nl == 1 || g.cls == g.kv * g.chunk);
-  char* host0 = g.cpu_ptr + g.startoff + static_cast<int64_t>(g.start_layer + l0) * g.cls;
-  int64_t soff = 0;
-  auto push = [&](char* h, int64_t bytes) {
-    if (!runs.empty() && runs.back().host + runs.back().bytes == h &&
-        runs.back().staging_off + runs.back().bytes == soff) {
-      runs.back().bytes += bytes;
-    } else {
-      runs.push_back({soff, h, bytes});
-    }
-    soff += bytes;
-  };
-  for (int i = b0; i < b0 + nb; ++i) {
-    char* hb = host0 + g.cids[i] * g.cbs;
-    if (row_contig) {
-      push(hb, row_chunks * g.chunk);
-    } else {
-      for (int l = 0; l < nl; ++l)
-        for (int k = 0; k < g.kv; ++k) push(hb + l * g.cls + k * g.cks, g.chunk);
-    }
-  }
-}
-
-int sdma_engines_wanted() {
-  const char* e = getenv("FLEXKV_SDMA_ENGINES");
-  const int n = e ? atoi(e) : kDefaultSdmaEngines;
-  return std::max(1, std::min(n, 32));
-}
-
-std::mutex g_hsa_mu;
-bool g_hsa_loaded = false;
-
-// The HSA runtime behind HIP is the mapped copy that knows `hip_ptr`, a
-// device allocation HIP made: a process can map a second copy (a wheel's
-// bundled runtime next to the system one a profiling tool preloaded), and
-// which one HIP bound to depends on load order.
-int load_hsa(const void* hip_ptr) {
-  std::lock_guard<std::mutex> lk(g_hsa_mu);
-  if (g_hsa_loaded) return 0;
-  std::vector<std::string> paths;
-  if (FILE* f = fopen("/proc/self/maps", "r")) {
-    char line[4096];
-    while (fgets(line, sizeof(line), f)) {
-      const char* p = strchr(line, '/');
-      if (!p || !strstr(p, "libhsa-runtime64.so")) continue;
-      std::string path(p);
-      while (!path.empty() && (path.back() == '\n' || path.back() == ' ')) path.pop_back();
-      if (std::find(paths.begin(), paths.end(), path) == paths.end()) paths.push_back(path);
-    }
-    fclose(f);
-  }
-  void* lib = nullptr;
-  for (const std::string& path : paths) {
-    void* h = dlopen(path.c_str(), RTLD_NOW | RTLD_NOLOAD);
-    if (!h) continue;
-    auto info = reinterpret_cast<decltype(&::hsa_amd_pointer_info)>(dlsym(h, "hsa_amd_pointer_info"));
-    hsa_amd_pointer_info_t pi;
-    memset(&pi, 0, sizeof(pi));
-    pi.size = sizeof(pi);
-    if (info && info(hip_ptr, &pi, nullptr, nullptr, nullptr) == HSA_STATUS_SUCCESS &&
-        pi.type != HSA_EXT_POINTER_TYPE_UNKNOWN) {
-      lib = h;
-      break;
-    }
-    dlclose(h);
-  }
-  if (!lib) return fail(kInval, "no HSA runtime mapped into the process knows HIP's allocations");
-  HsaApi a;
-  int missing = 0;
-  auto sym = [&](auto& fn, const char* name) {
-    fn = reinterpret_cast<std::remove_reference_t<decltype(fn)>>(dlsym(lib, name));
-    if (!fn) ++missing;
-  };
-  sym(a.iterate_agents, "hsa_iterate_agents");
-  sym(a.pointer_info, "hsa_amd_pointer_info");
-  sym(a.agent_get_info, "hsa_agent_get_info");
-  sym(a.status_string, "hsa_status_string");
-  sym(a.signal_create, "hsa_signal_create");
-  sym(a.signal_store_screlease, "hsa_signal_store_screlease");
-  sym(a.signal_wait_scacquire, "hsa_signal_wait_scacquire");
-  sym(a.copy_engine_status, "hsa_amd_memory_copy_engine_status");
-  sym(a.async_copy_on_engine, "hsa_amd_memory_async_copy_on_engine");
-  if (missing) return fail(kInval, "the HSA runtime lacks %d entry points", missing);
-  g_hsa = a;
-  g_hsa_loaded = true;
-  return 0;
-}
-
-hsa_status_t first_cpu_agent(hsa_agent_t a, void* out) {
-  hsa_device_type_t t;
-  if (g_hsa.agent_get_info(a, HSA_AGENT_INFO_DEVICE, &t) == HSA_STATUS_SUCCESS &&
-      t == HSA_DEVICE_TYPE_CPU) {
-    *static_cast<hsa_agent_t*>(out) = a;
-    return HSA_STATUS_INFO_BREAK;
-  }
-  return HSA_STATUS_SUCCESS;
-}
-
-#define FKV_HSA(expr)                                                                   \
-  do {                                                                                  \
-    hsa_status_t st_ = (expr);                                                          \
-    if (st_ != HSA_STATUS_SUCCESS) {                                                    \
-      const char* m_ = nullptr;                                                         \
-      (void)g_hsa.status_string(st_, &m_);                                                \
-      return fail(static_cast<int>(hipErrorUnknown), "%s failed: %s", #expr, m_ ? m_ : "?"); \
-    }                                                                                   \
-  } while (0)
-
-// HSA agents and SDMA engines for the copy-engine path on device `dev`: the
-// GPU agent is the owner of `hip_ptr` (a device allocation HIP made on
-// `dev`), the host side is the GPU's nearest CPU agent when the runtime
-// reports one, else the first CPU agent.
-int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr) {
-  if (d.sdma_init) return 0;
-  if (int rc = load_hsa(hip_ptr)) return rc;
-  hsa_amd_pointer_info_t pi;
-  memset(&pi, 0, sizeof(pi));
-  pi.size = sizeof(pi);
-  FKV_HSA(g_hsa.pointer_info(hip_ptr, &pi, nullptr, nullptr, nullptr));
-  hsa_device_type_t t;
-  if (pi.agentOwner.handle == 0 ||
-      g_hsa.agent_get_info(pi.agentOwner, HSA_AGENT_INFO_DEVICE, &t) != HSA_STATUS_SUCCESS ||
-      t != HSA_DEVICE_TYPE_GPU)
-    return fail(kInval, "no GPU agent owns the staging buffer of device %d", dev);
-  struct {
-    hsa_agent_t gpu, cpu;
-  } q{pi.agentOwner, {0}};
-  const hsa_status_t it = g_hsa.iterate_agents(first_cpu_agent, &q.cpu);
-  if ((it != HSA_STATUS_SUCCESS && it != HSA_STATUS_INFO_BREAK) || q.cpu.handle == 0)
-    return fail(kInval, "no CPU agent found for device %d", dev);
-  hsa_agent_t nearest{};
-  if (g_hsa.agent_get_info(q.gpu, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_NEAREST_CPU),
-                           &nearest) == HSA_STATUS_SUCCESS && nearest.handle != 0)
-    q.cpu = nearest;
-  const int want = sdma_engines_wanted();
-  for (int dir = 0; dir < 2; ++dir) {
-    uint32_t mask = 0;
-    FKV_HSA(dir == 0 ? g_hsa.copy_engine_status(q.cpu, q.gpu, &mask)
-                     : g_hsa.copy_engine_status(q.gpu, q.cpu, &mask));
-    d.engines[dir].clear();
-    for (int b = 0; b < 32 && static_cast<int>(d.engines[dir].size()) < want; ++b)
-      if (mask & (1u << b))
-        d.engines[dir].push_back(static_cast<hsa_amd_sdma_engine_id_t>(1u << b));
-    if (d.engines[dir].empty())
-      return fail(kInval, "device %d reports no SDMA engine for %s copies", dev,
-                  dir == 0 ? "device-to-host" : "host-to-device");
-  }
-  for (int h = 0; h < 2; ++h)
-    FKV_HIP(hipEventCreateWithFlags(&d.ev_compute[h], hipEventDisableTiming));
-  d.gpu_agent = q.gpu;
-  d.cpu_agent = q.cpu;
-  d.sdma_init = true;
-  return 0;
-}
-
-int ensure_staging(DeviceState& d, size_t need_half) {
-  size_t want = g_staging_request.load();
-  if (want == 0) want = kDefaultStagingBytes;
-  want = std::max(want, 2 * need_half);
-  want = (want + 4095) & ~size_t(4095);
-  if (d.staging && d.staging_bytes == want) return 0;
-  if (d.staging) {
-    FKV_HIP(hipFree(d.staging));
-    d.staging = nullptr;
-    d.staging_bytes = 0;
-  }
-  void* p = nullptr;
-  FKV_HIP(hipMalloc(&p, want));
-  d.staging = static_cast<char*>(p);
-  d.staging_bytes = want;
-  return 0;
-}
-
-// Queue the copies of `runs` between the host cache and staging half `half`
-// on the device's SDMA engines, round robin, each with its own completion
-// signal.
-int issue_sdma(DeviceState& d, const std::vector<Run>& runs, char* staging, bool h2d, int half,
-               hsa_agent_t host_agent) {
-  const std::vector<hsa_amd_sdma_engine_id_t>& eng = d.engines[h2d ? 1 : 0];
-  std::vector<hsa_signal_t>& sigs = d.sigs[half];
-  while (sigs.size() < runs.size()) {
-    hsa_signal_t sg;
-    FKV_HSA(g_hsa.signal_create(1, 0, nullptr, &sg));
-    sigs.push_back(sg);
-  }
-  for (size_t i = 0; i < runs.size(); ++i) {
-    const Run& r = runs[i];
-    char* dev_p = staging + r.staging_off;
-    const hsa_amd_sdma_engine_id_t e = eng[i % eng.size()];
-    g_hsa.signal_store_screlease(sigs[i], 1);
-    const hsa_status_t st =
-        h2d ? g_hsa.async_copy_on_engine(dev_p, d.gpu_agent, r.host, host_agent,
-                                         static_cast<size_t>(r.bytes), 0, nullptr, sigs[i], e,
-                                         false)
-            : g_hsa.async_copy_on_engine(r.host, host_agent, dev_p, d.gpu_agent,
-                                         static_cast<size_t>(r.bytes), 0, nullptr, sigs[i], e,
-                                         false);
-    if (st != HSA_STATUS_SUCCESS) {
-      const char* m = nullptr;
-      (void)g_hsa.status_string(st, &m);
-      return fail(static_cast<int>(hipErrorUnknown), "SDMA copy of %lld bytes failed: %s",
-                  static_cast<long long>(r.bytes), m ? m : "?");
-    }
-    d.in_flight[half] = i + 1;
-  }
   return 0;
 }
 
@@ -1146,7 +521,7 @@ int contiguous_entry(int num_blocks, int num_layers, const int64_t* gpu_block_id
                      int64_t gpu_block_stride_bytes, int64_t chunk_size_bytes, void* buffer,
                      size_t buffer_bytes, fkv_stream_t stream, int is_mla, bool to_gpu) {
   try {
-    t_err.clear();
+    last_error().clear();
     if (num_blocks == 0 || num_layers == 0) return 0;
     if (num_blocks < 0 || num_layers < 0)
       return fail(kInval, "negative count: num_blocks=%d num_layers=%d", num_blocks, num_layers);
@@ -1402,7 +777,7 @@ int fkv_transfer_kv_blocks(int num_blocks, int start_layer_id, int num_layers,
                            int64_t chunk_size_bytes, fkv_stream_t stream, int transfer_cus,
                            int is_host_to_device, int use_ce_transfer, int is_mla) {
   try {
-    t_err.clear();
+    last_error().clear();
     if (use_ce_transfer < FKV_XFER_KERNEL || use_ce_transfer > FKV_XFER_CE_PER_CHUNK)
       return fail(kInval, "use_ce_transfer must be 0 (kernel), 1 (CE) or 2 (CE per chunk), got %d",
                   use_ce_transfer);
@@ -1430,7 +805,7 @@ int fkv_transfer_kv_blocks_kv_ptrs(int num_blocks, int start_layer_id, int num_l
                                    fkv_stream_t stream, int transfer_cus, int is_host_to_device,
                                    int use_ce_transfer, int is_mla) {
   try {
-    t_err.clear();
+    last_error().clear();
     if (use_ce_transfer < FKV_XFER_KERNEL || use_ce_transfer > FKV_XFER_CE_PER_CHUNK)
       return fail(kInval, "use_ce_transfer must be 0 (kernel), 1 (CE) or 2 (CE per chunk), got %d",
                   use_ce_transfer);
@@ -1476,7 +851,7 @@ int fkv_transfer_kv_blocks_layerwise(
     int64_t cpu_startoff_inside_chunks, int64_t chunk_size_bytes, fkv_stream_t stream,
     int transfer_cus, int is_host_to_device, int is_mla, fkv_transfer_handle* out) {
   try {
-    t_err.clear();
+    last_error().clear();
     if (!out) return fail(kInval, "out handle pointer is null");
     *out = nullptr;
     if (layer_granularity < 1) return fail(kInval, "layer_granularity must be >= 1");
@@ -1496,9 +871,9 @@ int fkv_transfer_kv_blocks_layerwise(
           (rc = ensure_device_basics(h->dev)) ||
           (rc = layerwise_enqueue(g, s, h->dev, transfer_cus, is_host_to_device != 0,
                                   layer_granularity, h))) {
-        const std::string msg = t_err;
+        const std::string msg = last_error();
         (void)handle_destroy(h);
-        t_err = msg;
+        last_error() = msg;
         return rc;
       }
     }
@@ -1512,13 +887,13 @@ int fkv_transfer_kv_blocks_layerwise(
 }
 
 int fkv_handle_num_groups(fkv_transfer_handle h) {
-  t_err.clear();
+  last_error().clear();
   if (!h) return fail(-1, "null handle");
   return static_cast<int>(h->done.size());
 }
 
 int fkv_handle_query(fkv_transfer_handle h, int group) {
-  t_err.clear();
+  last_error().clear();
   if (!h || group < 0 || group >= static_cast<int>(h->done.size()))
     return fail(-1, "bad handle or group %d", group);
   hipError_t e = hipEventQuery(h->done[group]);
@@ -1529,7 +904,7 @@ int fkv_handle_query(fkv_transfer_handle h, int group) {
 }
 
 int fkv_handle_wait(fkv_transfer_handle h, int group) {
-  t_err.clear();
+  last_error().clear();
   if (!h || group < 0 || group >= static_cast<int>(h->done.size()))
     return fail(kInval, "bad handle or group %d", group);
   FKV_HIP(hipEventSynchronize(h->done[group]));
@@ -1537,7 +912,7 @@ int fkv_handle_wait(fkv_transfer_handle h, int group) {
 }
 
 int fkv_handle_stream_wait(fkv_transfer_handle h, int group, fkv_stream_t other) {
-  t_err.clear();
+  last_error().clear();
   if (!h || group < 0 || group >= static_cast<int>(h->done.size()))
     return fail(kInval, "bad handle or group %d", group);
   FKV_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(other), h->done[group], 0));
@@ -1545,117 +920,10 @@ int fkv_handle_stream_wait(fkv_transfer_handle h, int group, fkv_stream_t other)
 }
 
 int fkv_handle_release(fkv_transfer_handle h) {
-  t_err.clear();
+  last_error().clear();
   if (!h) return 0;
   return handle_destroy(h);
 }
 
-int fkv_stream_create(int num_cus, fkv_stream_t* out) {
-  t_err.clear();
-  if (!out) return fail(kInval, "out stream pointer is null");
-  *out = nullptr;
-  int dev = 0;
-  FKV_HIP(hipGetDevice(&dev));
-  int ncu = 0;
-  FKV_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
-  if (num_cus < 0 || num_cus > ncu)
-    return fail(kInval, "num_cus must be in [0, %d], got %d", ncu, num_cus);
-  const int use = num_cus == 0 ? ncu : num_cus;
-  std::vector<uint32_t> mask(static_cast<size_t>((ncu + 31) / 32), 0u);
-  for (int c = 0; c < use; ++c) mask[c / 32] |= 1u << (c % 32);
-  hipStream_t st = nullptr;
-  FKV_HIP(hipExtStreamCreateWithCUMask(&st, static_cast<uint32_t>(mask.size()), mask.data()));
-  *out = st;
-  return 0;
-}
-
-int fkv_stream_destroy(fkv_stream_t s) {
-  t_err.clear();
-  if (s) FKV_HIP(hipStreamDestroy(static_cast<hipStream_t>(s)));
-  return 0;
-}
-
-const char* fkv_last_error(void) { return t_err.c_str(); }
-
-int fkv_host_alloc(void** out_ptr, size_t bytes, unsigned flags) {
-  t_err.clear();
-  if (!out_ptr) return fail(kInval, "out_ptr is null");
-  *out_ptr = nullptr;
-  if (bytes == 0) return fail(kInval, "zero-byte host allocation");
-  unsigned hf = hipHostMallocPortable | hipHostMallocMapped;
-  if (flags == FKV_HOST_COHERENT) hf |= hipHostMallocCoherent;
-  else if (flags == FKV_HOST_NONCOHERENT) hf |= hipHostMallocNonCoherent;
-  else if (flags != FKV_HOST_DEFAULT) return fail(kInval, "unknown host alloc flags %u", flags);
-  FKV_HIP(hipHostMalloc(out_ptr, bytes, hf));
-  return 0;
-}
-
-int fkv_host_free(void* ptr) {
-  t_err.clear();
-  if (!ptr) return 0;
-  FKV_HIP(hipHostFree(ptr));
-  return 0;
-}
-
-int fkv_host_register(void* ptr, size_t bytes, unsigned flags) {
-  t_err.clear();
-  (void)flags;
-  if (!ptr || bytes == 0) return fail(kInval, "null or empty range");
-  PtrInfo pi;
-  if (query_ptr(ptr, &pi) != 0 || !pi.host)
-    return fail(kInval,
-                "host range %p is not pinned; allocate the host cache pinned "
-                "(fkv_host_alloc or pin_memory=True) instead of registering pageable memory",
-                ptr);
-  if (!range_inside(static_cast<char*>(ptr), 0, static_cast<__int128>(bytes), pi))
-    return fail(kInval, "host range %p + %zu exceeds its pinned allocation (%zu bytes)", ptr,
-                bytes, pi.size);
-  return 0;
-}
-
-int fkv_host_unregister(void* ptr) {
-  (void)ptr;
-  t_err.clear();
-  return 0;
-}
-
-int fkv_set_staging_bytes(size_t bytes) {
-  t_err.clear();
-  g_staging_request.store(bytes);
-  return 0;
-}
-
-int fkv_release_staging(void) {
-  t_err.clear();
-  for (int dev = 0; dev < kMaxDevices; ++dev) {
-    DeviceState& d = g_dev[dev];
-    std::lock_guard<std::mutex> lk(d.mu);
-    if (d.staging) {
-      DeviceGuard guard;
-      int rc = guard.set(dev);
-      if (rc) return rc;
-      FKV_HIP(hipFree(d.staging));
-      d.staging = nullptr;
-      d.staging_bytes = 0;
-    }
-  }
-  return 0;
-}
-
-int fkv_profile_enable(int on) {
-  std::lock_guard<std::mutex> lk(g_prof_mu);
-  g_prof = fkv_profile{};
-  g_prof_on.store(on != 0);
-  return 0;
-}
-
-int fkv_profile_read(fkv_profile* out) {
-  if (!out) return kInval;
-  std::lock_guard<std::mutex> lk(g_prof_mu);
-  *out = g_prof;
-  return 0;
-}
-
-const char* fkv_version(void) { return "flexkv_hip 0.1 gfx950"; }
 
 }  // extern "C"
