@@ -194,16 +194,43 @@ int stream_device(hipStream_t s, int* dev);
 // ---------------------------------------------------------------------------
 // Copy engines (kv_sdma.cpp)
 
-// One contiguous DMA between staging and the host cache.
+// One DMA between staging and the host cache: `bytes` contiguous bytes or,
+// with slices > 0, `slices` pieces of `bytes` each, back to back in staging
+// and `host_pitch` apart in the host cache (one rect copy).
 struct Run {
   int64_t staging_off;
   char* host;
   int64_t bytes;
+  int32_t slices = 0;
+  int64_t host_pitch = 0;
 };
 
+// The host-side distance between consecutive (layer, K|V) chunks of a block
+// when an `nl`-layer window of the block is not one contiguous run but its
+// chunks still lie at one stride (layer-wise host layouts
+// [layer][K|V][block][chunk], MLA), so one rect copy moves the window; else 0.
+inline int64_t host_slice_pitch(const Geometry& g, int nl) {
+  const bool row_contig = (g.kv == 1 || g.cks == g.chunk) && (nl == 1 || g.cls == g.kv * g.chunk);
+  if (row_contig) return 0;
+  int64_t pitch = 0;
+  if (g.kv == 1)
+    pitch = g.cls;                      // slice = layer
+  else if (nl == 1)
+    pitch = g.cks;                      // slice = K|V
+  else if (g.cls == g.kv * g.cks)
+    pitch = g.cks;                      // slice = layer * kv + K|V
+  return pitch >= g.chunk ? pitch : 0;
+}
+
 // Host runs for blocks [b0, b0+nb) of a piece whose staging layout is
-// [block][layer][kv][chunk] over `nl` layers starting at `l0`.
-void build_runs(const Geometry& g, int b0, int nb, int l0, int nl, std::vector<Run>& runs);
+// [block][layer][kv][chunk] over `nl` layers starting at `l0`: maximal
+// contiguous runs when block rows are contiguous in the host cache, one rect
+// copy per block when `rect` and host_slice_pitch() allows it, else one run
+// per chunk.
+void build_runs(const Geometry& g, int b0, int nb, int l0, int nl, bool rect,
+                std::vector<Run>& runs);
+// Whether the HSA runtime offers rect copies (after ensure_sdma).
+bool sdma_rect_available();
 // HSA agents and SDMA engines for the copy-engine path on device `dev`, found
 // through `hip_ptr`, a device allocation HIP made on `dev`.
 int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr);

@@ -41,6 +41,7 @@ struct HsaApi {
   decltype(&::hsa_signal_wait_scacquire) signal_wait_scacquire = nullptr;
   decltype(&::hsa_amd_memory_copy_engine_status) copy_engine_status = nullptr;
   decltype(&::hsa_amd_memory_async_copy_on_engine) async_copy_on_engine = nullptr;
+  decltype(&::hsa_amd_memory_async_copy_rect) async_copy_rect = nullptr;   // optional
 };
 HsaApi g_hsa;
 
@@ -104,6 +105,8 @@ int load_hsa(const void* hip_ptr) {
   sym(a.copy_engine_status, "hsa_amd_memory_copy_engine_status");
   sym(a.async_copy_on_engine, "hsa_amd_memory_async_copy_on_engine");
   if (missing) return fail(kInval, "the HSA runtime lacks %d entry points", missing);
+  a.async_copy_rect = reinterpret_cast<decltype(a.async_copy_rect)>(
+      dlsym(lib, "hsa_amd_memory_async_copy_rect"));
   g_hsa = a;
   g_hsa_loaded = true;
   return 0;
@@ -139,11 +142,23 @@ void sdma_wait(DeviceState& d, int half) {
   d.in_flight[half] = 0;
 }
 
-void build_runs(const Geometry& g, int b0, int nb, int l0, int nl, std::vector<Run>& runs) {
+void build_runs(const Geometry& g, int b0, int nb, int l0, int nl, bool rect,
+                std::vector<Run>& runs) {
   runs.clear();
   const int64_t row_chunks = static_cast<int64_t>(nl) * g.kv;
   const bool row_contig = (g.kv == 1 || g.cks == g.chunk) && (nl == 1 || g.cls == g.kv * g.chunk);
+  const int64_t pitch = rect ? host_slice_pitch(g, nl) : 0;
   char* host0 = g.cpu_ptr + g.startoff + static_cast<int64_t>(g.start_layer + l0) * g.cls;
+  if (pitch > 0) {
+    for (int i = b0; i < b0 + nb; ++i) {
+      Run r{static_cast<int64_t>(i - b0) * row_chunks * g.chunk, host0 + g.cids[i] * g.cbs,
+            g.chunk};
+      r.slices = static_cast<int32_t>(row_chunks);
+      r.host_pitch = pitch;
+      runs.push_back(r);
+    }
+    return;
+  }
   int64_t soff = 0;
   auto push = [&](char* h, int64_t bytes) {
     if (!runs.empty() && runs.back().host + runs.back().bytes == h &&
@@ -238,24 +253,39 @@ int issue_sdma(DeviceState& d, const std::vector<Run>& runs, char* staging, bool
   for (size_t i = 0; i < runs.size(); ++i) {
     const Run& r = runs[i];
     char* dev_p = staging + r.staging_off;
-    const hsa_amd_sdma_engine_id_t e = eng[i % eng.size()];
     g_hsa.signal_store_screlease(sigs[i], 1);
-    const hsa_status_t st =
-        h2d ? g_hsa.async_copy_on_engine(dev_p, d.gpu_agent, r.host, host_agent,
-                                         static_cast<size_t>(r.bytes), 0, nullptr, sigs[i], e,
-                                         false)
-            : g_hsa.async_copy_on_engine(r.host, host_agent, dev_p, d.gpu_agent,
-                                         static_cast<size_t>(r.bytes), 0, nullptr, sigs[i], e,
-                                         false);
+    hsa_status_t st;
+    if (r.slices > 0) {
+      // the runtime puts rect copies on the device's own engine for the direction
+      hsa_pitched_ptr_t hp{r.host, static_cast<size_t>(r.bytes), static_cast<size_t>(r.host_pitch)};
+      hsa_pitched_ptr_t sp{dev_p, static_cast<size_t>(r.bytes), static_cast<size_t>(r.bytes)};
+      const hsa_dim3_t zero{0, 0, 0};
+      const hsa_dim3_t range{static_cast<uint32_t>(r.bytes), 1, static_cast<uint32_t>(r.slices)};
+      st = h2d ? g_hsa.async_copy_rect(&sp, &zero, &hp, &zero, &range, d.gpu_agent,
+                                       hsaHostToDevice, 0, nullptr, sigs[i])
+               : g_hsa.async_copy_rect(&hp, &zero, &sp, &zero, &range, d.gpu_agent,
+                                       hsaDeviceToHost, 0, nullptr, sigs[i]);
+    } else {
+      const hsa_amd_sdma_engine_id_t e = eng[i % eng.size()];
+      st = h2d ? g_hsa.async_copy_on_engine(dev_p, d.gpu_agent, r.host, host_agent,
+                                            static_cast<size_t>(r.bytes), 0, nullptr, sigs[i], e,
+                                            false)
+               : g_hsa.async_copy_on_engine(r.host, host_agent, dev_p, d.gpu_agent,
+                                            static_cast<size_t>(r.bytes), 0, nullptr, sigs[i], e,
+                                            false);
+    }
     if (st != HSA_STATUS_SUCCESS) {
       const char* m = nullptr;
       (void)g_hsa.status_string(st, &m);
-      return fail(static_cast<int>(hipErrorUnknown), "SDMA copy of %lld bytes failed: %s",
-                  static_cast<long long>(r.bytes), m ? m : "?");
+      return fail(static_cast<int>(hipErrorUnknown), "SDMA %s of %lld bytes x %d failed: %s",
+                  r.slices > 0 ? "rect copy" : "copy", static_cast<long long>(r.bytes),
+                  std::max(1, static_cast<int>(r.slices)), m ? m : "?");
     }
     d.in_flight[half] = i + 1;
   }
   return 0;
 }
+
+bool sdma_rect_available() { return g_hsa.async_copy_rect != nullptr; }
 
 }  // namespace fkv_detail

@@ -430,8 +430,8 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   auto queue_copies = [&](int pi) -> int {
     const Piece& p = pieces[pi];
     const int h = pi & 1;
-    build_runs(g, p.b0, p.nb, p.l0, p.nl, runs);
-    for (const Run& r : runs) dma_bytes += r.bytes;
+    build_runs(g, p.b0, p.nb, p.l0, p.nl, sdma_rect_available(), runs);
+    for (const Run& r : runs) dma_bytes += r.bytes * std::max<int64_t>(1, r.slices);
     dma_copies += static_cast<int64_t>(runs.size());
     pending[h] = true;
     return issue_sdma(d, runs, d.staging + h * half, h2d, h, host_agent);
@@ -727,11 +727,13 @@ Geometry make_geometry(int num_blocks, int start_layer_id, int num_layers,
 
 // Copy-engine mode hands a transfer to the SDMA engines only when the
 // engines pay off: the op moves at least FLEXKV_CE_MIN_BYTES (default 8 MiB)
-// and its contiguous host runs are at least 128 KiB.  Each engine copy costs
-// about 6 us and the host-side ordering about 40 us per call (MI355X: a
-// 1 MiB op of 64 KiB runs takes 77 us on the engines, 39 us in the zero-copy
-// kernel); smaller or finer-grained transfers, and caches in device memory,
-// go to the zero-copy kernel, with identical results.
+// and each engine copy moves at least 128 KiB: a contiguous host run, or one
+// block's layer window as a rect copy when the host layout puts its chunks at
+// one stride (layer-wise).  Each engine copy costs about 6 us and the
+// host-side ordering about 40 us per call (MI355X: a 1 MiB op of 64 KiB runs
+// takes 77 us on the engines, 39 us in the zero-copy kernel); smaller or
+// finer-grained transfers, and caches in device memory, go to the zero-copy
+// kernel, with identical results.
 constexpr int64_t kCeMinBytesDefault = int64_t(8) << 20;
 constexpr int64_t kCeMinRunBytes = int64_t(128) << 10;
 
@@ -743,7 +745,8 @@ bool ce_pays_off(const Geometry& g) {
   const int64_t total = static_cast<int64_t>(g.num_blocks) * g.num_layers * g.kv * g.chunk;
   const bool row_contig = (g.kv == 1 || g.cks == g.chunk) &&
                           (g.num_layers == 1 || g.cls == g.kv * g.chunk);
-  const int64_t run = row_contig ? static_cast<int64_t>(g.num_layers) * g.kv * g.chunk : g.chunk;
+  const int64_t row = static_cast<int64_t>(g.num_layers) * g.kv * g.chunk;
+  const int64_t run = (row_contig || host_slice_pitch(g, g.num_layers) > 0) ? row : g.chunk;
   return total >= min_bytes && (min_bytes == 0 || run >= kCeMinRunBytes);
 }
 

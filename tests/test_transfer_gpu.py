@@ -143,23 +143,27 @@ def test_geometries_match_oracle(dev, geo, mode):
 
 
 @pytest.mark.parametrize("h2d", [False, True])
-@pytest.mark.parametrize("layout", ["BLOCKWISE", "LAYERWISE"])
-def test_copy_engine_size_policy(dev, h2d, layout, monkeypatch):
-    """Copy-engine mode sends transfers under FLEXKV_CE_MIN_BYTES, or with
-    host runs under 128 KiB (layer-wise host layout: one 32 KiB chunk per
-    run), to the zero-copy kernel and the rest to the SDMA engines; 0 forces
-    the engines.  The bytes are the same either way.  The library's profile
-    counts SDMA batches."""
+@pytest.mark.parametrize("layout,heads", [("BLOCKWISE", 8), ("LAYERWISE", 8), ("BLOCKWISE", 1),
+                                          ("LAYERWISE", 1)])
+def test_copy_engine_size_policy(dev, h2d, layout, heads, monkeypatch):
+    """Copy-engine mode sends transfers under FLEXKV_CE_MIN_BYTES, or whose
+    engine copies would move under 128 KiB each, to the zero-copy kernel and
+    the rest to the SDMA engines; 0 forces the engines.  An engine copy is a
+    contiguous host run (block-wise host: a block's 4 layers) or one block's
+    chunks as a rect copy (layer-wise host): 256 KiB with 32 KiB chunks, 32 KiB
+    with 4 KiB chunks.  The bytes are the same either way.  The library's
+    profile counts SDMA batches."""
     from flexkv_amd import _lib
     from gpu_util import DeviceCase, abi_transfer
     case = KVCase(layers_total=4, num_layers=4, start_layer=0, kv=2, ng=64, nh=96, tokens=16,
-                  heads=8, dim=128, layout=layout).fill(seed=31)   # 32 KiB chunks
-    n = 20                                                          # 5 MiB moved
+                  heads=heads, dim=128, layout=layout).fill(seed=31)   # 32 or 4 KiB chunks
+    n = 20
     gids = inputs.distinct_ids(3, n, 64)
     cids = inputs.distinct_ids(4, n, 96)
     want = _oracle_d2h(case, gids, cids, 1)
-    total = n * 4 * 2 * 32768
-    rows = layout == "BLOCKWISE"
+    chunk = 16 * heads * 128 * 2
+    total = n * 4 * 2 * chunk
+    rows = 4 * 2 * chunk >= 128 << 10
     for env, engines in (("0", True), (None, False), (str(total), rows), (str(total + 1), False)):
         if env is None:
             monkeypatch.delenv("FLEXKV_CE_MIN_BYTES", raising=False)
@@ -182,6 +186,44 @@ def test_copy_engine_size_policy(dev, h2d, layout, monkeypatch):
                 expect = np.zeros_like(case.gpu[l])
                 expect[:, gids] = case.gpu[l][:, gids]
                 assert np.array_equal(g, expect), f"layer {l}"
+
+
+@pytest.mark.parametrize("mla,window", [(False, (0, 5)), (False, (2, 1)), (True, (0, 5)),
+                                        (False, (1, 3))])
+def test_layerwise_host_copy_engines_one_rect_per_block(dev, mla, window):
+    """On a layer-wise host cache ([layer][K|V][block][chunk]) copy-engine
+    mode moves each block's layer window with one rect copy: as many SDMA
+    copies as blocks in both directions; the host cache equals the oracle's
+    byte for byte and the round trip restores the blocks."""
+    from flexkv_amd import _lib
+    from gpu_util import DeviceCase, abi_transfer
+    start, nl = window
+    case = KVCase(layers_total=6, num_layers=nl, start_layer=start, kv=1 if mla else 2, ng=48,
+                  nh=80, tokens=16, heads=4, dim=128, layout="LAYERWISE").fill(seed=37)
+    n = 23
+    gids = inputs.distinct_ids(7, n, 48)
+    cids = inputs.distinct_ids(8, n, 80)
+    print(f"rect mla={mla} window={window}", flush=True)
+    dc = DeviceCase(case)
+    _lib.profile_enable(True)
+    abi_transfer(dc, gids, cids, h2d=False, mode=1)
+    prof = _lib.profile_read()
+    torch.cuda.synchronize()
+    assert prof["dma_copies"] == n, prof
+    assert np.array_equal(dc.host_np(), _oracle_d2h(case, gids, cids, 1))
+    zero = [np.zeros_like(g) for g in case.gpu]
+    dc.set_gpu(zero)
+    _lib.profile_enable(True)
+    abi_transfer(dc, gids, cids, h2d=True, mode=1)
+    prof = _lib.profile_read()
+    _lib.profile_enable(False)
+    torch.cuda.synchronize()
+    assert prof["dma_copies"] == n, prof
+    # the round trip restores the moved blocks into the zeroed layers
+    for l, g in enumerate(dc.gpu_np()):
+        expect = np.zeros_like(case.gpu[l])
+        expect[:, gids] = case.gpu[l][:, gids]
+        assert np.array_equal(g, expect), f"layer {l}"
 
 
 @pytest.mark.parametrize("mode", MODES)
