@@ -12,7 +12,8 @@ both directions use the copy-engine path: on MI355X it moves whole-block
 transfers as fast as the zero-copy kernel (56.3 / 56.6 GB/s against 56.5 /
 57.2) while leaving the compute units to the model (GEMMs beside a 2 GiB D2H
 slow down 7% instead of 120%), and it hands small or fine-grained transfers to
-the zero-copy kernel by itself.
+the zero-copy kernel by itself.  With a LAYERWISE host cache the copy engines
+move one rect copy per block at about 44 GB/s.
 """
 from __future__ import annotations
 
