@@ -6,7 +6,6 @@ import re
 import subprocess
 
 import numpy as np
-import pytest
 
 from flexkv_amd import _lib
 

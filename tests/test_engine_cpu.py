@@ -10,8 +10,7 @@ from flexkv_amd.cache.transfer_pattern import (add_virtual_op_for_multiple_finis
                                                convert_read_graph_to_layer_wise_graph,
                                                create_read_graph_cpu_storage,
                                                create_write_graph_cpu_storage)
-from flexkv_amd.common.transfer import (TransferOp, TransferOpGraph, TransferOpStatus,
-                                        TransferType)
+from flexkv_amd.common.transfer import TransferOp, TransferOpGraph, TransferType
 from flexkv_amd.transfer.scheduler import TransferScheduler
 
 

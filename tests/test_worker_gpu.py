@@ -3,13 +3,12 @@ check (tests/test_transfer_engine.py:55-161 with tests/test_utils.py:133-204),
 in process and through a spawned worker fed TensorSharedHandles."""
 import multiprocessing as mp
 
-import numpy as np
 import pytest
 import torch
 
 from gpu_util import zero_blocks
 from flexkv_amd.common.storage import KVCacheLayout, KVCacheLayoutType
-from flexkv_amd.common.transfer import DeviceType, TransferDescriptor, TransferOp, TransferType
+from flexkv_amd.common.transfer import TransferDescriptor, TransferOp, TransferType
 from flexkv_amd.storage.allocator import CPUAllocator
 from flexkv_amd.transfer.worker import GPUCPUTransferWorker, WorkerTransferOp
 
