@@ -222,12 +222,20 @@ inline int64_t host_slice_pitch(const Geometry& g, int nl) {
   return pitch >= g.chunk ? pitch : 0;
 }
 
-// Host runs for blocks [b0, b0+nb) of a piece whose staging layout is
-// [block][layer][kv][chunk] over `nl` layers starting at `l0`: maximal
-// contiguous runs when block rows are contiguous in the host cache, one rect
-// copy per block when `rect` and host_slice_pitch() allows it, else one run
-// per chunk.
-void build_runs(const Geometry& g, int b0, int nb, int l0, int nl, bool rect,
+// Whether a layer-wise host cache's ids come in runs of consecutive blocks
+// long enough that staging the blocks layer-major ([layer][K|V][block][chunk])
+// and copying each (layer, K|V) run linearly beats one rect copy per block:
+// the host block stride is one chunk and the average run moves at least
+// `min_run_bytes`.
+bool layer_major_pays_off(const Geometry& g, int64_t min_run_bytes);
+
+// Host runs for blocks [b0, b0+nb) of a piece over `nl` layers starting at
+// `l0`.  Staging block-major ([block][layer][K|V][chunk]): maximal contiguous
+// runs when block rows are contiguous in the host cache, one rect copy per
+// block when `rect` and host_slice_pitch() allows it, else one run per chunk.
+// Staging layer-major ([layer][K|V][block][chunk], `layer_major`): for each
+// (layer, K|V), maximal runs of consecutive host blocks.
+void build_runs(const Geometry& g, int b0, int nb, int l0, int nl, bool rect, bool layer_major,
                 std::vector<Run>& runs);
 // Whether the HSA runtime offers rect copies (after ensure_sdma).
 bool sdma_rect_available();

@@ -142,13 +142,36 @@ void sdma_wait(DeviceState& d, int half) {
   d.in_flight[half] = 0;
 }
 
-void build_runs(const Geometry& g, int b0, int nb, int l0, int nl, bool rect,
+bool layer_major_pays_off(const Geometry& g, int64_t min_run_bytes) {
+  const bool row_contig = (g.kv == 1 || g.cks == g.chunk) &&
+                          (g.num_layers == 1 || g.cls == g.kv * g.chunk);
+  if (row_contig || g.cbs != g.chunk || g.num_blocks < 2) return false;
+  int64_t runs = 1;
+  for (int i = 1; i < g.num_blocks; ++i) runs += g.cids[i] != g.cids[i - 1] + 1;
+  return static_cast<int64_t>(g.num_blocks) * g.chunk >= runs * min_run_bytes;
+}
+
+void build_runs(const Geometry& g, int b0, int nb, int l0, int nl, bool rect, bool layer_major,
                 std::vector<Run>& runs) {
   runs.clear();
   const int64_t row_chunks = static_cast<int64_t>(nl) * g.kv;
   const bool row_contig = (g.kv == 1 || g.cks == g.chunk) && (nl == 1 || g.cls == g.kv * g.chunk);
   const int64_t pitch = rect ? host_slice_pitch(g, nl) : 0;
   char* host0 = g.cpu_ptr + g.startoff + static_cast<int64_t>(g.start_layer + l0) * g.cls;
+  if (layer_major) {
+    int64_t soff = 0;
+    for (int l = 0; l < nl; ++l)
+      for (int k = 0; k < g.kv; ++k)
+        for (int i = b0; i < b0 + nb; ++i, soff += g.chunk) {
+          char* h = host0 + l * g.cls + k * g.cks + g.cids[i] * g.cbs;
+          if (i > b0 && runs.back().host + runs.back().bytes == h) {
+            runs.back().bytes += g.chunk;   // staging is contiguous along i
+          } else {
+            runs.push_back({soff, h, g.chunk});
+          }
+        }
+    return;
+  }
   if (pitch > 0) {
     for (int i = b0; i < b0 + nb; ++i) {
       Run r{static_cast<int64_t>(i - b0) * row_chunks * g.chunk, host0 + g.cids[i] * g.cbs,

@@ -109,6 +109,10 @@ constexpr int kAutoZeroCopyCus = 8;
 // Llama-3-8B load overlapped with per-layer GEMMs finishes in 42.8 ms on 2
 // CUs against 46.1 ms on 8.
 constexpr int kAutoLayerwiseH2DCus = 2;
+// Copy-engine size policy: smallest transfer, and smallest bytes per engine
+// copy, worth handing to the SDMA engines (ce_pays_off).
+constexpr int64_t kCeMinBytesDefault = int64_t(8) << 20;
+constexpr int64_t kCeMinRunBytes = int64_t(128) << 10;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // Every address the kernel touches is global memory (HBM or mapped pinned
@@ -407,6 +411,14 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   const int blocks_per_piece = static_cast<int>(std::max<size_t>(1, half / row_bytes));
   const int grid_cap = d.num_cus * (h2d ? d.occ_staged[1] : d.occ_staged[0]);
   const hsa_agent_t host_agent = d.cpu_agent;   // device-resident caches never get here
+  // Staging order: block-major [block][layer][K|V][chunk] (contiguous block
+  // rows, or one rect copy per block of a layer-wise cache), or layer-major
+  // [layer][K|V][block][chunk] when a layer-wise cache's ids come in runs of
+  // consecutive blocks long enough to copy each (layer, K|V) run linearly.
+  // FLEXKV_CE_LAYER_RUN_BYTES overrides the average run (default 128 KiB)
+  const char* lr = getenv("FLEXKV_CE_LAYER_RUN_BYTES");
+  const bool layer_major =
+      layer_major_pays_off(g, lr ? std::max<int64_t>(1, atoll(lr)) : kCeMinRunBytes);
 
   struct Piece {
     int l0, nl, b0, nb;
@@ -430,7 +442,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   auto queue_copies = [&](int pi) -> int {
     const Piece& p = pieces[pi];
     const int h = pi & 1;
-    build_runs(g, p.b0, p.nb, p.l0, p.nl, sdma_rect_available(), runs);
+    build_runs(g, p.b0, p.nb, p.l0, p.nl, sdma_rect_available(), layer_major, runs);
     for (const Run& r : runs) dma_bytes += r.bytes * std::max<int64_t>(1, r.slices);
     dma_copies += static_cast<int64_t>(runs.size());
     pending[h] = true;
@@ -438,10 +450,18 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   };
   auto launch = [&](int pi) -> int {
     const Piece& p = pieces[pi];
-    const int64_t cls = static_cast<int64_t>(g.kv) * g.chunk;   // staging layer stride
-    const int64_t cbs = static_cast<int64_t>(p.nl) * cls;       // staging block stride
+    // staging strides (K|V, layer, block) of the piece
+    int64_t cks, cls, cbs;
+    if (layer_major) {
+      cbs = g.chunk;
+      cks = g.kv == 1 ? 0 : static_cast<int64_t>(p.nb) * g.chunk;
+      cls = static_cast<int64_t>(g.kv) * p.nb * g.chunk;
+    } else {
+      cks = g.kv == 1 ? 0 : g.chunk;
+      cls = static_cast<int64_t>(g.kv) * g.chunk;
+      cbs = static_cast<int64_t>(p.nl) * cls;
+    }
     char* stg = d.staging + (pi & 1) * half;
-    const int64_t cks = g.kv == 1 ? 0 : g.chunk;
     return h2d ? launch_copy<true, true>(g, ids_dev, stg, cks, cls, cbs, p.b0, p.nb, p.l0, p.nl,
                                          grid_cap, stream, prof)
                : launch_copy<false, true>(g, ids_dev, stg, cks, cls, cbs, p.b0, p.nb, p.l0, p.nl,
@@ -734,9 +754,6 @@ Geometry make_geometry(int num_blocks, int start_layer_id, int num_layers,
 // takes 77 us on the engines, 39 us in the zero-copy kernel); smaller or
 // finer-grained transfers, and caches in device memory, go to the zero-copy
 // kernel, with identical results.
-constexpr int64_t kCeMinBytesDefault = int64_t(8) << 20;
-constexpr int64_t kCeMinRunBytes = int64_t(128) << 10;
-
 bool ce_pays_off(const Geometry& g) {
   // a "host" cache that is device memory has no PCIe copy to offload
   if (g.cpu_info.device) return false;

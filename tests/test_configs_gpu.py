@@ -153,17 +153,23 @@ class TestLlama3_8B:
         _round_trip(llama8b, runs(4096), runs(16384), ce)
 
 
+@pytest.mark.parametrize("run", [1, 8, 1024])
 @pytest.mark.parametrize("ce", [False, True])
-def test_llama3_8b_layerwise_host(ce):
-    """The same 1024 random ids against a layer-wise host cache
-    [32,2,16384,16,8,128] (the reference's default layout): the zero-copy
-    kernel, and copy-engine mode with one SDMA rect copy per block."""
+def test_llama3_8b_layerwise_host(ce, run):
+    """1024 ids in runs of `run` consecutive blocks against a layer-wise host
+    cache [32,2,16384,16,8,128] (the reference's default layout): the
+    zero-copy kernel, and copy-engine mode (one SDMA rect copy per block for
+    scattered ids, layer-major staging and one copy per (layer, K|V) run for
+    runs of 8 and more)."""
     case = FullCase(32, 2, 4096, 16384, 16, 8, 128, seed=1003, host_layout="LAYERWISE")
     try:
-        g = torch.Generator().manual_seed(1004)
-        gids = torch.randperm(4096, generator=g)[:1024]
-        cids = torch.randperm(16384, generator=g)[:1024]
-        _round_trip(case, gids, cids, ce)
+        g = torch.Generator().manual_seed(1004 + run)
+
+        def runs(universe):
+            slots = torch.randperm(universe // run, generator=g)[: 1024 // run]
+            return (slots[:, None] * run + torch.arange(run)[None, :]).reshape(-1)
+
+        _round_trip(case, runs(4096), runs(16384), ce)
     finally:
         case.free()
 

@@ -226,6 +226,48 @@ def test_layerwise_host_copy_engines_one_rect_per_block(dev, mla, window):
         assert np.array_equal(g, expect), f"layer {l}"
 
 
+@pytest.mark.parametrize("mla", [False, True])
+def test_layerwise_host_id_runs_stage_layer_major(dev, mla, monkeypatch):
+    """On a layer-wise host cache whose ids come in runs of consecutive blocks
+    (average run at least FLEXKV_CE_LAYER_RUN_BYTES), copy-engine mode stages
+    the blocks layer-major and copies each run of each (layer, K|V) linearly:
+    runs x layers x K|V SDMA copies instead of one rect copy per block.
+    Bytes as the oracle's, and the round trip restores the blocks."""
+    from flexkv_amd import _lib
+    from gpu_util import DeviceCase, abi_transfer
+    kv = 1 if mla else 2
+    case = KVCase(layers_total=5, num_layers=4, start_layer=1, kv=kv, ng=64, nh=96, tokens=16,
+                  heads=4, dim=128, layout="LAYERWISE").fill(seed=43)   # 16 KiB chunks
+    chunk = 16 * 4 * 128 * 2
+    cids = np.concatenate([np.arange(10, 18), np.arange(40, 52), np.arange(70, 75)])
+    n = len(cids)                                     # 3 runs, 25 blocks
+    gids = inputs.distinct_ids(9, n, 64)
+    monkeypatch.setenv("FLEXKV_CE_LAYER_RUN_BYTES", str(4 * chunk))
+    for order, ids, copies in (("layer-major", cids, 3 * 4 * kv),
+                               ("rect", inputs.distinct_ids(10, n, 96), n)):
+        print(f"runs mla={mla} order={order}", flush=True)
+        ids = np.ascontiguousarray(ids, dtype=np.int64)
+        dc = DeviceCase(case)
+        _lib.profile_enable(True)
+        abi_transfer(dc, gids, ids, h2d=False, mode=1)
+        prof = _lib.profile_read()
+        torch.cuda.synchronize()
+        assert prof["dma_copies"] == copies, (order, prof)
+        assert np.array_equal(dc.host_np(), _oracle_d2h(case, gids, ids, 1))
+        zero = [np.zeros_like(g) for g in case.gpu]
+        dc.set_gpu(zero)
+        _lib.profile_enable(True)
+        abi_transfer(dc, gids, ids, h2d=True, mode=1)
+        prof = _lib.profile_read()
+        _lib.profile_enable(False)
+        torch.cuda.synchronize()
+        assert prof["dma_copies"] == copies, (order, prof)
+        for l, g in enumerate(dc.gpu_np()):
+            expect = np.zeros_like(case.gpu[l])
+            expect[:, gids] = case.gpu[l][:, gids]
+            assert np.array_equal(g, expect), f"{order} layer {l}"
+
+
 @pytest.mark.parametrize("mode", MODES)
 def test_device_resident_cache_matches_oracle(dev, mode):
     """A "host" cache that lives in device memory (allowed by the API) moves
