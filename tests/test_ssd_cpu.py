@@ -154,6 +154,55 @@ def test_oracle_mapping_is_a_striping_bijection(D, F, rr):
         assert locs == sorted(locs)
 
 
+def _layerwise_view_ok(c, sids, cids):
+    """The layer-wise pin: file (dev, file) slot `slot` of each written block
+    holds the block's [layer][K|V] chunks, with the mapping of _mapping()."""
+    kv = 1 if c["mla"] else 2
+    chunk = c["cpu"].get_chunk_size() * c["es"]
+    nbf = c["per_file"].num_block
+    h = c["host"].reshape(c["L"], kv, c["N_cpu"], chunk)
+    for sb, ci in zip(sids, cids):
+        dev, fi, slot = _mapping(int(sb), 1, c["D"], c["F"])
+        f = c["files"][dev * c["F"] + fi].reshape(c["L"], kv, nbf, chunk)
+        if not np.array_equal(f[:, :, slot], h[:, :, ci]):
+            return False
+    return True
+
+
+def test_oracle_planted_mistakes_are_caught():
+    """Each plausible mistake, planted by calling the oracle with a wrong
+    argument, breaks the layer-wise file view that pins the SSD oracle:
+    layer and K|V strides transposed, a round-robin width other than the
+    worker's, MLA taken for K/V, a dropped start layer."""
+    def run(**wrong):
+        c = _oracle_roundtrip_case(LW, 2, 2, 1, False, 6)
+        sids = np.array([0, 5, 6, 11, 14, 3], np.int64)
+        cids = np.array([2, 9, 4, 0, 7, 11], np.int64)
+        es = c["es"]
+        args = dict(cpu_layer=c["cpu"].get_layer_stride() * es,
+                    cpu_kv=c["cpu"].get_kv_stride() * es,
+                    ssd_layer=c["per_file"].get_layer_stride() * es,
+                    ssd_kv=c["per_file"].get_kv_stride() * es, rr=1, mla=False, start=0)
+        args.update(wrong)
+        oracle.transfer_kv_blocks_ssd(
+            c["files"], c["D"], c["F"], args["start"], c["L"] - args["start"], c["host"], sids,
+            cids, args["cpu_layer"], args["cpu_kv"], args["ssd_layer"], args["ssd_kv"],
+            c["cpu"].get_chunk_size() * es, c["cpu"].get_block_stride() * es, False,
+            round_robin=args["rr"], is_mla=args["mla"])
+        return _layerwise_view_ok(c, sids, cids)
+
+    assert run()
+    c0 = _oracle_roundtrip_case(LW, 2, 2, 1, False, 6)
+    es = c0["es"]
+    lay, kvs = c0["cpu"].get_layer_stride() * es, c0["cpu"].get_kv_stride() * es
+    slay, skv = c0["per_file"].get_layer_stride() * es, c0["per_file"].get_kv_stride() * es
+    assert not run(cpu_layer=kvs, cpu_kv=lay)            # transposed host strides
+    assert not run(ssd_layer=skv, ssd_kv=slay)           # transposed file strides
+    assert not run(rr=2)                                 # wrong round-robin width
+    assert not run(mla=True)                             # V half dropped
+    assert not run(start=1)                              # layer 0 skipped
+
+
 @pytest.mark.parametrize("layout_type", [LW, BW])
 @pytest.mark.parametrize("mla", [False, True])
 def test_oracle_write_read_round_trip(layout_type, mla):
