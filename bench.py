@@ -94,6 +94,7 @@ class Workload:
         if host:
             log(f"pinned host cache {self.host.numel() * 2 / 2**30:.2f} GiB in "
                 f"{time.time() - t0:.1f}s")
+        self.seed = seed
         cpu_gen = torch.Generator().manual_seed(seed + 1)
         n = w["n"]
         if run:
@@ -389,6 +390,55 @@ def call_latency(wl: Workload, reps: int = 200):
                                          wl.cblk, wl.chunk, 0, -1, i % 2 == 0, ce, wl.mla)
                 ts.append(time.perf_counter() - t0)
             out[f"{path}_{nb}blk_{nl}layer_us"] = round(statistics.median(ts[5:]) * 1e6, 1)
+    return out
+
+
+def duplex(wl: Workload, reps: int = 3):
+    """A D2H of the step's blocks and an H2D of as many other blocks (other
+    GPU and host ids) at once, from two host threads on two streams, per
+    path: aggregate GB/s over both directions (best of `reps`).  PCIe is
+    full duplex; each copy-engine direction has its own staging and
+    engines."""
+    import threading
+
+    from flexkv_amd import c_ext
+    w = wl.w
+    n = len(wl.gids)
+    g = torch.Generator().manual_seed(wl.seed + 5)
+    free_g = torch.tensor(sorted(set(range(w["ng"])) - set(wl.gids.tolist())), dtype=torch.int64)
+    free_c = torch.tensor(sorted(set(range(w["nh"])) - set(wl.cids.tolist())), dtype=torch.int64)
+    g2 = free_g[torch.randperm(len(free_g), generator=g)[:n]].pin_memory()
+    c2 = free_c[torch.randperm(len(free_c), generator=g)[:n]].pin_memory()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    out = {}
+    for name, ce in (("kernel", False), ("ce", True)):
+        best = 0.0
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            errs = []
+
+            def move(i):
+                try:
+                    with torch.cuda.stream(streams[i]):
+                        ids = (wl.gids_p, wl.cids_p) if i == 0 else (g2, c2)
+                        c_ext.transfer_kv_blocks(ids[0], wl.ptrs, wl.gkv, wl.gblk, ids[1],
+                                                 wl.host, wl.ckv, wl.clay, wl.cblk, wl.chunk,
+                                                 0, -1, i == 1, ce, wl.mla)
+                except Exception as e:   # reported below
+                    errs.append(e)
+            th = [threading.Thread(target=move, args=(i,)) for i in range(2)]
+            t0 = time.perf_counter()
+            for t in th:
+                t.start()
+            for t in th:
+                t.join()
+            el = time.perf_counter() - t0
+            if errs:
+                raise errs[0]
+            best = max(best, 2 * wl.bytes_per_op / el / 1e9)
+        out[f"{name}_aggregate_gbps"] = round(best, 3)
+    out["what"] = ("one D2H and one H2D of 2 GiB each at once, two threads and streams; "
+                   "bytes of both over the wall time")
     return out
 
 
@@ -904,6 +954,8 @@ def main() -> int:
         log(f"call latency: {result['call_latency']}")
         result["overlap_with_compute"] = overlap_with_compute(wl)
         log(f"overlap with compute: {result['overlap_with_compute']}")
+        result["duplex"] = duplex(wl)
+        log(f"duplex: {result['duplex']}")
         if wl.mla:
             result["request_batch"] = request_batch(wl, args.steps)
             log(f"request batch: {result['request_batch']}")

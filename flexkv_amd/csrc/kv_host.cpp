@@ -315,15 +315,16 @@ int fkv_set_staging_bytes(size_t bytes) {
 int fkv_release_staging(void) {
   last_error().clear();
   for (int dev = 0; dev < kMaxDevices; ++dev) {
-    DeviceState& d = g_dev[dev];
-    std::lock_guard<std::mutex> lk(d.mu);
-    if (d.staging) {
-      DeviceGuard guard;
-      int rc = guard.set(dev);
-      if (rc) return rc;
-      FKV_HIP(hipFree(d.staging));
-      d.staging = nullptr;
-      d.staging_bytes = 0;
+    for (CopyLane& ln : g_dev[dev].lane) {
+      std::lock_guard<std::mutex> lk(ln.mu);
+      if (ln.staging) {
+        DeviceGuard guard;
+        int rc = guard.set(dev);
+        if (rc) return rc;
+        FKV_HIP(hipFree(ln.staging));
+        ln.staging = nullptr;
+        ln.staging_bytes = 0;
+      }
     }
   }
   return 0;

@@ -56,31 +56,40 @@ int query_ptr(const void* p, PtrInfo* out);
 bool range_inside(const char* p, __int128 lo, __int128 hi, const PtrInfo& info);
 
 // ---------------------------------------------------------------------------
-// Per-device state: staging buffer, copy engines, events, occupancy.
+// Per-device state: copy-engine lanes, copy engines, occupancy.
 
-struct DeviceState {
-  std::mutex mu;            // serialises copy-engine transfers on the device
-  bool init = false;
-  int num_cus = 0;
-  int occ_zero_copy[2] = {0, 0};
-  int occ_staged[2] = {0, 0};
+// One direction's copy-engine transfers: its staging buffer (two halves),
+// per half a pool of completion signals (one per queued copy, `in_flight` of
+// them in use) and one event (the gather/scatter kernel that last used the
+// half, on the caller's stream).  The two directions have a lane each, so a
+// device-to-host and a host-to-device transfer run at the same time.
+struct CopyLane {
+  std::mutex mu;            // serialises this direction's copy-engine transfers
   char* staging = nullptr;
   size_t staging_bytes = 0;
-  // Copy engines: the HSA agents of this GPU and of the host, the SDMA
-  // engines usable in each direction, and per staging half a pool of
-  // completion signals (one per queued copy, `in_flight` of them in use) and
-  // one event (the gather/scatter kernel that last used the half, on the
-  // caller's stream).
-  bool sdma_init = false;
-  hsa_agent_t gpu_agent{}, cpu_agent{};
-  std::vector<hsa_amd_sdma_engine_id_t> engines[2];   // [D2H, H2D]
   std::vector<hsa_signal_t> sigs[2];
   size_t in_flight[2] = {0, 0};
   hipEvent_t ev_compute[2] = {nullptr, nullptr};
 };
 
+struct DeviceState {
+  bool init = false;
+  int num_cus = 0;
+  int occ_zero_copy[2] = {0, 0};
+  int occ_staged[2] = {0, 0};
+  // Copy engines: the HSA agents of this GPU and of the host and the SDMA
+  // engines each direction pins its copies to (disjoint sets where the device
+  // has enough engines).
+  std::mutex sdma_mu;       // guards the set-up below
+  bool sdma_init = false;
+  hsa_agent_t gpu_agent{}, cpu_agent{};
+  std::vector<hsa_amd_sdma_engine_id_t> engines[2];   // [D2H, H2D]
+  CopyLane lane[2];                                    // [D2H, H2D]
+};
+
 extern DeviceState g_dev[kMaxDevices];
-// staging bytes per device asked for with fkv_set_staging_bytes (0: default)
+// staging bytes per device and direction asked for with
+// fkv_set_staging_bytes (0: default)
 extern std::atomic<size_t> g_staging_request;
 
 // Makes a device current for the guard's lifetime.
@@ -242,30 +251,31 @@ bool sdma_rect_available();
 // HSA agents and SDMA engines for the copy-engine path on device `dev`, found
 // through `hip_ptr`, a device allocation HIP made on `dev`.
 int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr);
-// A staging buffer of at least two halves of `need_half` bytes.
-int ensure_staging(DeviceState& d, size_t need_half);
+// A lane staging buffer of at least two halves of `need_half` bytes, and the
+// lane's events.
+int ensure_staging(CopyLane& lane, size_t need_half);
 // Queue the copies of `runs` between the host cache and staging half `half`
-// on the device's SDMA engines, round robin, each with its own completion
-// signal.
-int issue_sdma(DeviceState& d, const std::vector<Run>& runs, char* staging, bool h2d, int half,
-               hsa_agent_t host_agent);
+// of `lane` on the direction's SDMA engines, round robin, each with its own
+// completion signal.
+int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, char* staging,
+               bool h2d, int half, hsa_agent_t host_agent);
 // Wait until every copy queued on a staging half has finished.  Each copy
 // has its own signal: a counted signal shared by many copies would depend on
 // every layer between here and the engines decrementing it by exactly one.
-void sdma_wait(DeviceState& d, int half);
+void sdma_wait(CopyLane& lane, int half);
 
 // When a transfer fails after enqueueing work, wait for that work before the
 // call returns: a copy must not land in the caller's buffers, or read the
 // reused id and staging buffers, after the error has been reported.
 struct DrainOnError {
   hipStream_t stream;
-  DeviceState* dev_state;
+  CopyLane* lane;
   bool armed = true;
   ~DrainOnError() {
     if (!armed) return;
     (void)hipStreamSynchronize(stream);
-    if (dev_state && dev_state->sdma_init)
-      for (int h = 0; h < 2; ++h) sdma_wait(*dev_state, h);
+    if (lane)
+      for (int h = 0; h < 2; ++h) sdma_wait(*lane, h);
     (void)hipGetLastError();
   }
 };

@@ -134,7 +134,7 @@ hsa_status_t first_cpu_agent(hsa_agent_t a, void* out) {
 
 }  // namespace
 
-void sdma_wait(DeviceState& d, int half) {
+void sdma_wait(CopyLane& d, int half) {
   for (size_t i = 0; i < d.in_flight[half]; ++i)
     while (g_hsa.signal_wait_scacquire(d.sigs[half][i], HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX,
                                        HSA_WAIT_STATE_BLOCKED) >= 1) {
@@ -204,6 +204,7 @@ void build_runs(const Geometry& g, int b0, int nb, int l0, int nl, bool rect, bo
 }
 
 int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr) {
+  std::lock_guard<std::mutex> lk(d.sdma_mu);
   if (d.sdma_init) return 0;
   if (int rc = load_hsa(hip_ptr)) return rc;
   hsa_amd_pointer_info_t pi;
@@ -225,28 +226,36 @@ int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr) {
   if (g_hsa.agent_get_info(q.gpu, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_NEAREST_CPU),
                            &nearest) == HSA_STATUS_SUCCESS && nearest.handle != 0)
     q.cpu = nearest;
+  // Each direction takes `want` engines; host-to-device skips the engines
+  // device-to-host took while enough others remain, so the two directions
+  // run side by side on disjoint engines (MI355X: 69 GB/s in both
+  // directions together on engines 0-3 and 4-7, 56-57 GB/s one way).
   const int want = sdma_engines_wanted();
+  uint32_t taken = 0;
   for (int dir = 0; dir < 2; ++dir) {
     uint32_t mask = 0;
     FKV_HSA(dir == 0 ? g_hsa.copy_engine_status(q.cpu, q.gpu, &mask)
                      : g_hsa.copy_engine_status(q.gpu, q.cpu, &mask));
+    if (__builtin_popcount(mask & ~taken) >= want) mask &= ~taken;
     d.engines[dir].clear();
     for (int b = 0; b < 32 && static_cast<int>(d.engines[dir].size()) < want; ++b)
-      if (mask & (1u << b))
+      if (mask & (1u << b)) {
         d.engines[dir].push_back(static_cast<hsa_amd_sdma_engine_id_t>(1u << b));
+        taken |= 1u << b;
+      }
     if (d.engines[dir].empty())
       return fail(kInval, "device %d reports no SDMA engine for %s copies", dev,
                   dir == 0 ? "device-to-host" : "host-to-device");
   }
-  for (int h = 0; h < 2; ++h)
-    FKV_HIP(hipEventCreateWithFlags(&d.ev_compute[h], hipEventDisableTiming));
   d.gpu_agent = q.gpu;
   d.cpu_agent = q.cpu;
   d.sdma_init = true;
   return 0;
 }
 
-int ensure_staging(DeviceState& d, size_t need_half) {
+int ensure_staging(CopyLane& d, size_t need_half) {
+  for (int h = 0; h < 2; ++h)
+    if (!d.ev_compute[h]) FKV_HIP(hipEventCreateWithFlags(&d.ev_compute[h], hipEventDisableTiming));
   size_t want = g_staging_request.load();
   if (want == 0) want = kDefaultStagingBytes;
   want = std::max(want, 2 * need_half);
@@ -264,10 +273,10 @@ int ensure_staging(DeviceState& d, size_t need_half) {
   return 0;
 }
 
-int issue_sdma(DeviceState& d, const std::vector<Run>& runs, char* staging, bool h2d, int half,
-               hsa_agent_t host_agent) {
+int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, char* staging,
+               bool h2d, int half, hsa_agent_t host_agent) {
   const std::vector<hsa_amd_sdma_engine_id_t>& eng = d.engines[h2d ? 1 : 0];
-  std::vector<hsa_signal_t>& sigs = d.sigs[half];
+  std::vector<hsa_signal_t>& sigs = lane.sigs[half];
   while (sigs.size() < runs.size()) {
     hsa_signal_t sg;
     FKV_HSA(g_hsa.signal_create(1, 0, nullptr, &sg));
@@ -304,7 +313,7 @@ int issue_sdma(DeviceState& d, const std::vector<Run>& runs, char* staging, bool
                   r.slices > 0 ? "rect copy" : "copy", static_cast<long long>(r.bytes),
                   std::max(1, static_cast<int>(r.slices)), m ? m : "?");
     }
-    d.in_flight[half] = i + 1;
+    lane.in_flight[half] = i + 1;
   }
   return 0;
 }

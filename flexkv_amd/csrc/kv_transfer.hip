@@ -389,7 +389,27 @@ int transfer_zero_copy(const Geometry& g, hipStream_t stream, int dev, int trans
 //  half, queue the copies of the piece two ahead into it.
 int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   DeviceState& d = g_dev[dev];
-  std::lock_guard<std::mutex> lk(d.mu);
+  CopyLane& ln = d.lane[h2d ? 1 : 0];
+  // Staging order: block-major [block][layer][K|V][chunk] (contiguous block
+  // rows, or one rect copy per block of a layer-wise cache), or layer-major
+  // [layer][K|V][block][chunk] when a layer-wise cache's ids come in runs of
+  // consecutive blocks long enough to copy each (layer, K|V) run linearly.
+  // FLEXKV_CE_LAYER_RUN_BYTES overrides the average run (default 128 KiB)
+  const char* lr = getenv("FLEXKV_CE_LAYER_RUN_BYTES");
+  const bool layer_major =
+      layer_major_pays_off(g, lr ? std::max<int64_t>(1, atoll(lr)) : kCeMinRunBytes);
+  const bool row_contig = (g.kv == 1 || g.cks == g.chunk) &&
+                          (g.num_layers == 1 || g.cls == g.kv * g.chunk);
+  // A transfer of rect copies runs alone on the device: those go to the
+  // engine the runtime picks, and the runtime must not see them beside copies
+  // pinned to engines.  Other transfers hold their direction's lane only.
+  const bool rect_copies = !row_contig && !layer_major;
+  std::unique_lock<std::mutex> own(ln.mu, std::defer_lock);
+  std::unique_lock<std::mutex> other(d.lane[h2d ? 0 : 1].mu, std::defer_lock);
+  if (rect_copies)
+    std::lock(own, other);
+  else
+    own.lock();
   DeviceGuard guard;
   int rc = guard.set(dev);
   if (rc) return rc;
@@ -404,21 +424,13 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   int nl_piece = std::min(g.num_layers, g.layers_per_launch());
   while (nl_piece > 1 && static_cast<size_t>(nl_piece) * g.kv * g.chunk > half_default) nl_piece /= 2;
   const size_t row_bytes = static_cast<size_t>(nl_piece) * g.kv * g.chunk;
-  rc = ensure_staging(d, row_bytes);
+  rc = ensure_staging(ln, row_bytes);
   if (rc) return rc;
-  if ((rc = ensure_sdma(d, dev, d.staging))) return rc;
-  const size_t half = d.staging_bytes / 2;
+  if ((rc = ensure_sdma(d, dev, ln.staging))) return rc;
+  const size_t half = ln.staging_bytes / 2;
   const int blocks_per_piece = static_cast<int>(std::max<size_t>(1, half / row_bytes));
   const int grid_cap = d.num_cus * (h2d ? d.occ_staged[1] : d.occ_staged[0]);
   const hsa_agent_t host_agent = d.cpu_agent;   // device-resident caches never get here
-  // Staging order: block-major [block][layer][K|V][chunk] (contiguous block
-  // rows, or one rect copy per block of a layer-wise cache), or layer-major
-  // [layer][K|V][block][chunk] when a layer-wise cache's ids come in runs of
-  // consecutive blocks long enough to copy each (layer, K|V) run linearly.
-  // FLEXKV_CE_LAYER_RUN_BYTES overrides the average run (default 128 KiB)
-  const char* lr = getenv("FLEXKV_CE_LAYER_RUN_BYTES");
-  const bool layer_major =
-      layer_major_pays_off(g, lr ? std::max<int64_t>(1, atoll(lr)) : kCeMinRunBytes);
 
   struct Piece {
     int l0, nl, b0, nb;
@@ -433,7 +445,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   // Host-side waits order everything below against the caller's stream, so
   // work already queued on it comes first.
   FKV_HIP(hipStreamSynchronize(stream));
-  DrainOnError drain{stream, &d};
+  DrainOnError drain{stream, &ln};
   ProfRecorder prof;
   std::vector<Run> runs;
   bool pending[2] = {false, false};
@@ -446,7 +458,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
     for (const Run& r : runs) dma_bytes += r.bytes * std::max<int64_t>(1, r.slices);
     dma_copies += static_cast<int64_t>(runs.size());
     pending[h] = true;
-    return issue_sdma(d, runs, d.staging + h * half, h2d, h, host_agent);
+    return issue_sdma(d, ln, runs, ln.staging + h * half, h2d, h, host_agent);
   };
   auto launch = [&](int pi) -> int {
     const Piece& p = pieces[pi];
@@ -461,7 +473,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
       cls = static_cast<int64_t>(g.kv) * g.chunk;
       cbs = static_cast<int64_t>(p.nl) * cls;
     }
-    char* stg = d.staging + (pi & 1) * half;
+    char* stg = ln.staging + (pi & 1) * half;
     return h2d ? launch_copy<true, true>(g, ids_dev, stg, cks, cls, cbs, p.b0, p.nb, p.l0, p.nl,
                                          grid_cap, stream, prof)
                : launch_copy<false, true>(g, ids_dev, stg, cks, cls, cbs, p.b0, p.nb, p.l0, p.nl,
@@ -471,12 +483,12 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
     for (int pi = 0; pi < np; ++pi) {
       const int h = pi & 1;
       if (pending[h]) {
-        sdma_wait(d, h);
+        sdma_wait(ln, h);
         pending[h] = false;
       }
       if ((rc = launch(pi))) return rc;
-      FKV_HIP(hipEventRecord(d.ev_compute[h], stream));
-      FKV_HIP(hipEventSynchronize(d.ev_compute[h]));
+      FKV_HIP(hipEventRecord(ln.ev_compute[h], stream));
+      FKV_HIP(hipEventSynchronize(ln.ev_compute[h]));
       if ((rc = queue_copies(pi))) return rc;
     }
   } else {
@@ -484,20 +496,20 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
       if ((rc = queue_copies(pi))) return rc;
     for (int pi = 0; pi < np; ++pi) {
       const int h = pi & 1;
-      sdma_wait(d, h);
+      sdma_wait(ln, h);
       pending[h] = false;
       hipLaunchKernelGGL(acquire_system_kernel, dim3(d.num_cus), dim3(64), 0, stream);
       FKV_HIP(hipGetLastError());
       if ((rc = launch(pi))) return rc;
       if (pi + 2 < np) {
-        FKV_HIP(hipEventRecord(d.ev_compute[h], stream));
-        FKV_HIP(hipEventSynchronize(d.ev_compute[h]));
+        FKV_HIP(hipEventRecord(ln.ev_compute[h], stream));
+        FKV_HIP(hipEventSynchronize(ln.ev_compute[h]));
         if ((rc = queue_copies(pi + 2))) return rc;
       }
     }
   }
   for (int h = 0; h < 2; ++h)
-    if (pending[h]) sdma_wait(d, h);
+    if (pending[h]) sdma_wait(ln, h);
   FKV_HIP(hipStreamSynchronize(stream));
   drain.armed = false;
   if (prof.on) {

@@ -40,11 +40,16 @@ enum {
   /* Copy-engine path: a gather kernel packs the selected chunks into a
    * contiguous HBM staging buffer and the SDMA engines move maximal
    * contiguous host runs (D2H); H2D is SDMA into staging followed by a
-   * scatter kernel.  Staging is double-buffered; the PCIe copies take no
-   * compute units.  Transfers under FLEXKV_CE_MIN_BYTES (default 8 MiB) or
-   * with host runs under 128 KiB move with the zero-copy kernel instead,
-   * where the engines' per-copy cost would dominate.  Same role as the
-   * reference CE mode, csrc/transfer.cu:97-121. */
+   * scatter kernel.  A layer-wise host cache is served with one SDMA rect
+   * copy per block, or, when its ids come in runs of consecutive blocks,
+   * with one copy per (layer, K|V) run from layer-major staging.  Staging is
+   * double-buffered; the PCIe copies take no compute units.  Each direction
+   * has its own staging and engines, so a D2H and an H2D transfer from
+   * different threads run at the same time (a transfer of rect copies runs
+   * alone).  Transfers under FLEXKV_CE_MIN_BYTES (default 8 MiB) or whose
+   * engine copies would move under 128 KiB each move with the zero-copy
+   * kernel instead, where the engines' per-copy cost would dominate.  Same
+   * role as the reference CE mode, csrc/transfer.cu:97-121. */
   FKV_XFER_CE = 1,
   /* The reference's copy-engine algorithm restated literally: one
    * hipMemcpyAsync per (layer, K|V, block) chunk, csrc/transfer.cu:97-121.
@@ -248,9 +253,9 @@ int fkv_host_free(void* ptr);
 int fkv_host_register(void* ptr, size_t bytes, unsigned flags);
 int fkv_host_unregister(void* ptr);
 
-/* Staging buffer used by FKV_XFER_CE on each device (bytes, split in two
- * halves).  Takes effect at the next allocation on a device; 0 = default
- * (256 MiB).  fkv_release_staging frees every device's buffer. */
+/* Staging buffer used by FKV_XFER_CE on each device, one per direction
+ * (bytes, split in two halves).  Takes effect at the next allocation; 0 =
+ * default (256 MiB).  fkv_release_staging frees every device's buffers. */
 int fkv_set_staging_bytes(size_t bytes);
 int fkv_release_staging(void);
 

@@ -294,14 +294,17 @@ def test_device_resident_cache_matches_oracle(dev, mode):
     assert np.array_equal(got, _oracle_d2h(case, gids, cids, mode))
 
 
-def test_concurrent_threads_mixed_paths(dev):
+@pytest.mark.parametrize("layout", ["BLOCKWISE", "LAYERWISE"])
+def test_concurrent_threads_mixed_paths(dev, layout):
     """Four host threads, each with its own stream, move disjoint block sets
-    with different paths and directions at once (shared id buffers, staging
-    and SDMA state are per thread or locked); every result is bit-exact."""
+    with different paths and directions at once (id buffers are per thread;
+    copy-engine staging and SDMA state per direction, a D2H and an H2D
+    copy-engine transfer running side by side; rect transfers of a
+    layer-wise cache take both directions); every result is bit-exact."""
     import threading
     from gpu_util import DeviceCase, abi_transfer
     case = KVCase(layers_total=4, num_layers=4, start_layer=0, kv=2, ng=256, nh=256, tokens=16,
-                  heads=8, dim=128).fill(seed=43)
+                  heads=8, dim=128, layout=layout).fill(seed=43)
     dc = DeviceCase(case)
     perm_g = inputs.distinct_ids(7, 240, 256)
     perm_c = inputs.distinct_ids(8, 240, 256)
@@ -309,9 +312,16 @@ def test_concurrent_threads_mixed_paths(dev):
     plan = [(False, 0), (False, 1), (True, 1), (True, 0)]   # (h2d, mode) per thread
     # H2D threads read host blocks that hold distinct fresh values first
     fresh = case.host.copy()
+
+    def block(arr, c, l, k):      # host chunks [len(c), tp, tokens, heads, dim]
+        return arr[c, l, k] if layout == "BLOCKWISE" else arr[l, k, c]
+
     for (h2d, _), (g, c) in zip(plan, parts):
         if h2d:
-            fresh[c] ^= np.asarray(0x0F0F, dtype=case.dtype)
+            if layout == "BLOCKWISE":
+                fresh[c] ^= np.asarray(0x0F0F, dtype=case.dtype)
+            else:
+                fresh[:, :, c] ^= np.asarray(0x0F0F, dtype=case.dtype)
     dc.set_host(fresh)
     errors = []
 
@@ -340,11 +350,12 @@ def test_concurrent_threads_mixed_paths(dev):
         if h2d:
             for l in range(4):
                 for k in range(2):
-                    assert np.array_equal(gpu[l][k][g], fresh[c, l, k, 0]), (mode, l, k)
+                    assert np.array_equal(gpu[l][k][g], block(fresh, c, l, k)[:, 0]), (mode, l, k)
         else:
             for l in range(4):
                 for k in range(2):
-                    assert np.array_equal(host[c, l, k, 0], case.gpu[l][k][g]), (mode, l, k)
+                    assert np.array_equal(block(host, c, l, k)[:, 0], case.gpu[l][k][g]), \
+                        (mode, l, k)
 
 
 # Separate K and V allocations (fkv_transfer_kv_blocks_kv_ptrs): the same
