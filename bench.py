@@ -371,6 +371,68 @@ def engine_layerwise(wl: Workload, steps: int):
     return out
 
 
+def engine_put_get(wl: Workload, steps: int):
+    """A write graph (D2H of the step's blocks) and a read graph (H2D of as
+    many other blocks) submitted together to TransferEngine with thread
+    workers and the default copy-engine path: submit-to-both-complete time,
+    and each graph alone.  The engine runs one worker per direction, so the
+    two overlap on the full-duplex link."""
+    from flexkv_amd.cache.transfer_pattern import (create_read_graph_cpu_storage,
+                                                   create_write_graph_cpu_storage)
+    from flexkv_amd.common.config import CacheConfig, ModelConfig
+    from flexkv_amd.common.storage import KVCacheLayout, KVCacheLayoutType
+    from flexkv_amd.storage.allocator import AccessHandleType, StorageHandle
+    from flexkv_amd.transfer.transfer_engine import TransferEngine
+    w = wl.w
+    L = w["layers"]
+    n = len(wl.gids)
+    gl = KVCacheLayout(KVCacheLayoutType.LAYERWISE, L, w["ng"], w["tokens"], w["heads"],
+                       w["dim"], is_mla=wl.mla)
+    gpu_h = StorageHandle(AccessHandleType.TENSOR, wl.layers, gl, wl.dtype, gpu_device_id=0)
+    cpu_h = StorageHandle(AccessHandleType.TENSOR, wl.host, wl.cl, wl.dtype)
+    mc = ModelConfig(num_layers=L, num_kv_heads=w["heads"], head_size=w["dim"],
+                     use_mla=wl.mla, dtype=wl.dtype)
+    g = torch.Generator().manual_seed(wl.seed + 6)
+    free_g = torch.tensor(sorted(set(range(w["ng"])) - set(wl.gids.tolist())), dtype=torch.int64)
+    free_c = torch.tensor(sorted(set(range(w["nh"])) - set(wl.cids.tolist())), dtype=torch.int64)
+    g2 = free_g[torch.randperm(len(free_g), generator=g)[:n]]
+    c2 = free_c[torch.randperm(len(free_c), generator=g)[:n]]
+    none = torch.empty(0, dtype=torch.int64)
+    eng = TransferEngine([gpu_h], mc, CacheConfig(), cpu_handle=cpu_h)
+    eng.start()
+
+    def run(kinds):
+        graphs = []
+        for kind in kinds:
+            if kind == "put":
+                graphs.append(create_write_graph_cpu_storage(wl.gids, wl.cids, none,
+                                                             layer_num=L)[0])
+            else:
+                graphs.append(create_read_graph_cpu_storage(g2, c2, none, layer_num=L)[0])
+        t0 = time.perf_counter()
+        for gr in graphs:
+            eng.submit_transfer_graph(gr)
+        left = {gr.graph_id for gr in graphs}
+        while left:
+            for gid, op in eng.get_completed_graphs_and_ops(timeout=0.05):
+                if op == -1:
+                    left.discard(gid)
+        return time.perf_counter() - t0
+
+    out = {}
+    try:
+        for name, kinds in (("put", ["put"]), ("get", ["get"]), ("put_and_get", ["put", "get"])):
+            ts = [run(kinds) for _ in range(steps + 1)][1:]
+            med = statistics.median(ts)
+            out[name] = {"ms": round(med * 1e3, 2),
+                         "gbps": round(len(kinds) * wl.bytes_per_op / med / 1e9, 2)}
+    finally:
+        eng.shutdown()
+    out["what"] = ("TransferEngine, thread workers, copy-engine path: a 2 GiB write graph, a "
+                   "2 GiB read graph of other blocks, and both submitted together")
+    return out
+
+
 def call_latency(wl: Workload, reps: int = 200):
     """Wall time of small synchronous calls (1 block x 1 layer, 16 blocks x 1
     layer, 16 blocks x all layers), zero-copy and copy-engine paths,
@@ -950,6 +1012,8 @@ def main() -> int:
         log(f"layer-wise H2D: {result['layerwise_h2d']}")
         result["engine_layerwise_read"] = engine_layerwise(wl, args.steps)
         log(f"engine layer-wise read: {result['engine_layerwise_read']}")
+        result["engine_put_get"] = engine_put_get(wl, max(3, args.steps // 2))
+        log(f"engine put and get: {result['engine_put_get']}")
         result["call_latency"] = call_latency(wl)
         log(f"call latency: {result['call_latency']}")
         result["overlap_with_compute"] = overlap_with_compute(wl)

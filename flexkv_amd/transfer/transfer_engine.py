@@ -4,16 +4,20 @@ flexkv/transfer/transfer_engine.py:42-307, GPU<->CPU and CPU<->SSD tiers).
 Same interface as the reference: TransferEngine(gpu_handles, model_config,
 cache_config, cpu_handle, ssd_handle, ...), start(),
 submit_transfer_graph(graph), get_completed_graphs_and_ops(timeout) ->
-[(graph_id, op_id)] with op_id -1 for a finished graph, shutdown().  One
-GPU<->CPU worker per data-parallel group takes the H2D and D2H ops of that
-group (op.dp_id); with an SSD handle, one CPU<->SSD worker takes the DISK2H
-ops and another the H2DISK ops (transfer_engine.py:129-153).
+[(graph_id, op_id)] with op_id -1 for a finished graph, shutdown().  The
+GPU<->CPU ops of a data-parallel group (op.dp_id) go to that group's worker;
+with an SSD handle, one CPU<->SSD worker takes the DISK2H ops and another the
+H2DISK ops (transfer_engine.py:129-153).
 
 Differences:
   * workers run on threads of this process by default (worker_mode="thread"):
     the transfer releases the GIL, and the pinned host cache needs no
     inter-process sharing; worker_mode="process" spawns them as the
     reference does, each allocating its own pinned host cache;
+  * thread mode gives each group two GPU<->CPU workers, one for H2D and one
+    for D2H, so that a get and a put overlap on the full-duplex link (the
+    reference's single worker runs them in turn); a process worker owns its
+    host cache, so process mode keeps one per group;
   * the scheduler thread blocks on one event queue (new graphs and finished
     ops) instead of polling every millisecond;
   * eager_dispatch: an op whose unfinished predecessors are all already
@@ -73,13 +77,19 @@ class TransferEngine:
         self.op_id_to_op: Dict[int, TransferOp] = {}
         self._running = False
         self._workers: List = []
+        self._gpu_workers: Dict[tuple, object] = {}
         self._mp_finished = None
         self._forwarder: Optional[threading.Thread] = None
 
     # -- worker routing ---------------------------------------------------
-    @staticmethod
-    def _worker_key(op: TransferOp):
-        return ("gpucpu", op.dp_id) if op.transfer_type in _GPU_CPU else (op.transfer_type, 0)
+    def _worker_key(self, op: TransferOp):
+        if op.transfer_type in _GPU_CPU:
+            # thread workers: one per GPU and direction, so that a put (D2H)
+            # and a get (H2D) on one GPU overlap (PCIe is full duplex); a
+            # worker process owns its host cache, so there is one per GPU
+            split = self.worker_mode == "thread"
+            return ("gpucpu", op.dp_id, op.transfer_type if split else None)
+        return (op.transfer_type, 0)
 
     def _same_worker(self, op: TransferOp, pending_predecessors: List[TransferOp]) -> bool:
         if op.transfer_type == TransferType.VIRTUAL:
@@ -104,10 +114,13 @@ class TransferEngine:
                           transfer_sms_h2d=cfg.transfer_sms_h2d,
                           transfer_sms_d2h=cfg.transfer_sms_d2h)
             if self.worker_mode == "thread":
-                w = GPUCPUTransferWorker.create_worker_thread(
-                    i, self._events, gpu_blocks=g.get_tensor_list(),
-                    cpu_blocks=self._cpu_handle.get_tensor(), **common)
-                w.wait_ready(60)
+                for kind in (TransferType.H2D, TransferType.D2H):
+                    w = GPUCPUTransferWorker.create_worker_thread(
+                        i, self._events, gpu_blocks=g.get_tensor_list(),
+                        cpu_blocks=self._cpu_handle.get_tensor(), **common)
+                    w.wait_ready(60)
+                    self._gpu_workers[("gpucpu", i, kind)] = w
+                    self._workers.append(w)
             else:
                 import multiprocessing as mp
                 if self._mp_finished is None:
@@ -118,7 +131,8 @@ class TransferEngine:
                     **common)
                 if not w.ready_event.wait(120):
                     raise TimeoutError(f"worker {i} did not start")
-            self._workers.append(w)
+                self._gpu_workers[("gpucpu", i, None)] = w
+                self._workers.append(w)
         if self._ssd_handle is not None:
             common = dict(cpu_blocks=self._cpu_handle.get_tensor(),
                           ssd_files=self._ssd_handle.get_file_list(),
@@ -193,7 +207,7 @@ class TransferEngine:
 
     def _assign_op_to_worker(self, op: TransferOp) -> None:
         if op.transfer_type in _GPU_CPU:
-            self._workers[op.dp_id].submit_transfer(op)
+            self._gpu_workers[self._worker_key(op)].submit_transfer(op)
         elif op.transfer_type in _CPU_SSD and op.transfer_type in self._ssd_workers:
             self._ssd_workers[op.transfer_type].submit_transfer(op)
         else:
@@ -230,6 +244,7 @@ class TransferEngine:
             except Exception as e:
                 flexkv_logger.error(f"Error during worker shutdown: {e}")
         self._workers = []
+        self._gpu_workers = {}
         self._ssd_workers = {}
         if self._forwarder is not None:
             self._forwarder.join(timeout=5)
