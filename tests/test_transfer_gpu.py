@@ -628,23 +628,41 @@ def test_gather_scatter_match_oracle(dev, geo, buffer_on_host):
 from hypothesis import HealthCheck, given, settings, strategies as st  # noqa: E402
 
 
-@settings(max_examples=30, deadline=None, derandomize=True,
+def _run_ids(g, n, universe, run):
+    """n distinct ids in runs of `run` consecutive ids (the last run may be
+    shorter), runs at random non-overlapping starts."""
+    slots = g.permutation(universe // run)[: -(-n // run)]
+    ids = (slots[:, None] * run + np.arange(run)[None, :]).reshape(-1)[:n]
+    return np.ascontiguousarray(ids, dtype=np.int64)
+
+
+@settings(max_examples=40, deadline=None, derandomize=True,
           suppress_health_check=[HealthCheck.function_scoped_fixture])
 @given(layout=st.sampled_from(["BLOCKWISE", "LAYERWISE"]), kv=st.sampled_from([1, 2]),
        lt=st.integers(1, 6), tokens=st.sampled_from([1, 2, 16]), heads=st.sampled_from([1, 3]),
        dim=st.sampled_from([8, 64, 72, 128]), tp=st.sampled_from([1, 2]), mode=st.sampled_from(MODES),
-       seed=st.integers(0, 10**6))
-def test_random_geometries_match_oracle(dev, layout, kv, lt, tokens, heads, dim, tp, mode, seed):
+       run=st.sampled_from([1, 3]), layer_major=st.booleans(), seed=st.integers(0, 10**6))
+def test_random_geometries_match_oracle(dev, monkeypatch, layout, kv, lt, tokens, heads, dim, tp,
+                                        mode, run, layer_major, seed):
     """Seeded random geometries (layouts, MLA, layer windows, TP host chunks,
-    chunk sizes from 16 B up, block counts) in every mode, against the oracle."""
+    chunk sizes from 16 B up, block counts, ids scattered or in runs) in every
+    mode, against the oracle; `layer_major` lowers FLEXKV_CE_LAYER_RUN_BYTES
+    so that copy-engine transfers of layer-wise caches stage layer-major."""
+    if layer_major:
+        monkeypatch.setenv("FLEXKV_CE_LAYER_RUN_BYTES", "1")
+    else:
+        monkeypatch.delenv("FLEXKV_CE_LAYER_RUN_BYTES", raising=False)
     g = np.random.default_rng(seed)
     nl = int(g.integers(1, lt + 1))
     st_l = int(g.integers(0, lt - nl + 1))
-    ng, nh = int(g.integers(4, 60)), int(g.integers(4, 60))
-    n = int(g.integers(1, min(ng, nh) + 1))
+    ng, nh = int(g.integers(4 * run, 60)), int(g.integers(4 * run, 60))
+    n = int(g.integers(1, min(ng, nh) // run * run + 1))
     case = KVCase(layers_total=lt, num_layers=nl, start_layer=st_l, kv=kv, ng=ng, nh=nh,
                   tokens=tokens, heads=heads, dim=dim, layout=layout, tp=tp,
                   rank=int(g.integers(0, tp))).fill(seed=seed % 9973)
-    gids = inputs.distinct_ids(seed % 7919 + 1, n, ng)
-    cids = inputs.distinct_ids(seed % 7907 + 2, n, nh)
+    if run == 1:
+        gids = inputs.distinct_ids(seed % 7919 + 1, n, ng)
+        cids = inputs.distinct_ids(seed % 7907 + 2, n, nh)
+    else:
+        gids, cids = _run_ids(g, n, ng, run), _run_ids(g, n, nh, run)
     check_case(case, gids, cids, mode)
