@@ -82,6 +82,9 @@ struct DeviceState {
   // has enough engines).
   std::mutex sdma_mu;       // guards the set-up below
   bool sdma_init = false;
+  // set-up failed: copy-engine transfers on this device use the zero-copy
+  // kernel from then on
+  std::atomic<bool> sdma_failed{false};
   hsa_agent_t gpu_agent{}, cpu_agent{};
   std::vector<hsa_amd_sdma_engine_id_t> engines[2];   // [D2H, H2D]
   CopyLane lane[2];                                    // [D2H, H2D]

@@ -45,10 +45,11 @@ struct HsaApi {
 };
 HsaApi g_hsa;
 
+// Engines per direction; FLEXKV_SDMA_ENGINES=0 turns the engines off.
 int sdma_engines_wanted() {
   const char* e = getenv("FLEXKV_SDMA_ENGINES");
   const int n = e ? atoi(e) : kDefaultSdmaEngines;
-  return std::max(1, std::min(n, 32));
+  return std::max(0, std::min(n, 32));
 }
 
 std::mutex g_hsa_mu;
@@ -231,6 +232,7 @@ int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr) {
   // run side by side on disjoint engines (MI355X: 69 GB/s in both
   // directions together on engines 0-3 and 4-7, 56-57 GB/s one way).
   const int want = sdma_engines_wanted();
+  if (want == 0) return fail(kInval, "copy engines turned off (FLEXKV_SDMA_ENGINES=0)");
   uint32_t taken = 0;
   for (int dir = 0; dir < 2; ++dir) {
     uint32_t mask = 0;

@@ -113,6 +113,9 @@ constexpr int kAutoLayerwiseH2DCus = 2;
 // copy, worth handing to the SDMA engines (ce_pays_off).
 constexpr int64_t kCeMinBytesDefault = int64_t(8) << 20;
 constexpr int64_t kCeMinRunBytes = int64_t(128) << 10;
+// transfer_staged's return when the copy engines cannot be set up (nothing
+// was queued); not a hipError_t value
+constexpr int kSdmaUnavailable = -1000;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // Every address the kernel touches is global memory (HBM or mapped pinned
@@ -426,7 +429,15 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   const size_t row_bytes = static_cast<size_t>(nl_piece) * g.kv * g.chunk;
   rc = ensure_staging(ln, row_bytes);
   if (rc) return rc;
-  if ((rc = ensure_sdma(d, dev, ln.staging))) return rc;
+  if ((rc = ensure_sdma(d, dev, ln.staging))) {
+    // nothing has been queued yet: the caller moves this transfer, and every
+    // later one on the device, with the zero-copy kernel
+    if (!d.sdma_failed.exchange(true))
+      fprintf(stderr, "flexkv: copy engines unavailable on device %d (%s); copy-engine "
+              "transfers use the zero-copy kernel\n", dev, last_error().c_str());
+    last_error().clear();
+    return kSdmaUnavailable;
+  }
   const size_t half = ln.staging_bytes / 2;
   const int blocks_per_piece = static_cast<int>(std::max<size_t>(1, half / row_bytes));
   const int grid_cap = d.num_cus * (h2d ? d.occ_staged[1] : d.occ_staged[0]);
@@ -790,8 +801,10 @@ int transfer_entry(Geometry& g, hipStream_t s, int transfer_cus, bool h2d, int m
     case FKV_XFER_KERNEL:
       return transfer_zero_copy(g, s, dev, transfer_cus, h2d);
     case FKV_XFER_CE:
-      if (!ce_pays_off(g)) return transfer_zero_copy(g, s, dev, transfer_cus, h2d);
-      return transfer_staged(g, s, dev, h2d);
+      if (!ce_pays_off(g) || g_dev[dev].sdma_failed.load())
+        return transfer_zero_copy(g, s, dev, transfer_cus, h2d);
+      rc = transfer_staged(g, s, dev, h2d);
+      return rc == kSdmaUnavailable ? transfer_zero_copy(g, s, dev, transfer_cus, h2d) : rc;
     default:
       return transfer_ce_per_chunk(g, s, h2d);
   }
