@@ -48,8 +48,10 @@ enum {
    * different threads run at the same time (a transfer of rect copies runs
    * alone).  Transfers under FLEXKV_CE_MIN_BYTES (default 8 MiB) or whose
    * engine copies would move under 128 KiB each move with the zero-copy
-   * kernel instead, where the engines' per-copy cost would dominate.  Same
-   * role as the reference CE mode, csrc/transfer.cu:97-121. */
+   * kernel instead, where the engines' per-copy cost would dominate, and so
+   * does every transfer on a device whose engines cannot be set up (one
+   * warning on stderr; FLEXKV_SDMA_ENGINES=0 turns them off).  Same role as
+   * the reference CE mode, csrc/transfer.cu:97-121. */
   FKV_XFER_CE = 1,
   /* The reference's copy-engine algorithm restated literally: one
    * hipMemcpyAsync per (layer, K|V, block) chunk, csrc/transfer.cu:97-121.
