@@ -88,3 +88,19 @@ def test_gpu_benchmark_runs(tmp_path, kind, ce):
                                          "--benchmark-round", "3"]))
     assert res["bytes"] == 48 * 16 * 4 * 2 * 64 * 2 * 2
     assert res["path"] == ("ce" if ce else "kernel") and res["gb_per_s"] > 0
+
+
+REFERENCE_CONFIG = "/root/reference/benchmarks/example_config.json"
+
+
+@pytest.mark.skipif(not __import__("os").path.exists(REFERENCE_CONFIG),
+                    reason="the reference tree is not present")
+def test_reference_example_config_loads():
+    """The reference's own benchmark config (read from the reference tree
+    where it is present) loads: its remote, trace and GDS keys are dropped,
+    layout names become layout types."""
+    model, cache, bench = bw.make_configs(bw.parse_args(["--config", REFERENCE_CONFIG,
+                                                         "--transfer-type", "D2H"]))
+    assert model.num_layers > 0 and model.dtype in (torch.bfloat16, torch.float16)
+    assert isinstance(cache.cpu_kv_layout_type, KVCacheLayoutType)
+    assert bench.transfer_type == TransferType.D2H
