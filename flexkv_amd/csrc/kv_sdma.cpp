@@ -22,9 +22,12 @@ namespace fkv_detail {
 
 namespace {
 
-// SDMA engines the copy-engine path spreads its copies over: measured on
-// MI355X with 2 MiB copies, one engine moves 45 GB/s, four 56 GB/s in either
-// direction, all sixteen 46 GB/s device-to-host.
+// SDMA engines each direction spreads its copies over.  Measured on MI355X
+// (16 engines) with 2 MiB copies: four move 56-57 GB/s either way, and
+// device-to-host drops to 47 GB/s on eight.  Host-to-device on eight engines
+// moves 256 KiB copies faster (55 against 42 GB/s on four), but compute
+// kernels running beside it then take twice as long (160 bf16 GEMMs: 65 ms
+// against 36 ms) and a D2H and an H2D together drop from 69 to 61 GB/s.
 constexpr int kDefaultSdmaEngines = 4;
 
 // The HSA entry points the copy-engine path needs, resolved from the HSA
@@ -37,6 +40,8 @@ struct HsaApi {
   decltype(&::hsa_agent_get_info) agent_get_info = nullptr;
   decltype(&::hsa_status_string) status_string = nullptr;
   decltype(&::hsa_signal_create) signal_create = nullptr;
+  decltype(&::hsa_amd_signal_create) amd_signal_create = nullptr;
+  decltype(&::hsa_signal_load_scacquire) signal_load_scacquire = nullptr;
   decltype(&::hsa_signal_store_screlease) signal_store_screlease = nullptr;
   decltype(&::hsa_signal_wait_scacquire) signal_wait_scacquire = nullptr;
   decltype(&::hsa_amd_memory_copy_engine_status) copy_engine_status = nullptr;
@@ -101,6 +106,8 @@ int load_hsa(const void* hip_ptr) {
   sym(a.agent_get_info, "hsa_agent_get_info");
   sym(a.status_string, "hsa_status_string");
   sym(a.signal_create, "hsa_signal_create");
+  sym(a.amd_signal_create, "hsa_amd_signal_create");
+  sym(a.signal_load_scacquire, "hsa_signal_load_scacquire");
   sym(a.signal_store_screlease, "hsa_signal_store_screlease");
   sym(a.signal_wait_scacquire, "hsa_signal_wait_scacquire");
   sym(a.copy_engine_status, "hsa_amd_memory_copy_engine_status");
@@ -136,11 +143,17 @@ hsa_status_t first_cpu_agent(hsa_agent_t a, void* out) {
 }  // namespace
 
 void sdma_wait(CopyLane& d, int half) {
-  for (size_t i = 0; i < d.in_flight[half]; ++i)
-    while (g_hsa.signal_wait_scacquire(d.sigs[half][i], HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX,
+  for (hsa_signal_t s : d.wake[half])
+    while (g_hsa.signal_wait_scacquire(s, HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX,
                                        HSA_WAIT_STATE_BLOCKED) >= 1) {
     }
-  d.in_flight[half] = 0;
+  for (hsa_signal_t s : d.queued[half])
+    if (g_hsa.signal_load_scacquire(s) >= 1)
+      while (g_hsa.signal_wait_scacquire(s, HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX,
+                                         HSA_WAIT_STATE_ACTIVE) >= 1) {
+      }
+  d.queued[half].clear();
+  d.wake[half].clear();
 }
 
 bool layer_major_pays_off(const Geometry& g, int64_t min_run_bytes) {
@@ -278,16 +291,40 @@ int ensure_staging(CopyLane& d, size_t need_half) {
 int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, char* staging,
                bool h2d, int half, hsa_agent_t host_agent) {
   const std::vector<hsa_amd_sdma_engine_id_t>& eng = d.engines[h2d ? 1 : 0];
-  std::vector<hsa_signal_t>& sigs = lane.sigs[half];
-  while (sigs.size() < runs.size()) {
+  const size_t n = runs.size();
+  // The engine of each copy (rect copies: the runtime's one engine, key
+  // eng.size()) and whether it is that engine's last copy of the half.
+  std::vector<uint8_t> last(n, 0);
+  uint64_t seen = 0;   // bit per engine key (at most 33)
+  size_t tails = 0;
+  for (size_t i = n; i-- > 0;) {
+    const size_t key = runs[i].slices > 0 ? eng.size() : i % eng.size();
+    if (!(seen >> key & 1)) {
+      seen |= uint64_t(1) << key;
+      last[i] = 1;
+      ++tails;
+    }
+  }
+  std::vector<hsa_signal_t>& polled = lane.polled_pool[half];
+  std::vector<hsa_signal_t>& irq = lane.irq_pool[half];
+  while (polled.size() < n - tails) {
+    hsa_signal_t sg;
+    FKV_HSA(g_hsa.amd_signal_create(1, 0, nullptr, HSA_AMD_SIGNAL_AMD_GPU_ONLY, &sg));
+    polled.push_back(sg);
+  }
+  while (irq.size() < tails) {
     hsa_signal_t sg;
     FKV_HSA(g_hsa.signal_create(1, 0, nullptr, &sg));
-    sigs.push_back(sg);
+    irq.push_back(sg);
   }
-  for (size_t i = 0; i < runs.size(); ++i) {
+  lane.queued[half].clear();
+  lane.wake[half].clear();
+  size_t np = 0, ni = 0;
+  for (size_t i = 0; i < n; ++i) {
     const Run& r = runs[i];
     char* dev_p = staging + r.staging_off;
-    g_hsa.signal_store_screlease(sigs[i], 1);
+    const hsa_signal_t sig = last[i] ? irq[ni++] : polled[np++];
+    g_hsa.signal_store_screlease(sig, 1);
     hsa_status_t st;
     if (r.slices > 0) {
       // the runtime puts rect copies on the device's own engine for the direction
@@ -296,16 +333,16 @@ int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, cha
       const hsa_dim3_t zero{0, 0, 0};
       const hsa_dim3_t range{static_cast<uint32_t>(r.bytes), 1, static_cast<uint32_t>(r.slices)};
       st = h2d ? g_hsa.async_copy_rect(&sp, &zero, &hp, &zero, &range, d.gpu_agent,
-                                       hsaHostToDevice, 0, nullptr, sigs[i])
+                                       hsaHostToDevice, 0, nullptr, sig)
                : g_hsa.async_copy_rect(&hp, &zero, &sp, &zero, &range, d.gpu_agent,
-                                       hsaDeviceToHost, 0, nullptr, sigs[i]);
+                                       hsaDeviceToHost, 0, nullptr, sig);
     } else {
       const hsa_amd_sdma_engine_id_t e = eng[i % eng.size()];
       st = h2d ? g_hsa.async_copy_on_engine(dev_p, d.gpu_agent, r.host, host_agent,
-                                            static_cast<size_t>(r.bytes), 0, nullptr, sigs[i], e,
+                                            static_cast<size_t>(r.bytes), 0, nullptr, sig, e,
                                             false)
                : g_hsa.async_copy_on_engine(r.host, host_agent, dev_p, d.gpu_agent,
-                                            static_cast<size_t>(r.bytes), 0, nullptr, sigs[i], e,
+                                            static_cast<size_t>(r.bytes), 0, nullptr, sig, e,
                                             false);
     }
     if (st != HSA_STATUS_SUCCESS) {
@@ -315,7 +352,8 @@ int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, cha
                   r.slices > 0 ? "rect copy" : "copy", static_cast<long long>(r.bytes),
                   std::max(1, static_cast<int>(r.slices)), m ? m : "?");
     }
-    lane.in_flight[half] = i + 1;
+    lane.queued[half].push_back(sig);
+    if (last[i]) lane.wake[half].push_back(sig);
   }
   return 0;
 }
