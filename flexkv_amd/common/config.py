@@ -9,11 +9,11 @@ and are not present.  Defaults that differ from the reference: the host and
 SSD layouts are BLOCKWISE (one block's layers contiguous, which the device
 path and the SSD path both move as single runs), the host cache is pinned, and
 both directions use the copy-engine path: on MI355X it moves whole-block
-transfers as fast as the zero-copy kernel (56.3 / 56.6 GB/s against 56.5 /
+transfers as fast as the zero-copy kernel (56.4 / 56.7 GB/s against 56.5 /
 57.2) while leaving the compute units to the model (GEMMs beside a 2 GiB D2H
 slow down 7% instead of 120%), and it hands small or fine-grained transfers to
 the zero-copy kernel by itself.  With a LAYERWISE host cache the copy engines
-move one rect copy per block at about 44 GB/s.
+move one rect copy per block at about 47 GB/s.
 """
 from __future__ import annotations
 
