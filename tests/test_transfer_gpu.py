@@ -268,6 +268,39 @@ def test_layerwise_host_id_runs_stage_layer_major(dev, mla, monkeypatch):
             assert np.array_equal(g, expect), f"{order} layer {l}"
 
 
+def test_layer_major_threshold_per_direction(dev, monkeypatch):
+    """Default thresholds: runs of 256 KiB per (layer, K|V) are staged
+    layer-major device-to-host (threshold 192 KiB) but move as one rect copy
+    per block host-to-device (threshold 384 KiB); both round-trip exactly."""
+    from flexkv_amd import _lib
+    from gpu_util import DeviceCase, abi_transfer
+    monkeypatch.delenv("FLEXKV_CE_LAYER_RUN_BYTES", raising=False)
+    case = KVCase(layers_total=4, num_layers=4, start_layer=0, kv=2, ng=64, nh=96, tokens=16,
+                  heads=4, dim=128, layout="LAYERWISE").fill(seed=47)   # 16 KiB chunks
+    cids = np.concatenate([np.arange(0, 16), np.arange(30, 46), np.arange(60, 76)])
+    n = len(cids)                                     # 3 runs of 16 blocks = 256 KiB
+    gids = inputs.distinct_ids(11, n, 64)
+    ids = np.ascontiguousarray(cids, dtype=np.int64)
+    dc = DeviceCase(case)
+    _lib.profile_enable(True)
+    abi_transfer(dc, gids, ids, h2d=False, mode=1)
+    prof = _lib.profile_read()
+    torch.cuda.synchronize()
+    assert prof["dma_copies"] == 3 * 4 * 2, prof      # runs x layers x K|V
+    assert np.array_equal(dc.host_np(), _oracle_d2h(case, gids, ids, 1))
+    dc.set_gpu([np.zeros_like(g) for g in case.gpu])
+    _lib.profile_enable(True)
+    abi_transfer(dc, gids, ids, h2d=True, mode=1)
+    prof = _lib.profile_read()
+    _lib.profile_enable(False)
+    torch.cuda.synchronize()
+    assert prof["dma_copies"] == n, prof              # one rect copy per block
+    for l, g in enumerate(dc.gpu_np()):
+        expect = np.zeros_like(case.gpu[l])
+        expect[:, gids] = case.gpu[l][:, gids]
+        assert np.array_equal(g, expect), f"layer {l}"
+
+
 @pytest.mark.parametrize("mode", MODES)
 def test_device_resident_cache_matches_oracle(dev, mode):
     """A "host" cache that lives in device memory (allowed by the API) moves
