@@ -600,12 +600,15 @@ def test_c_ext_dropin_on_side_stream(dev, use_ce):
 
 
 @pytest.mark.parametrize("geo", [(4, 2, 64, 16, 8, 128, 37), (130, 2, 8, 1, 1, 64, 5),
-                                 (5, 1, 30, 64, 1, 576, 11), (3, 2, 20, 1, 1, 24, 7)],
-                         ids=["8b-like", "130-layers", "mla", "48B-chunk"])
+                                 (5, 1, 30, 64, 1, 576, 11), (3, 2, 20, 1, 1, 24, 7),
+                                 (3, 1, 24, 32, 1, 1024, 9)],
+                         ids=["8b-like", "130-layers", "mla", "48B-chunk", "mla-64KiB"])
 @pytest.mark.parametrize("buffer_on_host", [False, True])
 def test_gather_scatter_match_oracle(dev, geo, buffer_on_host):
     """fkv_gather/scatter_kv_blocks against the oracle with the contiguous
-    buffer described as a block-wise cache [n, L, kv, chunk] and ids 0..n-1."""
+    buffer described as a block-wise cache [n, L, kv, chunk] and ids 0..n-1.
+    32 KiB and 64 KiB chunks (whole 32-row groups) take the gather's
+    whole-group kernel variant, the others the general one."""
     import ctypes
     from flexkv_amd import _lib
     from flexkv_amd.storage.allocator import pinned_empty
