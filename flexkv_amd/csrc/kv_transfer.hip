@@ -16,7 +16,9 @@
 // kUnroll rows, issuing all loads of a group before any store.  Rows are
 // ordered block -> layer -> K|V -> offset, which is host-address order for the
 // block-wise host layout.  Layer base pointers travel in the kernel argument
-// block (scalar loads, no PCIe round trip per chunk).
+// block (scalar loads, no PCIe round trip per chunk).  Staging gathers whose
+// chunks are whole groups of 32 rows address each group from one buffer
+// resource per side instead of a 64-bit base per row.
 //
 // This file holds the kernels, the transfer paths that launch them and the
 // transfer entry points of the C ABI; kv_host.cpp holds validation, id staging
@@ -361,7 +363,8 @@ int ensure_device_basics(int dev) {
 // several per tile so one LDS id load serves more rows.  Rows per tile stay
 // below 2^31.  Measured on MI355X (2 GiB gather at the Llama-3-8B shape):
 // 32 rows in flight per wavefront with one workgroup per tile and 16 tiles
-// per slot reaches the device's plain-copy rate (~5.9 TB/s).
+// per slot is the best shape (6.0 TB/s with whole-group addressing; 4 and 8
+// tiles per slot 5.93 / 6.00, 32 tiles 5.44).
 void choose_tiles(int nb, int nl, int kv, int rpc, int grid_cap, int factor, CopyArgs* a) {
   const int64_t target = factor * static_cast<int64_t>(std::max(1, grid_cap));
   auto tiles = [&](int tb, int tl) {
