@@ -63,7 +63,8 @@ bool range_inside(const char* p, __int128 lo, __int128 hi, const PtrInfo& info);
 // gather/scatter kernel that last used the half, on the caller's stream).
 // Every copy has a signal of its own.  Each engine's last copy of a half
 // signals an interrupt signal (`wake`), the host's blocking wait; the others
-// signal polled signals, which add no interrupt to the engine's work (small
+// signal polled signals (GPU-only consumers: the host reads their values but
+// never waits on them), which add no interrupt to the engine's work (small
 // copies run 5-25% faster on MI355X).  The two directions have a lane each,
 // so a device-to-host and a host-to-device transfer run at the same time.
 struct CopyLane {
@@ -269,7 +270,7 @@ int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, cha
 // Wait until every copy queued on a staging half has finished: block on the
 // interrupt signals of the engines' last copies, then check every copy's own
 // signal.  An engine runs its copies in order, so the check normally finds
-// them done; if one is not, the wait polls until it is.  A counted signal
+// them done; if one is not, the check reloads it until it is.  A counted signal
 // shared by many copies would instead depend on every layer between here and
 // the engines decrementing it by exactly one.
 void sdma_wait(CopyLane& lane, int half);

@@ -13,6 +13,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <type_traits>
 #include <vector>
 
@@ -147,11 +148,10 @@ void sdma_wait(CopyLane& d, int half) {
     while (g_hsa.signal_wait_scacquire(s, HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX,
                                        HSA_WAIT_STATE_BLOCKED) >= 1) {
     }
+  // The polled signals are created for GPU consumers, so the host only ever
+  // loads their values (any agent may) and never waits on them.
   for (hsa_signal_t s : d.queued[half])
-    if (g_hsa.signal_load_scacquire(s) >= 1)
-      while (g_hsa.signal_wait_scacquire(s, HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX,
-                                         HSA_WAIT_STATE_ACTIVE) >= 1) {
-      }
+    while (g_hsa.signal_load_scacquire(s) >= 1) std::this_thread::yield();
   d.queued[half].clear();
   d.wake[half].clear();
 }
