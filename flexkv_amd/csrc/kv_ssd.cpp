@@ -15,7 +15,7 @@
 // (transfer_ssd.cpp:201), like the reference.  The kernel cannot do direct
 // I/O into host memory that HIP pinned (hipHostMalloc memory is not
 // page-pinnable by get_user_pages: O_DIRECT reads into it fail with EFAULT),
-// so direct reads land in 1 MiB page-aligned bounce buffers of ordinary
+// so direct reads land in page-aligned bounce buffers of ordinary
 // memory and are copied into the host cache from there.  Unlike the reference's one
 // request per chunk, chunks adjacent in both the file and the host cache are
 // merged into one request (up to FLEXKV_SSD_MAX_REQUEST_BYTES, default
@@ -356,7 +356,10 @@ struct ErrorSlot {
 bool direct_ok(const Request& r) { return r.bytes % 4096 == 0 && r.off % 4096 == 0; }
 
 // Bytes of one O_DIRECT read and of each bounce buffer.
-constexpr int64_t kBounceBytes = int64_t(1) << 20;
+// Measured on MI355X hosts (ext4, 1 GiB of O_DIRECT reads into random
+// pinned host blocks, 32 threads): 4 MiB buffers read 4.9-5.3 GB/s, 1 MiB
+// buffers 4.5 GB/s on the same boxes.
+constexpr int64_t kBounceBytes = int64_t(4) << 20;
 
 // Page-aligned bounce buffers of ordinary memory, kept for the handle's
 // lifetime and shared by its calls.
@@ -475,19 +478,23 @@ void run_threads(fkv_ssd_s* h, const Plan& p, int threads_per_device, ErrorSlot&
   for (auto& t : threads) t.join();
 }
 
-// Bounce memory of a ring: regions of FKV_SSD_RING_PIECE_KIB, at most one
-// per ring slot and FKV_SSD_RING_BOUNCE_MIB in all.  Measured on an MI355X
-// host (ext4, 2 GiB of O_DIRECT reads into pinned host memory, depth 256):
-// 256 KiB pieces (256 in flight) read 5.6-6.0 GB/s, 1 MiB pieces (64 in
-// flight) 5.2-5.7 GB/s.
-#ifndef FKV_SSD_RING_PIECE_KIB
-#define FKV_SSD_RING_PIECE_KIB 256
-#endif
-#ifndef FKV_SSD_RING_BOUNCE_MIB
-#define FKV_SSD_RING_BOUNCE_MIB 64
-#endif
-constexpr int64_t kRingPiece = int64_t(FKV_SSD_RING_PIECE_KIB) << 10;
-constexpr int64_t kRingBounceTotal = int64_t(FKV_SSD_RING_BOUNCE_MIB) << 20;
+// Bounce memory of a ring: regions of FLEXKV_SSD_RING_PIECE_KIB (default
+// 1024, a multiple of 4 KiB), at most one per ring slot and
+// FLEXKV_SSD_RING_BOUNCE_MIB (default 256) in all, read when the ring first
+// needs them.  The disk wants many bytes in flight: measured on MI355X hosts
+// (ext4, 1 GiB of O_DIRECT reads into random pinned host blocks, depth 256),
+// 1 MiB pieces with 256 MiB in all read 5.8-6.9 GB/s, 256 KiB pieces with
+// 64 MiB in all 2.9-3.5 GB/s on the same boxes.
+int64_t ring_piece_bytes() {
+  const char* e = getenv("FLEXKV_SSD_RING_PIECE_KIB");
+  int64_t v = (e ? atoll(e) : 1024) << 10;
+  v = std::max<int64_t>(v, 4096) & ~int64_t(4095);   // O_DIRECT offsets stay page aligned
+  return std::min<int64_t>(v, int64_t(1) << 30);      // an io_uring length is 32-bit
+}
+int64_t ring_bounce_total() {
+  const char* e = getenv("FLEXKV_SSD_RING_BOUNCE_MIB");
+  return std::max<int64_t>(1, e ? atoll(e) : 256) << 20;
+}
 
 // Every request of every device through the handle's ring, at most depth()
 // entries in flight.  Direct reads are cut into bounce-region-sized pieces,
@@ -503,11 +510,12 @@ void run_uring(fkv_ssd_s* h, const Plan& p, ErrorSlot& err) {
   std::vector<unsigned> free_slots(u.depth());
   for (unsigned i = 0; i < u.depth(); ++i) free_slots[i] = u.depth() - 1 - i;
   if (p.direct && !h->ring_bounce) {
+    const int64_t piece = ring_piece_bytes();
     const unsigned regions = static_cast<unsigned>(
-        std::max<int64_t>(1, std::min<int64_t>(u.depth(), kRingBounceTotal / kRingPiece)));
+        std::max<int64_t>(1, std::min<int64_t>(u.depth(), ring_bounce_total() / piece)));
     h->ring_bounce = static_cast<char*>(
-        std::aligned_alloc(4096, static_cast<size_t>(kRingPiece) * regions));
-    h->ring_piece = h->ring_bounce ? kRingPiece : 0;
+        std::aligned_alloc(4096, static_cast<size_t>(piece) * regions));
+    h->ring_piece = h->ring_bounce ? piece : 0;
     h->ring_regions = h->ring_bounce ? regions : 0;
   }
   const int64_t piece_bytes = h->ring_piece;
