@@ -858,7 +858,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the transfer path is per-GPU (one PCIe link, one HBM); "
-              "multi-GPU runs are out of scope for this build", file=sys.stderr)
+              "multi-GPU runs are out of scope for this package", file=sys.stderr)
         return 2
     ceilings = None if (args.quick or args.counters) else device_ceilings()
     if not torch.cuda.is_available():

@@ -96,7 +96,7 @@ def make_configs(args: argparse.Namespace) -> Tuple[ModelConfig, CacheConfig, Be
                             shuffle_ids=args.shuffle_ids, warmup_round=args.warmup_round,
                             benchmark_round=args.benchmark_round)
     if model.tp_size != 1:
-        raise ValueError("this build runs one GPU per worker: tp_size must be 1")
+        raise ValueError("this package runs one GPU per worker: tp_size must be 1")
     return model, cache, bench
 
 

@@ -25,7 +25,7 @@ class TensorSharedHandle:
     def get_tensor(self) -> torch.Tensor:
         try:
             tensor = self.rebuild_func(*self.rebuild_args)
-        except Exception as e:  # pragma: no cover - exercised only on GPU boxes
+        except Exception as e:  # pragma: no cover - exercised only with a GPU
             raise RuntimeError(f"importing shared device tensor failed: {e}") from e
         if not isinstance(tensor, torch.Tensor):
             raise RuntimeError("shared handle did not rebuild a tensor")

@@ -1,7 +1,8 @@
 """CPU oracle for the GPU<->CPU KV-block transfer.
 
 TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()``
-and the ``cpu_baseline`` leg of ``bench.py`` as the checker / CPU baseline.
+and the ``cpu_baseline`` leg of ``bench.py``, as the parity oracle and the CPU
+baseline.
 The product package ``flexkv_amd`` never imports it.
 
 ``transfer_kv_blocks`` calls the C restatement in ``kv_oracle.c`` (built into

@@ -1,7 +1,7 @@
 /*
  * kv_oracle.c - CPU restatement of FlexKV's GPU<->CPU KV-block transfer.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the checker for the HIP transfer
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity oracle for the HIP transfer
  * library and the CPU baseline that bench.py times; it is never linked into
  * or called by the product path (flexkv_amd), which fails loudly when its
  * HIP library is missing.
