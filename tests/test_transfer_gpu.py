@@ -457,19 +457,24 @@ def test_zero_copy_cu_limits(dev, cus):
     check_case(case, inputs.distinct_ids(1, 64, 80), inputs.distinct_ids(2, 64, 80), 0, cus)
 
 
+@pytest.mark.parametrize("heads", [2, 8])
 @pytest.mark.parametrize("run", [1, 8, 64])
-def test_staged_runs_and_small_staging(dev, run):
+def test_staged_runs_and_small_staging(dev, run, heads):
     """Copy-engine path with a tiny staging buffer: many pieces, run merging
-    across consecutive host ids, and a layer window split."""
+    across consecutive host ids, and a layer window split.  8 KiB chunks take
+    the general gather; 32 KiB chunks (8 heads, host layers 2..9 of 10) the
+    whole-group gather, with pieces that start past layer 0."""
     from flexkv_amd import _lib
     _lib.set_staging_bytes(1 << 20)
     try:
-        case = KVCase(layers_total=8, num_layers=8, start_layer=0, kv=2, ng=256, nh=512,
-                      tokens=16, heads=2, dim=128).fill(seed=run)
+        start = 2 if heads == 8 else 0
+        case = KVCase(layers_total=8 + start, num_layers=8, start_layer=start, kv=2, ng=256,
+                      nh=512, tokens=16, heads=heads, dim=128).fill(seed=run)
         gids = inputs.run_ids(3, 128, 256, run)
         cids = inputs.run_ids(4, 128, 512, run)
         check_case(case, gids, cids, 1)
-        # one block row (8*2*8 KiB = 128 KiB) per half would not fit 64 KiB
+        # one block row (8*2*8 KiB = 128 KiB, or 512 KiB) per half would not
+        # fit 64 KiB: the layer window splits
         _lib.release_staging()
         _lib.set_staging_bytes(128 << 10)
         check_case(case, gids, cids, 1)
