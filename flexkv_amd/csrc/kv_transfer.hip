@@ -163,6 +163,8 @@ struct CopyArgs {
   int32_t tile_blocks;       // a tile is tile_blocks blocks x tile_layers layers
   int32_t tile_layers;
   int32_t tiles_b;           // tiles along the block axis
+  int32_t tiles_r;           // row ranges per tile (small transfers split a tile's rows)
+  uint32_t split_rows;       // rows per range: a whole tile, or a multiple of the unroll
   int32_t num_tiles;
   int32_t ptrs_per_layer;    // 1: layer_ptr[l] + k*gpu_kv_stride; kv: layer_ptr[l*kv + k]
   uint64_t layer_ptr[kMaxLayersPerLaunch];
@@ -205,8 +207,9 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
   const bool full_rows = (a.chunk_vec & 63) == 0;
 
   for (int tile = blockIdx.x; tile < a.num_tiles; tile += gridDim.x) {
-    const int tb = tile % a.tiles_b;
-    const int tl = tile / a.tiles_b;
+    const int tr = tile % a.tiles_r;
+    const int tb = (tile / a.tiles_r) % a.tiles_b;
+    const int tl = (tile / a.tiles_r) / a.tiles_b;
     const int b0 = tb * a.tile_blocks;
     const int nb = min(a.tile_blocks, a.num_blocks - b0);
     const int l0 = tl * a.tile_layers;
@@ -220,11 +223,14 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
     }
     __syncthreads();
 
+    // this workgroup's rows of the tile: [g_begin, g_end)
     const uint32_t rows = static_cast<uint32_t>(nb) * items_per_block * rpc;
+    const uint32_t g_begin = static_cast<uint32_t>(tr) * a.split_rows;
+    const uint32_t g_end = min(rows, g_begin + a.split_rows);
     if constexpr (kWhole) {
       // Groups start at multiples of kUnroll, so each lies inside one chunk:
       // consecutive 1 KiB rows on both sides.
-      for (uint32_t g = static_cast<uint32_t>(wave) * kUnroll; g < rows;
+      for (uint32_t g = g_begin + static_cast<uint32_t>(wave) * kUnroll; g < g_end;
            g += kWaves * kUnroll) {
         const uint32_t item = g / rpc;
         const uint32_t rr = g - item * rpc;
@@ -258,7 +264,7 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
                                                  kNtStore ? kCachePolicyNt : 0);
       }
     } else {
-      for (uint32_t g = static_cast<uint32_t>(wave) * kUnroll; g < rows;
+      for (uint32_t g = g_begin + static_cast<uint32_t>(wave) * kUnroll; g < g_end;
            g += kWaves * kUnroll) {
         // Decompose the group's first row once; later rows advance a cursor
         // over (block, layer, K|V, row) in that order.
@@ -283,7 +289,7 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
                       static_cast<int64_t>(k) * a.gpu_kv_stride + gid * a.gpu_block_stride + row_off;
           char* cpu = a.cpu_base + static_cast<int64_t>(layer) * a.cpu_layer_stride +
                       static_cast<int64_t>(k) * a.cpu_kv_stride + cid * a.cpu_block_stride + row_off;
-          live[u] = (g + u < rows) &&
+          live[u] = (g + u < g_end) &&
                     (full_rows || static_cast<int64_t>(rr) * 64 + lane < a.chunk_vec);
           src[u] = kH2D ? cpu : gpu;
           dst[u] = kH2D ? gpu : cpu;
@@ -365,7 +371,14 @@ int ensure_device_basics(int dev) {
 // 32 rows in flight per wavefront with one workgroup per tile and 16 tiles
 // per slot is the best shape (6.0 TB/s with whole-group addressing; 4 and 8
 // tiles per slot 5.93 / 6.00, 32 tiles 5.44).
-void choose_tiles(int nb, int nl, int kv, int rpc, int grid_cap, int factor, CopyArgs* a) {
+//
+// A transfer too small for that many tiles even one (block, layer) per tile
+// splits each tile's rows into up to `factor`-filling ranges of at least one
+// `unroll`-row group per wavefront, so more wavefronts share its few chunks:
+// one block of one layer moves in one round of loads instead of several
+// (zero-copy latency is bound by PCIe round trips).
+void choose_tiles(int nb, int nl, int kv, int rpc, int grid_cap, int factor, int unroll,
+                  CopyArgs* a) {
   const int64_t target = factor * static_cast<int64_t>(std::max(1, grid_cap));
   auto tiles = [&](int tb, int tl) {
     return static_cast<int64_t>((nb + tb - 1) / tb) * ((nl + tl - 1) / tl);
@@ -375,10 +388,21 @@ void choose_tiles(int nb, int nl, int kv, int rpc, int grid_cap, int factor, Cop
   while (tb < kMaxTileBlocks && tiles(tb * 2, tl) >= target) tb *= 2;
   while (tb > 1 && static_cast<int64_t>(tb) * tl * kv * rpc >= (int64_t(1) << 31)) tb /= 2;
   while (tl > 1 && static_cast<int64_t>(tb) * tl * kv * rpc >= (int64_t(1) << 31)) tl = (tl + 1) / 2;
+  const int64_t t = tiles(tb, tl);
+  const int64_t tile_rows = static_cast<int64_t>(tb) * tl * kv * rpc;
+  int64_t tr = 1, split = tile_rows;
+  if (t < target) {
+    const int64_t min_split = static_cast<int64_t>(unroll) * kWaves;
+    tr = std::min<int64_t>(std::max<int64_t>(1, tile_rows / min_split), (target + t - 1) / t);
+    split = ((tile_rows + tr - 1) / tr + unroll - 1) / unroll * unroll;
+    tr = (tile_rows + split - 1) / split;
+  }
   a->tile_blocks = tb;
   a->tile_layers = tl;
   a->tiles_b = (nb + tb - 1) / tb;
-  a->num_tiles = static_cast<int32_t>(tiles(tb, tl));
+  a->tiles_r = static_cast<int32_t>(tr);
+  a->split_rows = static_cast<uint32_t>(split);
+  a->num_tiles = static_cast<int32_t>(t * tr);
 }
 
 // Fill the per-launch part of CopyArgs and launch over `nb` blocks starting at
@@ -405,9 +429,11 @@ int launch_copy(const Geometry& g, char* ids_dev, char* cpu_base, int64_t cks, i
   a.ptrs_per_layer = g.ptrs_per_layer;
   for (int i = 0; i < nl * g.ptrs_per_layer; ++i)
     a.layer_ptr[i] = reinterpret_cast<uint64_t>(g.layer_ptrs[l0 * g.ptrs_per_layer + i]);
+  constexpr int kLaunchUnroll = kIota ? (kH2D ? FKV_UNROLL_SCATTER : kUnrollHbm)
+                                     : (kH2D ? FKV_UNROLL_ZC_H2D : FKV_UNROLL_ZC_D2H);
   choose_tiles(nb, nl, g.kv, a.rows_per_chunk, grid_cap,
                kIota ? (kH2D ? FKV_TILE_FACTOR_SCATTER : FKV_TILE_FACTOR_HBM) : FKV_TILE_FACTOR,
-               &a);
+               kLaunchUnroll, &a);
   int grid = std::max(1, std::min(grid_cap, a.num_tiles));
   if (kIota && FKV_HBM_ONEPASS) grid = a.num_tiles;
   hipEvent_t ev = nullptr;
