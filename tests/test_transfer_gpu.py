@@ -484,6 +484,23 @@ def test_staged_runs_and_small_staging(dev, run, heads):
 
 
 @pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("shape", [(1, 1, 32776, 1, 1), (3, 2, 32776, 1, 1),
+                                   (1, 1, 128, 8, 16), (1, 1, 256, 16, 16)],
+                         ids=["65-rows-1x1", "65-rows-3x2", "32KiB-1x1", "128KiB-1x1"])
+def test_small_transfers_split_rows(dev, mode, shape):
+    """Transfers with fewer (block, layer) tiles than grid slots split each
+    tile's rows over several workgroups.  Chunks of 64 KiB + 16 B (65 rows,
+    the last a single vector) put range boundaries inside chunks and partial
+    rows at range ends; 32 KiB chunks split in the zero-copy kernels; 128 KiB
+    chunks (256 rows per tile) split in the staging kernels too, through the
+    whole-group gather in copy-engine mode."""
+    n, nl, dim, heads, tokens = shape
+    case = KVCase(layers_total=nl, num_layers=nl, start_layer=0, kv=2, ng=8, nh=12,
+                  tokens=tokens, heads=heads, dim=dim).fill(seed=n * 10 + nl)
+    check_case(case, inputs.distinct_ids(n + 40, n, 8), inputs.distinct_ids(n + 41, n, 12), mode)
+
+
+@pytest.mark.parametrize("mode", MODES)
 def test_duplicate_sources_and_single_block(dev, mode):
     case = KVCase(layers_total=2, num_layers=2, start_layer=0, kv=2, ng=8, nh=16, tokens=16,
                   heads=2, dim=64).fill(seed=2)
