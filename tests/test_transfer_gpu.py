@@ -65,7 +65,8 @@ def check_case(case, gids, cids, mode, transfer_cus=-1):
         "layers_total", "num_layers", "start_layer", "kv", "ng", "nh", "tokens", "heads", "dim",
         "dtype", "layout", "tp", "rank")})
     case2.fill(seed=99)
-    case2.host = want ^ np.asarray(0x1234, dtype=case.dtype)
+    flip = 0x1234 & ((1 << (8 * np.dtype(case.dtype).itemsize)) - 1)
+    case2.host = want ^ np.asarray(flip, dtype=case.dtype)
     init = case2.gpu
     dc.set_host(case2.host)
     dc.set_gpu(init)
@@ -128,6 +129,7 @@ GEOMETRIES = [
     (2, 2, 0, 2, 40, 40, 16, 2, 128, np.uint16, "BLOCKWISE", 4, 3, 25),   # TP host chunk, rank 3
     (130, 130, 0, 2, 6, 8, 1, 1, 64, np.uint16, "BLOCKWISE", 1, 0, 5),    # >128 layers: 2 launches
     (2, 2, 0, 2, 600, 700, 2, 2, 32, np.uint32, "BLOCKWISE", 1, 0, 520),  # many tiles
+    (4, 4, 0, 2, 64, 96, 16, 8, 128, np.uint8, "LAYERWISE", 1, 0, 40),    # 1-byte (fp8) cache
 ]
 
 
