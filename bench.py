@@ -849,6 +849,9 @@ def main() -> int:
                     help="D2H/H2D path reported as value (default: the product default)")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--quick", action="store_true", help="skip baselines (for profiling runs)")
+    ap.add_argument("--layerwise-only", action="store_true",
+                    help="run only the layer-wise H2D section (sync per layer, async handle, "
+                         "overlap with per-layer GEMMs) and print its JSON (for profiling runs)")
     ap.add_argument("--seed", type=int, default=1001)
     ap.add_argument("--counters", action="store_true",
                     help="run only the kernels a PMC pass needs: a 1 GiB plain device copy "
@@ -860,7 +863,8 @@ def main() -> int:
         print("bench.py measures one GPU: the transfer path is per-GPU (one PCIe link, one HBM); "
               "multi-GPU runs are out of scope for this package", file=sys.stderr)
         return 2
-    ceilings = None if (args.quick or args.counters) else device_ceilings()
+    ceilings = (None if (args.quick or args.counters or args.layerwise_only)
+                else device_ceilings())
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 2
@@ -875,6 +879,10 @@ def main() -> int:
     default_ce = {"kernel": False, "ce": True}[args.path] if args.path else cfg.use_ce_transfer_d2h
     wl = Workload(args.workload, args.seed, args.run, host_layout=args.host_layout)
     gb = wl.bytes_per_op / 1e9
+    if args.layerwise_only:
+        wl.transfer(False, default_ce)   # the host cache holds the blocks read back below
+        print(json.dumps({"layerwise_h2d": layerwise_h2d(wl, args.steps)}), flush=True)
+        return 0
 
     # primary: D2H on the default path, library kernel timing on
     _lib.profile_enable(True)
