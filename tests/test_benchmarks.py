@@ -104,3 +104,17 @@ def test_reference_example_config_loads():
     assert model.num_layers > 0 and model.dtype in (torch.bfloat16, torch.float16)
     assert isinstance(cache.cpu_kv_layout_type, KVCacheLayoutType)
     assert bench.transfer_type == TransferType.D2H
+
+
+@pytest.mark.parametrize("gpus", ["2", "8"])
+def test_bench_refuses_more_than_one_gpu(gpus):
+    """bench.py measures one GPU; asked for more it exits with status 2 and
+    says so, before touching any device."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", gpus],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
