@@ -272,8 +272,11 @@ int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, cha
 // signal.  An engine runs its copies in order, so the check normally finds
 // them done; if one is not, the check reloads it until it is.  A counted signal
 // shared by many copies would instead depend on every layer between here and
-// the engines decrementing it by exactly one.
-void sdma_wait(CopyLane& lane, int half);
+// the engines decrementing it by exactly one.  `spin` waits actively instead
+// of sleeping: for the last wait of a call, where the host's wake-up from a
+// sleep that lasted the whole transfer (15-30 us measured) would add to the
+// call's time; a wait overlapped with the other half's copies sleeps.
+void sdma_wait(CopyLane& lane, int half, bool spin = false);
 
 // When a transfer fails after enqueueing work, wait for that work before the
 // call returns: a copy must not land in the caller's buffers, or read the

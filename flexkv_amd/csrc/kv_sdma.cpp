@@ -143,10 +143,10 @@ hsa_status_t first_cpu_agent(hsa_agent_t a, void* out) {
 
 }  // namespace
 
-void sdma_wait(CopyLane& d, int half) {
+void sdma_wait(CopyLane& d, int half, bool spin) {
+  const hsa_wait_state_t how = spin ? HSA_WAIT_STATE_ACTIVE : HSA_WAIT_STATE_BLOCKED;
   for (hsa_signal_t s : d.wake[half])
-    while (g_hsa.signal_wait_scacquire(s, HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX,
-                                       HSA_WAIT_STATE_BLOCKED) >= 1) {
+    while (g_hsa.signal_wait_scacquire(s, HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX, how) >= 1) {
     }
   // The polled signals are created for GPU consumers, so the host only ever
   // loads their values (any agent may) and never waits on them.

@@ -610,7 +610,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
       if ((rc = queue_copies(pi))) return rc;
     for (int pi = 0; pi < np; ++pi) {
       const int h = pi & 1;
-      sdma_wait(ln, h);
+      sdma_wait(ln, h, /*spin=*/pi + 1 == np);   // the last piece has nothing behind it
       pending[h] = false;
       hipLaunchKernelGGL(acquire_system_kernel, dim3(d.num_cus), dim3(64), 0, stream);
       FKV_HIP(hipGetLastError());
@@ -623,7 +623,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
     }
   }
   for (int h = 0; h < 2; ++h)
-    if (pending[h]) sdma_wait(ln, h);
+    if (pending[h]) sdma_wait(ln, h, /*spin=*/true);
   FKV_HIP(hipStreamSynchronize(stream));
   drain.armed = false;
   if (prof.on) {
