@@ -310,6 +310,7 @@ def layerwise_h2d(wl: Workload, steps: int):
     comp_s, _, _ = time_steps(compute_only, steps, 1)
     ser_s, _, _ = time_steps(serial, steps, 1)
     ovl_s, _, _ = time_steps(overlapped, steps, 1)
+    c_ext.release_transfer_stream(xfer)
     gb = wl.bytes_per_op / 1e9
     return {
         "granularity_layers": 1,
@@ -552,6 +553,7 @@ def overlap_with_compute(wl: Workload, steps: int = 3, gemms: int = 160):
             key = ("h2d" if h2d else "d2h") + ("_ce" if ce else "_kernel")
             out[key] = {"gemm_ms": round(statistics.median(r["gemm"] for r in rs) * 1e3, 2),
                         "transfer_ms": round(statistics.median(r["xfer"] for r in rs) * 1e3, 2)}
+    c_ext.release_transfer_stream(xfer)
     out["what"] = (f"{gemms} GEMMs on a compute stream beside one {wl.bytes_per_op / 2**30:.0f} "
                    "GiB transfer on a transfer stream")
     return out

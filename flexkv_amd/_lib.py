@@ -8,6 +8,7 @@ must not hold two HIP runtimes, and ``load()`` verifies it does not).
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
 import os
 import threading
@@ -51,6 +52,7 @@ EXPORTED_SYMBOLS = (
     "fkv_host_unregister",
     "fkv_set_staging_bytes",
     "fkv_release_staging",
+    "fkv_finalize",
     "fkv_profile_enable",
     "fkv_profile_read",
     "fkv_version",
@@ -89,6 +91,9 @@ class SsdStats(ctypes.Structure):
 
 _lock = threading.Lock()
 _lib = None
+# Counts finalize() calls: handles and streams made before the latest one
+# are gone, and their objects skip the library call when released.
+generation = 0
 
 
 def _declare(lib: ctypes.CDLL) -> None:
@@ -146,6 +151,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.fkv_set_staging_bytes.argtypes = [c_sz]
     lib.fkv_release_staging.restype = c_int
     lib.fkv_release_staging.argtypes = []
+    lib.fkv_finalize.restype = c_int
+    lib.fkv_finalize.argtypes = []
     lib.fkv_profile_enable.restype = c_int
     lib.fkv_profile_enable.argtypes = [c_int]
     lib.fkv_profile_read.restype = c_int
@@ -187,7 +194,26 @@ def load() -> ctypes.CDLL:
             if len(runtimes) > 1:
                 raise ImportError(f"two HIP runtimes are mapped into this process: {runtimes}")
             _lib = lib
+            atexit.register(finalize)
     return _lib
+
+
+def finalize() -> None:
+    """Release every resource the library holds (fkv_finalize): unreleased
+    layer-wise handles, streams from fkv_stream_create, copy-engine signals,
+    events and staging, pinned id buffers.  Registered with atexit when the
+    library loads, so these objects are destroyed while the interpreter is
+    still running, before the HIP and HSA runtimes run their own exit-time
+    finalizers; otherwise the runtimes would tear them down themselves, in an
+    order no caller controls.  A no-op when the library was never loaded."""
+    global generation
+    if _lib is None:
+        return
+    generation += 1
+    rc = _lib.fkv_finalize()
+    if rc != 0:
+        import sys
+        print(f"flexkv: fkv_finalize failed (status {rc}): {last_error()}", file=sys.stderr)
 
 
 def last_error() -> str:

@@ -16,6 +16,7 @@ from . import _lib
 __all__ = ["transfer_kv_blocks", "transfer_kv_blocks_kv_ptrs", "gather_kv_blocks",
            "scatter_kv_blocks",
            "transfer_kv_blocks_layerwise", "LayerwiseTransfer", "transfer_stream",
+           "release_transfer_stream",
            "SSDIOCTX", "transfer_kv_blocks_ssd"]
 
 
@@ -191,6 +192,7 @@ class LayerwiseTransfer:
     def __init__(self, handle: int, keep_alive: tuple) -> None:
         self._h = handle
         self._keep = keep_alive
+        self._gen = _lib.generation
         lib = _lib.load()
         self.num_groups = lib.fkv_handle_num_groups(handle) if handle else 0
 
@@ -225,10 +227,11 @@ class LayerwiseTransfer:
                    "fkv_handle_stream_wait")
 
     def release(self) -> None:
-        """Wait for every group, then free the handle (idempotent)."""
+        """Wait for every group, then free the handle (idempotent; after
+        the library's exit-time finalize the handle is already gone)."""
         h, self._h = self._h, None
         self._keep = ()
-        if h:
+        if h and self._gen == _lib.generation:
             _lib.check(_lib.load().fkv_handle_release(h), "fkv_handle_release")
 
     def __enter__(self) -> "LayerwiseTransfer":
@@ -283,13 +286,31 @@ def transfer_kv_blocks_layerwise(gpu_block_id_tensor: torch.Tensor,
 def transfer_stream(num_cus: int = 0) -> torch.cuda.ExternalStream:
     """A torch stream on its own hardware queue (fkv_stream_create) for
     transfers meant to overlap with compute; num_cus = 0 keeps every compute
-    unit.  The stream lives until the process ends."""
+    unit.  Destroy it with release_transfer_stream once no work uses it; one
+    still alive at process exit is destroyed by the library's exit hook."""
     import ctypes
 
     lib = _lib.load()
     out = ctypes.c_void_p()
     _lib.check(lib.fkv_stream_create(int(num_cus), ctypes.byref(out)), "fkv_stream_create")
+    _stream_gen[out.value] = _lib.generation
     return torch.cuda.ExternalStream(out.value)
+
+
+# raw handle -> library generation of each stream made by transfer_stream
+_stream_gen = {}
+
+
+def release_transfer_stream(stream: torch.cuda.ExternalStream) -> None:
+    """Synchronise and destroy a stream made by transfer_stream
+    (fkv_stream_destroy).  The stream object must not be used afterwards."""
+    gen = _stream_gen.pop(stream.cuda_stream, None)
+    if gen is None:
+        raise RuntimeError("not a stream made by transfer_stream, or already released")
+    if gen != _lib.generation:
+        return                      # the library's finalize destroyed it already
+    stream.synchronize()
+    _lib.check(_lib.load().fkv_stream_destroy(stream.cuda_stream), "fkv_stream_destroy")
 
 
 class SSDIOCTX:

@@ -86,35 +86,80 @@ namespace {
 std::mutex g_prof_mu;
 fkv_profile g_prof{};
 
-// Thread-local pinned buffer holding the packed (gpu_id, cpu_id) pairs the
-// kernels read.  Calls are synchronous, so the previous call's kernels have
-// finished before the buffer is rewritten or regrown.  Buffers are not freed
-// at thread exit (the runtime may already be gone at process exit).
-struct PinnedIds {
-  int64_t* p = nullptr;
-  char* dev = nullptr;
-  size_t cap = 0;  // bytes
-};
-thread_local PinnedIds t_ids;
+// The pool of pinned id buffers (ids_acquire / ids_release).
+std::mutex g_ids_mu;
+std::vector<IdBuf> g_ids_free;
+
+// Streams made by fkv_stream_create and not destroyed yet; fkv_finalize
+// destroys them.
+std::mutex g_streams_mu;
+std::vector<hipStream_t> g_streams;
 }  // namespace
 
-int pinned_ids(size_t bytes, int64_t** host, char** dev) {
-  if (bytes > t_ids.cap) {
-    if (t_ids.p) FKV_HIP(hipHostFree(t_ids.p));
-    t_ids.p = nullptr;
-    t_ids.cap = 0;
-    size_t cap = std::max<size_t>(bytes, 64 << 10);
-    void* p = nullptr;
-    FKV_HIP(hipHostMalloc(&p, cap, hipHostMallocPortable | hipHostMallocMapped | hipHostMallocCoherent));
-    void* dp = nullptr;
-    FKV_HIP(hipHostGetDevicePointer(&dp, p, 0));
-    t_ids.p = static_cast<int64_t*>(p);
-    t_ids.dev = static_cast<char*>(dp);
-    t_ids.cap = cap;
+int ids_acquire(size_t bytes, IdBuf* out) {
+  {
+    std::lock_guard<std::mutex> lk(g_ids_mu);
+    size_t best = g_ids_free.size();
+    for (size_t i = 0; i < g_ids_free.size(); ++i)
+      if (g_ids_free[i].cap >= bytes &&
+          (best == g_ids_free.size() || g_ids_free[i].cap < g_ids_free[best].cap))
+        best = i;
+    if (best != g_ids_free.size()) {
+      *out = g_ids_free[best];
+      g_ids_free.erase(g_ids_free.begin() + static_cast<long>(best));
+      return 0;
+    }
   }
-  *host = t_ids.p;
-  *dev = t_ids.dev;
+  IdBuf b;
+  b.cap = std::max<size_t>(bytes, 64 << 10);
+  void* p = nullptr;
+  FKV_HIP(hipHostMalloc(&p, b.cap, hipHostMallocPortable | hipHostMallocMapped | hipHostMallocCoherent));
+  void* dp = nullptr;
+  const hipError_t e = hipHostGetDevicePointer(&dp, p, 0);
+  if (e != hipSuccess) {
+    (void)hipHostFree(p);
+    return fail(static_cast<int>(e), "hipHostGetDevicePointer failed: %s", hipGetErrorString(e));
+  }
+  b.host = static_cast<int64_t*>(p);
+  b.dev = static_cast<char*>(dp);
+  *out = b;
   return 0;
+}
+
+void ids_release(const IdBuf& b) {
+  std::lock_guard<std::mutex> lk(g_ids_mu);
+  g_ids_free.push_back(b);
+}
+
+int ids_pool_free() {
+  std::vector<IdBuf> bufs;
+  {
+    std::lock_guard<std::mutex> lk(g_ids_mu);
+    bufs.swap(g_ids_free);
+  }
+  int rc = 0;
+  for (const IdBuf& b : bufs) {
+    const hipError_t e = hipHostFree(b.host);
+    if (e != hipSuccess && rc == 0)
+      rc = fail(static_cast<int>(e), "hipHostFree of an id buffer: %s", hipGetErrorString(e));
+  }
+  return rc;
+}
+
+int streams_destroy_all() {
+  std::vector<hipStream_t> streams;
+  {
+    std::lock_guard<std::mutex> lk(g_streams_mu);
+    streams.swap(g_streams);
+  }
+  int rc = 0;
+  for (hipStream_t s : streams) {
+    hipError_t e = hipStreamSynchronize(s);
+    if (e == hipSuccess) e = hipStreamDestroy(s);
+    if (e != hipSuccess && rc == 0)
+      rc = fail(static_cast<int>(e), "destroying a library stream: %s", hipGetErrorString(e));
+  }
+  return rc;
 }
 
 int validate(Geometry& g, int mode) {
@@ -213,11 +258,11 @@ void pack_ids_into(const Geometry& g, int64_t* h) {
   }
 }
 
-int pack_ids(const Geometry& g, char** ids_dev) {
-  int64_t* h = nullptr;
-  int rc = pinned_ids(static_cast<size_t>(g.num_blocks) * 16, &h, ids_dev);
+int pack_ids(const Geometry& g, IdLease& lease, char** ids_dev) {
+  int rc = ids_acquire(static_cast<size_t>(g.num_blocks) * 16, &lease.buf);
   if (rc) return rc;
-  pack_ids_into(g, h);
+  pack_ids_into(g, lease.buf.host);
+  *ids_dev = lease.buf.dev;
   return 0;
 }
 
@@ -252,13 +297,25 @@ int fkv_stream_create(int num_cus, fkv_stream_t* out) {
   for (int c = 0; c < use; ++c) mask[c / 32] |= 1u << (c % 32);
   hipStream_t st = nullptr;
   FKV_HIP(hipExtStreamCreateWithCUMask(&st, static_cast<uint32_t>(mask.size()), mask.data()));
+  {
+    std::lock_guard<std::mutex> lk(g_streams_mu);
+    g_streams.push_back(st);
+  }
   *out = st;
   return 0;
 }
 
 int fkv_stream_destroy(fkv_stream_t s) {
   last_error().clear();
-  if (s) FKV_HIP(hipStreamDestroy(static_cast<hipStream_t>(s)));
+  if (!s) return 0;
+  {
+    std::lock_guard<std::mutex> lk(g_streams_mu);
+    auto it = std::find(g_streams.begin(), g_streams.end(), static_cast<hipStream_t>(s));
+    if (it == g_streams.end())
+      return fail(kInval, "stream %p was not made by fkv_stream_create or is already destroyed", s);
+    g_streams.erase(it);
+  }
+  FKV_HIP(hipStreamDestroy(static_cast<hipStream_t>(s)));
   return 0;
 }
 
@@ -317,7 +374,8 @@ int fkv_release_staging(void) {
   for (int dev = 0; dev < kMaxDevices; ++dev) {
     for (CopyLane& ln : g_dev[dev].lane) {
       std::lock_guard<std::mutex> lk(ln.mu);
-      if (ln.staging) {
+      // a stalled lane's engine may still write its staging buffer
+      if (ln.staging && !ln.stalled) {
         DeviceGuard guard;
         int rc = guard.set(dev);
         if (rc) return rc;

@@ -17,6 +17,7 @@
 
 #include "flexkv_hip.h"
 #include "fkv_error.h"
+#include "kv_wait.h"
 
 namespace fkv_detail {
 #pragma GCC visibility push(hidden)
@@ -75,6 +76,12 @@ struct CopyLane {
   std::vector<hsa_signal_t> queued[2];   // signal of every copy queued on the half
   std::vector<hsa_signal_t> wake[2];     // the interrupt signals among them
   hipEvent_t ev_compute[2] = {nullptr, nullptr};
+  // A wait on this lane timed out: an engine may still write its staging
+  // buffer or decrement its signals, so neither is freed or reused again
+  // (the device's copy-engine transfers use the zero-copy kernel from then
+  // on).  The signals of the copies given up on are kept here, never destroyed.
+  bool stalled = false;
+  std::vector<hsa_signal_t> abandoned;
 };
 
 struct DeviceState {
@@ -197,14 +204,40 @@ struct ProfRecorder {
   }
 };
 
-// The calling thread's pinned, device-mapped buffer of at least `bytes`.
-// Calls are synchronous, so the previous call's kernels have finished
-// before the buffer is rewritten or regrown.
-int pinned_ids(size_t bytes, int64_t** host, char** dev);
+// Pinned, device-mapped id buffers (the packed (gpu_id, cpu_id) pairs the
+// kernels read) come from one process-wide pool: a call takes a buffer of at
+// least `bytes` and gives it back once its kernels have finished (synchronous
+// calls: at return; layer-wise handles: at release).  fkv_finalize frees the
+// pool.
+struct IdBuf {
+  int64_t* host = nullptr;
+  char* dev = nullptr;
+  size_t cap = 0;
+};
+int ids_acquire(size_t bytes, IdBuf* out);
+void ids_release(const IdBuf& b);
+// Frees every buffer in the pool.  A buffer on loan at that moment goes back
+// into the pool when its call ends and stays there until the next free.
+int ids_pool_free();
+// Holds a pool buffer for the scope of a synchronous call.  Declare it before
+// the call's DrainOnError, so the drain runs first and no kernel still reads
+// the buffer when it goes back to the pool.
+struct IdLease {
+  IdBuf buf;
+  IdLease() = default;
+  IdLease(const IdLease&) = delete;
+  IdLease& operator=(const IdLease&) = delete;
+  ~IdLease() {
+    if (buf.host) ids_release(buf);
+  }
+};
+// Synchronises and destroys every stream made by fkv_stream_create and not
+// destroyed yet (fkv_finalize).
+int streams_destroy_all();
 // The ids as (gpu_id, cpu_id) pairs.
 void pack_ids_into(const Geometry& g, int64_t* h);
-// Pack ids into the thread's pinned buffer as (gpu_id, cpu_id) pairs.
-int pack_ids(const Geometry& g, char** ids_dev);
+// Pack ids into a pool buffer held by `lease` as (gpu_id, cpu_id) pairs.
+int pack_ids(const Geometry& g, IdLease& lease, char** ids_dev);
 // The device a stream belongs to (the current device for the null stream).
 int stream_device(hipStream_t s, int* dev);
 
@@ -276,21 +309,33 @@ int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, cha
 // of sleeping: for the last wait of a call, where the host's wake-up from a
 // sleep that lasted the whole transfer (15-30 us measured) would add to the
 // call's time; a wait overlapped with the other half's copies sleeps.
-void sdma_wait(CopyLane& lane, int half, bool spin = false);
+// Bounded: after FLEXKV_SDMA_TIMEOUT_MS (default 20 s) it gives up, marks the
+// lane stalled and the device's engines failed, and returns
+// hipErrorLaunchTimeOut with the error message set; otherwise 0.
+int sdma_wait(DeviceState& d, CopyLane& lane, int half, bool spin = false);
+// Waits for a lane's queued copies, then destroys its pooled signals and
+// events and frees its staging buffer (a stalled lane keeps its staging and
+// signals).  The lane's mutex must be held.
+int lane_release(DeviceState& d, CopyLane& lane);
 
 // When a transfer fails after enqueueing work, wait for that work before the
 // call returns: a copy must not land in the caller's buffers, or read the
 // reused id and staging buffers, after the error has been reported.
+// The message of the error being reported is kept: the drain's own waits
+// must not replace it.
 struct DrainOnError {
   hipStream_t stream;
-  CopyLane* lane;
+  DeviceState* dev = nullptr;
+  CopyLane* lane = nullptr;
   bool armed = true;
   ~DrainOnError() {
     if (!armed) return;
+    const std::string msg = last_error();
     (void)hipStreamSynchronize(stream);
-    if (lane)
-      for (int h = 0; h < 2; ++h) sdma_wait(*lane, h);
+    if (lane && dev)
+      for (int h = 0; h < 2; ++h) (void)sdma_wait(*dev, *lane, h);
     (void)hipGetLastError();
+    last_error() = msg;
   }
 };
 

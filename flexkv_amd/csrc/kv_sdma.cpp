@@ -7,6 +7,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -41,6 +42,8 @@ struct HsaApi {
   decltype(&::hsa_agent_get_info) agent_get_info = nullptr;
   decltype(&::hsa_status_string) status_string = nullptr;
   decltype(&::hsa_signal_create) signal_create = nullptr;
+  decltype(&::hsa_signal_destroy) signal_destroy = nullptr;
+  decltype(&::hsa_system_get_info) system_get_info = nullptr;
   decltype(&::hsa_amd_signal_create) amd_signal_create = nullptr;
   decltype(&::hsa_signal_load_scacquire) signal_load_scacquire = nullptr;
   decltype(&::hsa_signal_store_screlease) signal_store_screlease = nullptr;
@@ -60,6 +63,26 @@ int sdma_engines_wanted() {
 
 std::mutex g_hsa_mu;
 bool g_hsa_loaded = false;
+// HSA timestamp ticks per millisecond (the unit of a wait's timeout hint);
+// 1 GHz until the runtime reports its frequency.
+uint64_t g_ticks_per_ms = 1000000;
+
+// FLEXKV_SDMA_TIMEOUT_MS bounds each host wait on a staging half.
+int64_t sdma_timeout_ms() {
+  const char* e = getenv("FLEXKV_SDMA_TIMEOUT_MS");
+  const int64_t v = e ? atoll(e) : kDefaultSdmaTimeoutMs;
+  return v > 0 ? v : kDefaultSdmaTimeoutMs;
+}
+
+// The signal operations wait_copies needs, on the runtime's own calls.
+struct HsaSignalOps {
+  hsa_signal_value_t wait(hsa_signal_t s, uint64_t hint, bool spin) {
+    return g_hsa.signal_wait_scacquire(s, HSA_SIGNAL_CONDITION_LT, 1, hint,
+                                       spin ? HSA_WAIT_STATE_ACTIVE : HSA_WAIT_STATE_BLOCKED);
+  }
+  hsa_signal_value_t load(hsa_signal_t s) { return g_hsa.signal_load_scacquire(s); }
+  uint64_t ticks_per_ms() const { return g_ticks_per_ms; }
+};
 
 // The HSA runtime behind HIP is the mapped copy that knows `hip_ptr`, a
 // device allocation HIP made: a process can map a second copy (a wheel's
@@ -107,6 +130,8 @@ int load_hsa(const void* hip_ptr) {
   sym(a.agent_get_info, "hsa_agent_get_info");
   sym(a.status_string, "hsa_status_string");
   sym(a.signal_create, "hsa_signal_create");
+  sym(a.signal_destroy, "hsa_signal_destroy");
+  sym(a.system_get_info, "hsa_system_get_info");
   sym(a.amd_signal_create, "hsa_amd_signal_create");
   sym(a.signal_load_scacquire, "hsa_signal_load_scacquire");
   sym(a.signal_store_screlease, "hsa_signal_store_screlease");
@@ -116,6 +141,10 @@ int load_hsa(const void* hip_ptr) {
   if (missing) return fail(kInval, "the HSA runtime lacks %d entry points", missing);
   a.async_copy_rect = reinterpret_cast<decltype(a.async_copy_rect)>(
       dlsym(lib, "hsa_amd_memory_async_copy_rect"));
+  uint64_t freq = 0;
+  if (a.system_get_info(HSA_SYSTEM_INFO_TIMESTAMP_FREQUENCY, &freq) == HSA_STATUS_SUCCESS &&
+      freq >= 1000)
+    g_ticks_per_ms = freq / 1000;
   g_hsa = a;
   g_hsa_loaded = true;
   return 0;
@@ -143,17 +172,78 @@ hsa_status_t first_cpu_agent(hsa_agent_t a, void* out) {
 
 }  // namespace
 
-void sdma_wait(CopyLane& d, int half, bool spin) {
-  const hsa_wait_state_t how = spin ? HSA_WAIT_STATE_ACTIVE : HSA_WAIT_STATE_BLOCKED;
-  for (hsa_signal_t s : d.wake[half])
-    while (g_hsa.signal_wait_scacquire(s, HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX, how) >= 1) {
-    }
+int sdma_wait(DeviceState& dev, CopyLane& d, int half, bool spin) {
+  if (d.queued[half].empty()) return 0;
   // The polled signals are created for GPU consumers, so the host only ever
   // loads their values (any agent may) and never waits on them.
-  for (hsa_signal_t s : d.queued[half])
-    while (g_hsa.signal_load_scacquire(s) >= 1) std::this_thread::yield();
+  HsaSignalOps ops;
+  const int64_t limit_ms = sdma_timeout_ms();
+  const WaitOutcome w = wait_copies(ops, d.wake[half], d.queued[half], spin,
+                                    std::chrono::steady_clock::now() +
+                                        std::chrono::milliseconds(limit_ms));
+  if (!w.done) {
+    // Give up on this half: its copies may still complete (or never), so
+    // their signals and the staging buffer are never reused or freed.
+    for (hsa_signal_t s : d.queued[half]) d.abandoned.push_back(s);
+    for (int h = 0; h < 2; ++h) {
+      auto drop = [&](std::vector<hsa_signal_t>& pool) {
+        pool.erase(std::remove_if(pool.begin(), pool.end(),
+                                  [&](hsa_signal_t s) {
+                                    for (hsa_signal_t a : d.abandoned)
+                                      if (a.handle == s.handle) return true;
+                                    return false;
+                                  }),
+                   pool.end());
+      };
+      drop(d.polled_pool[h]);
+      drop(d.irq_pool[h]);
+    }
+    d.queued[half].clear();
+    d.wake[half].clear();
+    d.stalled = true;
+    dev.sdma_failed.store(true);
+    return fail(static_cast<int>(hipErrorLaunchTimeOut),
+                "copy-engine copies of staging half %d did not finish within %lld ms (a "
+                "completion signal still reads %lld); copy-engine transfers on this device "
+                "use the zero-copy kernel from now on (FLEXKV_SDMA_TIMEOUT_MS sets the limit)",
+                half, static_cast<long long>(limit_ms), static_cast<long long>(w.value));
+  }
   d.queued[half].clear();
   d.wake[half].clear();
+  return 0;
+}
+
+int lane_release(DeviceState& dev, CopyLane& d) {
+  int rc = 0;
+  for (int h = 0; h < 2; ++h) {
+    const int r = sdma_wait(dev, d, h, false);
+    if (r && !rc) rc = r;
+  }
+  if (d.stalled) return rc;   // an engine may still use the staging buffer and signals
+  if (g_hsa_loaded) {
+    for (int h = 0; h < 2; ++h) {
+      for (hsa_signal_t s : d.polled_pool[h]) (void)g_hsa.signal_destroy(s);
+      for (hsa_signal_t s : d.irq_pool[h]) (void)g_hsa.signal_destroy(s);
+      d.polled_pool[h].clear();
+      d.irq_pool[h].clear();
+    }
+  }
+  for (int h = 0; h < 2; ++h) {
+    if (d.ev_compute[h]) {
+      const hipError_t e = hipEventDestroy(d.ev_compute[h]);
+      if (e != hipSuccess && !rc)
+        rc = fail(static_cast<int>(e), "hipEventDestroy: %s", hipGetErrorString(e));
+      d.ev_compute[h] = nullptr;
+    }
+  }
+  if (d.staging) {
+    const hipError_t e = hipFree(d.staging);
+    if (e != hipSuccess && !rc)
+      rc = fail(static_cast<int>(e), "hipFree of a staging buffer: %s", hipGetErrorString(e));
+    d.staging = nullptr;
+    d.staging_bytes = 0;
+  }
+  return rc;
 }
 
 bool layer_major_pays_off(const Geometry& g, int64_t min_run_bytes) {
@@ -269,6 +359,7 @@ int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr) {
 }
 
 int ensure_staging(CopyLane& d, size_t need_half) {
+  if (d.stalled) return fail(kInval, "the copy engines of this lane stalled earlier");
   for (int h = 0; h < 2; ++h)
     if (!d.ev_compute[h]) FKV_HIP(hipEventCreateWithFlags(&d.ev_compute[h], hipEventDisableTiming));
   size_t want = g_staging_request.load();

@@ -211,6 +211,7 @@ class Uring {
   // Pass every available completion to fn(user_data, res); returns the count.
   template <class Fn>
   unsigned reap(Fn&& fn) {
+    if (!enabled()) return 0;
     unsigned head = *cq_head_, n = 0;
     const unsigned tail = __atomic_load_n(cq_tail_, __ATOMIC_ACQUIRE);
     for (; head != tail; ++head, ++n) {
@@ -234,8 +235,14 @@ class Uring {
     if (fd_ >= 0) close(fd_);
     sqes_ = nullptr;
     sq_ptr_ = cq_ptr_ = nullptr;
+    sq_head_ = sq_tail_ = sq_flags_ = sq_array_ = nullptr;
+    cq_head_ = cq_tail_ = nullptr;
+    cqes_ = nullptr;
+    sq_mask_ = cq_mask_ = 0;
     fd_ = -1;
     depth_ = 0;
+    tail_ = 0;
+    unsubmitted_ = 0;
   }
 
   int fd_ = -1;
@@ -761,10 +768,14 @@ int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, voi
     p.dev_cpu[d].push_back(c);
   }
   ErrorSlot err;
+  // The ring is checked under its lock: a call on another thread whose ring
+  // broke shuts the ring down under the same lock, and this call then runs on
+  // threads instead of driving a ring that is gone.
+  std::unique_lock<std::mutex> ring_lock(h->uring_mu);
   if (h->uring.enabled()) {
-    std::lock_guard<std::mutex> lk(h->uring_mu);
     run_uring(h, p, err);
   } else {
+    ring_lock.unlock();
     run_threads(h, p, num_threads_per_device, err);
   }
   if (err.failed) return ssd_fail("%s", err.msg.c_str());

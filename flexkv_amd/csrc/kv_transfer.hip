@@ -458,9 +458,10 @@ int transfer_zero_copy(const Geometry& g, hipStream_t stream, int dev, int trans
                        bool h2d) {
   DeviceState& d = g_dev[dev];
   char* ids_dev = nullptr;
-  int rc = pack_ids(g, &ids_dev);
+  IdLease ids;
+  int rc = pack_ids(g, ids, &ids_dev);
   if (rc) return rc;
-  DrainOnError drain{stream, nullptr};
+  DrainOnError drain{stream};
   int cus = transfer_cus <= 0 ? std::min(kAutoZeroCopyCus, d.num_cus)
                               : std::min(transfer_cus, d.num_cus);
   const int grid_cap = cus * (h2d ? d.occ_zero_copy[1] : d.occ_zero_copy[0]);
@@ -520,7 +521,8 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   int rc = guard.set(dev);
   if (rc) return rc;
   char* ids_dev = nullptr;
-  rc = pack_ids(g, &ids_dev);
+  IdLease ids;
+  rc = pack_ids(g, ids, &ids_dev);
   if (rc) return rc;
 
   // A piece is a run of whole blocks over a layer window; the window covers
@@ -559,7 +561,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   // Host-side waits order everything below against the caller's stream, so
   // work already queued on it comes first.
   FKV_HIP(hipStreamSynchronize(stream));
-  DrainOnError drain{stream, &ln};
+  DrainOnError drain{stream, &d, &ln};
   ProfRecorder prof;
   std::vector<Run> runs;
   bool pending[2] = {false, false};
@@ -597,8 +599,8 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
     for (int pi = 0; pi < np; ++pi) {
       const int h = pi & 1;
       if (pending[h]) {
-        sdma_wait(ln, h);
         pending[h] = false;
+        if ((rc = sdma_wait(d, ln, h))) return rc;
       }
       if ((rc = launch(pi))) return rc;
       FKV_HIP(hipEventRecord(ln.ev_compute[h], stream));
@@ -610,8 +612,9 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
       if ((rc = queue_copies(pi))) return rc;
     for (int pi = 0; pi < np; ++pi) {
       const int h = pi & 1;
-      sdma_wait(ln, h, /*spin=*/pi + 1 == np);   // the last piece has nothing behind it
       pending[h] = false;
+      // the last piece has nothing behind it
+      if ((rc = sdma_wait(d, ln, h, /*spin=*/pi + 1 == np))) return rc;
       hipLaunchKernelGGL(acquire_system_kernel, dim3(d.num_cus), dim3(64), 0, stream);
       FKV_HIP(hipGetLastError());
       if ((rc = launch(pi))) return rc;
@@ -623,7 +626,10 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
     }
   }
   for (int h = 0; h < 2; ++h)
-    if (pending[h]) sdma_wait(ln, h, /*spin=*/true);
+    if (pending[h]) {
+      pending[h] = false;
+      if ((rc = sdma_wait(d, ln, h, /*spin=*/true))) return rc;
+    }
   FKV_HIP(hipStreamSynchronize(stream));
   drain.armed = false;
   if (prof.on) {
@@ -641,10 +647,11 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
 int transfer_contiguous(const Geometry& g, hipStream_t stream, int dev, bool to_gpu) {
   DeviceState& d = g_dev[dev];
   char* ids_dev = nullptr;
-  int rc = pack_ids(g, &ids_dev);
+  IdLease ids;
+  int rc = pack_ids(g, ids, &ids_dev);
   if (rc) return rc;
   const int grid_cap = d.num_cus * (to_gpu ? d.occ_staged[1] : d.occ_staged[0]);
-  DrainOnError drain{stream, nullptr};
+  DrainOnError drain{stream};
   ProfRecorder prof;
   const int per_launch = g.layers_per_launch();
   for (int l0 = 0; l0 < g.num_layers; l0 += per_launch) {
@@ -710,7 +717,7 @@ int contiguous_entry(int num_blocks, int num_layers, const int64_t* gpu_block_id
 // The reference copy-engine loop, csrc/transfer.cu:97-121: one async copy per
 // (layer, K|V, block) chunk, issued layer-major then K|V then block.
 int transfer_ce_per_chunk(const Geometry& g, hipStream_t stream, bool h2d) {
-  DrainOnError drain{stream, nullptr};
+  DrainOnError drain{stream};
   ProfRecorder prof;
   hipEvent_t ev = nullptr;
   int rc = prof.begin(stream, &ev);
@@ -740,49 +747,9 @@ int transfer_ce_per_chunk(const Geometry& g, hipStream_t stream, bool h2d) {
 
 // ---------------------------------------------------------------------------
 // Asynchronous layer-grouped transfers.  A handle owns a pinned id buffer
-// from a process-wide pool (returned at release) and one event per group.
-
-struct PoolBuf {
-  int64_t* host = nullptr;
-  char* dev = nullptr;
-  size_t cap = 0;
-};
-std::mutex g_pool_mu;
-std::vector<PoolBuf> g_pool;   // free buffers
-
-int pool_get(size_t bytes, PoolBuf* out) {
-  {
-    std::lock_guard<std::mutex> lk(g_pool_mu);
-    size_t best = g_pool.size();
-    for (size_t i = 0; i < g_pool.size(); ++i)
-      if (g_pool[i].cap >= bytes && (best == g_pool.size() || g_pool[i].cap < g_pool[best].cap))
-        best = i;
-    if (best != g_pool.size()) {
-      *out = g_pool[best];
-      g_pool.erase(g_pool.begin() + static_cast<long>(best));
-      return 0;
-    }
-  }
-  PoolBuf b;
-  b.cap = std::max<size_t>(bytes, 64 << 10);
-  void* p = nullptr;
-  FKV_HIP(hipHostMalloc(&p, b.cap, hipHostMallocPortable | hipHostMallocMapped | hipHostMallocCoherent));
-  void* dp = nullptr;
-  hipError_t e = hipHostGetDevicePointer(&dp, p, 0);
-  if (e != hipSuccess) {
-    (void)hipHostFree(p);
-    return fail(static_cast<int>(e), "hipHostGetDevicePointer failed: %s", hipGetErrorString(e));
-  }
-  b.host = static_cast<int64_t*>(p);
-  b.dev = static_cast<char*>(dp);
-  *out = b;
-  return 0;
-}
-
-void pool_put(const PoolBuf& b) {
-  std::lock_guard<std::mutex> lk(g_pool_mu);
-  g_pool.push_back(b);
-}
+// from the id pool (returned at release) and one event per group.  Live
+// handles are registered, so a stale or released handle is refused and
+// fkv_finalize can release the ones left.
 
 }  // namespace
 
@@ -790,17 +757,39 @@ struct fkv_transfer_handle_s {
   int dev = 0;
   hipStream_t stream = nullptr;
   std::vector<hipEvent_t> done;   // one per layer group, in order
-  PoolBuf ids;
+  IdBuf ids;
   ProfRecorder prof;
   bool enqueued = false;          // every group was enqueued
 };
 
 namespace {
 
+std::mutex g_handles_mu;
+std::vector<fkv_transfer_handle_s*> g_handles;   // live handles
+
+void handle_register(fkv_transfer_handle_s* h) {
+  std::lock_guard<std::mutex> lk(g_handles_mu);
+  g_handles.push_back(h);
+}
+
+// Removes h from the registry; false when it is not a live handle.
+bool handle_unregister(fkv_transfer_handle_s* h) {
+  std::lock_guard<std::mutex> lk(g_handles_mu);
+  auto it = std::find(g_handles.begin(), g_handles.end(), h);
+  if (it == g_handles.end()) return false;
+  g_handles.erase(it);
+  return true;
+}
+
+bool handle_live(fkv_transfer_handle_s* h) {
+  std::lock_guard<std::mutex> lk(g_handles_mu);
+  return std::find(g_handles.begin(), g_handles.end(), h) != g_handles.end();
+}
+
 int layerwise_enqueue(const Geometry& g, hipStream_t stream, int dev, int transfer_cus, bool h2d,
                       int granularity, fkv_transfer_handle_s* h) {
   DeviceState& d = g_dev[dev];
-  int rc = pool_get(static_cast<size_t>(g.num_blocks) * 16, &h->ids);
+  int rc = ids_acquire(static_cast<size_t>(g.num_blocks) * 16, &h->ids);
   if (rc) return rc;
   pack_ids_into(g, h->ids.host);
   const int automatic = h2d ? kAutoLayerwiseH2DCus : kAutoZeroCopyCus;
@@ -841,7 +830,7 @@ int handle_destroy(fkv_transfer_handle_s* h) {
   }
   h->prof.flush();
   for (hipEvent_t ev : h->done) (void)hipEventDestroy(ev);
-  if (h->ids.host) pool_put(h->ids);
+  if (h->ids.host) ids_release(h->ids);
   delete h;
   return rc;
 }
@@ -1025,6 +1014,7 @@ int fkv_transfer_kv_blocks_layerwise(
         return rc;
       }
     }
+    handle_register(h);
     *out = h;
     return 0;
   } catch (const std::exception& e) {
@@ -1036,13 +1026,13 @@ int fkv_transfer_kv_blocks_layerwise(
 
 int fkv_handle_num_groups(fkv_transfer_handle h) {
   last_error().clear();
-  if (!h) return fail(-1, "null handle");
+  if (!h || !handle_live(h)) return fail(-1, "null, released or unknown handle");
   return static_cast<int>(h->done.size());
 }
 
 int fkv_handle_query(fkv_transfer_handle h, int group) {
   last_error().clear();
-  if (!h || group < 0 || group >= static_cast<int>(h->done.size()))
+  if (!h || !handle_live(h) || group < 0 || group >= static_cast<int>(h->done.size()))
     return fail(-1, "bad handle or group %d", group);
   hipError_t e = hipEventQuery(h->done[group]);
   if (e == hipSuccess) return 1;
@@ -1053,7 +1043,7 @@ int fkv_handle_query(fkv_transfer_handle h, int group) {
 
 int fkv_handle_wait(fkv_transfer_handle h, int group) {
   last_error().clear();
-  if (!h || group < 0 || group >= static_cast<int>(h->done.size()))
+  if (!h || !handle_live(h) || group < 0 || group >= static_cast<int>(h->done.size()))
     return fail(kInval, "bad handle or group %d", group);
   FKV_HIP(hipEventSynchronize(h->done[group]));
   return 0;
@@ -1061,7 +1051,7 @@ int fkv_handle_wait(fkv_transfer_handle h, int group) {
 
 int fkv_handle_stream_wait(fkv_transfer_handle h, int group, fkv_stream_t other) {
   last_error().clear();
-  if (!h || group < 0 || group >= static_cast<int>(h->done.size()))
+  if (!h || !handle_live(h) || group < 0 || group >= static_cast<int>(h->done.size()))
     return fail(kInval, "bad handle or group %d", group);
   FKV_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(other), h->done[group], 0));
   return 0;
@@ -1070,7 +1060,52 @@ int fkv_handle_stream_wait(fkv_transfer_handle h, int group, fkv_stream_t other)
 int fkv_handle_release(fkv_transfer_handle h) {
   last_error().clear();
   if (!h) return 0;
+  if (!handle_unregister(h)) return fail(kInval, "handle %p is released or unknown", (void*)h);
   return handle_destroy(h);
+}
+
+int fkv_finalize(void) {
+  try {
+    last_error().clear();
+    int rc = 0;
+    auto keep = [&rc](int r) {
+      if (r && !rc) rc = r;
+    };
+    // 1. layer-wise handles the caller never released: wait for their groups
+    std::vector<fkv_transfer_handle_s*> handles;
+    {
+      std::lock_guard<std::mutex> lk(g_handles_mu);
+      handles.swap(g_handles);
+    }
+    for (fkv_transfer_handle_s* h : handles) keep(handle_destroy(h));
+    // 2. streams made by fkv_stream_create (each is synchronised first)
+    keep(streams_destroy_all());
+    // 3. copy-engine lanes: queued copies, signals, events, staging
+    for (int dev = 0; dev < kMaxDevices; ++dev) {
+      DeviceState& d = g_dev[dev];
+      for (CopyLane& ln : d.lane) {
+        std::lock_guard<std::mutex> lk(ln.mu);
+        const bool used = ln.staging || ln.ev_compute[0] || ln.ev_compute[1] ||
+                          !ln.polled_pool[0].empty() || !ln.irq_pool[0].empty() ||
+                          !ln.polled_pool[1].empty() || !ln.irq_pool[1].empty();
+        if (!used) continue;
+        DeviceGuard guard;
+        const int r = guard.set(dev);
+        if (r) {
+          keep(r);
+          continue;
+        }
+        keep(lane_release(d, ln));
+      }
+    }
+    // 4. pinned id buffers
+    keep(ids_pool_free());
+    return rc;
+  } catch (const std::exception& e) {
+    return fail(static_cast<int>(hipErrorUnknown), "exception: %s", e.what());
+  } catch (...) {
+    return fail(static_cast<int>(hipErrorUnknown), "unknown exception");
+  }
 }
 
 

@@ -1,0 +1,79 @@
+// kv_wait.h - the bounded wait for copy-engine completion signals.
+//
+// Header-only and free of HIP, so a CPU-only test can drive it with stub
+// signal operations.  Every copy the copy-engine path queues carries a
+// completion signal that starts at 1 and drops to 0 when the engine is done.
+// The wait blocks (or spins) on the few interrupt signals of each engine's
+// last copy, then checks every copy's own signal by loading it, and gives up
+// at a deadline instead of waiting forever on an engine that stalled.
+#pragma once
+
+#include <hsa/hsa.h>
+
+#include <chrono>
+#include <cstddef>
+#include <cstdint>
+#include <thread>
+#include <vector>
+
+namespace fkv_detail {
+
+// How long one host wait on a copy-engine half may take before the transfer
+// fails (FLEXKV_SDMA_TIMEOUT_MS; default 20 s).  A staging half holds at most
+// a few hundred MiB, which the link moves in milliseconds.
+constexpr int64_t kDefaultSdmaTimeoutMs = 20000;
+
+// The outcome of wait_copies: every signal reached 0, or the deadline passed
+// with `stuck` still at 1 or more.
+struct WaitOutcome {
+  bool done = true;
+  hsa_signal_t stuck{0};
+  hsa_signal_value_t value = 0;
+};
+
+// Ops provides:
+//   hsa_signal_value_t wait(hsa_signal_t s, uint64_t hint_ticks, bool spin)
+//       one bounded host wait on an interrupt signal for its value to drop
+//       below 1 (a blocking or spinning hsa_signal_wait_scacquire with a
+//       finite timeout hint); returns the value observed;
+//   hsa_signal_value_t load(hsa_signal_t s)   an acquire load;
+//   uint64_t ticks_per_ms() const              timestamp ticks per millisecond.
+// `deadline` bounds the whole call.
+template <class Ops>
+WaitOutcome wait_copies(Ops& ops, const std::vector<hsa_signal_t>& wake,
+                        const std::vector<hsa_signal_t>& queued, bool spin,
+                        std::chrono::steady_clock::time_point deadline) {
+  using clock = std::chrono::steady_clock;
+  WaitOutcome out;
+  // Waits are cut into slices of at most 1 ms of the runtime's timestamp
+  // clock; the timeout argument of an HSA wait is only a hint, so the clock
+  // decides.
+  const uint64_t slice = ops.ticks_per_ms() > 0 ? ops.ticks_per_ms() : 1;
+  for (hsa_signal_t s : wake) {
+    hsa_signal_value_t v;
+    while ((v = ops.wait(s, slice, spin)) >= 1) {
+      if (clock::now() >= deadline) {
+        out.done = false;
+        out.stuck = s;
+        out.value = v;
+        return out;
+      }
+    }
+  }
+  for (hsa_signal_t s : queued) {
+    hsa_signal_value_t v;
+    unsigned polls = 0;
+    while ((v = ops.load(s)) >= 1) {
+      if ((++polls & 63) == 0 && clock::now() >= deadline) {
+        out.done = false;
+        out.stuck = s;
+        out.value = v;
+        return out;
+      }
+      std::this_thread::yield();
+    }
+  }
+  return out;
+}
+
+}  // namespace fkv_detail

@@ -261,6 +261,19 @@ int fkv_host_unregister(void* ptr);
 int fkv_set_staging_bytes(size_t bytes);
 int fkv_release_staging(void);
 
+/* Release everything the library holds for the process: waits for and frees
+ * layer-wise handles never released, synchronises and destroys streams made
+ * by fkv_stream_create, waits for queued copy-engine copies and destroys
+ * their completion signals and events, frees the staging buffers and the
+ * pinned id buffers.  Meant for process exit (the Python loader calls it from
+ * an atexit hook), so these objects are gone before the HIP and HSA runtimes
+ * run their own exit-time finalizers; the library stays usable afterwards and
+ * re-creates what it needs.  Handles released here are invalid afterwards
+ * (the handle calls refuse them).  Must not race with transfers on other
+ * threads.  No counterpart in the reference, whose extension holds no such
+ * resources (csrc/transfer.cu keeps only a cached occupancy). */
+int fkv_finalize(void);
+
 /* Optional per-process timing of the library's kernels and DMA batches,
  * measured with HIP events on the stream each one runs on. */
 typedef struct fkv_profile {

@@ -90,6 +90,38 @@ def test_gpu_cpu_round_trip(use_mla, layout):
         te.shutdown()
 
 
+@pytest.mark.parametrize("use_mla", [False, True])
+@pytest.mark.parametrize("layout", [KVCacheLayoutType.LAYERWISE, KVCacheLayoutType.BLOCKWISE])
+def test_write_graph_host_bytes(use_mla, layout):
+    """Every byte of the host cache after a write graph through the engine,
+    against tensor indexing on the host layout's own shape."""
+    mc, gt, gpu, te = _setup(use_mla, layout)
+    try:
+        host = te._test_host
+        host.view(torch.int16).fill_(0x5A5A)
+        before = host.clone()
+        g = torch.Generator().manual_seed(12)
+        gids = torch.randperm(128, generator=g)[:33]
+        cids = torch.randperm(CACHE["num_cpu_blocks"], generator=g)[:33]
+        wg, _ = create_write_graph_cpu_storage(gids, cids, torch.tensor([], dtype=torch.int64),
+                                               gpu_device_id=0, layer_num=mc.num_layers)
+        te.submit_transfer_graph(wg)
+        _wait(te, wg.graph_id)
+        cl = KVCacheLayout(layout, mc.num_layers, CACHE["num_cpu_blocks"],
+                           CACHE["tokens_per_block"], mc.num_kv_heads, mc.head_size,
+                           is_mla=use_mla)
+        exp = before.view(tuple(cl.kv_shape)).clone()
+        for l, t in enumerate(gt):
+            for k in range(t.shape[0]):
+                if layout == KVCacheLayoutType.BLOCKWISE:
+                    exp[cids, l, k] = t[k, gids]
+                else:
+                    exp[l, k, cids] = t[k, gids]
+        assert torch.equal(host.view(torch.int16), exp.reshape(-1).view(torch.int16))
+    finally:
+        te.shutdown()
+
+
 @pytest.mark.parametrize("eager", [False, True])
 def test_layer_wise_read_graph(eager):
     """Read back one layer per op (convert_read_graph_to_layer_wise_graph);

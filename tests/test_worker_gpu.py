@@ -134,3 +134,55 @@ def test_spawned_worker_with_shared_gpu_tensors():
             assert torch.equal(gpu[l].cpu(), gt[l])
     finally:
         handle.shutdown()
+
+
+def _host_expected(before, cl, gt, gids, cids):
+    """The host cache after a D2H of GPU blocks `gids` into host blocks
+    `cids`, by tensor indexing on the layout's own shape ([N, L, kv, ...]
+    block-wise, [L, kv, N, ...] layer-wise), not by byte strides."""
+    exp = before.clone().view(tuple(cl.kv_shape))
+    for l, t in enumerate(gt):
+        for k in range(t.shape[0]):
+            if cl.type == KVCacheLayoutType.BLOCKWISE:
+                exp[cids, l, k] = t[k, gids]
+            else:
+                exp[l, k, cids] = t[k, gids]
+    return exp.reshape(-1)
+
+
+@pytest.mark.parametrize("mla", [False, True])
+@pytest.mark.parametrize("layout", [KVCacheLayoutType.LAYERWISE, KVCacheLayoutType.BLOCKWISE])
+@pytest.mark.parametrize("ce", [False, True])
+def test_worker_d2h_host_bytes(mla, layout, ce):
+    """Every byte of the host cache after a D2H op through the worker,
+    untouched blocks included (a layer-wise stride mistake that a round trip
+    would undo shows up here)."""
+    gl, gt = _ground_truth(mla, seed=11)
+    gpu = [t.cuda() for t in gt]
+    cl = KVCacheLayout(layout, L, NH, T, H, D, is_mla=mla)
+    cpu = CPUAllocator.allocate(cl, torch.float16).get_tensor()
+    cpu.view(torch.int16).fill_(0x5A5A)
+    before = cpu.clone()
+    w = GPUCPUTransferWorker(0, None, None, gpu, cpu, gl, cl, torch.float16, 0,
+                             use_ce_transfer_h2d=ce, use_ce_transfer_d2h=ce)
+    g = torch.Generator().manual_seed(5)
+    gids = torch.randperm(NG, generator=g)[:45]
+    cids = torch.randperm(NH, generator=g)[:45]
+    w.launch_transfer(WorkerTransferOp(_op(TransferType.D2H, gids, cids)))
+    assert w.failed_ops == []
+    exp = _host_expected(before, cl, gt, gids, cids)
+    assert torch.equal(cpu.view(torch.int16), exp.view(torch.int16))
+    # one layer group (layers 1..2) of an H2D op lands in those layers only
+    for t in gpu:
+        t.zero_()
+    torch.cuda.synchronize()
+    w.launch_transfer(WorkerTransferOp(_op(TransferType.H2D, cids, gids, 1, 2)))
+    for l in range(L):
+        got = gpu[l].cpu()
+        if l in (1, 2):
+            assert torch.equal(got[:, gids], gt[l][:, gids]), f"layer {l}"
+            rest = torch.ones(NG, dtype=torch.bool)
+            rest[gids] = False
+            assert not got[:, rest].any(), f"layer {l}: blocks outside the op were written"
+        else:
+            assert not got.any(), f"layer {l} outside the op's layer window was written"
