@@ -40,8 +40,14 @@ if ROOT not in sys.path:
 
 METRIC = "KV-block transfer GB/s D2H & H2D at Llama-3-8B shape; % of host-link/HBM peak"
 HBM_PEAK_GBS = 8000.0
+# PCIe Gen5 x16, per direction: 32 GT/s x 16 lanes x 128/130 line coding
+PCIE_GEN5_X16_GBS = 63.0
 
 WORKLOADS = {
+    "plumbing": dict(layers=4, kv=2, ng=256, nh=512, tokens=16, heads=8, dim=128, n=64,
+                     dtype="float16",
+                     desc="CPU-plumbing shape: 4 layers, K/V [256,16,8,128] fp16 <-> host "
+                          "[512,4,2,16,8,128]; 64 random distinct ids"),
     "llama3-8b": dict(layers=32, kv=2, ng=4096, nh=16384, tokens=16, heads=8, dim=128, n=1024,
                       desc="Llama-3-8B KV: 32 layers, K/V [4096,16,8,128] bf16 <-> pinned "
                            "block-wise host [16384,32,2,16,8,128]; 1024 random distinct ids"),
@@ -70,7 +76,7 @@ class Workload:
         self.dev = torch.device("cuda:0")
         L, kv = w["layers"], w["kv"]
         mla = kv == 1
-        self.dtype = torch.bfloat16
+        self.dtype = getattr(torch, w.get("dtype", "bfloat16"))
         gl = KVCacheLayout(KVCacheLayoutType.LAYERWISE, L, w["ng"], w["tokens"], w["heads"],
                            w["dim"], is_mla=mla)
         cl = KVCacheLayout(KVCacheLayoutType[host_layout], L, w["nh"], w["tokens"], w["heads"],
@@ -242,11 +248,17 @@ def layerwise_h2d(wl: Workload, steps: int):
 
     * reference schedule: one synchronous call per layer (the layer-wise read
       graph's ops, each run by the worker with its own stream sync);
-    * async: fkv_transfer_kv_blocks_layerwise, host waits per group;
-    * overlap: a compute stream waits on each group's event on the device, then
-      runs a per-layer GEMM; compared with the same GEMMs after a synchronous
-      transfer.
+    * async: fkv_transfer_kv_blocks_layerwise, host waits per group, on the
+      zero-copy kernel ("kernel") and on the copy-engine pipeline ("ce");
+    * overlap: a compute stream waits on each group's event, then runs a
+      per-layer GEMM; compared with the transfer alone plus one layer's
+      compute (the bound) and with the same GEMMs after a synchronous
+      transfer;
+    * GEMMs beside: 160 GEMMs with no waits, alone and beside one async
+      layer-wise transfer on each path.
     """
+    import threading
+
     from flexkv_amd import c_ext
     L = wl.w["layers"]
     args = (wl.gkv, wl.gblk, wl.cids_p, wl.host, wl.ckv, wl.clay, wl.cblk, wl.chunk)
@@ -260,27 +272,19 @@ def layerwise_h2d(wl: Workload, steps: int):
 
     ref_s, _, _ = time_steps(per_layer_sync, steps, 1)
     xfer = c_ext.transfer_stream()   # own hardware queue, every CU
-    first, total = [], []
-    for _ in range(steps + 1):
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        with torch.cuda.stream(xfer):
-            h = c_ext.transfer_kv_blocks_layerwise(wl.gids_p, wl.ptrs, wl.gkv, wl.gblk, *args[2:],
-                                                   0, 1, -1, True, wl.mla)
-        h.wait(0)
-        t1 = time.perf_counter()
-        h.wait()
-        t2 = time.perf_counter()
-        h.release()
-        first.append(t1 - t0)
-        total.append(t2 - t0)
-    first, total = first[1:], total[1:]
     # compute proxy: per layer, bf16 GEMMs of [8192 x 4096] x [4096 x 4096]
     a = torch.randn(8192, 4096, device=wl.dev, dtype=torch.bfloat16)
     b = torch.randn(4096, 4096, device=wl.dev, dtype=torch.bfloat16)
     c = torch.empty(8192, 4096, device=wl.dev, dtype=torch.bfloat16)
     reps = 4
     comp = torch.cuda.Stream()
+    gb = wl.bytes_per_op / 1e9
+
+    def start(ce):
+        with torch.cuda.stream(xfer):
+            return c_ext.transfer_kv_blocks_layerwise(wl.gids_p, wl.ptrs, wl.gkv, wl.gblk,
+                                                      *args[2:], 0, 1, -1, True, wl.mla,
+                                                      use_ce_transfer=ce)
 
     def compute_layers(hnd=None):
         with torch.cuda.stream(comp):
@@ -290,40 +294,76 @@ def layerwise_h2d(wl: Workload, steps: int):
                 for _ in range(reps):
                     torch.mm(a, b, out=c)
 
-    def serial():
-        wl.transfer(True, False)
-        compute_layers()
-        comp.synchronize()
-
-    def overlapped():
-        with torch.cuda.stream(xfer):
-            hnd = c_ext.transfer_kv_blocks_layerwise(wl.gids_p, wl.ptrs, wl.gkv, wl.gblk,
-                                                     *args[2:], 0, 1, -1, True, wl.mla)
-        compute_layers(hnd)
-        comp.synchronize()
-        hnd.release()
-
     def compute_only():
         compute_layers()
         comp.synchronize()
 
+    def gemms_ms():
+        with torch.cuda.stream(comp):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(160):
+                torch.mm(a, b, out=c)
+            e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1)
+
     comp_s, _, _ = time_steps(compute_only, steps, 1)
-    ser_s, _, _ = time_steps(serial, steps, 1)
-    ovl_s, _, _ = time_steps(overlapped, steps, 1)
+    gemms_ms()
+    gemm_alone = statistics.median(gemms_ms() for _ in range(3))
+    out = {"granularity_layers": 1,
+           "reference_schedule_ms": round(ref_s * 1e3, 2),
+           "reference_schedule_gbps": round(gb / ref_s, 2),
+           "compute_only_ms": round(comp_s * 1e3, 2),
+           "compute_proxy": f"{reps} bf16 GEMMs [8192x4096]x[4096x4096] per layer",
+           "gemm_alone_ms": round(gemm_alone, 2)}
+    for name, ce in (("kernel", False), ("ce", True)):
+        first, total = [], []
+        for _ in range(steps + 1):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            h = start(ce)
+            h.wait(0)
+            t1 = time.perf_counter()
+            h.wait()
+            t2 = time.perf_counter()
+            h.release()
+            first.append(t1 - t0)
+            total.append(t2 - t0)
+        first, total = first[1:], total[1:]
+
+        def serial():
+            wl.transfer(True, ce)
+            compute_layers()
+            comp.synchronize()
+
+        def overlapped():
+            hnd = start(ce)
+            compute_layers(hnd)
+            comp.synchronize()
+            hnd.release()
+
+        ser_s, _, _ = time_steps(serial, steps, 1)
+        ovl_s, _, _ = time_steps(overlapped, steps, 1)
+        beside = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            hnd = start(ce)
+            beside.append(gemms_ms())
+            hnd.release()
+        xfer_ms = statistics.median(total) * 1e3
+        bound = xfer_ms + comp_s * 1e3 / L
+        out[name] = {"async_total_ms": round(xfer_ms, 2),
+                     "async_gbps": round(gb / (xfer_ms * 1e-3), 2),
+                     "async_first_group_ms": round(statistics.median(first) * 1e3, 3),
+                     "transfer_then_compute_ms": round(ser_s * 1e3, 2),
+                     "layerwise_overlapped_ms": round(ovl_s * 1e3, 2),
+                     "bound_transfer_plus_one_layer_ms": round(bound, 2),
+                     "overlapped_over_bound": round(ovl_s * 1e3 / bound, 4),
+                     "gemm_beside_ms": round(statistics.median(beside), 2),
+                     "gemm_slowdown": round(statistics.median(beside) / gemm_alone, 4)}
     c_ext.release_transfer_stream(xfer)
-    gb = wl.bytes_per_op / 1e9
-    return {
-        "granularity_layers": 1,
-        "reference_schedule_ms": round(ref_s * 1e3, 2),
-        "reference_schedule_gbps": round(gb / ref_s, 2),
-        "async_total_ms": round(statistics.median(total) * 1e3, 2),
-        "async_gbps": round(gb / statistics.median(total), 2),
-        "async_first_group_ms": round(statistics.median(first) * 1e3, 3),
-        "overlap": {"compute_only_ms": round(comp_s * 1e3, 2),
-                    "transfer_then_compute_ms": round(ser_s * 1e3, 2),
-                    "layerwise_overlapped_ms": round(ovl_s * 1e3, 2),
-                    "compute_proxy": f"{reps} bf16 GEMMs [8192x4096]x[4096x4096] per layer"},
-    }
+    return out
 
 
 def engine_layerwise(wl: Workload, steps: int):
@@ -562,7 +602,9 @@ def overlap_with_compute(wl: Workload, steps: int = 3, gemms: int = 160):
 def request_batch(wl: Workload, steps: int, num_requests: int = 32, max_blocks: int = 128):
     """Requests of U{1..max_blocks} blocks with distinct random ids (seeded),
     moved one synchronous call per request and as one batched call, both
-    directions, zero-copy path; the batched D2H result is checked bit-exact."""
+    directions, on the copy-engine and the zero-copy path; each path's
+    batched D2H result is checked bit-exact, and its H2D into zeroed blocks
+    restores them."""
     from flexkv_amd import c_ext
     L, kv = wl.w["layers"], wl.w["kv"]
     g = torch.Generator().manual_seed(1006)
@@ -575,23 +617,162 @@ def request_batch(wl: Workload, steps: int, num_requests: int = 32, max_blocks: 
             for i in range(num_requests)]
     nbytes = total * L * kv * wl.chunk
 
-    def call(gi, ci, h2d):
+    def call(gi, ci, h2d, ce):
         c_ext.transfer_kv_blocks(gi, wl.ptrs, wl.gkv, wl.gblk, ci, wl.host, wl.ckv, wl.clay,
-                                 wl.cblk, wl.chunk, 0, -1, h2d, False, wl.mla)
+                                 wl.cblk, wl.chunk, 0, -1, h2d, ce, wl.mla)
 
     out = {"requests": num_requests, "blocks": total, "bytes": nbytes}
-    for h2d in (False, True):
-        name = "h2d" if h2d else "d2h"
-        per, _, _ = time_steps(lambda: [call(gi, ci, h2d) for gi, ci in reqs], steps, 1)
-        bat, _, _ = time_steps(lambda: call(gids, cids, h2d), steps, 1)
-        out[f"{name}_per_request_gbps"] = round(nbytes / per / 1e9, 2)
-        out[f"{name}_batched_gbps"] = round(nbytes / bat / 1e9, 2)
-    call(gids, cids, False)
     saved = wl.gids, wl.cids
     wl.gids, wl.cids = gids, cids
-    out["bit_exact"] = wl.check()
-    wl.gids, wl.cids = saved
+    try:
+        for path, ce in (("ce", True), ("kernel", False)):
+            res = {}
+            for h2d in (False, True):
+                name = "h2d" if h2d else "d2h"
+                per, _, _ = time_steps(lambda: [call(gi, ci, h2d, ce) for gi, ci in reqs],
+                                       steps, 1)
+                bat, _, _ = time_steps(lambda: call(gids, cids, h2d, ce), steps, 1)
+                res[f"{name}_per_request_gbps"] = round(nbytes / per / 1e9, 2)
+                res[f"{name}_batched_gbps"] = round(nbytes / bat / 1e9, 2)
+            res["bit_exact"] = round_trip_bit_exact(wl, ce)
+            out[path] = res
+    finally:
+        wl.gids, wl.cids = saved
     return out
+
+
+def round_trip_bit_exact(wl: Workload, ce) -> bool:
+    """D2H of the workload's blocks, the host rows checked against the GPU
+    blocks; then the GPU blocks zeroed in place, H2D, and the blocks compared
+    with a saved copy.  Both must hold bit for bit."""
+    g = wl.gids.to(wl.dev)
+    saved = [t.index_select(1, g) for t in wl.layers]
+    gi = wl.gids.pin_memory()
+    ci = wl.cids.pin_memory()
+    from flexkv_amd import c_ext
+
+    def move(h2d):
+        c_ext.transfer_kv_blocks(gi, wl.ptrs, wl.gkv, wl.gblk, ci, wl.host, wl.ckv, wl.clay,
+                                 wl.cblk, wl.chunk, 0, -1, h2d, ce, wl.mla)
+    move(False)
+    ok = wl.check()
+    for t in wl.layers:
+        t.index_fill_(1, g, 0)
+    torch.cuda.synchronize()
+    ok &= all(not t.index_select(1, g).any() for t in wl.layers)   # really cleared
+    move(True)
+    ok &= all(torch.equal(t.index_select(1, g), s) for t, s in zip(wl.layers, saved))
+    del saved
+    return bool(ok)
+
+
+def path_rates(wl: Workload, steps: int, peaks: dict, paths=(("ce", True), ("kernel", False))):
+    """D2H and H2D GB/s of the workload's step on each path, as fractions of
+    the measured link and of the nominal PCIe Gen5 x16 rate; for the
+    copy-engine path also the average rate of the gather and scatter pieces
+    it launched (the library's event timing, HBM bytes = 2 x moved)."""
+    from flexkv_amd import _lib
+    gb = wl.bytes_per_op / 1e9
+    out = {}
+    for name, ce in paths:
+        res = {}
+        for h2d in (False, True):
+            d = "h2d" if h2d else "d2h"
+            _lib.profile_enable(True)
+            s, _, _ = time_steps(lambda: wl.transfer(h2d, ce), steps, 1)
+            prof = _lib.profile_read()
+            _lib.profile_enable(False)
+            rate = gb / s
+            res[f"{d}_gbps"] = round(rate, 3)
+            res[f"{d}_frac_link"] = round(rate / peaks[d], 4)
+            res[f"{d}_frac_pcie_gen5_x16"] = round(rate / PCIE_GEN5_X16_GBS, 4)
+            if ce and prof["dma_batches"] and prof["kernel_ms"] > 0:
+                piece = 2 * prof["kernel_bytes"] / (prof["kernel_ms"] * 1e-3) / 1e9
+                key = "scatter" if h2d else "gather"
+                res[f"{key}_piece_gbps_hbm"] = round(piece, 1)
+                res[f"{key}_piece_frac_hbm"] = round(piece / HBM_PEAK_GBS, 4)
+                res[f"{key}_pieces_per_step"] = prof["kernel_launches"] // (steps + 1)
+            elif ce:
+                res[f"{d}_moved_by"] = "zero-copy kernel (size or layout policy)"
+        out[name] = res
+    return out
+
+
+def standalone_gather(wl: Workload, steps: int):
+    """The device gather and scatter of the whole step in one launch each,
+    into and out of one packed HBM buffer; rates from the library's events."""
+    from flexkv_amd import _lib
+    buf = torch.empty(wl.bytes_per_op, dtype=torch.uint8, device=wl.dev)
+    out = {}
+    for name, sc in (("gather", False), ("scatter", True)):
+        _lib.profile_enable(True)
+        time_steps(lambda: wl.gather(buf, scatter=sc), steps, 1)
+        prof = _lib.profile_read()
+        _lib.profile_enable(False)
+        rate = 2 * prof["kernel_bytes"] / (prof["kernel_ms"] * 1e-3) / 1e9
+        out[f"{name}_gbps_hbm"] = round(rate, 1)
+        out[f"{name}_frac_hbm"] = round(rate / HBM_PEAK_GBS, 4)
+    del buf
+    torch.cuda.empty_cache()
+    return out
+
+
+def set_ids(wl: Workload, gids: torch.Tensor, cids: torch.Tensor) -> None:
+    wl.gids, wl.cids = gids, cids
+    wl.gids_p, wl.cids_p = gids.pin_memory(), cids.pin_memory()
+
+
+def fragmentation_sweep(wl: Workload, steps: int, peaks: dict):
+    """Config 2: the Llama-3-8B tensors with 1024 ids in contiguous runs of
+    1, 8, 64 and 1024 (random non-overlapping run starts on both sides,
+    seeded), both directions on both paths, each run length's D2H -> zeroed
+    GPU blocks -> H2D round trip checked bit-exact."""
+    saved = wl.gids, wl.cids
+    w = wl.w
+    out = {}
+    try:
+        for run in (1, 8, 64, 1024):
+            gen = torch.Generator().manual_seed(wl.seed + 100 + run)
+            set_ids(wl, _run_ids(gen, w["n"], w["ng"], run), _run_ids(gen, w["n"], w["nh"], run))
+            res = path_rates(wl, steps, peaks)
+            res["bit_exact"] = all(round_trip_bit_exact(wl, ce) for ce in (True, False))
+            out[f"run_{run}"] = res
+            log(f"cfg2 run {run}: {res}")
+    finally:
+        set_ids(wl, *saved)
+    return out
+
+
+def other_workload(name: str, args, peaks: dict, host_layout: str = "BLOCKWISE",
+                   rect_copies: bool = False):
+    """Configs 3 and 4, and config 1 on a layer-wise host cache: a workload of
+    its own (allocated here, freed on return) through both paths, the device
+    gather/scatter in one launch, bit-exact round trips; MLA adds the
+    per-request / batched request mix."""
+    import gc
+    wl = Workload(name, args.seed, host_layout=host_layout)
+    try:
+        out = {"workload": WORKLOADS[name]["desc"] +
+               ("" if host_layout == "BLOCKWISE" else f"; {host_layout.lower()} host cache"),
+               "bytes_per_step": wl.bytes_per_op}
+        steps = max(3, args.steps // 2)
+        out.update(path_rates(wl, steps, peaks))
+        if rect_copies:
+            os.environ["FLEXKV_CE_RECT_COPIES"] = "1"
+            try:
+                out["ce_rect_copies"] = path_rates(wl, steps, peaks, (("ce_rect", True),))["ce_rect"]
+            finally:
+                os.environ.pop("FLEXKV_CE_RECT_COPIES", None)
+        out["device_gather"] = standalone_gather(wl, steps)
+        out["bit_exact"] = all(round_trip_bit_exact(wl, ce) for ce in (True, False))
+        if wl.mla:
+            out["request_batch"] = request_batch(wl, steps)
+            out["bit_exact"] &= all(out["request_batch"][p]["bit_exact"] for p in ("ce", "kernel"))
+        return out
+    finally:
+        del wl
+        gc.collect()
+        torch.cuda.empty_cache()
 
 
 def disk_ceilings(d: str, nbytes: int):
@@ -797,18 +978,37 @@ def cpu_baseline(wl: Workload, budget_s: float):
     return threads, out
 
 
-def measured_traffic(workload: str, run: int, alg_bytes: int):
+def source_sha16(path: str) -> str:
+    import hashlib
+    with open(path, "rb") as fh:
+        return hashlib.sha256(fh.read()).hexdigest()[:16]
+
+
+KERNEL_SOURCE = os.path.join(ROOT, "flexkv_amd", "csrc", "kv_transfer.hip")
+
+
+def measured_traffic(workload: str, run: int, alg_bytes: int) -> dict:
     """HBM bytes per gather launch from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE passes (calibrated against a plain 1 GiB copy), when they were
-    taken on this workload; else None."""
+    taken on this workload, this launch size and this kernel source (the
+    profile records the sha of kv_transfer.hip it was taken with); else
+    null, with the reason."""
     path = os.path.join(ROOT, "profiles", f"kv_gather_{workload}_counters.json")
+    rel = os.path.relpath(path, ROOT)
     if run or not os.path.exists(path):
-        return None
+        return {"bytes": None, "source": f"no counter profile for this workload ({rel})"}
     with open(path) as fh:
-        g = json.load(fh)["gather"]
+        prof = json.load(fh)
+    g = prof["gather"]
     if g["algorithmic_bytes_per_launch"] != alg_bytes:
-        return None
-    return g["traffic_bytes_per_launch"]
+        return {"bytes": None, "source": f"{rel} was taken at another launch size"}
+    want = source_sha16(KERNEL_SOURCE)
+    if prof.get("kv_transfer_sha16") != want:
+        return {"bytes": None, "source": f"{rel} was taken with another kv_transfer.hip "
+                                         f"({prof.get('kv_transfer_sha16')} != {want})"}
+    return {"bytes": g["traffic_bytes_per_launch"],
+            "source": f"{rel} (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes of "
+                      f"bench.py --counters, kv_transfer.hip sha {want})"}
 
 
 def counters_pass(args) -> int:
@@ -836,6 +1036,47 @@ def counters_pass(args) -> int:
                       "scatter_launches": 3, "d2h_launches": 3, "h2d_launches": 3,
                       "moved_bytes_per_launch": wl.bytes_per_op}), flush=True)
     return 0
+
+
+def configs_on_step(args, wl: Workload, peaks: dict, result: dict) -> dict:
+    """Configs 1 and 2 on the step's own tensors: both paths of the Llama-3-8B
+    step and its fragmentation sweep."""
+    cfg = {}
+    steps = max(3, args.steps // 2)
+    c1 = {"workload": WORKLOADS["llama3-8b"]["desc"], "bytes_per_step": wl.bytes_per_op}
+    c1.update(path_rates(wl, steps, peaks))
+    c1["device_gather"] = {"gather_gbps_hbm": result["roofline"]["achieved"],
+                           "gather_frac_hbm": result["roofline"]["frac"],
+                           "scatter_gbps_hbm": result["roofline"]["scatter"]["achieved"],
+                           "scatter_frac_hbm": result["roofline"]["scatter"]["frac"]}
+    c1["bit_exact"] = all(round_trip_bit_exact(wl, ce) for ce in (True, False))
+    cfg["cfg1_llama3-8b"] = c1
+    log(f"cfg1: {c1}")
+    cfg["cfg2_llama3-8b_fragmentation"] = fragmentation_sweep(wl, steps, peaks)
+    return cfg
+
+
+def other_configs(args, peaks: dict, cfg: dict) -> dict:
+    """The configurations with tensors of their own, each allocated and freed
+    in turn: the CPU plumbing shape, Llama-3-8B on a layer-wise host cache,
+    the Llama-3-70B TP-8 shard and the DeepSeek-V3 MLA latent cache with its
+    request mix.  Every entry of the benchmark set (with configs_on_step's)
+    gives GB/s on both paths with fractions of the measured link and of
+    nominal PCIe Gen5 x16, the copy-engine path's gather/scatter piece rates,
+    the device gather/scatter in one launch, and a bit-exact round trip."""
+    t0 = time.perf_counter()
+    for key, name, layout, rect in (("cfg0_plumbing", "plumbing", "BLOCKWISE", False),
+                                    ("cfg1_llama3-8b_layerwise_host", "llama3-8b", "LAYERWISE",
+                                     True),
+                                    ("cfg3_llama3-70b-tp8", "llama3-70b-tp8", "BLOCKWISE", False),
+                                    ("cfg4_mla-dsv3", "mla-dsv3", "BLOCKWISE", False)):
+        cfg[key] = other_workload(name, args, peaks, layout, rect)
+        log(f"{key}: {cfg[key]}")
+    cfg["bit_exact"] = all(v.get("bit_exact", True) for v in cfg.values()
+                           if isinstance(v, dict)) and all(
+        r["bit_exact"] for r in cfg["cfg2_llama3-8b_fragmentation"].values())
+    cfg["seconds"] = round(time.perf_counter() - t0, 1)
+    return cfg
 
 
 def main() -> int:
@@ -927,6 +1168,20 @@ def main() -> int:
 
     g_ms, g_bytes, g_rate = kernel_rate(prof_g)
     s_ms, s_bytes, s_rate = kernel_rate(prof_s)
+    traffic = measured_traffic(args.workload, args.run, int(g_bytes))
+    # the gather and scatter pieces the copy-engine path itself launched in
+    # the timed D2H / H2D steps (library event timing on the launch stream)
+    in_path = {}
+    if default_ce:
+        for key, prof in (("gather", prof_d2h), ("scatter", prof_h2d)):
+            if prof["dma_batches"] and prof["kernel_launches"]:
+                p_ms, p_bytes, p_rate = kernel_rate(prof)
+                in_path[key] = {"achieved": round(p_rate, 1),
+                                "frac": round(p_rate / HBM_PEAK_GBS, 4),
+                                "avg_piece_ms": round(p_ms, 4),
+                                "algorithmic_bytes_per_piece": int(p_bytes),
+                                "pieces_per_step": round(prof["kernel_launches"] /
+                                                         (args.steps + args.warmup), 2)}
     z_ms = prof_d2h["kernel_ms"] / max(1, prof_d2h["kernel_launches"])
     log(f"device gather {g_rate:.0f} GB/s, scatter {s_rate:.0f} GB/s of HBM; packed bytes "
         f"bit-exact: {gather_ok}")
@@ -967,13 +1222,14 @@ def main() -> int:
                                "step's blocks into one packed HBM buffer",
                      "achieved": round(g_rate, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(g_rate / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(args.workload, args.run, int(g_bytes)),
+                     "traffic": traffic["bytes"],
+                     "traffic_source": traffic["source"],
                      "avg_launch_ms": round(g_ms, 4), "launches": prof_g["kernel_launches"],
                      "algorithmic_bytes_per_launch": int(g_bytes),
                      "bytes_rule": "2 x moved bytes (scattered 32 KiB reads + packed writes)",
-                     "traffic_source": "profiles/kv_gather_<workload>_counters.json",
                      "scatter": {"achieved": round(s_rate, 1), "frac": round(s_rate / HBM_PEAK_GBS, 4),
                                  "avg_launch_ms": round(s_ms, 4)},
+                     **({"in_path": in_path} if in_path else {}),
                      **({"device_ceilings": {
                          "read_gbps": ceilings["read_gbps"], "write_gbps": ceilings["write_gbps"],
                          "copy_gbps": ceilings["copy_gbps"],
@@ -995,6 +1251,9 @@ def main() -> int:
             "h2d_peak_gbps_measured": round(peaks["h2d"], 2),
             "d2h_frac": round((gb / d2h_s) / peaks["d2h"], 4),
             "h2d_frac": round((gb / h2d_s) / peaks["h2d"], 4),
+            "pcie_gen5_x16_gbps_nominal": PCIE_GEN5_X16_GBS,
+            "d2h_frac_pcie_gen5_x16": round((gb / d2h_s) / PCIE_GEN5_X16_GBS, 4),
+            "h2d_frac_pcie_gen5_x16": round((gb / h2d_s) / PCIE_GEN5_X16_GBS, 4),
             **({} if default_ce else
                {"d2h_kernel_frac": round((gb / (z_ms * 1e-3)) / peaks["d2h"], 4)}),
             "d2d_copy_gbps_measured": round(peaks["d2d_copy_read_plus_write"], 1),
@@ -1047,6 +1306,15 @@ def main() -> int:
             "single_thread_gbps": round(v1, 3),
         }
         log(f"CPU baseline: {v:.2f} GB/s on {threads} threads, {v1:.2f} GB/s on 1")
+        if args.workload == "llama3-8b" and not args.run and args.host_layout == "BLOCKWISE":
+            import gc
+            cfg = configs_on_step(args, wl, peaks, result)
+            del wl
+            gc.collect()
+            torch.cuda.empty_cache()
+            result["configs"] = other_configs(args, peaks, cfg)
+            parity = parity and result["configs"]["bit_exact"]
+            result["bit_exact"] = result["bit_exact"] and result["configs"]["bit_exact"]
 
     print(json.dumps(result), flush=True)
     return 0 if (parity and gather_ok) else 1

@@ -113,7 +113,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     f = lib.fkv_transfer_kv_blocks_layerwise
     f.restype = c_int
     f.argtypes = [c_int, c_int, c_int, c_int, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64,
-                  c_i64, c_i64, c_i64, c_vp, c_int, c_int, c_int, ctypes.POINTER(c_vp)]
+                  c_i64, c_i64, c_i64, c_vp, c_int, c_int, c_int, c_int, ctypes.POINTER(c_vp)]
     for name, extra in (("fkv_handle_num_groups", []), ("fkv_handle_query", [c_int]),
                         ("fkv_handle_wait", [c_int]), ("fkv_handle_stream_wait", [c_int, c_vp]),
                         ("fkv_handle_release", [])):

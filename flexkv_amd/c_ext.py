@@ -21,31 +21,42 @@ __all__ = ["transfer_kv_blocks", "transfer_kv_blocks_kv_ptrs", "gather_kv_blocks
 
 
 _device_visible = None
+_raw_stream = None      # torch's current-raw-stream query, once a device is seen
+_current_device = None
 
 
 def _stream_handle(fn_name: str) -> int:
     """Raw handle of the current torch stream of the current device.  Raises
     when no HIP device is visible (checked once per process)."""
-    global _device_visible
+    global _device_visible, _raw_stream, _current_device
+    if _raw_stream is not None:
+        return _raw_stream(_current_device())
     if _device_visible is None:
         _device_visible = torch.cuda.is_available()
     if not _device_visible:
         raise RuntimeError(f"{fn_name} needs a HIP device; none is visible")
     raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
-    if raw is not None:      # avoids building a Stream object per call
-        return raw(torch._C._cuda_getDevice())
-    return torch.cuda.current_stream().cuda_stream
+    if raw is None:
+        return torch.cuda.current_stream().cuda_stream
+    _current_device = torch._C._cuda_getDevice
+    _raw_stream = raw       # avoids building a Stream object per call
+    return raw(_current_device())
+
+
+_I64 = torch.int64
 
 
 def _require_int64_host(t: torch.Tensor, name: str) -> None:
+    # one combined test on the common path; the detailed checks only on failure
+    if isinstance(t, torch.Tensor) and t.dtype is _I64 and not t.is_cuda and t.is_contiguous():
+        return
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
     if t.dtype != torch.int64:
         raise TypeError(f"{name} must be int64, got {t.dtype}")
     if t.device.type != "cpu":
         raise RuntimeError(f"{name} must be a host tensor (pinned), got device {t.device}")
-    if not t.is_contiguous():
-        raise RuntimeError(f"{name} must be contiguous")
+    raise RuntimeError(f"{name} must be contiguous")
 
 
 def transfer_kv_blocks(gpu_block_id_tensor: torch.Tensor,
@@ -255,10 +266,16 @@ def transfer_kv_blocks_layerwise(gpu_block_id_tensor: torch.Tensor,
                                  cpu_block_stride_in_bytes: int, chunk_size_in_bytes: int,
                                  start_layer_id: int, layer_granularity: int,
                                  transfer_sms: int = -1, is_host_to_device: bool = True,
-                                 is_mla: bool = False) -> LayerwiseTransfer:
-    """Enqueue the transfer of every layer group on the current stream and
-    return at once (extension; the reference issues one synchronous call per
-    layer group).  Arguments as transfer_kv_blocks plus layer_granularity."""
+                                 is_mla: bool = False,
+                                 use_ce_transfer: bool = False) -> LayerwiseTransfer:
+    """Start the transfer of every layer group, after the work queued on the
+    current stream, and return at once (extension; the reference issues one
+    synchronous call per layer group).  Arguments as transfer_kv_blocks plus
+    layer_granularity.  use_ce_transfer=False enqueues the zero-copy kernel
+    of every group on the current stream; True moves a host-to-device
+    transfer from block-wise host rows on the copy engines, driven by a
+    library thread, with each group's event recorded once its copies have
+    landed (other transfers take the kernel)."""
     import ctypes
 
     _require_int64_host(gpu_block_id_tensor, "gpu_block_id_tensor")
@@ -277,7 +294,9 @@ def transfer_kv_blocks_layerwise(gpu_block_id_tensor: torch.Tensor,
         cpu_block_id_tensor.data_ptr(), cpu_tensor.data_ptr(), int(cpu_kv_stride_in_bytes),
         int(cpu_layer_stride_in_bytes), int(cpu_block_stride_in_bytes), 0,
         int(chunk_size_in_bytes), stream, int(transfer_sms),
-        1 if is_host_to_device else 0, 1 if is_mla else 0, ctypes.byref(out))
+        1 if is_host_to_device else 0,
+        _lib.FKV_XFER_CE if use_ce_transfer else _lib.FKV_XFER_KERNEL,
+        1 if is_mla else 0, ctypes.byref(out))
     if rc != 0:
         raise RuntimeError(_lib.last_error() or f"fkv_transfer_kv_blocks_layerwise failed ({rc})")
     return LayerwiseTransfer(out.value, (cpu_tensor,))

@@ -258,11 +258,10 @@ void pack_ids_into(const Geometry& g, int64_t* h) {
   }
 }
 
-int pack_ids(const Geometry& g, IdLease& lease, char** ids_dev) {
+int pack_ids(const Geometry& g, IdLease& lease) {
   int rc = ids_acquire(static_cast<size_t>(g.num_blocks) * 16, &lease.buf);
   if (rc) return rc;
   pack_ids_into(g, lease.buf.host);
-  *ids_dev = lease.buf.dev;
   return 0;
 }
 

@@ -24,7 +24,12 @@ namespace fkv_detail {
 
 constexpr int kMaxLayersPerLaunch = 128;    // layer pointers in kernel args
 constexpr int kMaxDevices = 64;
-constexpr size_t kDefaultStagingBytes = size_t(256) << 20;
+// Staging per device and direction (two halves).  Launch size sets the
+// gather/scatter rate (MI355X, in a copy-engine transfer at the Llama-3-8B
+// shape: gather 4.95 / 5.46 / 5.78 TB/s and scatter 3.58 / 4.32 / 4.78 TB/s
+// with 256 MiB / 512 MiB / 1 GiB of staging); 1 GiB is 0.35% of the
+// device's 288 GB.
+constexpr size_t kDefaultStagingBytes = size_t(1) << 30;
 constexpr int kInval = static_cast<int>(hipErrorInvalidValue);
 
 // Set the calling thread's error message; returns `code`.
@@ -82,6 +87,10 @@ struct CopyLane {
   // on).  The signals of the copies given up on are kept here, never destroyed.
   bool stalled = false;
   std::vector<hsa_signal_t> abandoned;
+  // stream (own hardware queue) of the copy-engine layer-wise pipeline's
+  // scatter kernels, made on first use under stream_mu
+  std::mutex stream_mu;
+  hipStream_t pipeline_stream = nullptr;
 };
 
 struct DeviceState {
@@ -99,6 +108,9 @@ struct DeviceState {
   std::atomic<bool> sdma_failed{false};
   hsa_agent_t gpu_agent{}, cpu_agent{};
   std::vector<hsa_amd_sdma_engine_id_t> engines[2];   // [D2H, H2D]
+  // host-to-device engines of the copy-engine layer-wise pipeline: every
+  // engine device-to-host did not take, up to FLEXKV_SDMA_ENGINES_LAYERWISE
+  std::vector<hsa_amd_sdma_engine_id_t> engines_wide;
   CopyLane lane[2];                                    // [D2H, H2D]
 };
 
@@ -237,7 +249,7 @@ int streams_destroy_all();
 // The ids as (gpu_id, cpu_id) pairs.
 void pack_ids_into(const Geometry& g, int64_t* h);
 // Pack ids into a pool buffer held by `lease` as (gpu_id, cpu_id) pairs.
-int pack_ids(const Geometry& g, IdLease& lease, char** ids_dev);
+int pack_ids(const Geometry& g, IdLease& lease);
 // The device a stream belongs to (the current device for the null stream).
 int stream_device(hipStream_t s, int* dev);
 
@@ -296,10 +308,11 @@ int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr);
 // lane's events.
 int ensure_staging(CopyLane& lane, size_t need_half);
 // Queue the copies of `runs` between the host cache and staging half `half`
-// of `lane` on the direction's SDMA engines, round robin, each with its own
+// of `lane` on the direction's SDMA engines (`wide`: the layer-wise
+// pipeline's wider host-to-device set), round robin, each with its own
 // completion signal.  The half must have no copies queued (sdma_wait).
 int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, char* staging,
-               bool h2d, int half, hsa_agent_t host_agent);
+               bool h2d, int half, hsa_agent_t host_agent, bool wide = false);
 // Wait until every copy queued on a staging half has finished: block on the
 // interrupt signals of the engines' last copies, then check every copy's own
 // signal.  An engine runs its copies in order, so the check normally finds

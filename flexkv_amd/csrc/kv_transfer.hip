@@ -29,12 +29,14 @@
 #include <algorithm>
 #include <atomic>
 #include <chrono>
+#include <condition_variable>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "kv_internal.h"
@@ -74,13 +76,18 @@ namespace {
 #endif
 // Staging gather / scatter: chunks of whole row groups take the kernel
 // variant that addresses each group from one base (1) or the row-by-row one
-// (0).  Measured on MI355X at the Llama-3-8B shape: gather 6.06 against
-// 5.91 TB/s, scatter 5.25 against 5.42 TB/s.
+// (0).  The whole-group variant keeps no per-row address and spills nothing.
+// Measured on MI355X at the Llama-3-8B shape (TB/s of HBM traffic by launch
+// size 128 MiB / 256 MiB / 512 MiB / 2 GiB): gather 5.41/5.71/5.89/6.07
+// against 5.46/5.67/5.89/6.05 row by row; scatter 4.67/4.97/5.08/5.26
+// against 4.01/4.67/5.10/5.42.  So the scatter takes the whole-group
+// variant up to kWholeScatterMaxBytes per launch (every copy-engine piece)
+// and the row-by-row one above.
 #ifndef FKV_WHOLE_GATHER
 #define FKV_WHOLE_GATHER 1
 #endif
 #ifndef FKV_WHOLE_SCATTER
-#define FKV_WHOLE_SCATTER 0
+#define FKV_WHOLE_SCATTER 1
 #endif
 // Cache hints: loads are non-temporal everywhere; stores are non-temporal
 // into HBM but plain into pinned host memory (about 2% faster D2H over PCIe).
@@ -100,6 +107,25 @@ namespace {
 #ifndef FKV_TILE_FACTOR_SCATTER
 #define FKV_TILE_FACTOR_SCATTER FKV_TILE_FACTOR_HBM
 #endif
+// Staging gather/scatter: hand each XCD a contiguous range of tiles instead
+// of every eighth tile (workgroups are dispatched to the 8 XCDs round robin).
+#ifndef FKV_XCD_REMAP
+#define FKV_XCD_REMAP 0
+#endif
+// Tile order of the staging gather / scatter: 1 = block-major (consecutive
+// workgroups take the layer windows of one block, so the packed side is
+// walked in address order), 0 = layer-window-major (consecutive workgroups
+// take one layer window of consecutive blocks).
+#ifndef FKV_BLOCK_MAJOR_GATHER
+#define FKV_BLOCK_MAJOR_GATHER 0
+#endif
+#ifndef FKV_BLOCK_MAJOR_SCATTER
+#define FKV_BLOCK_MAJOR_SCATTER 0
+#endif
+// Dynamic LDS per staging workgroup (bytes), to cap its occupancy.
+#ifndef FKV_HBM_LDS_PAD
+#define FKV_HBM_LDS_PAD 0
+#endif
 #ifndef FKV_NT_LOAD_SCATTER
 #define FKV_NT_LOAD_SCATTER FKV_NT_LOAD
 #endif
@@ -108,9 +134,14 @@ namespace {
 #endif
 
 constexpr int kThreads = 256;               // 4 wavefronts of 64 lanes
+constexpr int64_t kWholeScatterMaxBytes = int64_t(512) << 20;
 constexpr int kWaves = kThreads / 64;
 constexpr int kUnrollHbm = FKV_UNROLL_HBM;
 constexpr int kMaxTileBlocks = 64;
+// Transfers of at most this many blocks carry their (gpu_id, cpu_id) pairs in
+// the kernel arguments, so no workgroup reads them over PCIe first (one host
+// round trip less per call; a one-block zero-copy call is latency-bound).
+constexpr int kInlineIds = 32;
 // Compute units of the zero-copy kernel when the caller passes -1: enough
 // loads/stores in flight to saturate the PCIe Gen5 x16 link (measured on
 // MI355X: 8 CUs reach the link's copy rate; more add contention).
@@ -132,6 +163,12 @@ constexpr int64_t kCeMinRunBytes = int64_t(128) << 10;
 // 128 KiB 41.2 / 32.4 GB/s (D2H / H2D), 256 KiB 51.1 / 42.0, 512 KiB
 // 55.3 / 51.7.
 constexpr int64_t kLayerRunBytes[2] = {int64_t(192) << 10, int64_t(384) << 10};   // [D2H, H2D]
+// The average run from which layer-major staging is used;
+// FLEXKV_CE_LAYER_RUN_BYTES overrides kLayerRunBytes.
+int64_t layer_run_bytes(bool h2d) {
+  const char* lr = getenv("FLEXKV_CE_LAYER_RUN_BYTES");
+  return lr ? std::max<int64_t>(1, atoll(lr)) : kLayerRunBytes[h2d ? 1 : 0];
+}
 // transfer_staged's return when the copy engines cannot be set up (nothing
 // was queued); not a hipError_t value
 constexpr int kSdmaUnavailable = -1000;
@@ -148,7 +185,7 @@ constexpr int kCachePolicyNt = 2;
 typedef __attribute__((address_space(1))) u32x4 gvec;
 
 struct CopyArgs {
-  const int64_t* ids;        // device-visible (gpu_id, cpu_id) pairs
+  const int64_t* ids;        // device-visible (gpu_id, cpu_id) pairs (inline_n == 0)
   char* cpu_base;            // CPU side of launch layer 0, block index 0
   int64_t gpu_kv_stride;
   int64_t gpu_block_stride;
@@ -163,11 +200,15 @@ struct CopyArgs {
   int32_t tile_blocks;       // a tile is tile_blocks blocks x tile_layers layers
   int32_t tile_layers;
   int32_t tiles_b;           // tiles along the block axis
+  int32_t tiles_l;           // tiles along the layer axis
+  int32_t block_major;       // tile order: layer windows of a block are consecutive tiles
   int32_t tiles_r;           // row ranges per tile (small transfers split a tile's rows)
   uint32_t split_rows;       // rows per range: a whole tile, or a multiple of the unroll
   int32_t num_tiles;
   int32_t ptrs_per_layer;    // 1: layer_ptr[l] + k*gpu_kv_stride; kv: layer_ptr[l*kv + k]
+  int32_t inline_n;          // > 0: the launch's pairs are inline_ids, not ids
   uint64_t layer_ptr[kMaxLayersPerLaunch];
+  int64_t inline_ids[2 * kInlineIds];
 };
 
 // A value every lane of the wavefront holds, moved to a scalar register.
@@ -206,10 +247,16 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
   // true when every row of a chunk is a full 64-lane row
   const bool full_rows = (a.chunk_vec & 63) == 0;
 
-  for (int tile = blockIdx.x; tile < a.num_tiles; tile += gridDim.x) {
+  int first = blockIdx.x;
+  if (kIotaCpu && FKV_XCD_REMAP && (gridDim.x & 7) == 0) {
+    const int per = gridDim.x >> 3;
+    first = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  }
+  for (int tile = first; tile < a.num_tiles; tile += gridDim.x) {
     const int tr = tile % a.tiles_r;
-    const int tb = (tile / a.tiles_r) % a.tiles_b;
-    const int tl = (tile / a.tiles_r) / a.tiles_b;
+    const int tq = tile / a.tiles_r;
+    const int tb = a.block_major ? tq / a.tiles_l : tq % a.tiles_b;
+    const int tl = a.block_major ? tq % a.tiles_l : tq / a.tiles_b;
     const int b0 = tb * a.tile_blocks;
     const int nb = min(a.tile_blocks, a.num_blocks - b0);
     const int l0 = tl * a.tile_layers;
@@ -217,9 +264,10 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
     const uint32_t items_per_block = nl * kv;
     __syncthreads();  // previous tile's readers are done with the LDS ids
     if (threadIdx.x < nb) {
-      const int64_t* pr = a.ids + 2 * static_cast<int64_t>(b0 + threadIdx.x);
+      const int j = b0 + threadIdx.x;
+      const int64_t* pr = a.inline_n ? a.inline_ids + 2 * j : a.ids + 2 * static_cast<int64_t>(j);
       s_gid[threadIdx.x] = pr[0];
-      s_cid[threadIdx.x] = kIotaCpu ? static_cast<int64_t>(b0 + threadIdx.x) : pr[1];
+      s_cid[threadIdx.x] = kIotaCpu ? static_cast<int64_t>(j) : pr[1];
     }
     __syncthreads();
 
@@ -372,19 +420,41 @@ int ensure_device_basics(int dev) {
 // per slot is the best shape (6.0 TB/s with whole-group addressing; 4 and 8
 // tiles per slot 5.93 / 6.00, 32 tiles 5.44).
 //
+// `balanced` (the HBM-bound staging kernels): a workgroup's wavefronts take
+// the tile's unrolled row groups in turn, so a tile whose rows are not a
+// multiple of kWaves * unroll leaves some wavefronts idle while the others
+// finish (a one-layer Llama-3-8B tile, 64 rows, keeps two of four busy; a
+// one-layer MLA tile, 72 rows, fills 56% of the group slots).  The layer
+// window is then halved only while that fill does not drop, and row ranges
+// (below) are whole multiples of kWaves * unroll.  Measured on MI355X, 128 MiB
+// launches: Llama-3-8B gather 5.08 -> 5.40 TB/s, 70B-shard (4 KiB chunks)
+// gather 2.39 -> 3.66 TB/s.
+//
 // A transfer too small for that many tiles even one (block, layer) per tile
 // splits each tile's rows into up to `factor`-filling ranges of at least one
 // `unroll`-row group per wavefront, so more wavefronts share its few chunks:
 // one block of one layer moves in one round of loads instead of several
 // (zero-copy latency is bound by PCIe round trips).
 void choose_tiles(int nb, int nl, int kv, int rpc, int grid_cap, int factor, int unroll,
-                  CopyArgs* a) {
+                  bool balanced, CopyArgs* a) {
   const int64_t target = factor * static_cast<int64_t>(std::max(1, grid_cap));
   auto tiles = [&](int tb, int tl) {
     return static_cast<int64_t>((nb + tb - 1) / tb) * ((nl + tl - 1) / tl);
   };
+  auto rows_of = [&](int tb_, int tl_) { return static_cast<int64_t>(tb_) * tl_ * kv * rpc; };
+  const int64_t wave_groups = static_cast<int64_t>(unroll) * kWaves;   // rows of one round
+  // rows of a tile over the row slots its wavefronts' rounds provide
+  auto fill_below = [&](int64_t ra, int64_t rb) {   // fill(ra) < fill(rb)
+    const int64_t ca = (ra + wave_groups - 1) / wave_groups * wave_groups;
+    const int64_t cb = (rb + wave_groups - 1) / wave_groups * wave_groups;
+    return static_cast<__int128>(ra) * cb < static_cast<__int128>(rb) * ca;
+  };
   int tb = 1, tl = nl;
-  while (tl > 1 && tiles(tb, tl) < target) tl = (tl + 1) / 2;
+  while (tl > 1 && tiles(tb, tl) < target) {
+    const int half = (tl + 1) / 2;
+    if (balanced && fill_below(rows_of(tb, half), rows_of(tb, tl))) break;
+    tl = half;
+  }
   while (tb < kMaxTileBlocks && tiles(tb * 2, tl) >= target) tb *= 2;
   while (tb > 1 && static_cast<int64_t>(tb) * tl * kv * rpc >= (int64_t(1) << 31)) tb /= 2;
   while (tl > 1 && static_cast<int64_t>(tb) * tl * kv * rpc >= (int64_t(1) << 31)) tl = (tl + 1) / 2;
@@ -392,14 +462,16 @@ void choose_tiles(int nb, int nl, int kv, int rpc, int grid_cap, int factor, int
   const int64_t tile_rows = static_cast<int64_t>(tb) * tl * kv * rpc;
   int64_t tr = 1, split = tile_rows;
   if (t < target) {
-    const int64_t min_split = static_cast<int64_t>(unroll) * kWaves;
+    const int64_t min_split = wave_groups;
+    const int64_t quantum = balanced ? wave_groups : unroll;
     tr = std::min<int64_t>(std::max<int64_t>(1, tile_rows / min_split), (target + t - 1) / t);
-    split = ((tile_rows + tr - 1) / tr + unroll - 1) / unroll * unroll;
+    split = ((tile_rows + tr - 1) / tr + quantum - 1) / quantum * quantum;
     tr = (tile_rows + split - 1) / split;
   }
   a->tile_blocks = tb;
   a->tile_layers = tl;
   a->tiles_b = (nb + tb - 1) / tb;
+  a->tiles_l = (nl + tl - 1) / tl;
   a->tiles_r = static_cast<int32_t>(tr);
   a->split_rows = static_cast<uint32_t>(split);
   a->num_tiles = static_cast<int32_t>(t * tr);
@@ -408,13 +480,22 @@ void choose_tiles(int nb, int nl, int kv, int rpc, int grid_cap, int factor, int
 // Fill the per-launch part of CopyArgs and launch over `nb` blocks starting at
 // block `b0` of the (already packed) id list, for GPU layers [l0, l0 + nl).
 // `cpu_base` is the CPU-side address of launch layer 0 of block index 0.
+// `ids` holds the packed pairs: `host` for the host's view, `dev` for the
+// device's (the same pinned buffer).
 template <bool kH2D, bool kIota>
-int launch_copy(const Geometry& g, char* ids_dev, char* cpu_base, int64_t cks, int64_t cls,
+int launch_copy(const Geometry& g, const IdBuf& ids, char* cpu_base, int64_t cks, int64_t cls,
                 int64_t cbs, int b0, int nb, int l0, int nl, int grid_cap,
                 hipStream_t stream, ProfRecorder& prof) {
+  if (nl < 1 || static_cast<int64_t>(nl) * g.ptrs_per_layer > kMaxLayersPerLaunch)
+    return fail(kInval, "internal: a launch of %d layers exceeds the %d layer pointers of the "
+                "kernel arguments", nl, kMaxLayersPerLaunch / g.ptrs_per_layer);
   CopyArgs a;
   memset(&a, 0, sizeof(a));
-  a.ids = reinterpret_cast<const int64_t*>(ids_dev) + 2 * static_cast<int64_t>(b0);
+  a.ids = reinterpret_cast<const int64_t*>(ids.dev) + 2 * static_cast<int64_t>(b0);
+  if (nb <= kInlineIds) {
+    a.inline_n = nb;
+    memcpy(a.inline_ids, ids.host + 2 * static_cast<int64_t>(b0), sizeof(int64_t) * 2 * nb);
+  }
   a.cpu_base = cpu_base;
   a.gpu_kv_stride = g.gks;
   a.gpu_block_stride = g.gbs;
@@ -433,7 +514,8 @@ int launch_copy(const Geometry& g, char* ids_dev, char* cpu_base, int64_t cks, i
                                      : (kH2D ? FKV_UNROLL_ZC_H2D : FKV_UNROLL_ZC_D2H);
   choose_tiles(nb, nl, g.kv, a.rows_per_chunk, grid_cap,
                kIota ? (kH2D ? FKV_TILE_FACTOR_SCATTER : FKV_TILE_FACTOR_HBM) : FKV_TILE_FACTOR,
-               kLaunchUnroll, &a);
+               kLaunchUnroll, /*balanced=*/kIota, &a);
+  a.block_major = kIota && (kH2D ? FKV_BLOCK_MAJOR_SCATTER : FKV_BLOCK_MAJOR_GATHER);
   int grid = std::max(1, std::min(grid_cap, a.num_tiles));
   if (kIota && FKV_HBM_ONEPASS) grid = a.num_tiles;
   hipEvent_t ev = nullptr;
@@ -442,14 +524,19 @@ int launch_copy(const Geometry& g, char* ids_dev, char* cpu_base, int64_t cks, i
   // staging launches whose chunks are whole groups of full rows take the
   // kernel variant that addresses each group from one base
   constexpr int kStagedUnroll = kH2D ? FKV_UNROLL_SCATTER : kUnrollHbm;
-  const bool whole = kIota && (kH2D ? FKV_WHOLE_SCATTER : FKV_WHOLE_GATHER) &&
-                     a.chunk_vec % 64 == 0 &&
+  const bool whole_variant =
+      kH2D ? (FKV_WHOLE_SCATTER &&
+              static_cast<int64_t>(nb) * nl * g.kv * g.chunk <= kWholeScatterMaxBytes)
+           : FKV_WHOLE_GATHER;
+  const bool whole = kIota && whole_variant && a.chunk_vec % 64 == 0 &&
                      a.rows_per_chunk % kStagedUnroll == 0;
+  const unsigned lds = kIota ? FKV_HBM_LDS_PAD : 0;
   if (whole)
-    hipLaunchKernelGGL((kv_chunk_copy_kernel<kH2D, kIota, kIota>), dim3(grid), dim3(kThreads), 0,
+    hipLaunchKernelGGL((kv_chunk_copy_kernel<kH2D, kIota, kIota>), dim3(grid), dim3(kThreads), lds,
                        stream, a);
   else
-    hipLaunchKernelGGL((kv_chunk_copy_kernel<kH2D, kIota>), dim3(grid), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((kv_chunk_copy_kernel<kH2D, kIota>), dim3(grid), dim3(kThreads), lds,
+                       stream, a);
   FKV_HIP(hipGetLastError());
   return prof.end(stream, ev, static_cast<int64_t>(nb) * nl * g.kv * g.chunk, 0, false);
 }
@@ -457,9 +544,8 @@ int launch_copy(const Geometry& g, char* ids_dev, char* cpu_base, int64_t cks, i
 int transfer_zero_copy(const Geometry& g, hipStream_t stream, int dev, int transfer_cus,
                        bool h2d) {
   DeviceState& d = g_dev[dev];
-  char* ids_dev = nullptr;
   IdLease ids;
-  int rc = pack_ids(g, ids, &ids_dev);
+  int rc = pack_ids(g, ids);
   if (rc) return rc;
   DrainOnError drain{stream};
   int cus = transfer_cus <= 0 ? std::min(kAutoZeroCopyCus, d.num_cus)
@@ -472,9 +558,9 @@ int transfer_zero_copy(const Geometry& g, hipStream_t stream, int dev, int trans
   for (int l0 = 0; l0 < g.num_layers; l0 += per_launch) {
     const int nl = std::min(per_launch, g.num_layers - l0);
     char* base = cpu_dev + static_cast<int64_t>(l0) * g.cls;
-    rc = h2d ? launch_copy<true, false>(g, ids_dev, base, g.cks, g.cls, g.cbs, 0,
+    rc = h2d ? launch_copy<true, false>(g, ids.buf, base, g.cks, g.cls, g.cbs, 0,
                                         g.num_blocks, l0, nl, grid_cap, stream, prof)
-             : launch_copy<false, false>(g, ids_dev, base, g.cks, g.cls, g.cbs, 0,
+             : launch_copy<false, false>(g, ids.buf, base, g.cks, g.cls, g.cbs, 0,
                                          g.num_blocks, l0, nl, grid_cap, stream, prof);
     if (rc) return rc;
   }
@@ -501,10 +587,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   // rows, or one rect copy per block of a layer-wise cache), or layer-major
   // [layer][K|V][block][chunk] when a layer-wise cache's ids come in runs of
   // consecutive blocks long enough to copy each (layer, K|V) run linearly.
-  // FLEXKV_CE_LAYER_RUN_BYTES overrides the average run (kLayerRunBytes)
-  const char* lr = getenv("FLEXKV_CE_LAYER_RUN_BYTES");
-  const bool layer_major = layer_major_pays_off(
-      g, lr ? std::max<int64_t>(1, atoll(lr)) : kLayerRunBytes[h2d ? 1 : 0]);
+  const bool layer_major = layer_major_pays_off(g, layer_run_bytes(h2d));
   const bool row_contig = (g.kv == 1 || g.cks == g.chunk) &&
                           (g.num_layers == 1 || g.cls == g.kv * g.chunk);
   // A transfer of rect copies runs alone on the device: those go to the
@@ -520,9 +603,8 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   DeviceGuard guard;
   int rc = guard.set(dev);
   if (rc) return rc;
-  char* ids_dev = nullptr;
   IdLease ids;
-  rc = pack_ids(g, ids, &ids_dev);
+  rc = pack_ids(g, ids);
   if (rc) return rc;
 
   // A piece is a run of whole blocks over a layer window; the window covers
@@ -590,9 +672,9 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
       cbs = static_cast<int64_t>(p.nl) * cls;
     }
     char* stg = ln.staging + (pi & 1) * half;
-    return h2d ? launch_copy<true, true>(g, ids_dev, stg, cks, cls, cbs, p.b0, p.nb, p.l0, p.nl,
+    return h2d ? launch_copy<true, true>(g, ids.buf, stg, cks, cls, cbs, p.b0, p.nb, p.l0, p.nl,
                                          grid_cap, stream, prof)
-               : launch_copy<false, true>(g, ids_dev, stg, cks, cls, cbs, p.b0, p.nb, p.l0, p.nl,
+               : launch_copy<false, true>(g, ids.buf, stg, cks, cls, cbs, p.b0, p.nb, p.l0, p.nl,
                                           grid_cap, stream, prof);
   };
   if (!h2d) {
@@ -646,9 +728,8 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
 // g.cids is 0..n-1.  Uses every compute unit: the copy is HBM-bound.
 int transfer_contiguous(const Geometry& g, hipStream_t stream, int dev, bool to_gpu) {
   DeviceState& d = g_dev[dev];
-  char* ids_dev = nullptr;
   IdLease ids;
-  int rc = pack_ids(g, ids, &ids_dev);
+  int rc = pack_ids(g, ids);
   if (rc) return rc;
   const int grid_cap = d.num_cus * (to_gpu ? d.occ_staged[1] : d.occ_staged[0]);
   DrainOnError drain{stream};
@@ -657,9 +738,9 @@ int transfer_contiguous(const Geometry& g, hipStream_t stream, int dev, bool to_
   for (int l0 = 0; l0 < g.num_layers; l0 += per_launch) {
     const int nl = std::min(per_launch, g.num_layers - l0);
     char* base = g.cpu_info.dev_ptr + static_cast<int64_t>(l0) * g.cls;
-    rc = to_gpu ? launch_copy<true, true>(g, ids_dev, base, g.cks, g.cls, g.cbs, 0, g.num_blocks,
+    rc = to_gpu ? launch_copy<true, true>(g, ids.buf, base, g.cks, g.cls, g.cbs, 0, g.num_blocks,
                                           l0, nl, grid_cap, stream, prof)
-                : launch_copy<false, true>(g, ids_dev, base, g.cks, g.cls, g.cbs, 0, g.num_blocks,
+                : launch_copy<false, true>(g, ids.buf, base, g.cks, g.cls, g.cbs, 0, g.num_blocks,
                                            l0, nl, grid_cap, stream, prof);
     if (rc) return rc;
   }
@@ -760,6 +841,23 @@ struct fkv_transfer_handle_s {
   IdBuf ids;
   ProfRecorder prof;
   bool enqueued = false;          // every group was enqueued
+  // Copy-engine pipeline: a driver thread queues each layer group's SDMA
+  // copies into staging and, once they have landed, the group's scatter on
+  // the lane's pipeline stream, then records done[g] there.  `recorded`
+  // counts the events recorded so far; a caller that waits on a group (on
+  // the host or through another stream) first waits for its event to exist.
+  bool ce = false;
+  std::thread driver;
+  hipEvent_t start = nullptr;     // the caller's stream at the call
+  std::mutex mu;
+  std::condition_variable cv;
+  int recorded = 0;
+  int err = 0;
+  std::string err_msg;
+  int granularity = 1;
+  Geometry geo;                   // points at the copies below
+  std::vector<int64_t> gids, cids;
+  std::vector<void*> ptrs;
 };
 
 namespace {
@@ -802,9 +900,9 @@ int layerwise_enqueue(const Geometry& g, hipStream_t stream, int dev, int transf
     for (int l0 = g0; l0 < gend; l0 += g.layers_per_launch()) {
       const int nl = std::min(g.layers_per_launch(), gend - l0);
       char* base = cpu_dev + static_cast<int64_t>(l0) * g.cls;
-      rc = h2d ? launch_copy<true, false>(g, h->ids.dev, base, g.cks, g.cls, g.cbs, 0,
+      rc = h2d ? launch_copy<true, false>(g, h->ids, base, g.cks, g.cls, g.cbs, 0,
                                           g.num_blocks, l0, nl, grid_cap, stream, h->prof)
-               : launch_copy<false, false>(g, h->ids.dev, base, g.cks, g.cls, g.cbs, 0,
+               : launch_copy<false, false>(g, h->ids, base, g.cks, g.cls, g.cbs, 0,
                                            g.num_blocks, l0, nl, grid_cap, stream, h->prof);
       if (rc) return rc;
     }
@@ -821,6 +919,8 @@ int layerwise_enqueue(const Geometry& g, hipStream_t stream, int dev, int transf
 // whose enqueue failed part-way.
 int handle_destroy(fkv_transfer_handle_s* h) {
   int rc = 0;
+  if (h->driver.joinable()) h->driver.join();   // every event is recorded once it ends
+  if (h->ce && h->err) rc = fail(h->err, "%s", h->err_msg.c_str());
   if (h->enqueued && !h->done.empty()) {
     hipError_t e = hipEventSynchronize(h->done.back());
     if (e != hipSuccess) rc = fail(static_cast<int>(e), "hipEventSynchronize: %s", hipGetErrorString(e));
@@ -830,9 +930,205 @@ int handle_destroy(fkv_transfer_handle_s* h) {
   }
   h->prof.flush();
   for (hipEvent_t ev : h->done) (void)hipEventDestroy(ev);
+  if (h->start) (void)hipEventDestroy(h->start);
   if (h->ids.host) ids_release(h->ids);
   delete h;
   return rc;
+}
+
+// Whether the copy-engine layer-wise pipeline takes this transfer: host to
+// device from pinned host memory whose layer groups are contiguous per block
+// (block-wise host rows), on a device whose engines work.  Anything else
+// moves with the zero-copy kernel, as the synchronous path's policy would.
+bool layerwise_ce_fits(const Geometry& g, int dev, bool h2d, int granularity) {
+  if (!h2d || g.cpu_info.device || g_dev[dev].sdma_failed.load()) return false;
+  const int nl = std::min(granularity, g.num_layers);
+  return (g.kv == 1 || g.cks == g.chunk) && (nl == 1 || g.cls == g.kv * g.chunk);
+}
+
+// The lane's pipeline stream: a stream with a full CU mask, so it has a
+// hardware queue of its own and its scatters never wait behind compute
+// kernels queued on a shared queue.
+int pipeline_stream(CopyLane& ln, int dev, hipStream_t* out) {
+  std::lock_guard<std::mutex> lk(ln.stream_mu);
+  if (!ln.pipeline_stream) {
+    DeviceGuard guard;
+    int rc = guard.set(dev);
+    if (rc) return rc;
+    int ncu = 0;
+    FKV_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+    std::vector<uint32_t> mask(static_cast<size_t>((ncu + 31) / 32), 0u);
+    for (int c = 0; c < ncu; ++c) mask[c / 32] |= 1u << (c % 32);
+    FKV_HIP(hipExtStreamCreateWithCUMask(&ln.pipeline_stream, static_cast<uint32_t>(mask.size()),
+                                         mask.data()));
+  }
+  *out = ln.pipeline_stream;
+  return 0;
+}
+
+// The driver's work: layer groups in order, each cut into pieces of whole
+// blocks that fit a staging half; SDMA copies (one per block: the group's
+// rows are contiguous in block-wise host memory) on the wide engine set,
+// double-buffered; each piece's scatter on the pipeline stream after a
+// system-scope acquire; done[g] after the group's last piece.  The host
+// waits for a piece's scatter before reusing its half.
+int layerwise_ce_run(fkv_transfer_handle_s* h, CopyLane& ln, hipStream_t work) {
+  DeviceState& d = g_dev[h->dev];
+  const Geometry& g = h->geo;
+  DeviceGuard guard;
+  int rc = guard.set(h->dev);
+  if (rc) return rc;
+  FKV_HIP(hipEventSynchronize(h->start));   // the caller's earlier work is done
+  const int G = h->granularity;
+  const size_t req = g_staging_request.load();
+  const size_t half_default = (req ? req : kDefaultStagingBytes) / 2;
+  const int nl_max = std::min({G, g.num_layers, g.layers_per_launch()});
+  const size_t row_max = static_cast<size_t>(nl_max) * g.kv * g.chunk;
+  // a half holds at least one block's row of one layer, so every window fits
+  const size_t one_layer = static_cast<size_t>(g.kv) * g.chunk;
+  if ((rc = ensure_staging(ln, std::max(std::min(row_max, half_default), one_layer)))) return rc;
+  if ((rc = ensure_sdma(d, h->dev, ln.staging))) return rc;
+  const size_t half = ln.staging_bytes / 2;
+  struct Piece {
+    int l0, nl, b0, nb, group;
+    bool last;
+  };
+  std::vector<Piece> pieces;
+  for (int grp = 0, l0 = 0; l0 < g.num_layers; ++grp, l0 += G) {
+    const int nl = std::min(G, g.num_layers - l0);
+    // a group moves in layer windows whose block rows fit a staging half and
+    // whose layer pointers fit one launch's kernel arguments
+    int win = std::min(nl, g.layers_per_launch());
+    while (win > 1 && static_cast<size_t>(win) * g.kv * g.chunk > half) win = (win + 1) / 2;
+    for (int w0 = l0; w0 < l0 + nl; w0 += win) {
+      const int wn = std::min(win, l0 + nl - w0);
+      const size_t row = static_cast<size_t>(wn) * g.kv * g.chunk;
+      const int bpp = static_cast<int>(std::max<size_t>(1, half / row));
+      for (int b0 = 0; b0 < g.num_blocks; b0 += bpp)
+        pieces.push_back({w0, wn, b0, std::min(bpp, g.num_blocks - b0), grp, false});
+    }
+    pieces.back().last = true;
+  }
+  const int np = static_cast<int>(pieces.size());
+  const int grid_cap = d.num_cus * d.occ_staged[1];
+  std::vector<Run> runs;
+  bool pending[2] = {false, false};
+  int64_t dma_copies = 0, dma_bytes = 0;
+  const auto t0 = std::chrono::steady_clock::now();
+  DrainOnError drain{work, &d, &ln};
+  auto queue_copies = [&](int pi) -> int {
+    const Piece& p = pieces[pi];
+    build_runs(g, p.b0, p.nb, p.l0, p.nl, false, false, runs);
+    for (const Run& r : runs) dma_bytes += r.bytes;
+    dma_copies += static_cast<int64_t>(runs.size());
+    pending[pi & 1] = true;
+    return issue_sdma(d, ln, runs, ln.staging + (pi & 1) * half, true, pi & 1, d.cpu_agent,
+                      /*wide=*/true);
+  };
+  for (int pi = 0; pi < std::min(np, 2); ++pi)
+    if ((rc = queue_copies(pi))) return rc;
+  for (int pi = 0; pi < np; ++pi) {
+    const Piece& p = pieces[pi];
+    const int hf = pi & 1;
+    pending[hf] = false;
+    if ((rc = sdma_wait(d, ln, hf, /*spin=*/true))) return rc;
+    hipLaunchKernelGGL(acquire_system_kernel, dim3(d.num_cus), dim3(64), 0, work);
+    FKV_HIP(hipGetLastError());
+    const int64_t cks = g.kv == 1 ? 0 : g.chunk;
+    const int64_t cls = static_cast<int64_t>(g.kv) * g.chunk;
+    const int64_t cbs = static_cast<int64_t>(p.nl) * cls;
+    // launch_copy reads the group's layer pointers from call layer p.l0 on
+    if ((rc = launch_copy<true, true>(g, h->ids, ln.staging + hf * half, cks, cls, cbs, p.b0,
+                                      p.nb, p.l0, p.nl, grid_cap, work, h->prof)))
+      return rc;
+    if (p.last) {
+      FKV_HIP(hipEventRecord(h->done[p.group], work));
+      std::lock_guard<std::mutex> lk(h->mu);
+      h->recorded = p.group + 1;
+      h->cv.notify_all();
+    }
+    if (pi + 2 < np) {
+      FKV_HIP(hipEventRecord(ln.ev_compute[hf], work));
+      FKV_HIP(hipEventSynchronize(ln.ev_compute[hf]));
+      if ((rc = queue_copies(pi + 2))) return rc;
+    }
+  }
+  drain.armed = false;
+  if (h->prof.on) {
+    FKV_HIP(hipStreamSynchronize(work));
+    prof_add_dma(std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0)
+                     .count(),
+                 dma_copies, dma_bytes);
+  }
+  return 0;
+}
+
+void layerwise_ce_drive(fkv_transfer_handle_s* h, hipStream_t work) {
+  CopyLane& ln = g_dev[h->dev].lane[1];
+  int rc = 0;
+  std::string msg;
+  {
+    std::lock_guard<std::mutex> own(ln.mu);
+    try {
+      rc = layerwise_ce_run(h, ln, work);
+    } catch (const std::exception& e) {
+      rc = fail(static_cast<int>(hipErrorUnknown), "exception: %s", e.what());
+    }
+    if (rc) msg = last_error();
+  }
+  std::lock_guard<std::mutex> lk(h->mu);
+  if (rc) {
+    // every group's event is recorded even on failure, so no waiter blocks
+    // for good; the handle reports the error
+    h->err = rc;
+    h->err_msg = msg;
+    (void)hipSetDevice(h->dev);
+    for (size_t gi = static_cast<size_t>(h->recorded); gi < h->done.size(); ++gi)
+      (void)hipEventRecord(h->done[gi], work);
+  }
+  h->recorded = static_cast<int>(h->done.size());
+  h->cv.notify_all();
+}
+
+// Set up the copy-engine pipeline of a handle and start its driver.  The
+// caller's id lists and layer pointers are copied, since the driver reads
+// them after the call returns.
+int layerwise_ce_start(const Geometry& g, hipStream_t stream, int dev, int granularity,
+                       fkv_transfer_handle_s* h) {
+  h->ce = true;
+  h->granularity = granularity;
+  h->gids.assign(g.gids, g.gids + g.num_blocks);
+  h->cids.assign(g.cids, g.cids + g.num_blocks);
+  h->ptrs.assign(g.layer_ptrs, g.layer_ptrs + static_cast<int64_t>(g.num_layers) * g.ptrs_per_layer);
+  h->geo = g;
+  h->geo.gids = h->gids.data();
+  h->geo.cids = h->cids.data();
+  h->geo.layer_ptrs = h->ptrs.data();
+  int rc = ids_acquire(static_cast<size_t>(g.num_blocks) * 16, &h->ids);
+  if (rc) return rc;
+  pack_ids_into(h->geo, h->ids.host);
+  hipStream_t work = nullptr;
+  if ((rc = pipeline_stream(g_dev[dev].lane[1], dev, &work))) return rc;
+  for (int g0 = 0; g0 < g.num_layers; g0 += granularity) {
+    hipEvent_t ev = nullptr;
+    FKV_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    h->done.push_back(ev);
+  }
+  FKV_HIP(hipEventCreateWithFlags(&h->start, hipEventDisableTiming));
+  FKV_HIP(hipEventRecord(h->start, stream));
+  FKV_HIP(hipStreamWaitEvent(work, h->start, 0));
+  h->driver = std::thread(layerwise_ce_drive, h, work);
+  h->enqueued = true;
+  return 0;
+}
+
+// A copy-engine handle's group g: wait until its event is recorded.  0, or
+// the pipeline's error.
+int ce_group_recorded(fkv_transfer_handle_s* h, int group) {
+  std::unique_lock<std::mutex> lk(h->mu);
+  h->cv.wait(lk, [&] { return h->recorded > group; });
+  if (h->err) return fail(h->err, "%s", h->err_msg.c_str());
+  return 0;
 }
 
 Geometry make_geometry(int num_blocks, int start_layer_id, int num_layers,
@@ -869,7 +1165,16 @@ Geometry make_geometry(int num_blocks, int start_layer_id, int num_layers,
 // takes 77 us on the engines, 39 us in the zero-copy kernel); smaller or
 // finer-grained transfers, and caches in device memory, go to the zero-copy
 // kernel, with identical results.
-bool ce_pays_off(const Geometry& g) {
+//
+// A layer-wise host cache whose ids do not come in runs long enough for
+// layer-major staging needs one rect copy per block, and the runtime runs
+// every rect copy on a single engine per direction: 46.8 / 47.0 GB/s
+// (D2H / H2D) at the Llama-3-8B shape, 82% of the link, against 56.5 /
+// 57.2 GB/s for the zero-copy kernel.  Such transfers therefore move with
+// the zero-copy kernel, which holds compute units for the whole transfer
+// (160 bf16 GEMMs beside a 2 GiB D2H take 71 ms instead of 36 ms beside the
+// rect copies); FLEXKV_CE_RECT_COPIES=1 keeps them on the engines.
+bool ce_pays_off(const Geometry& g, bool h2d) {
   // a "host" cache that is device memory has no PCIe copy to offload
   if (g.cpu_info.device) return false;
   const char* e = getenv("FLEXKV_CE_MIN_BYTES");
@@ -878,7 +1183,12 @@ bool ce_pays_off(const Geometry& g) {
   const bool row_contig = (g.kv == 1 || g.cks == g.chunk) &&
                           (g.num_layers == 1 || g.cls == g.kv * g.chunk);
   const int64_t row = static_cast<int64_t>(g.num_layers) * g.kv * g.chunk;
-  const int64_t run = (row_contig || host_slice_pitch(g, g.num_layers) > 0) ? row : g.chunk;
+  const bool rect = !row_contig && host_slice_pitch(g, g.num_layers) > 0;
+  if (rect && !layer_major_pays_off(g, layer_run_bytes(h2d))) {
+    const char* r = getenv("FLEXKV_CE_RECT_COPIES");
+    if (!(r && atoi(r) == 1)) return false;
+  }
+  const int64_t run = (row_contig || rect) ? row : g.chunk;
   return total >= min_bytes && (min_bytes == 0 || run >= kCeMinRunBytes);
 }
 
@@ -893,7 +1203,7 @@ int transfer_entry(Geometry& g, hipStream_t s, int transfer_cus, bool h2d, int m
     case FKV_XFER_KERNEL:
       return transfer_zero_copy(g, s, dev, transfer_cus, h2d);
     case FKV_XFER_CE:
-      if (!ce_pays_off(g) || g_dev[dev].sdma_failed.load())
+      if (!ce_pays_off(g, h2d) || g_dev[dev].sdma_failed.load())
         return transfer_zero_copy(g, s, dev, transfer_cus, h2d);
       rc = transfer_staged(g, s, dev, h2d);
       return rc == kSdmaUnavailable ? transfer_zero_copy(g, s, dev, transfer_cus, h2d) : rc;
@@ -986,10 +1296,14 @@ int fkv_transfer_kv_blocks_layerwise(
     int64_t gpu_block_stride_bytes, const int64_t* cpu_block_ids, void* cpu_ptr,
     int64_t cpu_kv_stride_bytes, int64_t cpu_layer_stride_bytes, int64_t cpu_block_stride_bytes,
     int64_t cpu_startoff_inside_chunks, int64_t chunk_size_bytes, fkv_stream_t stream,
-    int transfer_cus, int is_host_to_device, int is_mla, fkv_transfer_handle* out) {
+    int transfer_cus, int is_host_to_device, int use_ce_transfer, int is_mla,
+    fkv_transfer_handle* out) {
   try {
     last_error().clear();
     if (!out) return fail(kInval, "out handle pointer is null");
+    if (use_ce_transfer != FKV_XFER_KERNEL && use_ce_transfer != FKV_XFER_CE)
+      return fail(kInval, "use_ce_transfer must be 0 (kernel) or 1 (copy engines), got %d",
+                  use_ce_transfer);
     *out = nullptr;
     if (layer_granularity < 1) return fail(kInval, "layer_granularity must be >= 1");
     if (num_blocks < 0 || num_layers < 0)
@@ -1004,10 +1318,13 @@ int fkv_transfer_kv_blocks_layerwise(
     h->stream = s;
     int rc = 0;
     if (num_blocks > 0 && num_layers > 0) {
+      const bool h2d = is_host_to_device != 0;
       if ((rc = validate(g, FKV_XFER_KERNEL)) || (rc = stream_device(s, &h->dev)) ||
           (rc = ensure_device_basics(h->dev)) ||
-          (rc = layerwise_enqueue(g, s, h->dev, transfer_cus, is_host_to_device != 0,
-                                  layer_granularity, h))) {
+          (rc = (use_ce_transfer == FKV_XFER_CE &&
+                 layerwise_ce_fits(g, h->dev, h2d, layer_granularity))
+                    ? layerwise_ce_start(g, s, h->dev, layer_granularity, h)
+                    : layerwise_enqueue(g, s, h->dev, transfer_cus, h2d, layer_granularity, h))) {
         const std::string msg = last_error();
         (void)handle_destroy(h);
         last_error() = msg;
@@ -1034,6 +1351,11 @@ int fkv_handle_query(fkv_transfer_handle h, int group) {
   last_error().clear();
   if (!h || !handle_live(h) || group < 0 || group >= static_cast<int>(h->done.size()))
     return fail(-1, "bad handle or group %d", group);
+  if (h->ce) {
+    std::lock_guard<std::mutex> lk(h->mu);
+    if (h->recorded <= group) return 0;
+    if (h->err) return fail(-h->err, "%s", h->err_msg.c_str());
+  }
   hipError_t e = hipEventQuery(h->done[group]);
   if (e == hipSuccess) return 1;
   (void)hipGetLastError();
@@ -1045,6 +1367,10 @@ int fkv_handle_wait(fkv_transfer_handle h, int group) {
   last_error().clear();
   if (!h || !handle_live(h) || group < 0 || group >= static_cast<int>(h->done.size()))
     return fail(kInval, "bad handle or group %d", group);
+  if (h->ce) {
+    const int rc = ce_group_recorded(h, group);
+    if (rc) return rc;
+  }
   FKV_HIP(hipEventSynchronize(h->done[group]));
   return 0;
 }
@@ -1053,6 +1379,12 @@ int fkv_handle_stream_wait(fkv_transfer_handle h, int group, fkv_stream_t other)
   last_error().clear();
   if (!h || !handle_live(h) || group < 0 || group >= static_cast<int>(h->done.size()))
     return fail(kInval, "bad handle or group %d", group);
+  if (h->ce) {
+    // the group's event exists once its copies have landed and its scatter
+    // is queued; only then can another stream wait on it
+    const int rc = ce_group_recorded(h, group);
+    if (rc) return rc;
+  }
   FKV_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(other), h->done[group], 0));
   return 0;
 }
@@ -1086,6 +1418,7 @@ int fkv_finalize(void) {
       for (CopyLane& ln : d.lane) {
         std::lock_guard<std::mutex> lk(ln.mu);
         const bool used = ln.staging || ln.ev_compute[0] || ln.ev_compute[1] ||
+                          ln.pipeline_stream ||
                           !ln.polled_pool[0].empty() || !ln.irq_pool[0].empty() ||
                           !ln.polled_pool[1].empty() || !ln.irq_pool[1].empty();
         if (!used) continue;

@@ -138,20 +138,35 @@ int fkv_scatter_kv_blocks(int num_blocks, int num_layers, const int64_t* gpu_blo
                           const void* buffer, size_t buffer_bytes, fkv_stream_t stream,
                           int is_mla);
 
-/* Asynchronous, layer-grouped transfer (zero-copy kernel path).  Layers
- * [0, num_layers) move in groups of `layer_granularity` consecutive layers,
- * in order, on `stream`; an event marks the end of each group.  The call
- * returns once everything is enqueued, with a handle the caller polls or waits
- * on per group: on the host (fkv_handle_query / fkv_handle_wait) or on the
- * device (fkv_handle_stream_wait makes another stream, e.g. the one running
- * layer l of the model, wait for group g without a host round trip).
- * Arguments and checks as in fkv_transfer_kv_blocks, except that
+/* Asynchronous, layer-grouped transfer.  Layers [0, num_layers) move in
+ * groups of `layer_granularity` consecutive layers, in order, after the work
+ * already queued on `stream`; an event marks the end of each group.  The
+ * call returns at once, with a handle the caller polls or waits on per
+ * group: on the host (fkv_handle_query / fkv_handle_wait) or on the device
+ * (fkv_handle_stream_wait makes another stream, e.g. the one running layer l
+ * of the model, wait for group g).
+ *
+ * use_ce_transfer = FKV_XFER_KERNEL: the zero-copy kernel, every group
+ * enqueued on `stream` before the call returns; fkv_handle_stream_wait makes
+ * the other stream wait on the device, without a host round trip.
  * transfer_cus = -1 selects 2 compute units for host-to-device transfers
- * (enough for the link, and the rest of the chip stays with the compute the
- * transfer overlaps) and 8 for device-to-host; the id lists are copied
- * before the call returns.  The caller keeps the GPU cache and host cache
- * alive until the handle is released; fkv_handle_release waits for all groups
- * and frees the handle.
+ * (enough for the link; the rest of the chip stays with the compute the
+ * transfer overlaps) and 8 for device-to-host.
+ * use_ce_transfer = FKV_XFER_CE (host to device from block-wise host rows;
+ * other transfers take the kernel): the copy engines, so the transfer holds
+ * no compute unit while its bytes cross the link.  A library thread queues
+ * each group's SDMA copies (one per block, on up to
+ * FLEXKV_SDMA_ENGINES_LAYERWISE engines, default 12) into double-buffered
+ * staging and, once they have landed, the group's scatter on a library stream
+ * with a hardware queue of its own; the group's event is recorded there.
+ * fkv_handle_stream_wait and fkv_handle_wait first wait on the host until
+ * the group's event exists (its copies have landed), fkv_handle_query
+ * reports 0 until then.
+ *
+ * Arguments and checks as in fkv_transfer_kv_blocks; the id lists and layer
+ * pointers are copied before the call returns.  The caller keeps the GPU
+ * cache and host cache alive until the handle is released;
+ * fkv_handle_release waits for all groups and frees the handle.
  *
  * The reference reaches the same layer-wise schedule with one synchronous
  * call per layer group (worker.py:293-295, layer-wise ops of
@@ -164,7 +179,8 @@ int fkv_transfer_kv_blocks_layerwise(
     int64_t gpu_block_stride_bytes, const int64_t* cpu_block_ids, void* cpu_ptr,
     int64_t cpu_kv_stride_bytes, int64_t cpu_layer_stride_bytes, int64_t cpu_block_stride_bytes,
     int64_t cpu_startoff_inside_chunks, int64_t chunk_size_bytes, fkv_stream_t stream,
-    int transfer_cus, int is_host_to_device, int is_mla, fkv_transfer_handle* out);
+    int transfer_cus, int is_host_to_device, int use_ce_transfer, int is_mla,
+    fkv_transfer_handle* out);
 int fkv_handle_num_groups(fkv_transfer_handle h);             /* groups, or -1 */
 int fkv_handle_query(fkv_transfer_handle h, int group);       /* 1 done, 0 pending, <0 error */
 int fkv_handle_wait(fkv_transfer_handle h, int group);        /* host blocks until done */
@@ -257,7 +273,7 @@ int fkv_host_unregister(void* ptr);
 
 /* Staging buffer used by FKV_XFER_CE on each device, one per direction
  * (bytes, split in two halves).  Takes effect at the next allocation; 0 =
- * default (256 MiB).  fkv_release_staging frees every device's buffers. */
+ * default (1 GiB).  fkv_release_staging frees every device's buffers. */
 int fkv_set_staging_bytes(size_t bytes);
 int fkv_release_staging(void);
 

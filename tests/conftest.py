@@ -10,6 +10,10 @@ if ROOT not in sys.path:
 # Copy-engine mode hands transfers under 8 MiB to the zero-copy kernel; the
 # parity tests use small shapes and must reach the SDMA path itself.
 os.environ["FLEXKV_CE_MIN_BYTES"] = "0"
+# Layer-wise host caches with scattered ids move with the zero-copy kernel by
+# default; the parity suite keeps their copy-engine form (one SDMA rect copy
+# per block) in play.  test_rect_policy_default checks the default itself.
+os.environ["FLEXKV_CE_RECT_COPIES"] = "1"
 
 
 def pytest_configure(config):

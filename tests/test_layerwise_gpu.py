@@ -13,7 +13,7 @@ from kvcase import KVCase
 pytestmark = pytest.mark.gpu
 
 
-def _abi_layerwise(dc, gids, cids, h2d, gran, stream=None, cus=-1):
+def _abi_layerwise(dc, gids, cids, h2d, gran, stream=None, cus=-1, ce=False):
     from flexkv_amd import _lib
     from flexkv_amd.c_ext import LayerwiseTransfer
     case = dc.case
@@ -27,7 +27,7 @@ def _abi_layerwise(dc, gids, cids, h2d, gran, stream=None, cus=-1):
     rc = lib.fkv_transfer_kv_blocks_layerwise(
         len(gids), case.start_layer, len(dc.gpu), gran, gids.ctypes.data, ptrs, s["gpu_kv"],
         s["gpu_block"], cids.ctypes.data, dc.host.data_ptr(), s["cpu_kv"], s["cpu_layer"],
-        s["cpu_block"], s["startoff"], s["chunk"], st, cus, int(h2d), int(case.kv == 1),
+        s["cpu_block"], s["startoff"], s["chunk"], st, cus, int(h2d), int(ce), int(case.kv == 1),
         ctypes.byref(out))
     _lib.check(rc, "fkv_transfer_kv_blocks_layerwise")
     # ids were copied by the call: overwrite ours to prove the handle kept its own
@@ -36,10 +36,11 @@ def _abi_layerwise(dc, gids, cids, h2d, gran, stream=None, cus=-1):
     return LayerwiseTransfer(out.value, ())
 
 
+@pytest.mark.parametrize("ce", [False, True], ids=["kernel", "ce"])
 @pytest.mark.parametrize("gran", [1, 3, 4, 200])
 @pytest.mark.parametrize("geo", [(4, 2, 64, 96, 16, 8, 128, 40), (130, 2, 6, 8, 1, 1, 64, 5),
                                  (6, 1, 30, 40, 64, 1, 576, 9)], ids=["8b-like", "130-layers", "mla"])
-def test_layerwise_matches_oracle(geo, gran):
+def test_layerwise_matches_oracle(geo, gran, ce):
     from gpu_util import DeviceCase
     L, kv, ng, nh, t, h, d, n = geo
     case = KVCase(layers_total=L, num_layers=L, start_layer=0, kv=kv, ng=ng, nh=nh, tokens=t,
@@ -60,7 +61,7 @@ def test_layerwise_matches_oracle(geo, gran):
     dc.set_host(fresh)
     zeros = [np.zeros_like(g) for g in case.gpu]
     dc.set_gpu(zeros)
-    with _abi_layerwise(dc, gids.copy(), cids.copy(), True, gran) as hnd:
+    with _abi_layerwise(dc, gids.copy(), cids.copy(), True, gran, ce=ce) as hnd:
         for g in range(hnd.num_groups):
             hnd.wait(g)
             assert hnd.query(g)
@@ -73,9 +74,12 @@ def test_layerwise_matches_oracle(geo, gran):
         assert np.array_equal(got, e)
 
 
-def test_stream_wait_orders_consumers():
-    """A consumer stream that waits on group g sees layer g's blocks, with no
-    host synchronisation between the transfer and the consumer."""
+@pytest.mark.parametrize("ce", [False, True], ids=["kernel", "ce"])
+def test_stream_wait_orders_consumers(ce):
+    """A consumer stream that waits on group g sees layer g's blocks (the
+    kernel path: with no host synchronisation between the transfer and the
+    consumer; the copy-engine path: the host waits for the group's event to
+    exist, the consumer stream for it to complete)."""
     from gpu_util import DeviceCase
     L, n = 16, 256
     case = KVCase(layers_total=L, num_layers=L, start_layer=0, kv=2, ng=512, nh=1024, tokens=16,
@@ -97,7 +101,7 @@ def test_stream_wait_orders_consumers():
     consumer = torch.cuda.Stream()
     outs = []
     with torch.cuda.stream(xfer):
-        hnd = _abi_layerwise(dc, gids.copy(), cids.copy(), True, 1, stream=xfer, cus=1)
+        hnd = _abi_layerwise(dc, gids.copy(), cids.copy(), True, 1, stream=xfer, cus=1, ce=ce)
     with torch.cuda.stream(consumer):
         for l in range(L):
             hnd.stream_wait(l, consumer)
@@ -179,3 +183,82 @@ def test_transfer_stream_helper(num_cus):
     out = ctypes.c_void_p()
     assert _lib.load().fkv_stream_create(100000, ctypes.byref(out)) == 1
     assert "num_cus" in _lib.last_error()
+
+
+@pytest.mark.parametrize("staging_kib,gran", [(0, 1), (256, 1), (256, 3), (96, 2)])
+def test_ce_pipeline_pieces_and_copies(staging_kib, gran):
+    """The copy-engine layer-wise pipeline with staging small enough that a
+    group spans several pieces, or a group's rows are cut into layer windows:
+    the blocks match the oracle, every group's event fires, and the engines
+    moved one copy per block and layer window (the library's profile)."""
+    from flexkv_amd import _lib
+    from gpu_util import DeviceCase
+    L, n = 6, 37
+    case = KVCase(layers_total=L, num_layers=L, start_layer=0, kv=2, ng=64, nh=96, tokens=16,
+                  heads=4, dim=64).fill(seed=60 + gran)              # 8 KiB chunks
+    s = case.strides()
+    gids = inputs.distinct_ids(61, n, 64)
+    cids = inputs.distinct_ids(62, n, 96)
+    dc = DeviceCase(case)
+    fresh = case.host ^ np.uint16(0x1E1E)
+    dc.set_host(fresh)
+    dc.set_gpu([np.zeros_like(g) for g in case.gpu])
+    _lib.set_staging_bytes(staging_kib << 10)
+    try:
+        _lib.profile_enable(True)
+        with _abi_layerwise(dc, gids.copy(), cids.copy(), True, gran, ce=True) as hnd:
+            assert hnd.num_groups == -(-L // gran)
+            for g in reversed(range(hnd.num_groups)):
+                hnd.wait(g)
+        prof = _lib.profile_read()
+        _lib.profile_enable(False)
+    finally:
+        _lib.set_staging_bytes(0)
+        _lib.release_staging()
+    exp = [np.zeros_like(g) for g in case.gpu]
+    oracle.transfer_kv_blocks(gids, exp, s["gpu_kv"], s["gpu_block"], cids, fresh, s["cpu_kv"],
+                              s["cpu_layer"], s["cpu_block"], s["chunk"], 0, True)
+    for got, e in zip(dc.gpu_np(), exp):
+        assert np.array_equal(got, e)
+    assert prof["dma_batches"] == 1, prof
+    half = (staging_kib << 9) if staging_kib else 1 << 29
+    # windows a group is cut into when its rows do not fit a half
+    win = gran
+    while win > 1 and win * 2 * s["chunk"] > half:
+        win = (win + 1) // 2
+    windows = sum(-(-min(gran, L - l0) // win) for l0 in range(0, L, gran))
+    assert prof["dma_copies"] == windows * n, (prof, windows)
+
+
+def test_ce_handle_stream_wait_and_query_before_arrival():
+    """query() reports a copy-engine group as pending until its copies land,
+    then done; stream_wait() on a later group than the one waited for still
+    orders the consumer; release() without waits drains the pipeline."""
+    from gpu_util import DeviceCase
+    L, n = 8, 200
+    case = KVCase(layers_total=L, num_layers=L, start_layer=0, kv=2, ng=256, nh=256, tokens=16,
+                  heads=8, dim=128).fill(seed=70)                  # 32 KiB chunks
+    gids = inputs.distinct_ids(71, n, 256)
+    cids = inputs.distinct_ids(72, n, 256)
+    dc = DeviceCase(case)
+    fresh = case.host ^ np.uint16(0x2D2D)
+    dc.set_host(fresh)
+    dc.set_gpu([np.zeros_like(g) for g in case.gpu])
+    hnd = _abi_layerwise(dc, gids.copy(), cids.copy(), True, 1, ce=True)
+    states = [hnd.query(g) for g in range(L)]           # some may still be pending
+    consumer = torch.cuda.Stream()
+    g_dev = torch.from_numpy(gids).cuda()
+    with torch.cuda.stream(consumer):
+        hnd.stream_wait(L - 1, consumer)
+        last = dc.gpu[L - 1][:, g_dev].clone()
+    consumer.synchronize()
+    assert all(hnd.query(g) for g in range(L)), states
+    hnd.release()
+    hv = case.host_view(fresh)
+    want = np.stack([hv[c, L - 1, :, 0] for c in cids], axis=1)
+    assert np.array_equal(last.cpu().numpy().view(np.uint16), want)
+    # a handle released at once
+    dc.set_gpu([np.zeros_like(g) for g in case.gpu])
+    _abi_layerwise(dc, gids.copy(), cids.copy(), True, 2, ce=True).release()
+    for l, g in enumerate(dc.gpu_np()):
+        assert np.array_equal(g[:, gids], np.stack([hv[c, l, :, 0] for c in cids], axis=1))

@@ -228,6 +228,40 @@ def test_layerwise_host_copy_engines_one_rect_per_block(dev, mla, window):
         assert np.array_equal(g, expect), f"layer {l}"
 
 
+def test_rect_policy_default(dev, monkeypatch):
+    """Without FLEXKV_CE_RECT_COPIES, copy-engine mode moves a layer-wise host
+    cache with scattered ids with the zero-copy kernel (no SDMA batch), and
+    one whose ids come in long runs with the engines (layer-major staging);
+    the bytes match the oracle either way."""
+    from flexkv_amd import _lib
+    from gpu_util import DeviceCase, abi_transfer
+    monkeypatch.delenv("FLEXKV_CE_RECT_COPIES", raising=False)
+    monkeypatch.delenv("FLEXKV_CE_LAYER_RUN_BYTES", raising=False)
+    case = KVCase(layers_total=4, num_layers=4, start_layer=0, kv=2, ng=64, nh=96, tokens=16,
+                  heads=4, dim=128, layout="LAYERWISE").fill(seed=53)   # 16 KiB chunks
+    runs = np.concatenate([np.arange(0, 32), np.arange(40, 72)])     # 512 KiB per run
+    for name, cids, engines in (("scattered", inputs.distinct_ids(12, 32, 96), False),
+                                ("runs", runs, True)):
+        cids = np.ascontiguousarray(cids, dtype=np.int64)
+        gids = inputs.distinct_ids(13, len(cids), 64)
+        print(f"rect policy {name}", flush=True)
+        dc = DeviceCase(case)
+        for h2d in (False, True):
+            if h2d:
+                dc.set_gpu([np.zeros_like(g) for g in case.gpu])
+            _lib.profile_enable(True)
+            abi_transfer(dc, gids, cids, h2d=h2d, mode=1)
+            prof = _lib.profile_read()
+            _lib.profile_enable(False)
+            torch.cuda.synchronize()
+            assert (prof["dma_batches"] > 0) == engines, (name, h2d, prof)
+        assert np.array_equal(dc.host_np(), _oracle_d2h(case, gids, cids, 1))
+        for l, g in enumerate(dc.gpu_np()):
+            expect = np.zeros_like(case.gpu[l])
+            expect[:, gids] = case.gpu[l][:, gids]
+            assert np.array_equal(g, expect), f"{name} layer {l}"
+
+
 @pytest.mark.parametrize("mla", [False, True])
 def test_layerwise_host_id_runs_stage_layer_major(dev, mla, monkeypatch):
     """On a layer-wise host cache whose ids come in runs of consecutive blocks
