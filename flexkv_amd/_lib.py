@@ -30,6 +30,7 @@ FKV_HOST_NONCOHERENT = 2
 EXPORTED_SYMBOLS = (
     "fkv_transfer_kv_blocks",
     "fkv_transfer_kv_blocks_kv_ptrs",
+    "fkv_transfer_kv_blocks_noalloc",
     "fkv_gather_kv_blocks",
     "fkv_scatter_kv_blocks",
     "fkv_transfer_kv_blocks_layerwise",
@@ -102,6 +103,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     f.restype = c_int
     f.argtypes = [c_int, c_int, c_int, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64,
                   c_i64, c_i64, c_i64, c_vp, c_int, c_int, c_int, c_int]
+    f = lib.fkv_transfer_kv_blocks_noalloc
+    f.restype = c_int
+    f.argtypes = [c_int, c_int, c_int, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64,
+                  c_i64, c_i64, c_i64, c_vp, c_int, c_int, c_int]
     f = lib.fkv_transfer_kv_blocks_kv_ptrs
     f.restype = c_int
     f.argtypes = [c_int, c_int, c_int, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64,

@@ -207,6 +207,7 @@ struct CopyArgs {
   int32_t num_tiles;
   int32_t ptrs_per_layer;    // 1: layer_ptr[l] + k*gpu_kv_stride; kv: layer_ptr[l*kv + k]
   int32_t inline_n;          // > 0: the launch's pairs are inline_ids, not ids
+  int32_t ids_split;         // > 0: ids holds gpu ids, and cpu ids ids_split entries later
   uint64_t layer_ptr[kMaxLayersPerLaunch];
   int64_t inline_ids[2 * kInlineIds];
 };
@@ -265,9 +266,19 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
     __syncthreads();  // previous tile's readers are done with the LDS ids
     if (threadIdx.x < nb) {
       const int j = b0 + threadIdx.x;
-      const int64_t* pr = a.inline_n ? a.inline_ids + 2 * j : a.ids + 2 * static_cast<int64_t>(j);
-      s_gid[threadIdx.x] = pr[0];
-      s_cid[threadIdx.x] = kIotaCpu ? static_cast<int64_t>(j) : pr[1];
+      int64_t gid, cid;
+      if (a.inline_n) {
+        gid = a.inline_ids[2 * j];
+        cid = a.inline_ids[2 * j + 1];
+      } else if (a.ids_split) {
+        gid = a.ids[j];
+        cid = a.ids[static_cast<int64_t>(a.ids_split) + j];
+      } else {
+        gid = a.ids[2 * static_cast<int64_t>(j)];
+        cid = a.ids[2 * static_cast<int64_t>(j) + 1];
+      }
+      s_gid[threadIdx.x] = gid;
+      s_cid[threadIdx.x] = kIotaCpu ? static_cast<int64_t>(j) : cid;
     }
     __syncthreads();
 
@@ -481,18 +492,21 @@ void choose_tiles(int nb, int nl, int kv, int rpc, int grid_cap, int factor, int
 // block `b0` of the (already packed) id list, for GPU layers [l0, l0 + nl).
 // `cpu_base` is the CPU-side address of launch layer 0 of block index 0.
 // `ids` holds the packed pairs: `host` for the host's view, `dev` for the
-// device's (the same pinned buffer).
+// device's (the same pinned buffer).  With `split` > 0, `dev` instead holds
+// the gpu ids and, `split` entries later, the cpu ids (device memory), and
+// `host` is null.
 template <bool kH2D, bool kIota>
 int launch_copy(const Geometry& g, const IdBuf& ids, char* cpu_base, int64_t cks, int64_t cls,
                 int64_t cbs, int b0, int nb, int l0, int nl, int grid_cap,
-                hipStream_t stream, ProfRecorder& prof) {
+                hipStream_t stream, ProfRecorder& prof, int32_t split = 0) {
   if (nl < 1 || static_cast<int64_t>(nl) * g.ptrs_per_layer > kMaxLayersPerLaunch)
     return fail(kInval, "internal: a launch of %d layers exceeds the %d layer pointers of the "
                 "kernel arguments", nl, kMaxLayersPerLaunch / g.ptrs_per_layer);
   CopyArgs a;
   memset(&a, 0, sizeof(a));
-  a.ids = reinterpret_cast<const int64_t*>(ids.dev) + 2 * static_cast<int64_t>(b0);
-  if (nb <= kInlineIds) {
+  a.ids = reinterpret_cast<const int64_t*>(ids.dev) + (split ? 1 : 2) * static_cast<int64_t>(b0);
+  a.ids_split = split;
+  if (nb <= kInlineIds && ids.host) {
     a.inline_n = nb;
     memcpy(a.inline_ids, ids.host + 2 * static_cast<int64_t>(b0), sizeof(int64_t) * 2 * nb);
   }
@@ -567,6 +581,92 @@ int transfer_zero_copy(const Geometry& g, hipStream_t stream, int dev, int trans
   FKV_HIP(hipStreamSynchronize(stream));
   drain.armed = false;
   prof.flush();
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// The entry point that allocates nothing (fkv_transfer_kv_blocks_noalloc):
+// the zero-copy transfer with its id lists staged in `scratch`, a fixed
+// device array, instead of a pinned buffer the library allocates.  Each GPU
+// holds its own copy of the array; host code reaches it only through the
+// address hipGetSymbolAddress returns for the device (the array's name is a
+// host-side stand-in, not a device address).  Every call on a device shares
+// that device's array, so calls that overlap on one device race.
+
+constexpr size_t kScratchBytes = size_t(1) << 20;
+// gpu ids in the first half, cpu ids in the second
+constexpr int kScratchMaxBlocks = static_cast<int>(kScratchBytes / (2 * sizeof(int64_t)));
+
+static __device__ __align__(256) int64_t scratch[kScratchBytes / sizeof(int64_t)];
+
+std::mutex g_scratch_mu;
+int64_t* g_scratch_dev[kMaxDevices];   // scratch's address on each device, once resolved
+
+// scratch's device address on `dev` (resolved once per device, with the
+// device current).
+int scratch_address(int dev, int64_t** out) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    DeviceGuard guard;
+    int rc = guard.set(dev);
+    if (rc) return rc;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(static_cast<int>(e == hipSuccess ? hipErrorInvalidSymbol : e),
+                  "hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_dev[dev] = static_cast<int64_t*>(p);
+  }
+  *out = g_scratch_dev[dev];
+  return 0;
+}
+
+int transfer_zero_copy_noalloc(const Geometry& g, hipStream_t stream, int dev, int transfer_cus,
+                               bool h2d) {
+  DeviceState& d = g_dev[dev];
+  if (g.num_blocks > kScratchMaxBlocks)
+    return fail(kInval, "fkv_transfer_kv_blocks_noalloc moves at most %d blocks per call "
+                "(its id scratch is %zu bytes), got %d", kScratchMaxBlocks, kScratchBytes,
+                g.num_blocks);
+  int64_t pairs[2 * kInlineIds];
+  IdBuf ids;
+  int32_t split = 0;
+  if (g.num_blocks <= kInlineIds) {
+    // the ids travel in the kernel arguments
+    pack_ids_into(g, pairs);
+    ids.host = pairs;
+  } else {
+    int64_t* sp = nullptr;
+    int rc = scratch_address(dev, &sp);
+    if (rc) return rc;
+    const size_t n = static_cast<size_t>(g.num_blocks) * sizeof(int64_t);
+    FKV_HIP(hipMemcpyAsync(sp, g.gids, n, hipMemcpyHostToDevice, stream));
+    FKV_HIP(hipMemcpyAsync(sp + kScratchMaxBlocks, g.cids, n, hipMemcpyHostToDevice, stream));
+    ids.dev = reinterpret_cast<char*>(sp);
+    split = kScratchMaxBlocks;
+  }
+  DrainOnError drain{stream};
+  const int cus = transfer_cus <= 0 ? std::min(kAutoZeroCopyCus, d.num_cus)
+                                    : std::min(transfer_cus, d.num_cus);
+  const int grid_cap = cus * (h2d ? d.occ_zero_copy[1] : d.occ_zero_copy[0]);
+  char* cpu_dev = g.cpu_info.dev_ptr + g.startoff + static_cast<int64_t>(g.start_layer) * g.cls;
+  ProfRecorder prof;
+  prof.on = false;   // profiling events are allocations
+  const int per_launch = g.layers_per_launch();
+  for (int l0 = 0; l0 < g.num_layers; l0 += per_launch) {
+    const int nl = std::min(per_launch, g.num_layers - l0);
+    char* base = cpu_dev + static_cast<int64_t>(l0) * g.cls;
+    const int rc = h2d ? launch_copy<true, false>(g, ids, base, g.cks, g.cls, g.cbs, 0,
+                                                  g.num_blocks, l0, nl, grid_cap, stream, prof,
+                                                  split)
+                       : launch_copy<false, false>(g, ids, base, g.cks, g.cls, g.cbs, 0,
+                                                   g.num_blocks, l0, nl, grid_cap, stream, prof,
+                                                   split);
+    if (rc) return rc;
+  }
+  FKV_HIP(hipStreamSynchronize(stream));
+  drain.armed = false;
   return 0;
 }
 
@@ -1264,6 +1364,37 @@ int fkv_transfer_kv_blocks_kv_ptrs(int num_blocks, int start_layer_id, int num_l
     g.ptrs_per_layer = g.kv;
     return transfer_entry(g, static_cast<hipStream_t>(stream), transfer_cus,
                           is_host_to_device != 0, use_ce_transfer);
+  } catch (const std::exception& e) {
+    return fail(static_cast<int>(hipErrorUnknown), "exception: %s", e.what());
+  } catch (...) {
+    return fail(static_cast<int>(hipErrorUnknown), "unknown exception");
+  }
+}
+
+int fkv_transfer_kv_blocks_noalloc(int num_blocks, int start_layer_id, int num_layers,
+                                   const int64_t* gpu_block_ids, void* const* gpu_layer_ptrs,
+                                   int64_t gpu_kv_stride_bytes, int64_t gpu_block_stride_bytes,
+                                   const int64_t* cpu_block_ids, void* cpu_ptr,
+                                   int64_t cpu_kv_stride_bytes, int64_t cpu_layer_stride_bytes,
+                                   int64_t cpu_block_stride_bytes,
+                                   int64_t cpu_startoff_inside_chunks, int64_t chunk_size_bytes,
+                                   fkv_stream_t stream, int transfer_cus, int is_host_to_device,
+                                   int is_mla) {
+  try {
+    last_error().clear();
+    if (num_blocks == 0 || num_layers == 0) return 0;
+    Geometry g = make_geometry(num_blocks, start_layer_id, num_layers, gpu_block_ids,
+                               gpu_layer_ptrs, gpu_kv_stride_bytes, gpu_block_stride_bytes,
+                               cpu_block_ids, cpu_ptr, cpu_kv_stride_bytes,
+                               cpu_layer_stride_bytes, cpu_block_stride_bytes,
+                               cpu_startoff_inside_chunks, chunk_size_bytes, is_mla);
+    int rc = validate(g, FKV_XFER_KERNEL);
+    if (rc) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int dev = 0;
+    if ((rc = stream_device(s, &dev))) return rc;
+    if ((rc = ensure_device_basics(dev))) return rc;
+    return transfer_zero_copy_noalloc(g, s, dev, transfer_cus, is_host_to_device != 0);
   } catch (const std::exception& e) {
     return fail(static_cast<int>(hipErrorUnknown), "exception: %s", e.what());
   } catch (...) {

@@ -120,6 +120,30 @@ int fkv_transfer_kv_blocks_kv_ptrs(int num_blocks, int start_layer_id, int num_l
                                    fkv_stream_t stream, int transfer_cus,
                                    int is_host_to_device, int use_ce_transfer, int is_mla);
 
+/* As fkv_transfer_kv_blocks in kernel mode (FKV_XFER_KERNEL), for callers
+ * that cannot allocate memory: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation.  No counterpart in the reference.
+ * It calls no hipMalloc, hipFree, pinned or other allocating routine:
+ * fkv_transfer_kv_blocks stages the id lists in pinned buffers the library
+ * allocates; this entry copies them (hipMemcpyAsync on `stream`) into a fixed
+ * 1 MiB device array compiled into the library, one per GPU, held until the
+ * process ends.  At most 65536 blocks per call; more is refused with
+ * hipErrorInvalidValue.  Transfers of up to 32 blocks carry their ids in the
+ * kernel arguments instead.  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (from several threads) race and must be
+ * serialised by the caller.  Same arguments (without use_ce_transfer),
+ * checks and synchronous return as fkv_transfer_kv_blocks; library
+ * profiling does not see these calls. */
+int fkv_transfer_kv_blocks_noalloc(int num_blocks, int start_layer_id, int num_layers,
+                                   const int64_t* gpu_block_ids, void* const* gpu_layer_ptrs,
+                                   int64_t gpu_kv_stride_bytes, int64_t gpu_block_stride_bytes,
+                                   const int64_t* cpu_block_ids, void* cpu_ptr,
+                                   int64_t cpu_kv_stride_bytes, int64_t cpu_layer_stride_bytes,
+                                   int64_t cpu_block_stride_bytes,
+                                   int64_t cpu_startoff_inside_chunks, int64_t chunk_size_bytes,
+                                   fkv_stream_t stream, int transfer_cus, int is_host_to_device,
+                                   int is_mla);
+
 /* Device-side gather / scatter between the per-layer GPU cache and one
  * contiguous buffer laid out [num_blocks][num_layers][K|V][chunk] (block i of
  * the id list at byte offset i * num_layers * kv * chunk).  This is the
