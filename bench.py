@@ -474,6 +474,92 @@ def engine_put_get(wl: Workload, steps: int):
     return out
 
 
+def worker_ops(wl: Workload, reps: int = 40, process: bool = True):
+    """Ops through GPUCPUTransferWorker, each submitted and waited for on the
+    finished-ops queue before the next, as the reference's worker benchmark
+    does (benchmarks/benchmark_workers.py:159-167,232-240): 16 blocks
+    (32 MiB at the Llama-3-8B shape) and the full step, both directions, on
+    the copy-engine and the zero-copy path; on a worker thread of this
+    process (this package's engine default) and, for 16 blocks, in a spawned
+    worker process fed IPC handles of the device layers (the reference's
+    worker model; its own pinned host cache of 1024 blocks).  Each op runs
+    inside a roctx range named as the reference names its NVTX range."""
+    import multiprocessing as mp
+    import queue
+
+    from flexkv_amd.common.memory_handle import TensorSharedHandle
+    from flexkv_amd.common.storage import KVCacheLayout, KVCacheLayoutType
+    from flexkv_amd.common.transfer import TransferDescriptor, TransferOp, TransferType
+    from flexkv_amd.storage.allocator import HostCacheSpec
+    from flexkv_amd.transfer.worker import GPUCPUTransferWorker
+    w = wl.w
+    L = w["layers"]
+    gl = KVCacheLayout(KVCacheLayoutType.LAYERWISE, L, w["ng"], w["tokens"], w["heads"],
+                       w["dim"], is_mla=wl.mla)
+
+    def op(kind, gids, cids):
+        src, dst = (gids, cids) if kind == TransferType.D2H else (cids, gids)
+        return TransferOp(graph_id=0, transfer_type=kind, layer_id=0, layer_granularity=L,
+                          src_descriptor=TransferDescriptor(physical_block_ids=src),
+                          dst_descriptor=TransferDescriptor(physical_block_ids=dst))
+
+    def timed(handle, q, kind, gids, cids, n_reps):
+        o = op(kind, gids, cids)
+        handle.submit_transfer(o)
+        assert q.get(timeout=120) == o.op_id
+        ts = []
+        for _ in range(n_reps):
+            o = op(kind, gids, cids)
+            t0 = time.perf_counter()
+            handle.submit_transfer(o)
+            got = q.get(timeout=120)
+            ts.append(time.perf_counter() - t0)
+            assert got == o.op_id
+        med = statistics.median(ts)
+        nbytes = len(gids) * L * w["kv"] * wl.chunk
+        return {"ms": round(med * 1e3, 3), "gbps": round(nbytes / med / 1e9, 2)}
+
+    out = {}
+    g16, c16 = wl.gids[:16].clone(), wl.cids[:16].clone()
+    for path, ce in (("ce", True), ("kernel", False)):
+        q = queue.Queue()
+        h = GPUCPUTransferWorker.create_worker_thread(
+            0, q, wl.layers, wl.host, gl, wl.cl, wl.dtype, 0, use_ce_transfer_h2d=ce,
+            use_ce_transfer_d2h=ce)
+        h.wait_ready()
+        try:
+            res = {}
+            for kind in (TransferType.D2H, TransferType.H2D):
+                d = kind.name.lower()
+                res[f"{d}_16blk"] = timed(h, q, kind, g16, c16, reps)
+                res[f"{d}_step"] = timed(h, q, kind, wl.gids, wl.cids, 3)
+            out[f"thread_{path}"] = res
+        finally:
+            h.shutdown()
+    if process:
+        ctx = mp.get_context("spawn")
+        q = ctx.Queue()
+        small = KVCacheLayout(wl.cl.type, L, 1024, w["tokens"], w["heads"], w["dim"],
+                              is_mla=wl.mla)
+        for path, ce in (("ce", True), ("kernel", False)):
+            h = GPUCPUTransferWorker.create_worker(
+                0, q, [TensorSharedHandle(t) for t in wl.layers], HostCacheSpec(small, wl.dtype),
+                gl, small, wl.dtype, 0, use_ce_transfer_h2d=ce, use_ce_transfer_d2h=ce)
+            try:
+                if not h.ready_event.wait(180):
+                    out[f"process_{path}"] = {"skipped": "worker process did not start"}
+                    continue
+                c_small = torch.randperm(1024, generator=torch.Generator().manual_seed(8))[:16]
+                out[f"process_{path}"] = {
+                    f"{k.name.lower()}_16blk": timed(h, q, k, g16, c_small, reps)
+                    for k in (TransferType.D2H, TransferType.H2D)}
+            finally:
+                h.shutdown()
+    out["what"] = ("16-block ops (32 MiB at this shape) and full-step ops, one at a time, "
+                   "submit to finished-ops queue; copy engines take ops of 8 MiB or more")
+    return out
+
+
 def call_latency(wl: Workload, reps: int = 200):
     """Wall time of small synchronous calls (1 block x 1 layer, 16 blocks x 1
     layer, 16 blocks x all layers), zero-copy and copy-engine paths,
@@ -1095,6 +1181,10 @@ def main() -> int:
     ap.add_argument("--layerwise-only", action="store_true",
                     help="run only the layer-wise H2D section (sync per layer, async handle, "
                          "overlap with per-layer GEMMs) and print its JSON (for profiling runs)")
+    ap.add_argument("--worker-ops", action="store_true",
+                    help="run only the worker-op section (thread and process workers, 16-block "
+                         "and full-step ops, each inside a roctx range) and print its JSON "
+                         "(for marker-trace profiling runs)")
     ap.add_argument("--seed", type=int, default=1001)
     ap.add_argument("--counters", action="store_true",
                     help="run only the kernels a PMC pass needs: a 1 GiB plain device copy "
@@ -1106,7 +1196,7 @@ def main() -> int:
         print("bench.py measures one GPU: the transfer path is per-GPU (one PCIe link, one HBM); "
               "multi-GPU runs are out of scope for this package", file=sys.stderr)
         return 2
-    ceilings = (None if (args.quick or args.counters or args.layerwise_only)
+    ceilings = (None if (args.quick or args.counters or args.layerwise_only or args.worker_ops)
                 else device_ceilings())
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
@@ -1125,6 +1215,10 @@ def main() -> int:
     if args.layerwise_only:
         wl.transfer(False, default_ce)   # the host cache holds the blocks read back below
         print(json.dumps({"layerwise_h2d": layerwise_h2d(wl, args.steps)}), flush=True)
+        return 0
+    if args.worker_ops:
+        print(json.dumps({"worker_ops": worker_ops(wl, reps=max(5, args.steps),
+                                                   process=not args.quick)}), flush=True)
         return 0
 
     # primary: D2H on the default path, library kernel timing on
@@ -1285,6 +1379,8 @@ def main() -> int:
         log(f"engine put and get: {result['engine_put_get']}")
         result["call_latency"] = call_latency(wl)
         log(f"call latency: {result['call_latency']}")
+        result["worker_ops"] = worker_ops(wl)
+        log(f"worker ops: {result['worker_ops']}")
         result["overlap_with_compute"] = overlap_with_compute(wl)
         log(f"overlap with compute: {result['overlap_with_compute']}")
         result["duplex"] = duplex(wl)

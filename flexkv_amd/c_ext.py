@@ -73,14 +73,15 @@ def transfer_kv_blocks(gpu_block_id_tensor: torch.Tensor,
                        transfer_sms: int = -1,
                        is_host_to_device: bool = True,
                        use_ce_transfer=False,
-                       is_mla: bool = False) -> None:
+                       is_mla: bool = False, *, stream: int = None) -> None:
     """Copy KV blocks between the per-layer GPU cache and the host cache.
 
     ``use_ce_transfer``: False -> zero-copy wavefront kernel; True -> copy
     engines behind an on-device gather/scatter through staging; the integer 2
     selects the reference's one-DMA-per-chunk loop (csrc/transfer.cu:97-121).
     ``transfer_sms`` bounds the compute units of the zero-copy kernel
-    (-1 = automatic).
+    (-1 = automatic).  ``stream`` (keyword only, an extension) is a raw
+    stream handle to run on instead of the current torch stream.
     """
     _require_int64_host(gpu_block_id_tensor, "gpu_block_id_tensor")
     _require_int64_host(cpu_block_id_tensor, "cpu_block_id_tensor")
@@ -97,7 +98,8 @@ def transfer_kv_blocks(gpu_block_id_tensor: torch.Tensor,
         mode = _lib.FKV_XFER_CE if use_ce_transfer else _lib.FKV_XFER_KERNEL
     else:
         mode = int(use_ce_transfer)
-    stream = _stream_handle("transfer_kv_blocks")
+    if stream is None:
+        stream = _stream_handle("transfer_kv_blocks")
     lib = _lib.load()
     rc = lib.fkv_transfer_kv_blocks(
         int(num_blocks), int(start_layer_id), int(num_layers),
@@ -125,7 +127,7 @@ def transfer_kv_blocks_kv_ptrs(gpu_block_id_tensor: torch.Tensor,
                                transfer_sms: int = -1,
                                is_host_to_device: bool = True,
                                use_ce_transfer=False,
-                               is_mla: bool = False) -> None:
+                               is_mla: bool = False, *, stream: int = None) -> None:
     """transfer_kv_blocks for K and V held in separate allocations
     (extension): ``gpu_kv_ptrs_tensor`` is an int64 host tensor of
     ``layers * kv`` base pointers ordered [layer][K|V] (kv = 1 for MLA)."""
@@ -147,7 +149,8 @@ def transfer_kv_blocks_kv_ptrs(gpu_block_id_tensor: torch.Tensor,
         mode = _lib.FKV_XFER_CE if use_ce_transfer else _lib.FKV_XFER_KERNEL
     else:
         mode = int(use_ce_transfer)
-    stream = _stream_handle("transfer_kv_blocks_kv_ptrs")
+    if stream is None:
+        stream = _stream_handle("transfer_kv_blocks_kv_ptrs")
     rc = _lib.load().fkv_transfer_kv_blocks_kv_ptrs(
         int(num_blocks), int(start_layer_id), int(gpu_kv_ptrs_tensor.numel() // kv),
         gpu_block_id_tensor.data_ptr(), gpu_kv_ptrs_tensor.data_ptr(),

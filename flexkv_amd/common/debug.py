@@ -26,6 +26,11 @@ class FlexkvLogger:
         else:
             self._log.setLevel(getattr(logging, level, logging.INFO))
 
+    def enabled(self, level: str) -> bool:
+        """Whether a message at `level` would be emitted (lets callers skip
+        building messages nobody reads)."""
+        return self._log.isEnabledFor(getattr(logging, level.upper(), logging.INFO))
+
     def debug(self, msg, *a) -> None:
         self._log.debug(msg, *a)
 

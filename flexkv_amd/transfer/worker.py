@@ -34,6 +34,7 @@ import torch
 from .. import _lib
 from ..c_ext import (SSDIOCTX, transfer_kv_blocks, transfer_kv_blocks_kv_ptrs,
                      transfer_kv_blocks_ssd)
+from ..common import trace
 from ..common.debug import flexkv_logger
 from ..common.memory_handle import TensorSharedHandle
 from ..common.storage import KVCacheLayout, KVCacheLayoutType
@@ -173,6 +174,8 @@ class TransferWorkerBase(ABC):
 
     def _log_transfer_performance(self, transfer_op: WorkerTransferOp, transfer_size: int,
                                   start_time: float, end_time: float) -> None:
+        if not flexkv_logger.enabled("INFO"):
+            return
         dt = max(end_time - start_time, 1e-12)
         flexkv_logger.info(
             f"{transfer_op.transfer_type.name} transfer request: {transfer_op.transfer_op_id} "
@@ -181,7 +184,8 @@ class TransferWorkerBase(ABC):
 
     def _execute(self, op: WorkerTransferOp) -> None:
         try:
-            self.launch_transfer(op)
+            with trace.op_range(trace.op_message(op)):    # worker.py:160-165
+                self.launch_transfer(op)
         except Exception as e:
             self.failed_ops.append(op.transfer_op_id)
             flexkv_logger.error(f"Error launching transfer: {e}\nFailed transfer op: {op}")
@@ -324,6 +328,7 @@ class GPUCPUTransferWorker(TransferWorkerBase):
         self.cpu_kv_stride_in_bytes = cpu_kv_layout.get_kv_stride() * es
         self.cpu_block_stride_in_bytes = cpu_kv_layout.get_block_stride() * es
         self.transfer_stream = torch.cuda.Stream()
+        self._stream_handle = self.transfer_stream.cuda_stream
         self.transfer_sms_h2d = transfer_sms_h2d
         self.transfer_sms_d2h = transfer_sms_d2h
         self.use_ce_transfer_h2d = use_ce_transfer_h2d
@@ -360,24 +365,28 @@ class GPUCPUTransferWorker(TransferWorkerBase):
                 gpu_id_t, ptrs, self.gpu_block_stride_in_bytes, cpu_id_t, self.cpu_tensor,
                 self.cpu_kv_stride_in_bytes, self.cpu_layer_stride_in_bytes,
                 self.cpu_block_stride_in_bytes, self.chunk_size_in_bytes, layer_id, sms,
-                transfer_type == TransferType.H2D, use_ce, self.is_mla)
+                transfer_type == TransferType.H2D, use_ce, self.is_mla,
+                stream=kwargs.get("stream"))
             return
         layer_ptrs = self.gpu_layer_ptrs[layer_id:layer_id + layer_granularity]
         transfer_kv_blocks(gpu_id_t, layer_ptrs, self.gpu_kv_stride_in_bytes,
                            self.gpu_block_stride_in_bytes, cpu_id_t, self.cpu_tensor,
                            self.cpu_kv_stride_in_bytes, self.cpu_layer_stride_in_bytes,
                            self.cpu_block_stride_in_bytes, self.chunk_size_in_bytes, layer_id,
-                           sms, transfer_type == TransferType.H2D, use_ce, self.is_mla)
+                           sms, transfer_type == TransferType.H2D, use_ce, self.is_mla,
+                           stream=kwargs.get("stream"))
 
     def launch_transfer(self, transfer_op: WorkerTransferOp) -> None:
         layer_id = 0 if transfer_op.layer_id == -1 else transfer_op.layer_id
         granularity = self.num_layers if transfer_op.layer_granularity == -1 \
             else transfer_op.layer_granularity
-        with torch.cuda.stream(self.transfer_stream):
-            start = time.time()
-            self._transfer_impl(transfer_op.src_block_ids, transfer_op.dst_block_ids,
-                                transfer_op.transfer_type, layer_id, granularity)
-            end = time.time()
+        # the transfer runs on the worker's own stream (worker.py:323), passed
+        # to the call instead of made current for it
+        start = time.time()
+        self._transfer_impl(transfer_op.src_block_ids, transfer_op.dst_block_ids,
+                            transfer_op.transfer_type, layer_id, granularity,
+                            stream=self._stream_handle)
+        end = time.time()
         kv_dim = 1 if self.is_mla else 2
         size = self.chunk_size_in_bytes * granularity * len(transfer_op.src_block_ids) * kv_dim
         self._log_transfer_performance(transfer_op, size, start, end)

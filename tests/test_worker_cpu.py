@@ -76,9 +76,11 @@ def test_spawned_worker_process_lifecycle():
 class _Recorder:
     def __init__(self):
         self.calls = []
+        self.streams = []
 
-    def __call__(self, *args):
+    def __call__(self, *args, stream=None):
         self.calls.append(args)
+        self.streams.append(stream)
 
 
 def _bare_gpu_worker(monkeypatch, mla=False):
@@ -151,10 +153,12 @@ def test_launch_transfer_defaults(monkeypatch):
     w, rec = _bare_gpu_worker(monkeypatch, mla=True)
     monkeypatch.setattr(torch.cuda, "stream", lambda s: _NullCtx())
     w.transfer_stream = None
+    w._stream_handle = 0x1234                                   # the worker's own stream
     op = W.WorkerTransferOp(make_op(TransferType.D2H, layer_id=-1, gran=-1))
     w.launch_transfer(op)
     a = rec.calls[-1]
     assert a[10] == 0 and len(a[1]) == 8 and a[14] is True       # all layers, is_mla
+    assert rec.streams[-1] == 0x1234
 
 
 class _NullCtx:
