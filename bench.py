@@ -1101,7 +1101,8 @@ def counters_pass(args) -> int:
     """Kernels for `rocprofv3 --pmc` passes: the calibration copy first, so the
     per-dispatch counter of a copy of known size scales the others; then 3
     gathers, 3 scatters, 3 zero-copy D2H and 3 zero-copy H2D transfers of the
-    step's blocks."""
+    step's blocks, then one copy-engine D2H and one H2D (their gather and
+    scatter pieces)."""
     wl = Workload(args.workload, args.seed, args.run, host=True)
     cal = torch.empty(1 << 30, dtype=torch.uint8, device=wl.dev)
     cal_dst = torch.empty_like(cal)
@@ -1117,9 +1118,13 @@ def counters_pass(args) -> int:
     for h2d in (False, True):
         for _ in range(3):
             wl.transfer(h2d, False)
+    # one copy-engine D2H and one H2D: their gather and scatter pieces
+    for h2d in (False, True):
+        wl.transfer(h2d, True)
     torch.cuda.synchronize()
     print(json.dumps({"calibration_copy_bytes": cal.numel(), "gather_launches": 3,
                       "scatter_launches": 3, "d2h_launches": 3, "h2d_launches": 3,
+                      "copy_engine_transfers": 2,
                       "moved_bytes_per_launch": wl.bytes_per_op}), flush=True)
     return 0
 
