@@ -26,17 +26,20 @@ namespace {
 
 // SDMA engines each direction spreads its copies over.  Measured on MI355X
 // (16 engines) with 2 MiB copies: four move 56-57 GB/s either way, and
-// device-to-host drops to 47 GB/s on eight.  Host-to-device on eight engines
-// moves 256 KiB copies faster (55 against 42 GB/s on four), but compute
-// kernels running beside it then take twice as long (160 bf16 GEMMs: 65 ms
-// against 36 ms) and a D2H and an H2D together drop from 69 to 61 GB/s.
+// device-to-host drops to 47 GB/s on eight.  A D2H and an H2D together move
+// 69 GB/s on engines 0-3 and 4-7.
 constexpr int kDefaultSdmaEngines = 4;
+// Engines 0-7.  Host-to-device copies on engines 8-15 slow compute kernels
+// running beside them about twice over, at any copy size: 160 bf16 GEMMs
+// [8192x4096]x[4096x4096] took 1.85x / 2.0x their time beside a 56.6 GB/s
+// H2D on engines 6-11 / 8-15, against 1.07x on engines 4-7 (MI355X; D2H on
+// engines 0-7: 1.09-1.12x).
+constexpr uint32_t kComputeFriendlyEngines = 0xFFu;
 // Engines of the copy-engine layer-wise host-to-device pipeline, whose
-// engine copies are one block's layer group (64 KiB for one Llama-3-8B
-// layer): such copies are bound by the engines' per-copy cost, so more
-// engines help.  Measured on MI355X, one-layer calls of 1024 blocks: 20.5 /
-// 34.1 / 50.9 GB/s on 4 / 8 / 16 engines.
-constexpr int kDefaultLayerwiseEngines = 12;
+// smaller windows' engine copies (one block's layer group: 64 KiB for one
+// Llama-3-8B layer) are bound by the engines' per-copy cost, so more engines
+// help; taken from engines 0-7, host-to-device's own first.
+constexpr int kDefaultLayerwiseEngines = 8;
 constexpr int64_t kDefaultMaxCopyBytes = int64_t(4) << 20;
 
 // The HSA entry points the copy-engine path needs, resolved from the HSA
@@ -361,10 +364,11 @@ int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr) {
   if (g_hsa.agent_get_info(q.gpu, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_NEAREST_CPU),
                            &nearest) == HSA_STATUS_SUCCESS && nearest.handle != 0)
     q.cpu = nearest;
-  // Each direction takes `want` engines; host-to-device skips the engines
-  // device-to-host took while enough others remain, so the two directions
-  // run side by side on disjoint engines (MI355X: 69 GB/s in both
-  // directions together on engines 0-3 and 4-7, 56-57 GB/s one way).
+  // Each direction takes `want` engines, from engines 0-7 first;
+  // host-to-device takes those device-to-host did not take before those it
+  // did, so with the default four the two directions run side by side on
+  // disjoint engines (MI355X: 69 GB/s in both directions together on
+  // engines 0-3 and 4-7, 56-57 GB/s one way).
   const int want = sdma_engines_wanted();
   if (want == 0) return fail(kInval, "copy engines turned off (FLEXKV_SDMA_ENGINES=0)");
   uint32_t taken = 0;
@@ -372,30 +376,38 @@ int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr) {
     uint32_t mask = 0;
     FKV_HSA(dir == 0 ? g_hsa.copy_engine_status(q.cpu, q.gpu, &mask)
                      : g_hsa.copy_engine_status(q.gpu, q.cpu, &mask));
-    if (__builtin_popcount(mask & ~taken) >= want) mask &= ~taken;
     d.engines[dir].clear();
-    for (int b = 0; b < 32 && static_cast<int>(d.engines[dir].size()) < want; ++b)
-      if (mask & (1u << b)) {
-        d.engines[dir].push_back(static_cast<hsa_amd_sdma_engine_id_t>(1u << b));
-        taken |= 1u << b;
-      }
+    const uint32_t tiers[3] = {mask & kComputeFriendlyEngines & ~taken,
+                               mask & kComputeFriendlyEngines & taken,
+                               mask & ~kComputeFriendlyEngines};
+    for (uint32_t tier : tiers)
+      for (int b = 0; b < 32 && static_cast<int>(d.engines[dir].size()) < want; ++b)
+        if (tier & (1u << b)) {
+          d.engines[dir].push_back(static_cast<hsa_amd_sdma_engine_id_t>(1u << b));
+          taken |= 1u << b;
+        }
     if (d.engines[dir].empty())
       return fail(kInval, "device %d reports no SDMA engine for %s copies", dev,
                   dir == 0 ? "device-to-host" : "host-to-device");
   }
   {
-    // the layer-wise pipeline's set: host-to-device engines device-to-host
-    // did not take
+    // the layer-wise pipeline's set, in order of preference: host-to-device
+    // engines among 0-7 that device-to-host did not take, then those it
+    // took, then (only when more are asked for) the others
     const char* e = getenv("FLEXKV_SDMA_ENGINES_LAYERWISE");
     const int wide = std::max(1, std::min(e ? atoi(e) : kDefaultLayerwiseEngines, 32));
     uint32_t mask = 0;
     FKV_HSA(g_hsa.copy_engine_status(q.gpu, q.cpu, &mask));
     uint32_t d2h_taken = 0;
     for (hsa_amd_sdma_engine_id_t id : d.engines[0]) d2h_taken |= static_cast<uint32_t>(id);
-    if (__builtin_popcount(mask & ~d2h_taken) >= 1) mask &= ~d2h_taken;
     d.engines_wide.clear();
-    for (int b = 0; b < 32 && static_cast<int>(d.engines_wide.size()) < wide; ++b)
-      if (mask & (1u << b)) d.engines_wide.push_back(static_cast<hsa_amd_sdma_engine_id_t>(1u << b));
+    const uint32_t tiers[3] = {mask & kComputeFriendlyEngines & ~d2h_taken,
+                               mask & kComputeFriendlyEngines & d2h_taken,
+                               mask & ~kComputeFriendlyEngines};
+    for (uint32_t tier : tiers)
+      for (int b = 0; b < 32 && static_cast<int>(d.engines_wide.size()) < wide; ++b)
+        if (tier & (1u << b))
+          d.engines_wide.push_back(static_cast<hsa_amd_sdma_engine_id_t>(1u << b));
     if (d.engines_wide.empty()) d.engines_wide = d.engines[1];
   }
   d.gpu_agent = q.gpu;

@@ -156,6 +156,14 @@ constexpr int kAutoLayerwiseH2DCus = 2;
 // copy, worth handing to the SDMA engines (ce_pays_off).
 constexpr int64_t kCeMinBytesDefault = int64_t(8) << 20;
 constexpr int64_t kCeMinRunBytes = int64_t(128) << 10;
+// Default smallest engine copy per block of the copy-engine layer-wise
+// pipeline (see layerwise_min_copy_bytes).  Measured on MI355X, Llama-3-8B
+// one-layer groups (64 KiB per block), 1024 random blocks, 8 engines: 21 /
+// 33 / 42 / 49 / 51 GB/s with windows up to 64 KiB / 128 KiB / 256 KiB /
+// 512 KiB / 1 MiB per block; per-layer GEMMs overlapped with it end within
+// 0.2 / 0.0 / 1.1 / 11.9 / 10.3% of the transfer plus one layer's compute,
+// GEMMs beside it slow by 8-9% throughout.
+constexpr int64_t kLayerwiseCeMinCopyBytes = int64_t(256) << 10;
 // Average host run (bytes per (layer, K|V) run of consecutive blocks) from
 // which a layer-wise host cache is staged layer-major and copied run by run
 // instead of one rect copy per block.  Measured on MI355X at the Llama-3-8B
@@ -1046,6 +1054,15 @@ bool layerwise_ce_fits(const Geometry& g, int dev, bool h2d, int granularity) {
   return (g.kv == 1 || g.cks == g.chunk) && (nl == 1 || g.cls == g.kv * g.chunk);
 }
 
+// Smallest engine copy per block the copy-engine layer-wise pipeline aims for
+// (bytes; FLEXKV_LAYERWISE_CE_MIN_COPY_BYTES), by carrying several layer
+// groups in one window.  0 or 1: one group per window.
+size_t layerwise_min_copy_bytes() {
+  const char* e = getenv("FLEXKV_LAYERWISE_CE_MIN_COPY_BYTES");
+  const long long v = e ? atoll(e) : static_cast<long long>(kLayerwiseCeMinCopyBytes);
+  return v > 0 ? static_cast<size_t>(v) : 1;
+}
+
 // The lane's pipeline stream: a stream with a full CU mask, so it has a
 // hardware queue of its own and its scatters never wait behind compute
 // kernels queued on a shared queue.
@@ -1090,22 +1107,44 @@ int layerwise_ce_run(fkv_transfer_handle_s* h, CopyLane& ln, hipStream_t work) {
   if ((rc = ensure_sdma(d, h->dev, ln.staging))) return rc;
   const size_t half = ln.staging_bytes / 2;
   struct Piece {
-    int l0, nl, b0, nb, group;
+    int l0, nl, b0, nb, group;   // group: the last layer group the piece completes
     bool last;
   };
+  // Consecutive groups share engine copies when a block's rows of several
+  // layers are contiguous in host memory: a full window carries at least
+  // layerwise_min_copy_bytes() per block, which the engines move faster than
+  // one-group copies.  Every group's event is recorded when the window
+  // holding it has landed.  Windows grow from one group (1, 2, 4, ...), so
+  // the first group arrives early, and near the end hold at most half of the
+  // groups left, so the compute a window releases ends while the rest
+  // arrive: a consumer that keeps up waits for one group's compute after the
+  // last transfer, as with one group per window.
+  const int lpl = g.layers_per_launch();
+  const int ngroups = (g.num_layers + G - 1) / G;
+  const size_t group_row = static_cast<size_t>(std::min(G, g.num_layers)) * g.kv * g.chunk;
+  const size_t min_copy = layerwise_min_copy_bytes();
+  int gpw = 1;   // groups per window
+  if (G <= lpl && g.cls == static_cast<int64_t>(g.kv) * g.chunk) {
+    gpw = static_cast<int>(std::max<size_t>(1, (min_copy + group_row - 1) / group_row));
+    gpw = std::max(1, std::min(gpw, lpl / G));
+    while (gpw > 1 && static_cast<size_t>(gpw) * group_row > half) --gpw;
+  }
   std::vector<Piece> pieces;
-  for (int grp = 0, l0 = 0; l0 < g.num_layers; ++grp, l0 += G) {
-    const int nl = std::min(G, g.num_layers - l0);
-    // a group moves in layer windows whose block rows fit a staging half and
-    // whose layer pointers fit one launch's kernel arguments
-    int win = std::min(nl, g.layers_per_launch());
+  for (int grp = 0, ramp = 1; grp < ngroups; ramp = std::min(2 * ramp, gpw)) {
+    const int take = std::min({gpw, ramp, std::max(1, (ngroups - grp) / 2)});
+    const int l0 = grp * G;
+    const int nl = std::min(take * G, g.num_layers - l0);
+    grp += take;
+    // a window moves in layer windows whose block rows fit a staging half
+    // and whose layer pointers fit one launch's kernel arguments
+    int win = std::min(nl, lpl);
     while (win > 1 && static_cast<size_t>(win) * g.kv * g.chunk > half) win = (win + 1) / 2;
     for (int w0 = l0; w0 < l0 + nl; w0 += win) {
       const int wn = std::min(win, l0 + nl - w0);
       const size_t row = static_cast<size_t>(wn) * g.kv * g.chunk;
       const int bpp = static_cast<int>(std::max<size_t>(1, half / row));
       for (int b0 = 0; b0 < g.num_blocks; b0 += bpp)
-        pieces.push_back({w0, wn, b0, std::min(bpp, g.num_blocks - b0), grp, false});
+        pieces.push_back({w0, wn, b0, std::min(bpp, g.num_blocks - b0), grp - 1, false});
     }
     pieces.back().last = true;
   }
@@ -1113,6 +1152,7 @@ int layerwise_ce_run(fkv_transfer_handle_s* h, CopyLane& ln, hipStream_t work) {
   const int grid_cap = d.num_cus * d.occ_staged[1];
   std::vector<Run> runs;
   bool pending[2] = {false, false};
+  int next_group = 0;   // the first group whose event is not yet recorded
   int64_t dma_copies = 0, dma_bytes = 0;
   const auto t0 = std::chrono::steady_clock::now();
   DrainOnError drain{work, &d, &ln};
@@ -1122,8 +1162,13 @@ int layerwise_ce_run(fkv_transfer_handle_s* h, CopyLane& ln, hipStream_t work) {
     for (const Run& r : runs) dma_bytes += r.bytes;
     dma_copies += static_cast<int64_t>(runs.size());
     pending[pi & 1] = true;
+    // Windows below the full copy size are bound by the engines' per-copy
+    // cost and spread over the wide engine set; full windows keep to the
+    // direction's own engines, which move them at the link's rate while
+    // slowing the kernels beside them least.
+    const bool wide = static_cast<size_t>(p.nl) * g.kv * g.chunk < min_copy;
     return issue_sdma(d, ln, runs, ln.staging + (pi & 1) * half, true, pi & 1, d.cpu_agent,
-                      /*wide=*/true);
+                      wide);
   };
   for (int pi = 0; pi < std::min(np, 2); ++pi)
     if ((rc = queue_copies(pi))) return rc;
@@ -1142,9 +1187,10 @@ int layerwise_ce_run(fkv_transfer_handle_s* h, CopyLane& ln, hipStream_t work) {
                                       p.nb, p.l0, p.nl, grid_cap, work, h->prof)))
       return rc;
     if (p.last) {
-      FKV_HIP(hipEventRecord(h->done[p.group], work));
+      for (int gi = next_group; gi <= p.group; ++gi) FKV_HIP(hipEventRecord(h->done[gi], work));
+      next_group = p.group + 1;
       std::lock_guard<std::mutex> lk(h->mu);
-      h->recorded = p.group + 1;
+      h->recorded = next_group;
       h->cv.notify_all();
     }
     if (pi + 2 < np) {

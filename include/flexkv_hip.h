@@ -40,13 +40,16 @@ enum {
   /* Copy-engine path: a gather kernel packs the selected chunks into a
    * contiguous HBM staging buffer and the SDMA engines move maximal
    * contiguous host runs (D2H); H2D is SDMA into staging followed by a
-   * scatter kernel.  A layer-wise host cache is served with one SDMA rect
-   * copy per block, or, when its ids come in runs of consecutive blocks,
-   * with one copy per (layer, K|V) run from layer-major staging.  Staging is
+   * scatter kernel.  A layer-wise host cache whose ids come in runs of
+   * consecutive blocks is served with one copy per (layer, K|V) run from
+   * layer-major staging; with scattered ids it moves with the zero-copy
+   * kernel, since the runtime runs the one SDMA rect copy per block such a
+   * transfer needs on a single engine (FLEXKV_CE_RECT_COPIES=1 keeps it on
+   * the engines; a transfer of rect copies runs alone).  Staging is
    * double-buffered; the PCIe copies take no compute units.  Each direction
    * has its own staging and engines, so a D2H and an H2D transfer from
-   * different threads run at the same time (a transfer of rect copies runs
-   * alone).  Transfers under FLEXKV_CE_MIN_BYTES (default 8 MiB) or whose
+   * different threads run at the same time.  Transfers under
+   * FLEXKV_CE_MIN_BYTES (default 8 MiB) or whose
    * engine copies would move under 128 KiB each move with the zero-copy
    * kernel instead, where the engines' per-copy cost would dominate, and so
    * does every transfer on a device whose engines cannot be set up (one
@@ -178,11 +181,18 @@ int fkv_scatter_kv_blocks(int num_blocks, int num_layers, const int64_t* gpu_blo
  * transfer overlaps) and 8 for device-to-host.
  * use_ce_transfer = FKV_XFER_CE (host to device from block-wise host rows;
  * other transfers take the kernel): the copy engines, so the transfer holds
- * no compute unit while its bytes cross the link.  A library thread queues
- * each group's SDMA copies (one per block, on up to
- * FLEXKV_SDMA_ENGINES_LAYERWISE engines, default 12) into double-buffered
- * staging and, once they have landed, the group's scatter on a library stream
- * with a hardware queue of its own; the group's event is recorded there.
+ * no compute unit while its bytes cross the link.  A library thread moves
+ * windows of consecutive groups: one SDMA copy per block and window into
+ * double-buffered staging, then, once they have landed, the window's
+ * scatter on a library stream with a hardware queue of its own, where the
+ * events of the window's groups are recorded.  Windows grow 1, 2, 4, ...
+ * groups up to FLEXKV_LAYERWISE_CE_MIN_COPY_BYTES per block (default
+ * 256 KiB) and near the end hold at most half of the groups left, so the
+ * first group arrives early and the compute a window releases ends while
+ * the rest arrive.  Windows below that size spread their copies over up to
+ * FLEXKV_SDMA_ENGINES_LAYERWISE engines (default 8, from engines 0-7:
+ * host-to-device copies on engines 8-15 slow compute kernels running beside
+ * them about twofold); full windows use the direction's own engines.
  * fkv_handle_stream_wait and fkv_handle_wait first wait on the host until
  * the group's event exists (its copies have landed), fkv_handle_query
  * reports 0 until then.

@@ -185,14 +185,47 @@ def test_transfer_stream_helper(num_cus):
     assert "num_cus" in _lib.last_error()
 
 
-@pytest.mark.parametrize("staging_kib,gran", [(0, 1), (256, 1), (256, 3), (96, 2)])
-def test_ce_pipeline_pieces_and_copies(staging_kib, gran):
+def _ce_copies_per_block(L, G, layer_row, half, min_copy, lpl=128):
+    """Engine copies per block the copy-engine layer-wise pipeline plans for a
+    block-wise host cache: windows of whole layer groups, up to `min_copy`
+    bytes per block, growing 1, 2, 4, ... groups and near the end holding at
+    most half of the groups left; each cut into layer windows whose rows fit
+    a staging half."""
+    ngroups = -(-L // G)
+    group_row = min(G, L) * layer_row
+    gpw = 1
+    if G <= lpl:
+        gpw = max(1, min(-(-min_copy // group_row), lpl // G))
+        while gpw > 1 and gpw * group_row > half:
+            gpw -= 1
+    copies, grp, ramp = 0, 0, 1
+    while grp < ngroups:
+        take = min(gpw, ramp, max(1, (ngroups - grp) // 2))
+        ramp = min(2 * ramp, gpw)
+        l0 = grp * G
+        nl = min(take * G, L - l0)
+        grp += take
+        win = min(nl, lpl)
+        while win > 1 and win * layer_row > half:
+            win = (win + 1) // 2
+        copies += -(-nl // win)
+    return copies
+
+
+@pytest.mark.parametrize("staging_kib,gran,min_copy",
+                         [(0, 1, None), (256, 1, None), (256, 3, None), (96, 2, None),
+                          (0, 1, 1), (0, 2, 64 << 10)])
+def test_ce_pipeline_pieces_and_copies(staging_kib, gran, min_copy, monkeypatch):
     """The copy-engine layer-wise pipeline with staging small enough that a
-    group spans several pieces, or a group's rows are cut into layer windows:
-    the blocks match the oracle, every group's event fires, and the engines
-    moved one copy per block and layer window (the library's profile)."""
+    group spans several pieces, or a group's rows are cut into layer windows,
+    and with several groups per engine copy: each group's layers match the
+    oracle as soon as that group alone is waited for, every group's event
+    fires, and the engines moved the planned copies per block (the library's
+    profile)."""
     from flexkv_amd import _lib
     from gpu_util import DeviceCase
+    if min_copy is not None:
+        monkeypatch.setenv("FLEXKV_LAYERWISE_CE_MIN_COPY_BYTES", str(min_copy))
     L, n = 6, 37
     case = KVCase(layers_total=L, num_layers=L, start_layer=0, kv=2, ng=64, nh=96, tokens=16,
                   heads=4, dim=64).fill(seed=60 + gran)              # 8 KiB chunks
@@ -203,31 +236,33 @@ def test_ce_pipeline_pieces_and_copies(staging_kib, gran):
     fresh = case.host ^ np.uint16(0x1E1E)
     dc.set_host(fresh)
     dc.set_gpu([np.zeros_like(g) for g in case.gpu])
+    exp = [np.zeros_like(g) for g in case.gpu]
+    oracle.transfer_kv_blocks(gids, exp, s["gpu_kv"], s["gpu_block"], cids, fresh, s["cpu_kv"],
+                              s["cpu_layer"], s["cpu_block"], s["chunk"], 0, True)
     _lib.set_staging_bytes(staging_kib << 10)
     try:
         _lib.profile_enable(True)
         with _abi_layerwise(dc, gids.copy(), cids.copy(), True, gran, ce=True) as hnd:
             assert hnd.num_groups == -(-L // gran)
-            for g in reversed(range(hnd.num_groups)):
+            for g in range(hnd.num_groups):
                 hnd.wait(g)
+                got = dc.gpu_np()
+                for l in range(g * gran, min(L, (g + 1) * gran)):
+                    assert np.array_equal(got[l], exp[l]), (g, l)
         prof = _lib.profile_read()
         _lib.profile_enable(False)
     finally:
         _lib.set_staging_bytes(0)
         _lib.release_staging()
-    exp = [np.zeros_like(g) for g in case.gpu]
-    oracle.transfer_kv_blocks(gids, exp, s["gpu_kv"], s["gpu_block"], cids, fresh, s["cpu_kv"],
-                              s["cpu_layer"], s["cpu_block"], s["chunk"], 0, True)
     for got, e in zip(dc.gpu_np(), exp):
         assert np.array_equal(got, e)
     assert prof["dma_batches"] == 1, prof
     half = (staging_kib << 9) if staging_kib else 1 << 29
-    # windows a group is cut into when its rows do not fit a half
-    win = gran
-    while win > 1 and win * 2 * s["chunk"] > half:
-        win = (win + 1) // 2
-    windows = sum(-(-min(gran, L - l0) // win) for l0 in range(0, L, gran))
-    assert prof["dma_copies"] == windows * n, (prof, windows)
+    per_block = _ce_copies_per_block(L, gran, 2 * s["chunk"], half,
+                                     256 << 10 if min_copy is None else min_copy)
+    assert prof["dma_copies"] == per_block * n, (prof, per_block)
+    if min_copy == 1:
+        assert per_block == L // gran       # one copy per block and group
 
 
 def test_ce_handle_stream_wait_and_query_before_arrival():
