@@ -65,6 +65,23 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def release_device_memory() -> None:
+    """Return torch's cached device memory to the driver, then wait while
+    the driver clears it.  The amdgpu driver clears freed VRAM in the
+    background on a copy engine that device-to-host copies share: on MI355X
+    copy-engine D2H ran at 15.5 GB/s instead of 46 GB/s for 630 ms after a
+    16 GiB free and 157 ms after a 4 GiB free (about 26 GB/s of clearing),
+    which would be charged to whatever is measured next."""
+    import gc
+    gc.collect()
+    before = torch.cuda.memory_reserved()
+    torch.cuda.empty_cache()
+    freed = max(0, before - torch.cuda.memory_reserved())
+    torch.cuda.synchronize()
+    if freed:
+        time.sleep(0.05 + freed / 20e9)
+
+
 class Workload:
     def __init__(self, name: str, seed: int, run: int = 0, host: bool = True,
                  host_layout: str = "BLOCKWISE"):
@@ -239,7 +256,7 @@ def link_peaks(wl: Workload, reps: int = 8):
         best = max(best, 2 * big.numel() / (a.elapsed_time(b) * 1e-3) / 1e9)
     res["d2d_copy_read_plus_write"] = best
     del big, big2, dbuf
-    torch.cuda.empty_cache()
+    release_device_memory()
     return res
 
 
@@ -799,7 +816,7 @@ def standalone_gather(wl: Workload, steps: int):
         out[f"{name}_gbps_hbm"] = round(rate, 1)
         out[f"{name}_frac_hbm"] = round(rate / HBM_PEAK_GBS, 4)
     del buf
-    torch.cuda.empty_cache()
+    release_device_memory()
     return out
 
 
@@ -830,14 +847,13 @@ def fragmentation_sweep(wl: Workload, steps: int, peaks: dict):
 
 
 def other_workload(name: str, args, peaks: dict, host_layout: str = "BLOCKWISE",
-                   rect_copies: bool = False, wl: "Workload | None" = None):
+                   rect_copies: bool = False):
     """Configs 3 and 4, and config 1 on a layer-wise host cache: a workload of
-    its own (allocated here unless given, freed on return) through both
-    paths, the device gather/scatter in one launch, bit-exact round trips;
-    MLA adds the per-request / batched request mix."""
+    its own (allocated here, freed on return) through both paths, the device
+    gather/scatter in one launch, bit-exact round trips; MLA adds the
+    per-request / batched request mix."""
     import gc
-    if wl is None:
-        wl = Workload(name, args.seed, host_layout=host_layout)
+    wl = Workload(name, args.seed, host_layout=host_layout)
     try:
         out = {"workload": WORKLOADS[name]["desc"] +
                ("" if host_layout == "BLOCKWISE" else f"; {host_layout.lower()} host cache"),
@@ -859,7 +875,7 @@ def other_workload(name: str, args, peaks: dict, host_layout: str = "BLOCKWISE",
     finally:
         del wl
         gc.collect()
-        torch.cuda.empty_cache()
+        release_device_memory()
 
 
 def disk_ceilings(d: str, nbytes: int):
@@ -1148,23 +1164,21 @@ def configs_on_step(args, wl: Workload, peaks: dict, result: dict) -> dict:
     return cfg
 
 
-def other_configs(args, peaks: dict, cfg: dict, early: dict) -> dict:
-    """The configurations with tensors of their own, each freed in turn: the
-    CPU plumbing shape (allocated by the caller before any host cache was
-    freed, handed over in `early` and dropped from it here), Llama-3-8B on
-    a layer-wise host cache, the Llama-3-70B TP-8 shard and the DeepSeek-V3
-    MLA latent cache with its request mix.  Every entry
-    of the benchmark set (with configs_on_step's) gives GB/s on both paths
-    with fractions of the measured link and of nominal PCIe Gen5 x16, the
-    copy-engine path's gather/scatter piece rates, the device gather/scatter
-    in one launch, and a bit-exact round trip."""
+def other_configs(args, peaks: dict, cfg: dict) -> dict:
+    """The configurations with tensors of their own, each allocated and freed
+    in turn: the CPU plumbing shape, Llama-3-8B on a layer-wise host cache,
+    the Llama-3-70B TP-8 shard and the DeepSeek-V3 MLA latent cache with its
+    request mix.  Every entry of the benchmark set (with configs_on_step's)
+    gives GB/s on both paths with fractions of the measured link and of
+    nominal PCIe Gen5 x16, the copy-engine path's gather/scatter piece rates,
+    the device gather/scatter in one launch, and a bit-exact round trip."""
     t0 = time.perf_counter()
     for key, name, layout, rect in (("cfg0_plumbing", "plumbing", "BLOCKWISE", False),
                                     ("cfg1_llama3-8b_layerwise_host", "llama3-8b", "LAYERWISE",
                                      True),
                                     ("cfg3_llama3-70b-tp8", "llama3-70b-tp8", "BLOCKWISE", False),
                                     ("cfg4_mla-dsv3", "mla-dsv3", "BLOCKWISE", False)):
-        cfg[key] = other_workload(name, args, peaks, layout, rect, early.pop(name, None))
+        cfg[key] = other_workload(name, args, peaks, layout, rect)
         log(f"{key}: {cfg[key]}")
     cfg["bit_exact"] = all(v.get("bit_exact", True) for v in cfg.values()
                            if isinstance(v, dict)) and all(
@@ -1220,12 +1234,6 @@ def main() -> int:
     default_ce = {"kernel": False, "ce": True}[args.path] if args.path else cfg.use_ce_transfer_d2h
     all_configs = (args.workload == "llama3-8b" and not args.run and args.host_layout == "BLOCKWISE"
                    and not (args.quick or args.layerwise_only or args.worker_ops))
-    # The plumbing shape's 128 MiB host cache is allocated first, as a serving
-    # process allocates its cache once at start: on MI355X, copy-engine writes
-    # into a small pinned buffer whose pages come straight back from freeing
-    # a 32 GiB pinned cache ran at 15 GB/s against 43 GB/s into fresh pages
-    # (256 KiB copies; host-to-device and the zero-copy kernel unaffected).
-    early = {"plumbing": Workload("plumbing", args.seed)} if all_configs else {}
     wl = Workload(args.workload, args.seed, args.run, host_layout=args.host_layout)
     gb = wl.bytes_per_op / 1e9
     if args.layerwise_only:
@@ -1268,7 +1276,7 @@ def main() -> int:
     _lib.profile_enable(False)
     gather_ok = bool(torch.equal(buf.view(torch.int16), wl.packed_expected().view(torch.int16)))
     del buf
-    torch.cuda.empty_cache()
+    release_device_memory()
 
     def kernel_rate(prof):
         launches = max(1, prof["kernel_launches"])
@@ -1423,8 +1431,8 @@ def main() -> int:
             cfg = configs_on_step(args, wl, peaks, result)
             del wl
             gc.collect()
-            torch.cuda.empty_cache()
-            result["configs"] = other_configs(args, peaks, cfg, early)
+            release_device_memory()
+            result["configs"] = other_configs(args, peaks, cfg)
             parity = parity and result["configs"]["bit_exact"]
             result["bit_exact"] = result["bit_exact"] and result["configs"]["bit_exact"]
 
