@@ -855,9 +855,13 @@ def other_workload(name: str, args, peaks: dict, host_layout: str = "BLOCKWISE",
     import gc
     wl = Workload(name, args.seed, host_layout=host_layout)
     try:
-        out = {"workload": WORKLOADS[name]["desc"] +
-               ("" if host_layout == "BLOCKWISE" else f"; {host_layout.lower()} host cache"),
-               "bytes_per_step": wl.bytes_per_op}
+        desc = WORKLOADS[name]["desc"]
+        if host_layout != "BLOCKWISE":
+            w = WORKLOADS[name]
+            left, ids = desc.split(" <-> ")[0], desc.split("; ", 1)[1]
+            desc = (f"{left} <-> pinned layer-wise host [{w['layers']},{w['kv']},{w['nh']},"
+                    f"{w['tokens']},{w['heads']},{w['dim']}]; {ids}")
+        out = {"workload": desc, "bytes_per_step": wl.bytes_per_op}
         steps = max(3, args.steps // 2)
         out.update(path_rates(wl, steps, peaks))
         if rect_copies:
