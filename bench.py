@@ -1085,21 +1085,28 @@ def cpu_baseline(wl: Workload, budget_s: float):
     return threads, out
 
 
-def source_sha16(path: str) -> str:
+KERNEL_SOURCE = os.path.join(ROOT, "flexkv_amd", "csrc", "kv_transfer.hip")
+# The kernel section of KERNEL_SOURCE ends where the next definition begins.
+KERNEL_SECTION_END = b"// A system-scope acquire in every workgroup."
+
+
+def kernel_section_sha16(path: str = KERNEL_SOURCE) -> str:
+    """sha256 prefix of the transfer kernel's source: kv_transfer.hip from its
+    start (build macros, CopyArgs) to the end of kv_chunk_copy_kernel, the
+    part that decides which bytes the kernel reads and writes."""
     import hashlib
     with open(path, "rb") as fh:
-        return hashlib.sha256(fh.read()).hexdigest()[:16]
-
-
-KERNEL_SOURCE = os.path.join(ROOT, "flexkv_amd", "csrc", "kv_transfer.hip")
+        text = fh.read()
+    end = text.find(KERNEL_SECTION_END)
+    return hashlib.sha256(text if end < 0 else text[:end]).hexdigest()[:16]
 
 
 def measured_traffic(workload: str, run: int, alg_bytes: int) -> dict:
     """HBM bytes per gather launch from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE passes (calibrated against a plain 1 GiB copy), when they were
     taken on this workload, this launch size and this kernel source (the
-    profile records the sha of kv_transfer.hip it was taken with); else
-    null, with the reason."""
+    profile records the sha of the kernel section of kv_transfer.hip it was
+    taken with); else null, with the reason."""
     path = os.path.join(ROOT, "profiles", f"kv_gather_{workload}_counters.json")
     rel = os.path.relpath(path, ROOT)
     if run or not os.path.exists(path):
@@ -1109,13 +1116,13 @@ def measured_traffic(workload: str, run: int, alg_bytes: int) -> dict:
     g = prof["gather"]
     if g["algorithmic_bytes_per_launch"] != alg_bytes:
         return {"bytes": None, "source": f"{rel} was taken at another launch size"}
-    want = source_sha16(KERNEL_SOURCE)
-    if prof.get("kv_transfer_sha16") != want:
-        return {"bytes": None, "source": f"{rel} was taken with another kv_transfer.hip "
-                                         f"({prof.get('kv_transfer_sha16')} != {want})"}
+    want = kernel_section_sha16()
+    if prof.get("kernel_sha16") != want:
+        return {"bytes": None, "source": f"{rel} was taken with another transfer kernel "
+                                         f"({prof.get('kernel_sha16')} != {want})"}
     return {"bytes": g["traffic_bytes_per_launch"],
             "source": f"{rel} (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes of "
-                      f"bench.py --counters, kv_transfer.hip sha {want})"}
+                      f"bench.py --counters, transfer kernel sha {want})"}
 
 
 def counters_pass(args) -> int:

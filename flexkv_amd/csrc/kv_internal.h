@@ -97,7 +97,8 @@ struct DeviceState {
   bool init = false;
   int num_cus = 0;
   int occ_zero_copy[2] = {0, 0};
-  int occ_staged[2] = {0, 0};
+  int occ_staged[2] = {0, 0};   // row-by-row staging kernels, per direction
+  int occ_whole[2] = {0, 0};    // whole-group staging kernels, per direction
   // Copy engines: the HSA agents of this GPU and of the host and the SDMA
   // engines each direction pins its copies to (disjoint sets where the device
   // has enough engines).

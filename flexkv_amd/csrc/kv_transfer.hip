@@ -156,6 +156,11 @@ constexpr int kAutoLayerwiseH2DCus = 2;
 // copy, worth handing to the SDMA engines (ce_pays_off).
 constexpr int64_t kCeMinBytesDefault = int64_t(8) << 20;
 constexpr int64_t kCeMinRunBytes = int64_t(128) << 10;
+// The piece of a copy-engine transfer that runs without engine copies beside
+// it (the first gather, the last scatter) is cut to 1 / kEdgePieceDiv of a
+// staging half when it moves at least kEdgePieceMinBytes.
+constexpr int kEdgePieceDiv = 8;
+constexpr int64_t kEdgePieceMinBytes = int64_t(128) << 20;
 // Default smallest engine copy per block of the copy-engine layer-wise
 // pipeline (see layerwise_min_copy_bytes).  Measured on MI355X, Llama-3-8B
 // one-layer groups (64 KiB per block), 1024 random blocks, 8 engines: 21 /
@@ -464,9 +469,9 @@ __global__ __launch_bounds__(64) void acquire_system_kernel() {
 
 std::mutex g_init_mu;
 
-template <bool H, bool I>
+template <bool H, bool I, bool W = false>
 void* kernel_ptr() {
-  return reinterpret_cast<void*>(&kv_chunk_copy_kernel<H, I>);
+  return reinterpret_cast<void*>(&kv_chunk_copy_kernel<H, I, W>);
 }
 
 int ensure_device_basics(int dev) {
@@ -483,6 +488,12 @@ int ensure_device_basics(int dev) {
   d.occ_staged[0] = std::max(1, o);
   FKV_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, kernel_ptr<true, true>(), kThreads, 0));
   d.occ_staged[1] = std::max(1, o);
+  FKV_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, kernel_ptr<false, true, true>(),
+                                                       kThreads, 0));
+  d.occ_whole[0] = std::max(1, o);
+  FKV_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, kernel_ptr<true, true, true>(),
+                                                       kThreads, 0));
+  d.occ_whole[1] = std::max(1, o);
   d.init = true;
   return 0;
 }
@@ -559,11 +570,14 @@ void choose_tiles(int nb, int nl, int kv, int rpc, int grid_cap, int factor, int
 // `ids` holds the packed pairs: `host` for the host's view, `dev` for the
 // device's (the same pinned buffer).  With `split` > 0, `dev` instead holds
 // the gpu ids and, `split` entries later, the cpu ids (device memory), and
-// `host` is null.
+// `host` is null.  `grid_cap` is compute units x occupancy of the kernel the
+// launch takes; staging launches that take the whole-group variant use
+// `whole_grid_cap` instead when it is given.
 template <bool kH2D, bool kIota>
 int launch_copy(const Geometry& g, const IdBuf& ids, char* cpu_base, int64_t cks, int64_t cls,
                 int64_t cbs, int b0, int nb, int l0, int nl, int grid_cap,
-                hipStream_t stream, ProfRecorder& prof, int32_t split = 0) {
+                hipStream_t stream, ProfRecorder& prof, int32_t split = 0,
+                int whole_grid_cap = 0) {
   if (nl < 1 || static_cast<int64_t>(nl) * g.ptrs_per_layer > kMaxLayersPerLaunch)
     return fail(kInval, "internal: a launch of %d layers exceeds the %d layer pointers of the "
                 "kernel arguments", nl, kMaxLayersPerLaunch / g.ptrs_per_layer);
@@ -591,6 +605,17 @@ int launch_copy(const Geometry& g, const IdBuf& ids, char* cpu_base, int64_t cks
     a.layer_ptr[i] = reinterpret_cast<uint64_t>(g.layer_ptrs[l0 * g.ptrs_per_layer + i]);
   constexpr int kLaunchUnroll = kIota ? (kH2D ? FKV_UNROLL_SCATTER : kUnrollHbm)
                                      : (kH2D ? FKV_UNROLL_ZC_H2D : FKV_UNROLL_ZC_D2H);
+  // staging launches whose chunks are whole groups of full rows take the
+  // kernel variant that addresses each group from one base; its occupancy
+  // sizes the tiling
+  constexpr int kStagedUnroll = kH2D ? FKV_UNROLL_SCATTER : kUnrollHbm;
+  const bool whole_variant =
+      kH2D ? (FKV_WHOLE_SCATTER &&
+              static_cast<int64_t>(nb) * nl * g.kv * g.chunk <= kWholeScatterMaxBytes)
+           : FKV_WHOLE_GATHER;
+  const bool whole = kIota && whole_variant && a.chunk_vec % 64 == 0 &&
+                     a.rows_per_chunk % kStagedUnroll == 0;
+  if (whole && whole_grid_cap > 0) grid_cap = whole_grid_cap;
   choose_tiles(nb, nl, g.kv, a.rows_per_chunk, grid_cap,
                kIota ? (kH2D ? FKV_TILE_FACTOR_SCATTER : FKV_TILE_FACTOR_HBM) : FKV_TILE_FACTOR,
                kLaunchUnroll, /*balanced=*/kIota, &a);
@@ -600,15 +625,6 @@ int launch_copy(const Geometry& g, const IdBuf& ids, char* cpu_base, int64_t cks
   hipEvent_t ev = nullptr;
   if (prof.begin(stream, &ev)) return kInval;
   (void)hipGetLastError();  // a stale error from elsewhere must not be blamed on this launch
-  // staging launches whose chunks are whole groups of full rows take the
-  // kernel variant that addresses each group from one base
-  constexpr int kStagedUnroll = kH2D ? FKV_UNROLL_SCATTER : kUnrollHbm;
-  const bool whole_variant =
-      kH2D ? (FKV_WHOLE_SCATTER &&
-              static_cast<int64_t>(nb) * nl * g.kv * g.chunk <= kWholeScatterMaxBytes)
-           : FKV_WHOLE_GATHER;
-  const bool whole = kIota && whole_variant && a.chunk_vec % 64 == 0 &&
-                     a.rows_per_chunk % kStagedUnroll == 0;
   const unsigned lds = kIota ? FKV_HBM_LDS_PAD : 0;
   if (whole)
     hipLaunchKernelGGL((kv_chunk_copy_kernel<kH2D, kIota, kIota>), dim3(grid), dim3(kThreads), lds,
@@ -793,6 +809,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   const size_t half = ln.staging_bytes / 2;
   const int blocks_per_piece = static_cast<int>(std::max<size_t>(1, half / row_bytes));
   const int grid_cap = d.num_cus * (h2d ? d.occ_staged[1] : d.occ_staged[0]);
+  const int whole_cap = d.num_cus * (h2d ? d.occ_whole[1] : d.occ_whole[0]);
   const hsa_agent_t host_agent = d.cpu_agent;   // device-resident caches never get here
 
   struct Piece {
@@ -803,6 +820,25 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
     for (int b0 = 0; b0 < g.num_blocks; b0 += blocks_per_piece)
       pieces.push_back({l0, std::min(nl_piece, g.num_layers - l0), b0,
                         std::min(blocks_per_piece, g.num_blocks - b0)});
+  // The first piece's gather (D2H) and the last piece's scatter (H2D) run
+  // with no engine copies beside them.  When that piece is large, an eighth
+  // of a half is cut off it, so the engines start, or the transfer ends,
+  // after a short kernel; smaller pieces are not cut, since every piece costs
+  // a host round trip.
+  if (!pieces.empty()) {
+    const size_t edge = h2d ? pieces.size() - 1 : 0;
+    const Piece p = pieces[edge];
+    const int64_t bytes = static_cast<int64_t>(p.nb) * p.nl * g.kv * g.chunk;
+    const int cut = std::min(p.nb - 1, std::max(1, blocks_per_piece / kEdgePieceDiv));
+    if (bytes >= kEdgePieceMinBytes && cut >= 1) {
+      Piece first = p, second = p;
+      first.nb = h2d ? p.nb - cut : cut;
+      second.b0 = p.b0 + first.nb;
+      second.nb = p.nb - first.nb;
+      pieces[edge] = first;
+      pieces.insert(pieces.begin() + static_cast<std::ptrdiff_t>(edge) + 1, second);
+    }
+  }
   const int np = static_cast<int>(pieces.size());
 
   // Host-side waits order everything below against the caller's stream, so
@@ -838,9 +874,9 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
     }
     char* stg = ln.staging + (pi & 1) * half;
     return h2d ? launch_copy<true, true>(g, ids.buf, stg, cks, cls, cbs, p.b0, p.nb, p.l0, p.nl,
-                                         grid_cap, stream, prof)
+                                         grid_cap, stream, prof, 0, whole_cap)
                : launch_copy<false, true>(g, ids.buf, stg, cks, cls, cbs, p.b0, p.nb, p.l0, p.nl,
-                                          grid_cap, stream, prof);
+                                          grid_cap, stream, prof, 0, whole_cap);
   };
   if (!h2d) {
     for (int pi = 0; pi < np; ++pi) {
@@ -897,6 +933,7 @@ int transfer_contiguous(const Geometry& g, hipStream_t stream, int dev, bool to_
   int rc = pack_ids(g, ids);
   if (rc) return rc;
   const int grid_cap = d.num_cus * (to_gpu ? d.occ_staged[1] : d.occ_staged[0]);
+  const int whole_cap = d.num_cus * (to_gpu ? d.occ_whole[1] : d.occ_whole[0]);
   DrainOnError drain{stream};
   ProfRecorder prof;
   const int per_launch = g.layers_per_launch();
@@ -904,9 +941,9 @@ int transfer_contiguous(const Geometry& g, hipStream_t stream, int dev, bool to_
     const int nl = std::min(per_launch, g.num_layers - l0);
     char* base = g.cpu_info.dev_ptr + static_cast<int64_t>(l0) * g.cls;
     rc = to_gpu ? launch_copy<true, true>(g, ids.buf, base, g.cks, g.cls, g.cbs, 0, g.num_blocks,
-                                          l0, nl, grid_cap, stream, prof)
+                                          l0, nl, grid_cap, stream, prof, 0, whole_cap)
                 : launch_copy<false, true>(g, ids.buf, base, g.cks, g.cls, g.cbs, 0, g.num_blocks,
-                                           l0, nl, grid_cap, stream, prof);
+                                           l0, nl, grid_cap, stream, prof, 0, whole_cap);
     if (rc) return rc;
   }
   FKV_HIP(hipStreamSynchronize(stream));
@@ -1207,6 +1244,7 @@ int layerwise_ce_run(fkv_transfer_handle_s* h, CopyLane& ln, hipStream_t work) {
   }
   const int np = static_cast<int>(pieces.size());
   const int grid_cap = d.num_cus * d.occ_staged[1];
+  const int whole_cap = d.num_cus * d.occ_whole[1];
   std::vector<Run> runs;
   bool pending[2] = {false, false};
   int next_group = 0;   // the first group whose event is not yet recorded
@@ -1241,7 +1279,8 @@ int layerwise_ce_run(fkv_transfer_handle_s* h, CopyLane& ln, hipStream_t work) {
     const int64_t cbs = static_cast<int64_t>(p.nl) * cls;
     // launch_copy reads the group's layer pointers from call layer p.l0 on
     if ((rc = launch_copy<true, true>(g, h->ids, ln.staging + hf * half, cks, cls, cbs, p.b0,
-                                      p.nb, p.l0, p.nl, grid_cap, work, h->prof)))
+                                      p.nb, p.l0, p.nl, grid_cap, work, h->prof, 0,
+                                      whole_cap)))
       return rc;
     if (p.last) {
       for (int gi = next_group; gi <= p.group; ++gi) FKV_HIP(hipEventRecord(h->done[gi], work));
