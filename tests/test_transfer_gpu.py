@@ -519,6 +519,33 @@ def test_staged_runs_and_small_staging(dev, run, heads):
         _lib.set_staging_bytes(0)
 
 
+@pytest.mark.parametrize("blocks,launches", [(384, 2), (192, 1)])
+def test_copy_engine_edge_piece(dev, blocks, launches):
+    """A copy-engine transfer whose piece without engine copies beside it (the
+    D2H's first gather, the H2D's last scatter) moves at least 128 MiB cuts
+    an eighth of a staging half off it: 384 blocks of 512 KiB (192 MiB) in
+    256 MiB halves go as 64 + 320 blocks (D2H) and 320 + 64 (H2D), 192 blocks
+    (96 MiB) as one piece.  Bytes match the oracle either way."""
+    from flexkv_amd import _lib
+    _lib.set_staging_bytes(512 << 20)
+    try:
+        case = KVCase(layers_total=8, num_layers=8, start_layer=0, kv=2, ng=512, nh=512,
+                      tokens=16, heads=8, dim=128).fill(seed=blocks)
+        gids = inputs.distinct_ids(5, blocks, 512)
+        cids = inputs.distinct_ids(6, blocks, 512)
+        _lib.profile_enable(True)
+        check_case(case, gids, cids, 1)
+        prof = _lib.profile_read()
+        _lib.profile_enable(False)
+        assert prof["dma_batches"] == 2, prof
+        assert prof["kernel_launches"] == 2 * launches, prof   # gathers + scatters
+        assert prof["kernel_bytes"] == 2 * blocks * 8 * 2 * 32768, prof
+    finally:
+        _lib.profile_enable(False)
+        _lib.release_staging()
+        _lib.set_staging_bytes(0)
+
+
 @pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("shape", [(1, 1, 32776, 1, 1), (3, 2, 32776, 1, 1),
                                    (1, 1, 128, 8, 16), (1, 1, 256, 16, 16)],
