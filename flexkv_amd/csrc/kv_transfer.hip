@@ -1177,6 +1177,33 @@ int pipeline_stream(CopyLane& ln, int dev, hipStream_t* out) {
   return 0;
 }
 
+// A copy-engine handle on a device whose engines cannot be set up: every
+// group moves host-to-device with the zero-copy kernel on the pipeline stream
+// (the layer-wise kernel path's compute units), its event recorded after it.
+int layerwise_kernel_groups(fkv_transfer_handle_s* h, hipStream_t work) {
+  const Geometry& g = h->geo;
+  DeviceState& d = g_dev[h->dev];
+  const int cus = std::min(kAutoLayerwiseH2DCus, d.num_cus);
+  const int grid_cap = cus * d.occ_zero_copy[1];
+  char* cpu_dev = g.cpu_info.dev_ptr + g.startoff + static_cast<int64_t>(g.start_layer) * g.cls;
+  int group = 0;
+  for (int g0 = 0; g0 < g.num_layers; g0 += h->granularity, ++group) {
+    const int gend = std::min(g.num_layers, g0 + h->granularity);
+    for (int l0 = g0; l0 < gend; l0 += g.layers_per_launch()) {
+      const int nl = std::min(g.layers_per_launch(), gend - l0);
+      char* base = cpu_dev + static_cast<int64_t>(l0) * g.cls;
+      int rc = launch_copy<true, false>(g, h->ids, base, g.cks, g.cls, g.cbs, 0, g.num_blocks,
+                                        l0, nl, grid_cap, work, h->prof);
+      if (rc) return rc;
+    }
+    FKV_HIP(hipEventRecord(h->done[group], work));
+    std::lock_guard<std::mutex> lk(h->mu);
+    h->recorded = group + 1;
+    h->cv.notify_all();
+  }
+  return 0;
+}
+
 // The driver's work: layer groups in order, each cut into pieces of whole
 // blocks that fit a staging half; SDMA copies (one per block: the group's
 // rows are contiguous in block-wise host memory) on the wide engine set,
@@ -1198,7 +1225,15 @@ int layerwise_ce_run(fkv_transfer_handle_s* h, CopyLane& ln, hipStream_t work) {
   // a half holds at least one block's row of one layer, so every window fits
   const size_t one_layer = static_cast<size_t>(g.kv) * g.chunk;
   if ((rc = ensure_staging(ln, std::max(std::min(row_max, half_default), one_layer)))) return rc;
-  if ((rc = ensure_sdma(d, h->dev, ln.staging))) return rc;
+  if ((rc = ensure_sdma(d, h->dev, ln.staging))) {
+    // nothing has been queued yet: this handle, and every later copy-engine
+    // transfer on the device, moves with the zero-copy kernel
+    if (!d.sdma_failed.exchange(true))
+      fprintf(stderr, "flexkv: copy engines unavailable on device %d (%s); copy-engine "
+              "transfers use the zero-copy kernel\n", h->dev, last_error().c_str());
+    last_error().clear();
+    return layerwise_kernel_groups(h, work);
+  }
   const size_t half = ln.staging_bytes / 2;
   struct Piece {
     int l0, nl, b0, nb, group;   // group: the last layer group the piece completes

@@ -297,3 +297,54 @@ def test_ce_handle_stream_wait_and_query_before_arrival():
     _abi_layerwise(dc, gids.copy(), cids.copy(), True, 2, ce=True).release()
     for l, g in enumerate(dc.gpu_np()):
         assert np.array_equal(g[:, gids], np.stack([hv[c, l, :, 0] for c in cids], axis=1))
+
+
+_NO_ENGINES_CHILD = r"""
+import sys
+sys.path.insert(0, {root!r}); sys.path.insert(0, {tests!r})
+import numpy as np, torch
+import oracle
+from oracle import inputs
+from kvcase import KVCase
+from gpu_util import DeviceCase
+from test_layerwise_gpu import _abi_layerwise
+L, n = 6, 40
+case = KVCase(layers_total=L, num_layers=L, start_layer=0, kv=2, ng=64, nh=96, tokens=16,
+              heads=4, dim=64).fill(seed=31)
+s = case.strides()
+dc = DeviceCase(case)
+for rnd in range(2):
+    gids = inputs.distinct_ids(40 + rnd, n, 64)
+    cids = inputs.distinct_ids(50 + rnd, n, 96)
+    fresh = case.host ^ np.uint16(0x0F0F + rnd)
+    dc.set_host(fresh)
+    dc.set_gpu([np.zeros_like(g) for g in case.gpu])
+    with _abi_layerwise(dc, gids.copy(), cids.copy(), True, 2, ce=True) as hnd:
+        for g in range(hnd.num_groups):
+            hnd.wait(g)
+    exp = [np.zeros_like(g) for g in case.gpu]
+    oracle.transfer_kv_blocks(gids, exp, s["gpu_kv"], s["gpu_block"], cids, fresh, s["cpu_kv"],
+                              s["cpu_layer"], s["cpu_block"], s["chunk"], 0, True)
+    assert all(np.array_equal(a, b) for a, b in zip(dc.gpu_np(), exp)), rnd
+print("layer-wise copy-engine handles match the oracle", flush=True)
+"""
+
+
+def test_ce_handle_without_engines():
+    """With the library's engines turned off (FLEXKV_SDMA_ENGINES=0), the first
+    copy-engine layer-wise handle finds the engines unavailable inside its
+    pipeline and moves every group with the zero-copy kernel; the second takes
+    the kernel path from the start.  Both match the oracle; the warning comes
+    once.  Runs in a child process, as the engine state is per process."""
+    import os
+    import subprocess
+    import sys
+    tests = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(tests)
+    code = _NO_ENGINES_CHILD.format(root=root, tests=tests)
+    res = subprocess.run([sys.executable, "-c", code], cwd=root, capture_output=True, text=True,
+                         env=dict(os.environ, FLEXKV_SDMA_ENGINES="0"), timeout=300)
+    print(res.stdout[-2000:], res.stderr[-2000:], flush=True)
+    assert res.returncode == 0, res.stderr[-2000:]
+    assert "match the oracle" in res.stdout
+    assert res.stderr.count("copy engines unavailable") == 1
