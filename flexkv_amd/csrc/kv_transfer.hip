@@ -1306,7 +1306,11 @@ int layerwise_ce_run(fkv_transfer_handle_s* h, CopyLane& ln, hipStream_t work) {
     const Piece& p = pieces[pi];
     const int hf = pi & 1;
     pending[hf] = false;
-    if ((rc = sdma_wait(d, ln, hf, /*spin=*/true))) return rc;
+    // The host sleeps while the other half's copies keep the engines busy;
+    // only the last wait, which nothing overlaps, spins (a wake from a sleep
+    // costs 15-30 us).  Spinning throughout would hold a host core for the
+    // whole transfer.
+    if ((rc = sdma_wait(d, ln, hf, /*spin=*/pi + 1 == np))) return rc;
     hipLaunchKernelGGL(acquire_system_kernel, dim3(d.num_cus), dim3(64), 0, work);
     FKV_HIP(hipGetLastError());
     const int64_t cks = g.kv == 1 ? 0 : g.chunk;
