@@ -28,18 +28,19 @@ namespace {
 // (16 engines) with 2 MiB copies: four move 56-57 GB/s either way, and
 // device-to-host drops to 47 GB/s on eight.  A D2H and an H2D together move
 // 69 GB/s on engines 0-3 and 4-7.
-constexpr int kDefaultSdmaEngines = 4;
+constexpr int kDefaultSdmaEngines[2] = {4, 4};   // [D2H, H2D]
 // Engines 0-7.  Host-to-device copies on engines 8-15 slow compute kernels
 // running beside them about twice over, at any copy size: 160 bf16 GEMMs
 // [8192x4096]x[4096x4096] took 1.85x / 2.0x their time beside a 56.6 GB/s
 // H2D on engines 6-11 / 8-15, against 1.07x on engines 4-7 (MI355X; D2H on
 // engines 0-7: 1.09-1.12x).
 constexpr uint32_t kComputeFriendlyEngines = 0xFFu;
-// Engines of the copy-engine layer-wise host-to-device pipeline, whose
-// smaller windows' engine copies (one block's layer group: 64 KiB for one
-// Llama-3-8B layer) are bound by the engines' per-copy cost, so more engines
-// help; taken from engines 0-7, host-to-device's own first.
-constexpr int kDefaultLayerwiseEngines = 8;
+// The wide engine set (FLEXKV_SDMA_ENGINES_WIDE): host-to-device copies bound
+// by the engines' per-copy cost spread over it, those of the copy-engine
+// layer-wise pipeline (one block's layer window, 64-256 KiB at Llama-3-8B)
+// and synchronous ones shorter than 1 MiB on average; taken from engines
+// 0-7, host-to-device's own first.
+constexpr int kDefaultWideEngines = 8;
 constexpr int64_t kDefaultMaxCopyBytes = int64_t(4) << 20;
 
 // The HSA entry points the copy-engine path needs, resolved from the HSA
@@ -65,9 +66,14 @@ struct HsaApi {
 HsaApi g_hsa;
 
 // Engines per direction; FLEXKV_SDMA_ENGINES=0 turns the engines off.
-int sdma_engines_wanted() {
-  const char* e = getenv("FLEXKV_SDMA_ENGINES");
-  const int n = e ? atoi(e) : kDefaultSdmaEngines;
+// Engines of one direction (0: device-to-host, 1: host-to-device):
+// FLEXKV_SDMA_ENGINES sets both, FLEXKV_SDMA_ENGINES_D2H / _H2D one.
+int sdma_engines_wanted(int dir) {
+  const char* both = getenv("FLEXKV_SDMA_ENGINES");
+  const char* one = getenv(dir == 0 ? "FLEXKV_SDMA_ENGINES_D2H" : "FLEXKV_SDMA_ENGINES_H2D");
+  int n = kDefaultSdmaEngines[dir];
+  if (both) n = atoi(both);
+  if (one) n = atoi(one);
   return std::max(0, std::min(n, 32));
 }
 
@@ -369,10 +375,11 @@ int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr) {
   // did, so with the default four the two directions run side by side on
   // disjoint engines (MI355X: 69 GB/s in both directions together on
   // engines 0-3 and 4-7, 56-57 GB/s one way).
-  const int want = sdma_engines_wanted();
-  if (want == 0) return fail(kInval, "copy engines turned off (FLEXKV_SDMA_ENGINES=0)");
+  if (sdma_engines_wanted(0) == 0 || sdma_engines_wanted(1) == 0)
+    return fail(kInval, "copy engines turned off (FLEXKV_SDMA_ENGINES=0)");
   uint32_t taken = 0;
   for (int dir = 0; dir < 2; ++dir) {
+    const int want = sdma_engines_wanted(dir);
     uint32_t mask = 0;
     FKV_HSA(dir == 0 ? g_hsa.copy_engine_status(q.cpu, q.gpu, &mask)
                      : g_hsa.copy_engine_status(q.gpu, q.cpu, &mask));
@@ -394,8 +401,9 @@ int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr) {
     // the layer-wise pipeline's set, in order of preference: host-to-device
     // engines among 0-7 that device-to-host did not take, then those it
     // took, then (only when more are asked for) the others
-    const char* e = getenv("FLEXKV_SDMA_ENGINES_LAYERWISE");
-    const int wide = std::max(1, std::min(e ? atoi(e) : kDefaultLayerwiseEngines, 32));
+    const char* e = getenv("FLEXKV_SDMA_ENGINES_WIDE");
+    if (!e) e = getenv("FLEXKV_SDMA_ENGINES_LAYERWISE");   // the earlier name
+    const int wide = std::max(1, std::min(e ? atoi(e) : kDefaultWideEngines, 32));
     uint32_t mask = 0;
     FKV_HSA(g_hsa.copy_engine_status(q.gpu, q.cpu, &mask));
     uint32_t d2h_taken = 0;

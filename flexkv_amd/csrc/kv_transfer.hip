@@ -156,6 +156,12 @@ constexpr int kAutoLayerwiseH2DCus = 2;
 // copy, worth handing to the SDMA engines (ce_pays_off).
 constexpr int64_t kCeMinBytesDefault = int64_t(8) << 20;
 constexpr int64_t kCeMinRunBytes = int64_t(128) << 10;
+// Host-to-device engine copies shorter than this on average spread over the
+// wide engine set (engines 0-7) instead of the direction's four.  Measured on
+// MI355X: 640 KiB copies (Llama-3-70B TP-8 shard) 51.9 -> 56.4 GB/s, 256 KiB
+// copies 39.5 -> 48.8 GB/s, 2 MiB copies 56.8 -> 57.0 GB/s; the four keep a
+// D2H beside it on engines of its own (69.8 GB/s together against 66.2).
+constexpr int64_t kWideCopyBytes = int64_t(1) << 20;
 // The piece of a copy-engine transfer that runs without engine copies beside
 // it (the first gather, the last scatter) is cut to 1 / kEdgePieceDiv of a
 // staging half when it moves at least kEdgePieceMinBytes.
@@ -854,10 +860,16 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
     const Piece& p = pieces[pi];
     const int h = pi & 1;
     build_runs(g, p.b0, p.nb, p.l0, p.nl, sdma_rect_available(), layer_major, runs);
-    for (const Run& r : runs) dma_bytes += r.bytes * std::max<int64_t>(1, r.slices);
+    int64_t piece_bytes = 0;
+    for (const Run& r : runs) piece_bytes += r.bytes * std::max<int64_t>(1, r.slices);
+    dma_bytes += piece_bytes;
     dma_copies += static_cast<int64_t>(runs.size());
     pending[h] = true;
-    return issue_sdma(d, ln, runs, ln.staging + h * half, h2d, h, host_agent);
+    // Host-to-device copies shorter than kWideCopyBytes on average are bound
+    // by the engines' per-copy cost and spread over the wide set
+    const bool wide = h2d && !runs.empty() &&
+                      piece_bytes < kWideCopyBytes * static_cast<int64_t>(runs.size());
+    return issue_sdma(d, ln, runs, ln.staging + h * half, h2d, h, host_agent, wide);
   };
   auto launch = [&](int pi) -> int {
     const Piece& p = pieces[pi];
@@ -1292,13 +1304,10 @@ int layerwise_ce_run(fkv_transfer_handle_s* h, CopyLane& ln, hipStream_t work) {
     for (const Run& r : runs) dma_bytes += r.bytes;
     dma_copies += static_cast<int64_t>(runs.size());
     pending[pi & 1] = true;
-    // Windows below the full copy size are bound by the engines' per-copy
-    // cost and spread over the wide engine set; full windows keep to the
-    // direction's own engines, which move them at the link's rate while
-    // slowing the kernels beside them least.
-    const bool wide = static_cast<size_t>(p.nl) * g.kv * g.chunk < min_copy;
+    // Copies of one block's window are bound by the engines' per-copy cost,
+    // so every window spreads over the wide engine set.
     return issue_sdma(d, ln, runs, ln.staging + (pi & 1) * half, true, pi & 1, d.cpu_agent,
-                      wide);
+                      /*wide=*/true);
   };
   for (int pi = 0; pi < std::min(np, 2); ++pi)
     if ((rc = queue_copies(pi))) return rc;
