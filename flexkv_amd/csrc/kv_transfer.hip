@@ -169,11 +169,11 @@ constexpr int kEdgePieceDiv = 8;
 constexpr int64_t kEdgePieceMinBytes = int64_t(128) << 20;
 // Default smallest engine copy per block of the copy-engine layer-wise
 // pipeline (see layerwise_min_copy_bytes).  Measured on MI355X, Llama-3-8B
-// one-layer groups (64 KiB per block), 1024 random blocks, 8 engines: 21 /
-// 33 / 42 / 49 / 51 GB/s with windows up to 64 KiB / 128 KiB / 256 KiB /
-// 512 KiB / 1 MiB per block; per-layer GEMMs overlapped with it end within
-// 0.2 / 0.0 / 1.1 / 11.9 / 10.3% of the transfer plus one layer's compute,
-// GEMMs beside it slow by 8-9% throughout.
+// one-layer groups (64 KiB per block), 1024 random blocks, engines 0-7:
+// 37.6 / 47.2 / 50.5 / 51.1 / 51.1 GB/s with windows up to 64 KiB / 128 KiB /
+// 256 KiB / 512 KiB / 1 MiB per block; per-layer GEMMs overlapped with it end
+// within 0.0 / 0.5 / 0.6 / 8.3 / 8.3% of the transfer plus one layer's
+// compute, and GEMMs beside it slow by 11-12% at every size.
 constexpr int64_t kLayerwiseCeMinCopyBytes = int64_t(256) << 10;
 // Average host run (bytes per (layer, K|V) run of consecutive blocks) from
 // which a layer-wise host cache is staged layer-major and copied run by run

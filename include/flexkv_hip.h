@@ -47,8 +47,10 @@ enum {
    * transfer needs on a single engine (FLEXKV_CE_RECT_COPIES=1 keeps it on
    * the engines; a transfer of rect copies runs alone).  Staging is
    * double-buffered; the PCIe copies take no compute units.  Each direction
-   * has its own staging and engines, so a D2H and an H2D transfer from
-   * different threads run at the same time.  Transfers under
+   * has its own staging and engines (device-to-host engines 0-3,
+   * host-to-device 4-7; host-to-device copies shorter than 1 MiB on average
+   * spread over engines 0-7), so a D2H and an H2D transfer from different
+   * threads run at the same time.  Transfers under
    * FLEXKV_CE_MIN_BYTES (default 8 MiB) or whose
    * engine copies would move under 128 KiB each move with the zero-copy
    * kernel instead, where the engines' per-copy cost would dominate, and so
@@ -189,10 +191,10 @@ int fkv_scatter_kv_blocks(int num_blocks, int num_layers, const int64_t* gpu_blo
  * groups up to FLEXKV_LAYERWISE_CE_MIN_COPY_BYTES per block (default
  * 256 KiB) and near the end hold at most half of the groups left, so the
  * first group arrives early and the compute a window releases ends while
- * the rest arrive.  Windows below that size spread their copies over up to
- * FLEXKV_SDMA_ENGINES_LAYERWISE engines (default 8, from engines 0-7:
+ * the rest arrive.  Every window spreads its copies over the wide engine
+ * set, FLEXKV_SDMA_ENGINES_WIDE engines (default 8, engines 0-7:
  * host-to-device copies on engines 8-15 slow compute kernels running beside
- * them about twofold); full windows use the direction's own engines.
+ * them about twofold).
  * fkv_handle_stream_wait and fkv_handle_wait first wait on the host until
  * the group's event exists (its copies have landed), fkv_handle_query
  * reports 0 until then.
