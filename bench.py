@@ -260,6 +260,64 @@ def link_peaks(wl: Workload, reps: int = 8):
     return res
 
 
+GEMM_WARM = 200   # GEMMs run before each measured window (about 40 ms)
+GEMM_LEAD = 20    # of which the last GEMM_LEAD run after the transfer starts
+
+
+def gemm_window(a, b, c, comp, start=None, n: int = 160):
+    """Time n bf16 GEMMs on `comp` with the GPU already at its working clocks.
+
+    The GFX clock drops within about 10 ms of idle compute and takes some
+    30 ms of GEMMs to climb back, so a batch started from a quiet GPU runs
+    6-9% slower than the same batch in a busy one.  Both the alone and the
+    beside measurement therefore queue GEMM_WARM GEMMs ahead of the window
+    with no gap; `start` (the transfer) is called when the warm-up has
+    GEMM_LEAD GEMMs left, so the window runs entirely under the transfer
+    for transfers longer than the window.  Returns (window ms, start's
+    return value)."""
+    with torch.cuda.stream(comp):
+        ready = torch.cuda.Event()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for i in range(GEMM_WARM):
+            torch.mm(a, b, out=c)
+            if i == GEMM_WARM - GEMM_LEAD - 1:
+                ready.record()
+        e0.record()
+        for _ in range(n):
+            torch.mm(a, b, out=c)
+        e1.record()
+    ready.synchronize()
+    started = start() if start is not None else None
+    e1.synchronize()
+    return e0.elapsed_time(e1), started
+
+
+GEMM_QUIET_S = 0.05   # idle time before a transfer-first window
+
+
+def gemm_window_transfer_first(a, b, c, comp, start=None, n: int = 160):
+    """The other order: from a GPU idle for GEMM_QUIET_S, `start` (the
+    transfer) is called first and the n GEMMs are queued right after it.
+    The alone measurement starts from the same idle state, so the clock
+    ramp is in both.  A zero-copy kernel launched first spreads its
+    workgroups over idle compute units, where every GEMM wave then meets
+    them; launched into running GEMMs it takes units as they free up."""
+    torch.cuda.synchronize()
+    time.sleep(GEMM_QUIET_S)
+    started = None
+    if start is not None:
+        started = start()
+        time.sleep(0.001)   # a transfer started on a thread has launched by now
+    with torch.cuda.stream(comp):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            torch.mm(a, b, out=c)
+        e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1), started
+
+
 def layerwise_h2d(wl: Workload, steps: int):
     """H2D of the step's blocks one layer group per layer.
 
@@ -272,7 +330,8 @@ def layerwise_h2d(wl: Workload, steps: int):
       compute (the bound) and with the same GEMMs after a synchronous
       transfer;
     * GEMMs beside: 160 GEMMs with no waits, alone and beside one async
-      layer-wise transfer on each path.
+      layer-wise transfer on each path, both behind the same warm-up
+      (gemm_window).
     """
     import threading
 
@@ -315,25 +374,22 @@ def layerwise_h2d(wl: Workload, steps: int):
         compute_layers()
         comp.synchronize()
 
-    def gemms_ms():
-        with torch.cuda.stream(comp):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(160):
-                torch.mm(a, b, out=c)
-            e1.record()
-        e1.synchronize()
-        return e0.elapsed_time(e1)
-
     comp_s, _, _ = time_steps(compute_only, steps, 1)
-    gemms_ms()
-    gemm_alone = statistics.median(gemms_ms() for _ in range(3))
+    gemm_alone = statistics.median(gemm_window(a, b, c, comp)[0] for _ in range(3))
+    gemm_alone_tf = statistics.median(gemm_window_transfer_first(a, b, c, comp)[0]
+                                      for _ in range(3))
     out = {"granularity_layers": 1,
            "reference_schedule_ms": round(ref_s * 1e3, 2),
            "reference_schedule_gbps": round(gb / ref_s, 2),
            "compute_only_ms": round(comp_s * 1e3, 2),
            "compute_proxy": f"{reps} bf16 GEMMs [8192x4096]x[4096x4096] per layer",
-           "gemm_alone_ms": round(gemm_alone, 2)}
+           "gemm_window": (f"160 GEMMs after {GEMM_WARM} back-to-back warm-up GEMMs; beside: "
+                           f"the handle starts {GEMM_LEAD} GEMMs before the window"),
+           "gemm_alone_ms": round(gemm_alone, 2),
+           "gemm_window_transfer_first": (f"160 GEMMs queued right after the handle starts, "
+                                          f"from a GPU idle {GEMM_QUIET_S * 1e3:.0f} ms; alone "
+                                          "from the same idle state"),
+           "gemm_alone_transfer_first_ms": round(gemm_alone_tf, 2)}
     for name, ce in (("kernel", False), ("ce", True)):
         first, total = [], []
         for _ in range(steps + 1):
@@ -362,11 +418,13 @@ def layerwise_h2d(wl: Workload, steps: int):
 
         ser_s, _, _ = time_steps(serial, steps, 1)
         ovl_s, _, _ = time_steps(overlapped, steps, 1)
-        beside = []
+        beside, beside_tf = [], []
         for _ in range(3):
-            torch.cuda.synchronize()
-            hnd = start(ce)
-            beside.append(gemms_ms())
+            ms, hnd = gemm_window(a, b, c, comp, start=lambda: start(ce))
+            beside.append(ms)
+            hnd.release()
+            ms, hnd = gemm_window_transfer_first(a, b, c, comp, start=lambda: start(ce))
+            beside_tf.append(ms)
             hnd.release()
         xfer_ms = statistics.median(total) * 1e3
         bound = xfer_ms + comp_s * 1e3 / L
@@ -378,7 +436,10 @@ def layerwise_h2d(wl: Workload, steps: int):
                      "bound_transfer_plus_one_layer_ms": round(bound, 2),
                      "overlapped_over_bound": round(ovl_s * 1e3 / bound, 4),
                      "gemm_beside_ms": round(statistics.median(beside), 2),
-                     "gemm_slowdown": round(statistics.median(beside) / gemm_alone, 4)}
+                     "gemm_slowdown": round(statistics.median(beside) / gemm_alone, 4),
+                     "gemm_beside_transfer_first_ms": round(statistics.median(beside_tf), 2),
+                     "gemm_slowdown_transfer_first": round(statistics.median(beside_tf)
+                                                           / gemm_alone_tf, 4)}
     c_ext.release_transfer_stream(xfer)
     return out
 
@@ -653,7 +714,8 @@ def overlap_with_compute(wl: Workload, steps: int = 3, gemms: int = 160):
     while the main thread runs bf16 GEMMs [8192x4096]x[4096x4096] on a compute
     stream: GEMM time alone and beside each path and direction.  The
     zero-copy kernel shares compute units with the GEMMs; the copy-engine
-    path leaves the PCIe copies to the SDMA engines."""
+    path leaves the PCIe copies to the SDMA engines.  Alone and beside, the
+    GEMMs run behind the same warm-up (gemm_window)."""
     import threading
 
     from flexkv_amd import c_ext
@@ -663,7 +725,7 @@ def overlap_with_compute(wl: Workload, steps: int = 3, gemms: int = 160):
     b = torch.randn(4096, 4096, device=wl.dev, dtype=torch.bfloat16)
     c = torch.empty(8192, 4096, device=wl.dev, dtype=torch.bfloat16)
 
-    def once(h2d, ce, with_xfer=True):
+    def once(h2d, ce, with_xfer=True, window=gemm_window):
         torch.cuda.synchronize()
         res = {}
 
@@ -672,33 +734,43 @@ def overlap_with_compute(wl: Workload, steps: int = 3, gemms: int = 160):
                 t0 = time.perf_counter()
                 wl.transfer(h2d, ce)
                 res["xfer"] = time.perf_counter() - t0
-        th = threading.Thread(target=move) if with_xfer else None
-        if th:
+
+        def start():
+            th = threading.Thread(target=move)
             th.start()
-        with torch.cuda.stream(comp):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(gemms):
-                torch.mm(a, b, out=c)
-            e1.record()
+            return th
+        ms, th = window(a, b, c, comp, start=start if with_xfer else None, n=gemms)
         if th:
             th.join()
         torch.cuda.synchronize()
-        res["gemm"] = e0.elapsed_time(e1) / 1e3
+        res["gemm"] = ms / 1e3
         return res
 
-    once(True, False)
-    out = {"gemm_alone_ms": round(statistics.median(
-        once(True, False, with_xfer=False)["gemm"] for _ in range(steps)) * 1e3, 2)}
+    once(True, False, with_xfer=False)
+    def med_ms(rs, key):
+        return round(statistics.median(r[key] for r in rs) * 1e3, 2)
+
+    out = {"gemm_alone_ms": med_ms([once(True, False, with_xfer=False)
+                                    for _ in range(steps)], "gemm")}
+    tf = {"gemm_alone_ms": med_ms([once(True, False, False, gemm_window_transfer_first)
+                                   for _ in range(steps)], "gemm")}
     for h2d in (False, True):
         for ce in (False, True):
-            rs = [once(h2d, ce) for _ in range(steps)]
             key = ("h2d" if h2d else "d2h") + ("_ce" if ce else "_kernel")
-            out[key] = {"gemm_ms": round(statistics.median(r["gemm"] for r in rs) * 1e3, 2),
-                        "transfer_ms": round(statistics.median(r["xfer"] for r in rs) * 1e3, 2)}
+            rs = [once(h2d, ce) for _ in range(steps)]
+            out[key] = {"gemm_ms": med_ms(rs, "gemm"), "transfer_ms": med_ms(rs, "xfer"),
+                        "gemm_slowdown": round(med_ms(rs, "gemm") / out["gemm_alone_ms"], 4)}
+            rs = [once(h2d, ce, True, gemm_window_transfer_first) for _ in range(steps)]
+            tf[key] = {"gemm_ms": med_ms(rs, "gemm"), "transfer_ms": med_ms(rs, "xfer"),
+                       "gemm_slowdown": round(med_ms(rs, "gemm") / tf["gemm_alone_ms"], 4)}
     c_ext.release_transfer_stream(xfer)
+    out["transfer_first"] = tf
     out["what"] = (f"{gemms} GEMMs on a compute stream beside one {wl.bytes_per_op / 2**30:.0f} "
-                   "GiB transfer on a transfer stream")
+                   f"GiB transfer on a transfer stream, started {GEMM_LEAD} GEMMs before the "
+                   f"window; alone and beside after {GEMM_WARM - GEMM_LEAD} warm-up GEMMs. "
+                   f"transfer_first: the transfer starts on a GPU idle "
+                   f"{GEMM_QUIET_S * 1e3:.0f} ms and the GEMMs are queued after it; alone from "
+                   "the same idle state")
     return out
 
 
@@ -1093,12 +1165,19 @@ KERNEL_SECTION_END = b"// A system-scope acquire in every workgroup."
 def kernel_section_sha16(path: str = KERNEL_SOURCE) -> str:
     """sha256 prefix of the transfer kernel's source: kv_transfer.hip from its
     start (build macros, CopyArgs) to the end of kv_chunk_copy_kernel, the
-    part that decides which bytes the kernel reads and writes."""
+    part that decides which bytes the kernel reads and writes.  Comments,
+    blank lines and indentation are left out, so a change to a comment keeps
+    the key and any change to the code changes it."""
     import hashlib
+    import re
     with open(path, "rb") as fh:
         text = fh.read()
     end = text.find(KERNEL_SECTION_END)
-    return hashlib.sha256(text if end < 0 else text[:end]).hexdigest()[:16]
+    code = (text if end < 0 else text[:end]).decode()
+    code = re.sub(r"/\*.*?\*/", " ", code, flags=re.S)
+    lines = (re.sub(r"//.*", "", ln).strip() for ln in code.splitlines())
+    code = "\n".join(ln for ln in lines if ln)
+    return hashlib.sha256(code.encode()).hexdigest()[:16]
 
 
 def measured_traffic(workload: str, run: int, alg_bytes: int) -> dict:

@@ -173,7 +173,7 @@ constexpr int64_t kEdgePieceMinBytes = int64_t(128) << 20;
 // 37.6 / 47.2 / 50.5 / 51.1 / 51.1 GB/s with windows up to 64 KiB / 128 KiB /
 // 256 KiB / 512 KiB / 1 MiB per block; per-layer GEMMs overlapped with it end
 // within 0.0 / 0.5 / 0.6 / 8.3 / 8.3% of the transfer plus one layer's
-// compute, and GEMMs beside it slow by 11-12% at every size.
+// compute, and GEMMs beside it slow by the same few percent at every size.
 constexpr int64_t kLayerwiseCeMinCopyBytes = int64_t(256) << 10;
 // Average host run (bytes per (layer, K|V) run of consecutive blocks) from
 // which a layer-wise host cache is staged layer-major and copied run by run
@@ -1462,8 +1462,9 @@ Geometry make_geometry(int num_blocks, int start_layer_id, int num_layers,
 // (D2H / H2D) at the Llama-3-8B shape, 82% of the link, against 56.5 /
 // 57.2 GB/s for the zero-copy kernel.  Such transfers therefore move with
 // the zero-copy kernel, which holds compute units for the whole transfer
-// (160 bf16 GEMMs beside a 2 GiB D2H take 71 ms instead of 36 ms beside the
-// rect copies); FLEXKV_CE_RECT_COPIES=1 keeps them on the engines.
+// (160 bf16 GEMMs queued after a 2 GiB D2H starts take 71 ms instead of
+// 36 ms beside the rect copies); FLEXKV_CE_RECT_COPIES=1 keeps them on the
+// engines.
 bool ce_pays_off(const Geometry& g, bool h2d) {
   // a "host" cache that is device memory has no PCIe copy to offload
   if (g.cpu_info.device) return false;

@@ -118,3 +118,33 @@ def test_bench_refuses_more_than_one_gpu(gpus):
                        capture_output=True, text=True, timeout=300)
     assert r.returncode == 2
     assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_kernel_section_key_ignores_comments_only(tmp_path):
+    """The counter profiles are keyed by the kernel section of kv_transfer.hip:
+    a comment or blank-line change keeps the key, a code change (even inside
+    a line that carries a comment) changes it, and text after the section's
+    end does not count."""
+    import os
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    sys.path.insert(0, root)
+    import bench
+    src = open(bench.KERNEL_SOURCE, "rb").read()
+    end = src.find(bench.KERNEL_SECTION_END)
+    assert end > 0
+    base = bench.kernel_section_sha16()
+
+    def key(data: bytes) -> str:
+        p = tmp_path / "k.hip"
+        p.write_bytes(data)
+        return bench.kernel_section_sha16(str(p))
+
+    assert key(src) == base
+    assert key(b"// another comment\n\n" + src) == base
+    assert key(src[:end].replace(b"\n", b"  // note\n", 1) + src[end:]) == base
+    assert key(src[:end] + src[end:] + b"\nint tail_change;\n") == base
+    assert key(b"#define FKV_EXTRA 1\n" + src) != base
+    first_code = src.find(b"\n#include")
+    assert first_code > 0
+    assert key(src[:first_code] + b"\nint x;  // a comment\n" + src[first_code:]) != base
