@@ -98,6 +98,7 @@ struct DeviceState {
   int num_cus = 0;
   int occ_zero_copy[2] = {0, 0};
   int occ_staged[2] = {0, 0};   // row-by-row staging kernels, per direction
+  int occ_small[2] = {1, 1};   // kv_small_copy_kernel, D2H / H2D
   int occ_whole[2] = {0, 0};    // whole-group staging kernels, per direction
   // Copy engines: the HSA agents of this GPU and of the host and the SDMA
   // engines each direction pins its copies to (disjoint sets where the device

@@ -563,6 +563,47 @@ def test_small_transfers_split_rows(dev, mode, shape):
     check_case(case, inputs.distinct_ids(n + 40, n, 8), inputs.distinct_ids(n + 41, n, 12), mode)
 
 
+SMALL_SHAPES = [
+    # (blocks, layers, kv, tokens, heads, dim, layout, tp, rank); chunk = tokens*heads*dim*2 B
+    (1, 1, 2, 16, 8, 128, "BLOCKWISE", 1, 0),   # 32 KiB chunks, two 16 KiB pieces each
+    (16, 1, 2, 16, 8, 128, "BLOCKWISE", 1, 0),  # 64 pieces: the default grid cap decides
+    (3, 2, 1, 1, 1, 8, "BLOCKWISE", 1, 0),      # MLA, 16 B chunks
+    (5, 3, 2, 10, 8, 128, "BLOCKWISE", 1, 0),   # 20 KiB chunks: a 16 KiB and a 4 KiB piece
+    (2, 1, 1, 64, 1, 576, "BLOCKWISE", 1, 0),   # 72 KiB MLA chunks: five pieces
+    (4, 2, 2, 16, 2, 64, "LAYERWISE", 2, 1),    # layer-wise host, TP host chunk of rank 1
+]
+
+
+@pytest.mark.parametrize("small", ["1", "0"], ids=["small-kernel", "general-kernel"])
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("shape", SMALL_SHAPES, ids=[f"s{i}" for i in range(len(SMALL_SHAPES))])
+def test_small_kernel_matches_oracle(dev, monkeypatch, small, mode, shape):
+    """Calls of at most 128 pieces of 16 KiB and 4 MiB take the small-transfer
+    kernel (per-piece addresses in the kernel arguments); the same calls with
+    FLEXKV_SMALL_KERNEL=0 take the general kernel.  Both match the oracle, in
+    kernel mode and in copy-engine mode (which sends calls this small to the
+    zero-copy kernels), with a start layer, MLA, partial pieces and a TP host
+    chunk."""
+    monkeypatch.setenv("FLEXKV_SMALL_KERNEL", small)
+    n, nl, kv, tokens, heads, dim, layout, tp, rank = shape
+    case = KVCase(layers_total=nl + 1, num_layers=nl, start_layer=1, kv=kv, ng=40, nh=48,
+                  tokens=tokens, heads=heads, dim=dim, layout=layout, tp=tp,
+                  rank=rank).fill(seed=n * 100 + nl * 10 + kv)
+    check_case(case, inputs.distinct_ids(n + 70, n, 40), inputs.distinct_ids(n + 71, n, 48), mode)
+
+
+@pytest.mark.parametrize("cus", [1, 2])
+def test_small_kernel_grid_cap(dev, cus):
+    """With few compute units allowed, a call whose pieces outnumber the
+    workgroups those units hold takes the general kernel; both sides of that
+    line match the oracle."""
+    for n in (1, 4, 16):
+        case = KVCase(layers_total=1, num_layers=1, start_layer=0, kv=2, ng=32, nh=32, tokens=16,
+                      heads=8, dim=128).fill(seed=n + cus)
+        check_case(case, inputs.distinct_ids(n + 5, n, 32), inputs.distinct_ids(n + 6, n, 32), 0,
+                   transfer_cus=cus)
+
+
 @pytest.mark.parametrize("mode", MODES)
 def test_duplicate_sources_and_single_block(dev, mode):
     case = KVCase(layers_total=2, num_layers=2, start_layer=0, kv=2, ng=8, nh=16, tokens=16,
