@@ -35,7 +35,10 @@ typedef void* fkv_stream_t;
 enum {
   /* Wavefront gather/scatter kernel that loads and stores pinned host memory
    * directly (zero-copy over PCIe).  Same role as the reference kernel mode,
-   * csrc/transfer.cu:123-129. */
+   * csrc/transfer.cu:123-129.  Calls of at most 128 pieces (16 KiB D2H,
+   * 8 KiB H2D, each within one chunk) and 4 MiB take a small-transfer kernel
+   * whose arguments carry every piece's addresses (FLEXKV_SMALL_KERNEL=0
+   * turns it off); larger calls take the tiled kernel. */
   FKV_XFER_KERNEL = 0,
   /* Copy-engine path: a gather kernel packs the selected chunks into a
    * contiguous HBM staging buffer and the SDMA engines move maximal
