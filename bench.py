@@ -225,6 +225,32 @@ def device_ceilings(timeout_s: float = 180.0):
     return out
 
 
+def c_abi_latency(timeout_s: float = 120.0):
+    """Per-call latency through the C-ABI from the call_latency program built
+    beside the library (1-block and 16-block kernel-mode calls with their
+    stream synchronisation, and the launch floors beside them), run as a
+    child process before this process touches the GPU.  None when the
+    program is missing or fails."""
+    exe = os.path.join(ROOT, "flexkv_amd", "call_latency")
+    if not os.path.exists(exe):
+        log("call_latency not built; C-ABI latency not measured")
+        return None
+    try:
+        res = subprocess.run([exe], capture_output=True, text=True, timeout=timeout_s)
+    except subprocess.TimeoutExpired:
+        log("call_latency timed out")
+        return None
+    if res.returncode != 0:
+        log(f"call_latency failed ({res.returncode}): {res.stderr.strip()[-300:]}")
+        return None
+    out = json.loads(res.stdout.strip().splitlines()[-1])
+    out["what"] = ("flexkv_amd/call_latency: median of 400 calls, each with "
+                   "hipStreamSynchronize, in a C++ process")
+    log(f"C-ABI call latency: 1 block {out['fkv_1x1_h2d_us']} / {out['fkv_1x1_d2h_us']} us "
+        f"(H2D / D2H), empty kernel with arguments {out['args_kernel_us']} us")
+    return out
+
+
 def link_peaks(wl: Workload, reps: int = 8):
     """Best-of-reps 1 GiB contiguous pinned copies each way, and a 4 GiB
     device-to-device copy, timed with events on one stream."""
@@ -1308,8 +1334,9 @@ def main() -> int:
         print("bench.py measures one GPU: the transfer path is per-GPU (one PCIe link, one HBM); "
               "multi-GPU runs are out of scope for this package", file=sys.stderr)
         return 2
-    ceilings = (None if (args.quick or args.counters or args.layerwise_only or args.worker_ops)
-                else device_ceilings())
+    full_run = not (args.quick or args.counters or args.layerwise_only or args.worker_ops)
+    ceilings = device_ceilings() if full_run else None
+    abi_latency = c_abi_latency() if full_run else None
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 2
@@ -1493,6 +1520,7 @@ def main() -> int:
         log(f"engine put and get: {result['engine_put_get']}")
         result["call_latency"] = call_latency(wl)
         log(f"call latency: {result['call_latency']}")
+        result["call_latency_c_abi"] = abi_latency
         result["worker_ops"] = worker_ops(wl)
         log(f"worker ops: {result['worker_ops']}")
         result["overlap_with_compute"] = overlap_with_compute(wl)

@@ -1,6 +1,8 @@
-"""Compile libflexkv_hip.so in-tree with hipcc for gfx950, and the
-hbm_ceiling program that measures the device's plain read / write / copy
-rates (bench.py reports them beside the gather's roofline).
+"""Compile libflexkv_hip.so in-tree with hipcc for gfx950, the hbm_ceiling
+program that measures the device's plain read / write / copy rates
+(bench.py reports them beside the gather's roofline), and the call_latency
+program that times small fkv_transfer_kv_blocks calls against the launch
+floors beside them.
 
     python -m flexkv_amd.build_ext
 """
@@ -18,6 +20,8 @@ SOURCES = [os.path.join(HERE, "csrc", f)
 OUT = os.path.join(HERE, "libflexkv_hip.so")
 CEILING_SOURCE = os.path.join(HERE, "csrc", "hbm_ceiling.hip")
 CEILING_OUT = os.path.join(HERE, "hbm_ceiling")
+LATENCY_SOURCE = os.path.join(HERE, "csrc", "call_latency.hip")
+LATENCY_OUT = os.path.join(HERE, "call_latency")
 ARCH = "gfx950"
 
 
@@ -44,6 +48,12 @@ def ceiling_command() -> list:
     return [hipcc(), f"--offload-arch={ARCH}", *COMMON, CEILING_SOURCE, "-o", CEILING_OUT + ".tmp"]
 
 
+def latency_command() -> list:
+    return [hipcc(), f"--offload-arch={ARCH}", *COMMON, "-I", os.path.join(ROOT, "include"),
+            LATENCY_SOURCE, "-o", LATENCY_OUT + ".tmp", "-L", HERE, "-lflexkv_hip",
+            "-Wl,-rpath,$ORIGIN"]
+
+
 def _run(cmd: list, out: str, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -56,6 +66,7 @@ def _run(cmd: list, out: str, verbose: bool) -> None:
 def build(verbose: bool = False) -> str:
     _run(command(), OUT, verbose)
     _run(ceiling_command(), CEILING_OUT, verbose)
+    _run(latency_command(), LATENCY_OUT, verbose)
     return OUT
 
 
