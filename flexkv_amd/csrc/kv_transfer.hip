@@ -1313,6 +1313,25 @@ size_t layerwise_min_copy_bytes() {
   return v > 0 ? static_cast<size_t>(v) : 1;
 }
 
+constexpr int kLayerwiseCeKernelGroups = 0;
+
+// Leading layer groups a copy-engine layer-wise handle moves with the
+// zero-copy kernel before its engines start (FLEXKV_LAYERWISE_CE_KERNEL_GROUPS,
+// default 0: every group on the engines; at most all groups but one).  A
+// one-group window is bound by the engines' per-copy cost (one copy per block
+// of one group's rows), while a consumer waiting for the first group has
+// nothing else to run, so the kernel's compute units cost it little then.
+// Measured on MI355X at the Llama-3-8B shape with one layer per group, one
+// kernel group brings the first group in after 1.3 ms instead of 2.1 ms and
+// ends a prefill overlapped with 8 or 12 bf16 GEMMs per layer 1.1-1.7%
+// sooner, but one with 4 GEMMs per layer, which the transfer outlasts,
+// 0.5% later.
+int layerwise_kernel_lead_groups(int ngroups) {
+  const char* e = getenv("FLEXKV_LAYERWISE_CE_KERNEL_GROUPS");
+  const int v = e ? atoi(e) : kLayerwiseCeKernelGroups;
+  return std::max(0, std::min(v, ngroups - 1));
+}
+
 // The lane's pipeline stream: a stream with a full CU mask, so it has a
 // hardware queue of its own and its scatters never wait behind compute
 // kernels queued on a shared queue.
@@ -1333,17 +1352,22 @@ int pipeline_stream(CopyLane& ln, int dev, hipStream_t* out) {
   return 0;
 }
 
-// A copy-engine handle on a device whose engines cannot be set up: every
-// group moves host-to-device with the zero-copy kernel on the pipeline stream
-// (the layer-wise kernel path's compute units), its event recorded after it.
-int layerwise_kernel_groups(fkv_transfer_handle_s* h, hipStream_t work) {
+// Groups [first_group, end_group) of a copy-engine handle (all groups when
+// end_group < 0) move host-to-device with the zero-copy kernel on the
+// pipeline stream (the layer-wise kernel path's compute units), each group's
+// event recorded after it: every group on a device whose engines cannot be
+// set up, and the leading groups a handle moves before its engines start.
+int layerwise_kernel_groups(fkv_transfer_handle_s* h, hipStream_t work, int first_group = 0,
+                            int end_group = -1) {
   const Geometry& g = h->geo;
   DeviceState& d = g_dev[h->dev];
   const int cus = std::min(kAutoLayerwiseH2DCus, d.num_cus);
   const int grid_cap = cus * d.occ_zero_copy[1];
   char* cpu_dev = g.cpu_info.dev_ptr + g.startoff + static_cast<int64_t>(g.start_layer) * g.cls;
-  int group = 0;
-  for (int g0 = 0; g0 < g.num_layers; g0 += h->granularity, ++group) {
+  const int end_layer = end_group < 0 ? g.num_layers
+                                      : std::min(g.num_layers, end_group * h->granularity);
+  int group = first_group;
+  for (int g0 = first_group * h->granularity; g0 < end_layer; g0 += h->granularity, ++group) {
     const int gend = std::min(g.num_layers, g0 + h->granularity);
     for (int l0 = g0; l0 < gend; l0 += g.layers_per_launch()) {
       const int nl = std::min(g.layers_per_launch(), gend - l0);
@@ -1360,8 +1384,9 @@ int layerwise_kernel_groups(fkv_transfer_handle_s* h, hipStream_t work) {
   return 0;
 }
 
-// The driver's work: layer groups in order, each cut into pieces of whole
-// blocks that fit a staging half; SDMA copies (one per block: the group's
+// The driver's work: the leading group(s) with the zero-copy kernel (see
+// layerwise_kernel_lead_groups), then the other layer groups in order, each
+// cut into pieces of whole blocks that fit a staging half; SDMA copies (one per block: the group's
 // rows are contiguous in block-wise host memory) on the wide engine set,
 // double-buffered; each piece's scatter on the pipeline stream after a
 // system-scope acquire; done[g] after the group's last piece.  The host
@@ -1414,8 +1439,11 @@ int layerwise_ce_run(fkv_transfer_handle_s* h, CopyLane& ln, hipStream_t work) {
     gpw = std::max(1, std::min(gpw, lpl / G));
     while (gpw > 1 && static_cast<size_t>(gpw) * group_row > half) --gpw;
   }
+  // The leading groups move with the zero-copy kernel, alone on the link;
+  // the engines start on the next group once they have landed.
+  const int lead = layerwise_kernel_lead_groups(ngroups);
   std::vector<Piece> pieces;
-  for (int grp = 0, ramp = 1; grp < ngroups; ramp = std::min(2 * ramp, gpw)) {
+  for (int grp = lead, ramp = 1; grp < ngroups; ramp = std::min(2 * ramp, gpw)) {
     const int take = std::min({gpw, ramp, std::max(1, (ngroups - grp) / 2)});
     const int l0 = grp * G;
     const int nl = std::min(take * G, g.num_layers - l0);
@@ -1453,6 +1481,13 @@ int layerwise_ce_run(fkv_transfer_handle_s* h, CopyLane& ln, hipStream_t work) {
     return issue_sdma(d, ln, runs, ln.staging + (pi & 1) * half, true, pi & 1, d.cpu_agent,
                       /*wide=*/true);
   };
+  if (lead > 0) {
+    if ((rc = layerwise_kernel_groups(h, work, 0, lead))) return rc;
+    next_group = lead;
+    // engine copies started beside the kernel share the link with it, and the
+    // first group lands no earlier than with the engines alone
+    FKV_HIP(hipEventSynchronize(h->done[lead - 1]));
+  }
   for (int pi = 0; pi < std::min(np, 2); ++pi)
     if ((rc = queue_copies(pi))) return rc;
   for (int pi = 0; pi < np; ++pi) {

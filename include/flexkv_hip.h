@@ -197,7 +197,9 @@ int fkv_scatter_kv_blocks(int num_blocks, int num_layers, const int64_t* gpu_blo
  * the rest arrive.  Every window spreads its copies over the wide engine
  * set, FLEXKV_SDMA_ENGINES_WIDE engines (default 8, engines 0-7:
  * host-to-device copies on engines 8-15 slow compute kernels running beside
- * them about twofold).
+ * them about twofold).  FLEXKV_LAYERWISE_CE_KERNEL_GROUPS=n (default 0)
+ * moves the first n groups with the zero-copy kernel before the engines
+ * start, so the first group lands sooner.
  * fkv_handle_stream_wait and fkv_handle_wait first wait on the host until
  * the group's event exists (its copies have landed), fkv_handle_query
  * reports 0 until then.

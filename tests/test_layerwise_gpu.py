@@ -185,12 +185,13 @@ def test_transfer_stream_helper(num_cus):
     assert "num_cus" in _lib.last_error()
 
 
-def _ce_copies_per_block(L, G, layer_row, half, min_copy, lpl=128):
+def _ce_copies_per_block(L, G, layer_row, half, min_copy, lpl=128, lead=0):
     """Engine copies per block the copy-engine layer-wise pipeline plans for a
-    block-wise host cache: windows of whole layer groups, up to `min_copy`
-    bytes per block, growing 1, 2, 4, ... groups and near the end holding at
-    most half of the groups left; each cut into layer windows whose rows fit
-    a staging half."""
+    block-wise host cache: the first `lead` groups (at most all but one) move
+    with the zero-copy kernel; then windows of whole layer groups, up to
+    `min_copy` bytes per block, growing 1, 2, 4, ... groups and near the end
+    holding at most half of the groups left; each cut into layer windows whose
+    rows fit a staging half."""
     ngroups = -(-L // G)
     group_row = min(G, L) * layer_row
     gpw = 1
@@ -198,7 +199,7 @@ def _ce_copies_per_block(L, G, layer_row, half, min_copy, lpl=128):
         gpw = max(1, min(-(-min_copy // group_row), lpl // G))
         while gpw > 1 and gpw * group_row > half:
             gpw -= 1
-    copies, grp, ramp = 0, 0, 1
+    copies, grp, ramp = 0, max(0, min(lead, ngroups - 1)), 1
     while grp < ngroups:
         take = min(gpw, ramp, max(1, (ngroups - grp) // 2))
         ramp = min(2 * ramp, gpw)
@@ -212,20 +213,24 @@ def _ce_copies_per_block(L, G, layer_row, half, min_copy, lpl=128):
     return copies
 
 
-@pytest.mark.parametrize("staging_kib,gran,min_copy",
-                         [(0, 1, None), (256, 1, None), (256, 3, None), (96, 2, None),
-                          (0, 1, 1), (0, 2, 64 << 10)])
-def test_ce_pipeline_pieces_and_copies(staging_kib, gran, min_copy, monkeypatch):
+@pytest.mark.parametrize("staging_kib,gran,min_copy,lead",
+                         [(0, 1, None, None), (256, 1, None, None), (256, 3, None, None),
+                          (96, 2, None, None), (0, 1, 1, None), (0, 2, 64 << 10, None),
+                          (0, 1, None, 1), (256, 1, None, 3), (0, 6, None, 1)])
+def test_ce_pipeline_pieces_and_copies(staging_kib, gran, min_copy, lead, monkeypatch):
     """The copy-engine layer-wise pipeline with staging small enough that a
     group spans several pieces, or a group's rows are cut into layer windows,
-    and with several groups per engine copy: each group's layers match the
-    oracle as soon as that group alone is waited for, every group's event
-    fires, and the engines moved the planned copies per block (the library's
-    profile)."""
+    with several groups per engine copy, and with 0 (the default), 1 or 3
+    leading groups on the zero-copy kernel (one group in all: none):
+    each group's layers match the oracle as soon as that group alone is
+    waited for, every group's event fires, and the engines moved the planned
+    copies per block (the library's profile)."""
     from flexkv_amd import _lib
     from gpu_util import DeviceCase
     if min_copy is not None:
         monkeypatch.setenv("FLEXKV_LAYERWISE_CE_MIN_COPY_BYTES", str(min_copy))
+    if lead is not None:
+        monkeypatch.setenv("FLEXKV_LAYERWISE_CE_KERNEL_GROUPS", str(lead))
     L, n = 6, 37
     case = KVCase(layers_total=L, num_layers=L, start_layer=0, kv=2, ng=64, nh=96, tokens=16,
                   heads=4, dim=64).fill(seed=60 + gran)              # 8 KiB chunks
@@ -259,7 +264,8 @@ def test_ce_pipeline_pieces_and_copies(staging_kib, gran, min_copy, monkeypatch)
     assert prof["dma_batches"] == 1, prof
     half = (staging_kib << 9) if staging_kib else 1 << 29
     per_block = _ce_copies_per_block(L, gran, 2 * s["chunk"], half,
-                                     256 << 10 if min_copy is None else min_copy)
+                                     256 << 10 if min_copy is None else min_copy,
+                                     lead=0 if lead is None else lead)
     assert prof["dma_copies"] == per_block * n, (prof, per_block)
     if min_copy == 1:
         assert per_block == L // gran       # one copy per block and group
