@@ -113,7 +113,24 @@ struct DeviceState {
   // host-to-device engines of the copy-engine layer-wise pipeline: every
   // engine device-to-host did not take, up to FLEXKV_SDMA_ENGINES_LAYERWISE
   std::vector<hsa_amd_sdma_engine_id_t> engines_wide;
+  // Engines each direction takes while the other direction's copy-engine
+  // transfer is in flight (FLEXKV_SDMA_DUPLEX_D2H of engines 0-7 for
+  // device-to-host, the rest of 0-7 for host-to-device); empty: no split.
+  std::vector<hsa_amd_sdma_engine_id_t> engines_duplex[2];
+  // copy-engine transfers in flight per direction [D2H, H2D]
+  std::atomic<int> busy[2] = {0, 0};
   CopyLane lane[2];                                    // [D2H, H2D]
+};
+
+// Counts a copy-engine transfer of one direction as in flight on a device
+// for its lifetime (DeviceState::busy), so the other direction's copies take
+// the duplex engine split meanwhile.
+struct BusyMark {
+  std::atomic<int>& n;
+  explicit BusyMark(std::atomic<int>& c) : n(c) { n.fetch_add(1, std::memory_order_relaxed); }
+  ~BusyMark() { n.fetch_sub(1, std::memory_order_relaxed); }
+  BusyMark(const BusyMark&) = delete;
+  BusyMark& operator=(const BusyMark&) = delete;
 };
 
 extern DeviceState g_dev[kMaxDevices];

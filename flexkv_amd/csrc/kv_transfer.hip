@@ -931,6 +931,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
     std::lock(own, other);
   else
     own.lock();
+  BusyMark busy(d.busy[h2d ? 1 : 0]);
   DeviceGuard guard;
   int rc = guard.set(dev);
   if (rc) return rc;
@@ -1415,6 +1416,7 @@ int layerwise_ce_run(fkv_transfer_handle_s* h, CopyLane& ln, hipStream_t work) {
     last_error().clear();
     return layerwise_kernel_groups(h, work);
   }
+  BusyMark busy(d.busy[1]);
   const size_t half = ln.staging_bytes / 2;
   struct Piece {
     int l0, nl, b0, nb, group;   // group: the last layer group the piece completes

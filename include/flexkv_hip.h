@@ -53,7 +53,9 @@ enum {
    * has its own staging and engines (device-to-host engines 0-3,
    * host-to-device 4-7; host-to-device copies shorter than 1 MiB on average
    * spread over engines 0-7), so a D2H and an H2D transfer from different
-   * threads run at the same time.  Transfers under
+   * threads run at the same time; while both run, their copies split
+   * engines 0-7 (device-to-host 0-4, host-to-device 5-7;
+   * FLEXKV_SDMA_DUPLEX_D2H), which balances the two.  Transfers under
    * FLEXKV_CE_MIN_BYTES (default 8 MiB) or whose
    * engine copies would move under 128 KiB each move with the zero-copy
    * kernel instead, where the engines' per-copy cost would dominate, and so
