@@ -26,8 +26,8 @@ namespace {
 
 // SDMA engines each direction spreads its copies over.  Measured on MI355X
 // (16 engines) with 2 MiB copies: four move 56-57 GB/s either way, and
-// device-to-host drops to 47 GB/s on eight.  A D2H and an H2D together move
-// 69 GB/s on engines 0-3 and 4-7.
+// device-to-host drops to 47 GB/s on eight.  While both directions run they
+// take the duplex split instead (kDefaultDuplexD2HEngines).
 constexpr int kDefaultSdmaEngines[2] = {4, 4};   // [D2H, H2D]
 // Engines 0-7.  Host-to-device copies on engines 8-15 slow compute kernels
 // running beside them about twice over, at any copy size: 160 bf16 GEMMs
@@ -382,9 +382,8 @@ int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr) {
     q.cpu = nearest;
   // Each direction takes `want` engines, from engines 0-7 first;
   // host-to-device takes those device-to-host did not take before those it
-  // did, so with the default four the two directions run side by side on
-  // disjoint engines (MI355X: 69 GB/s in both directions together on
-  // engines 0-3 and 4-7, 56-57 GB/s one way).
+  // did, so with the default four the two directions' one-way sets are
+  // disjoint (engines 0-3 and 4-7, 56-57 GB/s one way).
   if (sdma_engines_wanted(0) == 0 || sdma_engines_wanted(1) == 0)
     return fail(kInval, "copy engines turned off (FLEXKV_SDMA_ENGINES=0)");
   uint32_t taken = 0;

@@ -159,8 +159,9 @@ constexpr int64_t kCeMinRunBytes = int64_t(128) << 10;
 // Host-to-device engine copies shorter than this on average spread over the
 // wide engine set (engines 0-7) instead of the direction's four.  Measured on
 // MI355X: 640 KiB copies (Llama-3-70B TP-8 shard) 51.9 -> 56.4 GB/s, 256 KiB
-// copies 39.5 -> 48.8 GB/s, 2 MiB copies 56.8 -> 57.0 GB/s; the four keep a
-// D2H beside it on engines of its own (69.8 GB/s together against 66.2).
+// copies 39.5 -> 48.8 GB/s, 2 MiB copies 56.8 -> 57.0 GB/s, so longer copies
+// keep the direction's four.  While a D2H is in flight, host-to-device copies
+// of any size take the duplex split instead (issue_sdma).
 constexpr int64_t kWideCopyBytes = int64_t(1) << 20;
 // The piece of a copy-engine transfer that runs without engine copies beside
 // it (the first gather, the last scatter) is cut to 1 / kEdgePieceDiv of a
