@@ -10,7 +10,7 @@ predecessors are already queued on the same in-order worker.
 from __future__ import annotations
 
 from collections import OrderedDict
-from typing import Callable, Dict, List, Optional, Tuple
+from typing import Callable, List, Optional, Tuple
 
 from ..common.transfer import TransferOp, TransferOpGraph, TransferType
 

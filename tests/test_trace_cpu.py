@@ -1,7 +1,6 @@
 """Op trace ranges: the reference's range name for a worker op
 (flexkv/transfer/worker.py:160-162), ranges that nest and unwind on errors,
 and no-ops where roctx is switched off."""
-import numpy as np
 import pytest
 import torch
 

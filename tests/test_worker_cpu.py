@@ -2,7 +2,6 @@
 lifecycle, and GPUCPUTransferWorker's argument mapping
 (flexkv/transfer/worker.py:49-342)."""
 import multiprocessing as mp
-import time
 
 import numpy as np
 import pytest
