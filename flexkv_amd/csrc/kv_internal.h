@@ -108,6 +108,8 @@ struct DeviceState {
   // set-up failed: copy-engine transfers on this device use the zero-copy
   // kernel from then on
   std::atomic<bool> sdma_failed{false};
+  // a staging allocation failed for want of device memory (warned once)
+  std::atomic<bool> staging_oom_warned{false};
   hsa_agent_t gpu_agent{}, cpu_agent{};
   std::vector<hsa_amd_sdma_engine_id_t> engines[2];   // [D2H, H2D]
   // host-to-device engines of the copy-engine layer-wise pipeline: every

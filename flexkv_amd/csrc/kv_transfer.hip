@@ -912,6 +912,22 @@ int transfer_zero_copy_noalloc(const Geometry& g, hipStream_t stream, int dev, i
 //  H2D: queue the copies of the first two pieces; per piece: wait for its
 //  copies -> system-scope acquire -> scatter kernel; once that has read the
 //  half, queue the copies of the piece two ahead into it.
+// Staging for a copy-engine transfer (ensure_staging): 0; kSdmaUnavailable
+// when the device has no memory left for it, so the transfer moves with the
+// zero-copy kernel instead (warned once per device; later transfers try the
+// allocation again); or another error.
+int staging_or_fallback(DeviceState& d, int dev, CopyLane& ln, size_t need_half) {
+  const int rc = ensure_staging(ln, need_half);
+  if (rc != static_cast<int>(hipErrorOutOfMemory)) return rc;
+  (void)hipGetLastError();
+  if (!d.staging_oom_warned.exchange(true))
+    fprintf(stderr, "flexkv: no device memory for copy-engine staging on device %d (%s); "
+            "such transfers use the zero-copy kernel until the allocation succeeds\n", dev,
+            last_error().c_str());
+  last_error().clear();
+  return kSdmaUnavailable;
+}
+
 int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   DeviceState& d = g_dev[dev];
   CopyLane& ln = d.lane[h2d ? 1 : 0];
@@ -947,8 +963,8 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   int nl_piece = std::min(g.num_layers, g.layers_per_launch());
   while (nl_piece > 1 && static_cast<size_t>(nl_piece) * g.kv * g.chunk > half_default) nl_piece /= 2;
   const size_t row_bytes = static_cast<size_t>(nl_piece) * g.kv * g.chunk;
-  rc = ensure_staging(ln, row_bytes);
-  if (rc) return rc;
+  rc = staging_or_fallback(d, dev, ln, row_bytes);
+  if (rc) return rc;   // kSdmaUnavailable: the caller moves it with the zero-copy kernel
   if ((rc = ensure_sdma(d, dev, ln.staging))) {
     // nothing has been queued yet: the caller moves this transfer, and every
     // later one on the device, with the zero-copy kernel
@@ -1407,7 +1423,9 @@ int layerwise_ce_run(fkv_transfer_handle_s* h, CopyLane& ln, hipStream_t work) {
   const size_t row_max = static_cast<size_t>(nl_max) * g.kv * g.chunk;
   // a half holds at least one block's row of one layer, so every window fits
   const size_t one_layer = static_cast<size_t>(g.kv) * g.chunk;
-  if ((rc = ensure_staging(ln, std::max(std::min(row_max, half_default), one_layer)))) return rc;
+  rc = staging_or_fallback(d, h->dev, ln, std::max(std::min(row_max, half_default), one_layer));
+  if (rc == kSdmaUnavailable) return layerwise_kernel_groups(h, work);
+  if (rc) return rc;
   if ((rc = ensure_sdma(d, h->dev, ln.staging))) {
     // nothing has been queued yet: this handle, and every later copy-engine
     // transfer on the device, moves with the zero-copy kernel

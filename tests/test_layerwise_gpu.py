@@ -336,6 +336,41 @@ print("layer-wise copy-engine handles match the oracle", flush=True)
 """
 
 
+def test_ce_handle_without_staging_memory():
+    """A copy-engine layer-wise handle whose staging cannot be allocated moves
+    every group with the zero-copy kernel, events and bytes as the engines
+    would have left them."""
+    from flexkv_amd import _lib
+    from gpu_util import DeviceCase
+    L, n = 4, 64
+    case = KVCase(layers_total=L, num_layers=L, start_layer=0, kv=2, ng=128, nh=128, tokens=16,
+                  heads=8, dim=128).fill(seed=80)
+    s = case.strides()
+    gids = inputs.distinct_ids(81, n, 128)
+    cids = inputs.distinct_ids(82, n, 128)
+    dc = DeviceCase(case)
+    fresh = case.host ^ np.uint16(0x3C3C)
+    dc.set_host(fresh)
+    dc.set_gpu([np.zeros_like(g) for g in case.gpu])
+    exp = [np.zeros_like(g) for g in case.gpu]
+    oracle.transfer_kv_blocks(gids, exp, s["gpu_kv"], s["gpu_block"], cids, fresh, s["cpu_kv"],
+                              s["cpu_layer"], s["cpu_block"], s["chunk"], 0, True)
+    _lib.release_staging()
+    _lib.set_staging_bytes(1 << 40)
+    try:
+        _lib.profile_enable(True)
+        with _abi_layerwise(dc, gids.copy(), cids.copy(), True, 1, ce=True) as hnd:
+            for g in range(L):
+                hnd.wait(g)
+                assert np.array_equal(dc.gpu_np()[g], exp[g]), g
+        prof = _lib.profile_read()
+    finally:
+        _lib.profile_enable(False)
+        _lib.set_staging_bytes(0)
+        _lib.release_staging()
+    assert prof["dma_batches"] == 0 and prof["kernel_launches"] == L, prof
+
+
 def test_ce_handle_without_engines():
     """With the library's engines turned off (FLEXKV_SDMA_ENGINES=0), the first
     copy-engine layer-wise handle finds the engines unavailable inside its

@@ -604,6 +604,34 @@ def test_small_kernel_grid_cap(dev, cus):
                    transfer_cus=cus)
 
 
+def test_copy_engine_without_staging_memory(dev):
+    """When the staging buffer cannot be allocated (here: asked for 1 TiB, more
+    than the device holds), copy-engine transfers move with the zero-copy
+    kernel instead of failing, and nothing reaches the engines; with staging
+    back to its default the engines carry the same call again."""
+    from flexkv_amd import _lib
+    case = KVCase(layers_total=4, num_layers=4, start_layer=0, kv=2, ng=300, nh=300, tokens=16,
+                  heads=8, dim=128).fill(seed=5)          # 32 KiB chunks, 64 MiB per call
+    gids = inputs.distinct_ids(7, 256, 300)
+    cids = inputs.distinct_ids(8, 256, 300)
+    _lib.release_staging()
+    _lib.set_staging_bytes(1 << 40)
+    try:
+        _lib.profile_enable(True)
+        check_case(case, gids, cids, 1)
+        prof = _lib.profile_read()
+        assert prof["dma_batches"] == 0 and prof["kernel_launches"] >= 2, prof
+        _lib.set_staging_bytes(0)
+        _lib.profile_enable(True)
+        check_case(case, gids, cids, 1)
+        prof = _lib.profile_read()
+        assert prof["dma_batches"] == 2, prof
+    finally:
+        _lib.profile_enable(False)
+        _lib.set_staging_bytes(0)
+        _lib.release_staging()
+
+
 @pytest.mark.parametrize("mode", MODES)
 def test_duplicate_sources_and_single_block(dev, mode):
     case = KVCase(layers_total=2, num_layers=2, start_layer=0, kv=2, ng=8, nh=16, tokens=16,
