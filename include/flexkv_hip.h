@@ -60,7 +60,9 @@ enum {
    * engine copies would move under 128 KiB each move with the zero-copy
    * kernel instead, where the engines' per-copy cost would dominate, and so
    * does every transfer on a device whose engines cannot be set up (one
-   * warning on stderr; FLEXKV_SDMA_ENGINES=0 turns them off).  Same role as
+   * warning on stderr; FLEXKV_SDMA_ENGINES=0 turns them off) and every
+   * transfer whose staging buffer cannot be allocated for want of device
+   * memory (one warning; the next transfer tries again).  Same role as
    * the reference CE mode, csrc/transfer.cu:97-121. */
   FKV_XFER_CE = 1,
   /* The reference's copy-engine algorithm restated literally: one
