@@ -427,6 +427,54 @@ def test_concurrent_threads_mixed_paths(dev, layout):
                         (mode, l, k)
 
 
+def test_duplex_copy_engine_transfers(dev):
+    """A copy-engine D2H and a copy-engine H2D of 128 MiB each, repeated from
+    two threads so that they overlap over many staging halves: while both
+    are in flight their copies take the duplex engine split, and halves
+    issued before, during and after the overlap land on different engine
+    sets.  Every byte matches."""
+    import threading
+    from gpu_util import DeviceCase, abi_transfer
+    from flexkv_amd import _lib
+    case = KVCase(layers_total=8, num_layers=8, start_layer=0, kv=2, ng=600, nh=600, tokens=16,
+                  heads=8, dim=128).fill(seed=91)         # 32 KiB chunks
+    dc = DeviceCase(case)
+    g_all = inputs.distinct_ids(92, 512, 600)
+    c_all = inputs.distinct_ids(93, 512, 600)
+    (g_d, c_d), (g_h, c_h) = (g_all[:256], c_all[:256]), (g_all[256:], c_all[256:])
+    fresh = case.host.copy()
+    fresh[c_h] ^= np.asarray(0x5A5A, dtype=case.dtype)
+    dc.set_host(fresh)
+    _lib.set_staging_bytes(64 << 20)                       # 32 MiB halves: 4+ halves a call
+    errors = []
+
+    def run(h2d):
+        try:
+            st = torch.cuda.Stream()
+            g, c = (g_h, c_h) if h2d else (g_d, c_d)
+            for _ in range(6):
+                abi_transfer(dc, g, c, h2d=h2d, mode=1, stream=st)
+            st.synchronize()
+        except Exception as e:   # surfaced below
+            errors.append(e)
+    try:
+        th = [threading.Thread(target=run, args=(h,)) for h in (False, True)]
+        for t in th:
+            t.start()
+        for t in th:
+            t.join()
+    finally:
+        _lib.set_staging_bytes(0)
+        _lib.release_staging()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    host, gpu = dc.host_np(), dc.gpu_np()
+    for l in range(8):
+        for k in range(2):
+            assert np.array_equal(host[c_d, l, k][:, 0], case.gpu[l][k][g_d]), ("D2H", l, k)
+            assert np.array_equal(gpu[l][k][g_h], fresh[c_h, l, k][:, 0]), ("H2D", l, k)
+
+
 # Separate K and V allocations (fkv_transfer_kv_blocks_kv_ptrs): the same
 # bytes must move as with K and V halves of one allocation, so the oracle of
 # the combined layout is the expectation.  Geometry 7 (130 layers) needs three
