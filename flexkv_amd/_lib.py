@@ -53,6 +53,7 @@ EXPORTED_SYMBOLS = (
     "fkv_host_unregister",
     "fkv_set_staging_bytes",
     "fkv_release_staging",
+    "fkv_prepare",
     "fkv_finalize",
     "fkv_profile_enable",
     "fkv_profile_read",
@@ -156,6 +157,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.fkv_set_staging_bytes.argtypes = [c_sz]
     lib.fkv_release_staging.restype = c_int
     lib.fkv_release_staging.argtypes = []
+    lib.fkv_prepare.restype = c_int
+    lib.fkv_prepare.argtypes = [c_int]
     lib.fkv_finalize.restype = c_int
     lib.fkv_finalize.argtypes = []
     lib.fkv_profile_enable.restype = c_int
@@ -248,3 +251,8 @@ def set_staging_bytes(nbytes: int) -> None:
 
 def release_staging() -> None:
     check(load().fkv_release_staging(), "fkv_release_staging")
+
+
+def prepare(device: int = -1) -> None:
+    """fkv_prepare: set a device up for transfers before the first one."""
+    check(load().fkv_prepare(int(device)), "fkv_prepare")

@@ -347,6 +347,14 @@ int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, cha
 // lane stalled and the device's engines failed, and returns
 // hipErrorLaunchTimeOut with the error message set; otherwise 0.
 int sdma_wait(DeviceState& d, CopyLane& lane, int half, bool spin = false);
+// Readies a lane (its mutex held, its staging allocated, the engines set up)
+// before its first transfer: polled completion signals for `copies_per_half`
+// copies on each staging half (the pools grow on demand beyond that), and
+// one 4 KiB copy between `host` (pinned, at least 64 KiB) and staging on each
+// engine the direction may take, waited for, so work the driver queued on
+// those engines (clearing newly allocated device memory) is done first.
+int sdma_prepare_lane(DeviceState& d, CopyLane& lane, bool h2d, size_t copies_per_half,
+                      char* host, size_t host_bytes);
 // Waits for a lane's queued copies, then destroys its pooled signals and
 // events and frees its staging buffer (a stalled lane keeps its staging and
 // signals).  The lane's mutex must be held.

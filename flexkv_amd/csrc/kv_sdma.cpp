@@ -554,6 +554,61 @@ int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, cha
   return 0;
 }
 
+int sdma_prepare_lane(DeviceState& d, CopyLane& lane, bool h2d, size_t copies_per_half,
+                      char* host, size_t host_bytes) {
+  for (int h = 0; h < 2; ++h) {
+    while (lane.polled_pool[h].size() < copies_per_half) {
+      hsa_signal_t sg;
+      FKV_HSA(g_hsa.amd_signal_create(1, 0, nullptr, HSA_AMD_SIGNAL_AMD_GPU_ONLY, &sg));
+      lane.polled_pool[h].push_back(sg);
+    }
+  }
+  // every engine the direction may take: its one-way set, its side of the
+  // duplex split and, host-to-device, the wide set
+  const int dir = h2d ? 1 : 0;
+  std::vector<hsa_amd_sdma_engine_id_t> eng = d.engines[dir];
+  auto add = [&](const std::vector<hsa_amd_sdma_engine_id_t>& v) {
+    for (hsa_amd_sdma_engine_id_t e : v)
+      if (std::find(eng.begin(), eng.end(), e) == eng.end()) eng.push_back(e);
+  };
+  add(d.engines_duplex[dir]);
+  if (h2d) add(d.engines_wide);
+  const size_t bytes = 4096;
+  if (eng.size() * bytes > host_bytes || eng.size() * bytes > lane.staging_bytes)
+    return fail(kInval, "internal: %zu warm-up copies do not fit their buffers", eng.size());
+  std::vector<hsa_signal_t>& irq = lane.irq_pool[0];
+  while (irq.size() < eng.size()) {
+    hsa_signal_t sg;
+    FKV_HSA(g_hsa.signal_create(1, 0, nullptr, &sg));
+    irq.push_back(sg);
+  }
+  lane.queued[0].clear();
+  lane.wake[0].clear();
+  for (size_t i = 0; i < eng.size(); ++i) {
+    const hsa_signal_t sig = irq[i];
+    g_hsa.signal_store_screlease(sig, 1);
+    char* dev_p = lane.staging + i * bytes;
+    char* host_p = host + i * bytes;
+    const hsa_status_t st =
+        h2d ? g_hsa.async_copy_on_engine(dev_p, d.gpu_agent, host_p, d.cpu_agent, bytes, 0,
+                                         nullptr, sig, eng[i], false)
+            : g_hsa.async_copy_on_engine(host_p, d.cpu_agent, dev_p, d.gpu_agent, bytes, 0,
+                                         nullptr, sig, eng[i], false);
+    if (st != HSA_STATUS_SUCCESS) {
+      const char* m = nullptr;
+      (void)g_hsa.status_string(st, &m);
+      // copies queued so far are waited for below, so nothing is left in flight
+      const int w = sdma_wait(d, lane, 0, false);
+      (void)w;
+      return fail(static_cast<int>(hipErrorUnknown), "warm-up copy on an SDMA engine failed: %s",
+                  m ? m : "?");
+    }
+    lane.queued[0].push_back(sig);
+    lane.wake[0].push_back(sig);
+  }
+  return sdma_wait(d, lane, 0, false);
+}
+
 bool sdma_rect_available() { return g_hsa.async_copy_rect != nullptr; }
 
 }  // namespace fkv_detail

@@ -917,6 +917,12 @@ int transfer_zero_copy_noalloc(const Geometry& g, hipStream_t stream, int dev, i
 //  H2D: queue the copies of the first two pieces; per piece: wait for its
 //  copies -> system-scope acquire -> scatter kernel; once that has read the
 //  half, queue the copies of the piece two ahead into it.
+// fkv_prepare: polled completion signals it creates per staging half (one
+// per block of a 1024-block layer-wise window; the pools grow on demand),
+// and the pinned host buffer of its warm-up copies (4 KiB per engine).
+constexpr size_t kPrepareSignalsPerHalf = 1024;
+constexpr size_t kPrepareHostBytes = size_t(64) << 10;
+
 // Staging for a copy-engine transfer (ensure_staging): 0; kSdmaUnavailable
 // when the device has no memory left for it, so the transfer moves with the
 // zero-copy kernel instead (warned once per device; later transfers try the
@@ -1921,6 +1927,52 @@ int fkv_handle_release(fkv_transfer_handle h) {
   if (!h) return 0;
   if (!handle_unregister(h)) return fail(kInval, "handle %p is released or unknown", (void*)h);
   return handle_destroy(h);
+}
+
+int fkv_prepare(int device) {
+  try {
+    last_error().clear();
+    int dev = device;
+    if (dev < 0) FKV_HIP(hipGetDevice(&dev));
+    int count = 0;
+    FKV_HIP(hipGetDeviceCount(&count));
+    if (dev >= count || dev >= kMaxDevices)
+      return fail(kInval, "device %d out of range (%d devices)", dev, count);
+    DeviceGuard guard;
+    int rc = guard.set(dev);
+    if (rc) return rc;
+    if ((rc = ensure_device_basics(dev))) return rc;
+    // the library's code object is loaded with its first kernel launch
+    hipLaunchKernelGGL(acquire_system_kernel, dim3(1), dim3(64), 0, nullptr);
+    FKV_HIP(hipGetLastError());
+    FKV_HIP(hipStreamSynchronize(nullptr));
+    DeviceState& d = g_dev[dev];
+    if (d.sdma_failed.load()) return 0;   // copy-engine transfers use the zero-copy kernel
+    IdLease host;
+    if ((rc = ids_acquire(kPrepareHostBytes, &host.buf))) return rc;
+    for (int dir = 0; dir < 2; ++dir) {
+      CopyLane& ln = d.lane[dir];
+      std::lock_guard<std::mutex> lk(ln.mu);
+      rc = staging_or_fallback(d, dev, ln, 0);
+      if (rc == kSdmaUnavailable) return 0;   // no memory for staging: the transfer falls back
+      if (rc) return rc;
+      if ((rc = ensure_sdma(d, dev, ln.staging))) {
+        if (!d.sdma_failed.exchange(true))
+          fprintf(stderr, "flexkv: copy engines unavailable on device %d (%s); copy-engine "
+                  "transfers use the zero-copy kernel\n", dev, last_error().c_str());
+        last_error().clear();
+        return 0;
+      }
+      if ((rc = sdma_prepare_lane(d, ln, dir == 1, kPrepareSignalsPerHalf,
+                                  reinterpret_cast<char*>(host.buf.host), kPrepareHostBytes)))
+        return rc;
+    }
+    return 0;
+  } catch (const std::exception& e) {
+    return fail(static_cast<int>(hipErrorUnknown), "exception: %s", e.what());
+  } catch (...) {
+    return fail(static_cast<int>(hipErrorUnknown), "unknown exception");
+  }
 }
 
 int fkv_finalize(void) {

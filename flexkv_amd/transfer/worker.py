@@ -333,6 +333,10 @@ class GPUCPUTransferWorker(TransferWorkerBase):
         self.transfer_sms_d2h = transfer_sms_d2h
         self.use_ce_transfer_h2d = use_ce_transfer_h2d
         self.use_ce_transfer_d2h = use_ce_transfer_d2h
+        if use_ce_transfer_h2d or use_ce_transfer_d2h:
+            # staging, copy engines and their signals set up now, not in the
+            # first op (extension; the reference's worker has nothing to set up)
+            _lib.prepare(torch.cuda.current_device())
 
     def _transfer_impl(self, src_block_ids: np.ndarray, dst_block_ids: np.ndarray,
                        transfer_type: TransferType, layer_id: int, layer_granularity: int,

@@ -322,6 +322,19 @@ int fkv_host_unregister(void* ptr);
 int fkv_set_staging_bytes(size_t bytes);
 int fkv_release_staging(void);
 
+/* Set up `device` (-1: the current one) for transfers before the first one:
+ * loads the library's kernels, allocates both directions' copy-engine
+ * staging, sets up the SDMA engines, creates completion signals and runs one
+ * small copy on each engine the library may use, so work the driver queued
+ * there (clearing the new staging memory) is done.  Without it the first
+ * copy-engine transfer of each direction pays this, about 25 ms on MI355X.
+ * Copy engines that cannot be set up, or staging that does not fit in device
+ * memory, are not errors: transfers then use the zero-copy kernel, as they
+ * would have.  No counterpart in the reference; for callers that want their
+ * first transfer to cost what later ones do (a server before its first
+ * request; GPUCPUTransferWorker calls it when it uses the copy engines). */
+int fkv_prepare(int device);
+
 /* Release everything the library holds for the process: waits for and frees
  * layer-wise handles never released, synchronises and destroys streams made
  * by fkv_stream_create, waits for queued copy-engine copies and destroys

@@ -652,6 +652,34 @@ def test_small_kernel_grid_cap(dev, cus):
                    transfer_cus=cus)
 
 
+def test_prepare(dev):
+    """fkv_prepare sets up staging, engines and signals ahead of the first
+    transfer; it can run again, the transfers after it match the oracle, an
+    out-of-range device is refused, and staging that cannot be allocated is
+    not an error (transfers then fall back to the zero-copy kernel)."""
+    from flexkv_amd import _lib
+    _lib.release_staging()
+    _lib.prepare(-1)
+    _lib.prepare(0)
+    with pytest.raises(RuntimeError, match="out of range"):
+        _lib.prepare(4096)
+    case = KVCase(layers_total=4, num_layers=4, start_layer=0, kv=2, ng=300, nh=300, tokens=16,
+                  heads=8, dim=128).fill(seed=6)
+    gids = inputs.distinct_ids(9, 256, 300)
+    cids = inputs.distinct_ids(10, 256, 300)
+    try:
+        _lib.profile_enable(True)
+        check_case(case, gids, cids, 1)
+        assert _lib.profile_read()["dma_batches"] == 2
+        _lib.release_staging()
+        _lib.set_staging_bytes(1 << 40)
+        _lib.prepare(0)
+    finally:
+        _lib.profile_enable(False)
+        _lib.set_staging_bytes(0)
+        _lib.release_staging()
+
+
 def test_copy_engine_without_staging_memory(dev):
     """When the staging buffer cannot be allocated (here: asked for 1 TiB, more
     than the device holds), copy-engine transfers move with the zero-copy
