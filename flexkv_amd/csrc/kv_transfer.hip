@@ -1967,7 +1967,9 @@ int fkv_prepare(int device) {
                                   reinterpret_cast<char*>(host.buf.host), kPrepareHostBytes)))
         return rc;
     }
-    return 0;
+    // the stream of the copy-engine layer-wise pipeline's scatters
+    hipStream_t work = nullptr;
+    return pipeline_stream(d.lane[1], dev, &work);
   } catch (const std::exception& e) {
     return fail(static_cast<int>(hipErrorUnknown), "exception: %s", e.what());
   } catch (...) {

@@ -324,9 +324,10 @@ int fkv_release_staging(void);
 
 /* Set up `device` (-1: the current one) for transfers before the first one:
  * loads the library's kernels, allocates both directions' copy-engine
- * staging, sets up the SDMA engines, creates completion signals and runs one
- * small copy on each engine the library may use, so work the driver queued
- * there (clearing the new staging memory) is done.  Without it the first
+ * staging, sets up the SDMA engines, creates completion signals and the
+ * layer-wise pipeline's stream, and runs one small copy on each engine the
+ * library may use, so work the driver queued there (clearing the new staging
+ * memory) is done.  Without it the first
  * copy-engine transfer of each direction pays this, about 25 ms on MI355X.
  * Copy engines that cannot be set up, or staging that does not fit in device
  * memory, are not errors: transfers then use the zero-copy kernel, as they
