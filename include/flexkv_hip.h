@@ -328,7 +328,7 @@ int fkv_release_staging(void);
  * layer-wise pipeline's stream, and runs one small copy on each engine the
  * library may use, so work the driver queued there (clearing the new staging
  * memory) is done.  Without it the first
- * copy-engine transfer of each direction pays this, about 25 ms on MI355X.
+ * copy-engine transfer of each direction pays this, 25-50 ms on MI355X.
  * Copy engines that cannot be set up, or staging that does not fit in device
  * memory, are not errors: transfers then use the zero-copy kernel, as they
  * would have.  No counterpart in the reference; for callers that want their
