@@ -336,6 +336,58 @@ print("layer-wise copy-engine handles match the oracle", flush=True)
 """
 
 
+def test_mixed_copy_engine_load():
+    """Three threads at once on disjoint block sets, 40 rounds each: a
+    copy-engine D2H loop, a copy-engine H2D loop (the two share engines 0-7
+    through the duplex split) and copy-engine layer-wise handles (the H2D
+    lane, taken in turn with the H2D loop).  Every set's bytes match at the
+    end, and no call fails."""
+    import threading
+    from gpu_util import DeviceCase, abi_transfer
+    L, n = 8, 150
+    case = KVCase(layers_total=L, num_layers=L, start_layer=0, kv=2, ng=480, nh=480, tokens=16,
+                  heads=8, dim=128).fill(seed=95)                 # 32 KiB chunks, 75 MiB per op
+    g_all = inputs.distinct_ids(96, 3 * n, 480)
+    c_all = inputs.distinct_ids(97, 3 * n, 480)
+    sets = [(g_all[i * n:(i + 1) * n], c_all[i * n:(i + 1) * n]) for i in range(3)]
+    dc = DeviceCase(case)
+    fresh = case.host.copy()
+    for g, c in sets[1:]:
+        fresh[c] ^= np.asarray(0x6B6B, dtype=case.dtype)
+    dc.set_host(fresh)
+    errors = []
+
+    def loop(i):
+        try:
+            g, c = sets[i]
+            st = torch.cuda.Stream()
+            for _ in range(40):
+                if i < 2:
+                    abi_transfer(dc, g, c, h2d=(i == 1), mode=1, stream=st)
+                else:
+                    with _abi_layerwise(dc, g.copy(), c.copy(), True, 1, stream=st, ce=True) as h:
+                        for grp in range(L):
+                            h.wait(grp)
+            st.synchronize()
+        except Exception as e:   # surfaced below
+            errors.append((i, e))
+
+    th = [threading.Thread(target=loop, args=(i,)) for i in range(3)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    host, gpu = dc.host_np(), dc.gpu_np()
+    (ga, ca), (gb, cb), (gc, cc) = sets
+    for l in range(L):
+        for k in range(2):
+            assert np.array_equal(host[ca, l, k][:, 0], case.gpu[l][k][ga]), ("D2H", l, k)
+            assert np.array_equal(gpu[l][k][gb], fresh[cb, l, k][:, 0]), ("H2D", l, k)
+            assert np.array_equal(gpu[l][k][gc], fresh[cc, l, k][:, 0]), ("layer-wise", l, k)
+
+
 def test_ce_handle_without_staging_memory():
     """A copy-engine layer-wise handle whose staging cannot be allocated moves
     every group with the zero-copy kernel, events and bytes as the engines
