@@ -5,6 +5,7 @@
 //
 //   empty_kernel            an empty kernel without arguments
 //   args_kernel             an empty kernel with 1.6 KiB of arguments
+//   args{160,640,2560}_kernel  the same with 160 B, 640 B and 2.5 KiB
 //   copy_kernel_{h2d,d2h}   a plain 64 KiB copy kernel (16 workgroups, one
 //                           16-byte load and store per lane)
 //   memcpy_{h2d,d2h}        hipMemcpyAsync of one contiguous 64 KiB run
@@ -46,12 +47,14 @@ constexpr int64_t kCopyBytes = 64 << 10;
 
 __global__ void empty_kernel() {}
 
+template <int kWords>
 struct Blob {
-  uint64_t v[208];   // 1664 bytes of arguments
+  uint64_t v[kWords];
 };
 
-__global__ void args_kernel(Blob b, uint64_t* sink) {
-  if (threadIdx.x == 0 && b.v[0] == 12345) sink[0] = b.v[207];
+template <int kWords>
+__global__ void args_kernel(Blob<kWords> b, uint64_t* sink) {
+  if (threadIdx.x == 0 && b.v[0] == 12345) sink[0] = b.v[kWords - 1];
 }
 
 // n 16-byte vectors, one per thread (the launch covers exactly n threads)
@@ -72,6 +75,16 @@ double median_us(F f, int reps = 400) {
   }
   std::sort(t.begin(), t.end());
   return t[t.size() / 2];
+}
+
+// an empty kernel with kWords * 8 bytes of arguments, launched and synchronised
+template <int kWords>
+double args_us(hipStream_t s, uint64_t* sink) {
+  const Blob<kWords> blob{};
+  return median_us([&] {
+    hipLaunchKernelGGL(args_kernel<kWords>, dim3(1), dim3(64), 0, s, blob, sink);
+    CK(hipStreamSynchronize(s));
+  });
 }
 
 }  // namespace
@@ -104,15 +117,14 @@ int main() {
   std::memset(host, 2, kBlocks * 2 * kChunk);
 
   const int nvec = static_cast<int>(kCopyBytes / 16);
-  Blob blob{};
   const double empty = median_us([&] {
     hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, s);
     CK(hipStreamSynchronize(s));
   });
-  const double args = median_us([&] {
-    hipLaunchKernelGGL(args_kernel, dim3(1), dim3(64), 0, s, blob, sink);
-    CK(hipStreamSynchronize(s));
-  });
+  const double args = args_us<208>(s, sink);   // 1664 bytes
+  const double args160 = args_us<20>(s, sink);
+  const double args640 = args_us<80>(s, sink);
+  const double args2560 = args_us<320>(s, sink);
   const double copy_h2d = median_us([&] {
     hipLaunchKernelGGL(copy_kernel, dim3(nvec / 256), dim3(256), 0, s,
                        reinterpret_cast<const int4*>(host), reinterpret_cast<int4*>(dev64), nvec);
@@ -152,11 +164,13 @@ int main() {
   const double f16d = median_us([&] { fkv(16, ids16, ids16 + 16, 0); });
   const char* sk = std::getenv("FLEXKV_SMALL_KERNEL");
   std::printf("{\"small_kernel\": %s, \"empty_kernel_us\": %.2f, \"args_kernel_us\": %.2f, "
+              "\"args160_kernel_us\": %.2f, \"args640_kernel_us\": %.2f, \"args2560_kernel_us\": %.2f, "
               "\"copy_kernel_h2d_us\": %.2f, \"copy_kernel_d2h_us\": %.2f, "
               "\"memcpy_h2d_us\": %.2f, \"memcpy_d2h_us\": %.2f, \"memcpy_2x32k_h2d_us\": %.2f, "
               "\"fkv_1x1_h2d_us\": %.2f, \"fkv_1x1_d2h_us\": %.2f, "
               "\"fkv_16x1_h2d_us\": %.2f, \"fkv_16x1_d2h_us\": %.2f}\n",
-              (sk && std::atoi(sk) == 0) ? "false" : "true", empty, args, copy_h2d, copy_d2h,
+              (sk && std::atoi(sk) == 0) ? "false" : "true", empty, args, args160, args640,
+              args2560, copy_h2d, copy_d2h,
               memcpy_h2d, memcpy_d2h, memcpy_2x, f1h, f1d, f16h, f16d);
   if (fkv_finalize() != 0) std::fprintf(stderr, "fkv_finalize: %s\n", fkv_last_error());
   CK(hipStreamDestroy(s));
