@@ -665,9 +665,11 @@ def worker_ops(wl: Workload, reps: int = 40, process: bool = True):
 
 
 def call_latency(wl: Workload, reps: int = 200):
-    """Wall time of small synchronous calls (1 block x 1 layer, 16 blocks x 1
-    layer, 16 blocks x all layers), zero-copy and copy-engine paths,
-    alternating direction, median of `reps`."""
+    """Wall time of small synchronous calls from Python (1 block x 1 layer,
+    16 blocks x 1 layer, 16 blocks x all layers), zero-copy and copy-engine
+    paths, each direction, median of `reps` on the current stream; beside
+    them a one-element torch fill plus stream synchronisation, the cost of
+    the smallest torch device op from Python."""
     from flexkv_amd import c_ext
     out = {}
     L = wl.w["layers"]
@@ -676,13 +678,23 @@ def call_latency(wl: Workload, reps: int = 200):
             g = wl.gids_p[:nb].clone().pin_memory()
             c = wl.cids_p[:nb].clone().pin_memory()
             p = wl.ptrs[:nl].clone().pin_memory()
-            ts = []
-            for i in range(reps + 5):
-                t0 = time.perf_counter()
-                c_ext.transfer_kv_blocks(g, p, wl.gkv, wl.gblk, c, wl.host, wl.ckv, wl.clay,
-                                         wl.cblk, wl.chunk, 0, -1, i % 2 == 0, ce, wl.mla)
-                ts.append(time.perf_counter() - t0)
-            out[f"{path}_{nb}blk_{nl}layer_us"] = round(statistics.median(ts[5:]) * 1e6, 1)
+            for name, h2d in (("h2d", True), ("d2h", False)):
+                ts = []
+                for i in range(reps + 5):
+                    t0 = time.perf_counter()
+                    c_ext.transfer_kv_blocks(g, p, wl.gkv, wl.gblk, c, wl.host, wl.ckv, wl.clay,
+                                             wl.cblk, wl.chunk, 0, -1, h2d, ce, wl.mla)
+                    ts.append(time.perf_counter() - t0)
+                out[f"{path}_{nb}blk_{nl}layer_{name}_us"] = round(statistics.median(ts[5:]) * 1e6, 1)
+    x = torch.zeros(1, device=wl.dev)
+    st = torch.cuda.current_stream()
+    ts = []
+    for i in range(reps + 5):
+        t0 = time.perf_counter()
+        x.fill_(1.0)
+        st.synchronize()
+        ts.append(time.perf_counter() - t0)
+    out["torch_fill_sync_us"] = round(statistics.median(ts[5:]) * 1e6, 1)
     return out
 
 

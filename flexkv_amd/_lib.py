@@ -206,6 +206,34 @@ def load() -> ctypes.CDLL:
     return _lib
 
 
+_fast = None
+
+
+def fast():
+    """Load (once) and return the compiled module ``_fkv_py`` that carries the
+    per-call path of c_ext.transfer_kv_blocks, bound to the functions of the
+    library that load() returns; raise if it is not built."""
+    global _fast
+    if _fast is not None:
+        return _fast
+    lib = load()
+    with _lock:
+        if _fast is None:
+            try:
+                from . import _fkv_py
+            except ImportError as e:
+                raise ImportError(
+                    f"flexkv_amd/_fkv_py is not built ({e}); run `python -c 'import "
+                    "__graft_entry__ as g; g.build()'` from the repository root") from e
+
+            def addr(fn) -> int:
+                return ctypes.cast(fn, ctypes.c_void_p).value
+            _fkv_py.bind(addr(lib.fkv_transfer_kv_blocks), addr(lib.fkv_transfer_kv_blocks_kv_ptrs),
+                         addr(lib.fkv_last_error), FKV_XFER_KERNEL, FKV_XFER_CE)
+            _fast = _fkv_py
+    return _fast
+
+
 def finalize() -> None:
     """Release every resource the library holds (fkv_finalize): unreleased
     layer-wise handles, streams from fkv_stream_create, copy-engine signals,

@@ -2,7 +2,8 @@
 program that measures the device's plain read / write / copy rates
 (bench.py reports them beside the gather's roofline), and the call_latency
 program that times small fkv_transfer_kv_blocks calls against the launch
-floors beside them.
+floors beside them, and the CPython module _fkv_py (host C++ against torch's
+headers, built with g++) that carries c_ext.transfer_kv_blocks' per-call path.
 
     python -m flexkv_amd.build_ext
 """
@@ -12,6 +13,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -22,6 +24,8 @@ CEILING_SOURCE = os.path.join(HERE, "csrc", "hbm_ceiling.hip")
 CEILING_OUT = os.path.join(HERE, "hbm_ceiling")
 LATENCY_SOURCE = os.path.join(HERE, "csrc", "call_latency.hip")
 LATENCY_OUT = os.path.join(HERE, "call_latency")
+PY_SOURCE = os.path.join(HERE, "csrc", "py_fastcall.cpp")
+PY_OUT = os.path.join(HERE, "_fkv_py" + sysconfig.get_config_var("EXT_SUFFIX"))
 ARCH = "gfx950"
 
 
@@ -54,12 +58,28 @@ def latency_command() -> list:
             "-Wl,-rpath,$ORIGIN"]
 
 
+def py_command() -> list:
+    import torch
+    tdir = os.path.dirname(os.path.abspath(torch.__file__))
+    tlib = os.path.join(tdir, "lib")
+    abi = int(bool(torch._C._GLIBCXX_USE_CXX11_ABI))
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    return [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-Wall", "-fPIC", "-shared",
+            f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-D__HIP_PLATFORM_AMD__",
+            "-I", sysconfig.get_paths()["include"], "-I", os.path.join(tdir, "include"),
+            "-I", os.path.join(tdir, "include", "torch", "csrc", "api", "include"),
+            "-I", os.path.join(rocm, "include"),
+            PY_SOURCE, "-o", PY_OUT + ".tmp", "-L", tlib, "-ltorch_python", "-lc10", "-lc10_hip",
+            f"-Wl,-rpath,{tlib}"]
+
+
 def _run(cmd: list, out: str, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+        raise RuntimeError(f"{os.path.basename(cmd[0])} failed ({res.returncode}):\n"
+                           f"{res.stdout}\n{res.stderr}")
     os.replace(out + ".tmp", out)
 
 
@@ -67,6 +87,7 @@ def build(verbose: bool = False) -> str:
     _run(command(), OUT, verbose)
     _run(ceiling_command(), CEILING_OUT, verbose)
     _run(latency_command(), LATENCY_OUT, verbose)
+    _run(py_command(), PY_OUT, verbose)
     return OUT
 
 

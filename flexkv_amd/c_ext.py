@@ -48,7 +48,7 @@ _I64 = torch.int64
 
 def _require_int64_host(t: torch.Tensor, name: str) -> None:
     # one combined test on the common path; the detailed checks only on failure
-    if isinstance(t, torch.Tensor) and t.dtype is _I64 and not t.is_cuda and t.is_contiguous():
+    if isinstance(t, torch.Tensor) and t.dtype is _I64 and t.is_cpu and t.is_contiguous():
         return
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
@@ -82,36 +82,20 @@ def transfer_kv_blocks(gpu_block_id_tensor: torch.Tensor,
     ``transfer_sms`` bounds the compute units of the zero-copy kernel
     (-1 = automatic).  ``stream`` (keyword only, an extension) is a raw
     stream handle to run on instead of the current torch stream.
+
+    The compiled module ``_fkv_py`` unpacks and checks the tensors, takes the
+    current stream and calls ``fkv_transfer_kv_blocks`` with the GIL released;
+    when a check fails, ``_explain`` raises the error that names it.
     """
-    _require_int64_host(gpu_block_id_tensor, "gpu_block_id_tensor")
-    _require_int64_host(cpu_block_id_tensor, "cpu_block_id_tensor")
-    _require_int64_host(gpu_layer_ptrs_tensor, "gpu_layer_ptrs_tensor")
-    if not isinstance(cpu_tensor, torch.Tensor):
-        raise TypeError(f"cpu_tensor must be a torch.Tensor, got {type(cpu_tensor).__name__}")
-    num_blocks = gpu_block_id_tensor.numel()          # bindings.cpp:33
-    num_layers = gpu_layer_ptrs_tensor.numel()        # bindings.cpp:34
-    if cpu_block_id_tensor.numel() != num_blocks:
-        raise RuntimeError(
-            f"gpu_block_id_tensor has {num_blocks} ids but cpu_block_id_tensor has "
-            f"{cpu_block_id_tensor.numel()}")
-    if isinstance(use_ce_transfer, bool):
-        mode = _lib.FKV_XFER_CE if use_ce_transfer else _lib.FKV_XFER_KERNEL
-    else:
-        mode = int(use_ce_transfer)
-    if stream is None:
-        stream = _stream_handle("transfer_kv_blocks")
-    lib = _lib.load()
-    rc = lib.fkv_transfer_kv_blocks(
-        int(num_blocks), int(start_layer_id), int(num_layers),
-        gpu_block_id_tensor.data_ptr(), gpu_layer_ptrs_tensor.data_ptr(),
-        int(gpu_kv_stride_in_bytes), int(gpu_block_stride_in_bytes),
-        cpu_block_id_tensor.data_ptr(), cpu_tensor.data_ptr(),
-        int(cpu_kv_stride_in_bytes), int(cpu_layer_stride_in_bytes),
-        int(cpu_block_stride_in_bytes), 0, int(chunk_size_in_bytes),
-        stream, int(transfer_sms), 1 if is_host_to_device else 0, mode,
-        1 if is_mla else 0)
-    if rc != 0:
-        raise RuntimeError(_lib.last_error() or f"fkv_transfer_kv_blocks failed ({rc})")
+    f = _fast or _load_fast()
+    if f.transfer_kv_blocks(gpu_block_id_tensor, gpu_layer_ptrs_tensor, gpu_kv_stride_in_bytes,
+                            gpu_block_stride_in_bytes, cpu_block_id_tensor, cpu_tensor,
+                            cpu_kv_stride_in_bytes, cpu_layer_stride_in_bytes,
+                            cpu_block_stride_in_bytes, chunk_size_in_bytes, start_layer_id,
+                            transfer_sms, is_host_to_device, use_ce_transfer, is_mla,
+                            stream) is False:
+        _explain("transfer_kv_blocks", gpu_block_id_tensor, gpu_layer_ptrs_tensor,
+                 "gpu_layer_ptrs_tensor", cpu_block_id_tensor, cpu_tensor, 1, stream)
 
 
 def transfer_kv_blocks_kv_ptrs(gpu_block_id_tensor: torch.Tensor,
@@ -131,35 +115,46 @@ def transfer_kv_blocks_kv_ptrs(gpu_block_id_tensor: torch.Tensor,
     """transfer_kv_blocks for K and V held in separate allocations
     (extension): ``gpu_kv_ptrs_tensor`` is an int64 host tensor of
     ``layers * kv`` base pointers ordered [layer][K|V] (kv = 1 for MLA)."""
+    f = _fast or _load_fast()
+    if f.transfer_kv_blocks_kv_ptrs(gpu_block_id_tensor, gpu_kv_ptrs_tensor,
+                                    gpu_block_stride_in_bytes, cpu_block_id_tensor, cpu_tensor,
+                                    cpu_kv_stride_in_bytes, cpu_layer_stride_in_bytes,
+                                    cpu_block_stride_in_bytes, chunk_size_in_bytes,
+                                    start_layer_id, transfer_sms, is_host_to_device,
+                                    use_ce_transfer, is_mla, stream) is False:
+        _explain("transfer_kv_blocks_kv_ptrs", gpu_block_id_tensor, gpu_kv_ptrs_tensor,
+                 "gpu_kv_ptrs_tensor", cpu_block_id_tensor, cpu_tensor, 1 if is_mla else 2,
+                 stream)
+
+
+_fast = None
+
+
+def _load_fast():
+    global _fast
+    _fast = _lib.fast()
+    return _fast
+
+
+def _explain(fn_name: str, gpu_block_id_tensor, ptrs_tensor, ptrs_name: str,
+             cpu_block_id_tensor, cpu_tensor, per_layer: int, stream) -> None:
+    """Raise the error for arguments the compiled per-call path refused."""
     _require_int64_host(gpu_block_id_tensor, "gpu_block_id_tensor")
+    _require_int64_host(ptrs_tensor, ptrs_name)
     _require_int64_host(cpu_block_id_tensor, "cpu_block_id_tensor")
-    _require_int64_host(gpu_kv_ptrs_tensor, "gpu_kv_ptrs_tensor")
     if not isinstance(cpu_tensor, torch.Tensor):
         raise TypeError(f"cpu_tensor must be a torch.Tensor, got {type(cpu_tensor).__name__}")
-    kv = 1 if is_mla else 2
-    if gpu_kv_ptrs_tensor.numel() % kv:
-        raise RuntimeError(f"gpu_kv_ptrs_tensor holds {gpu_kv_ptrs_tensor.numel()} pointers, "
-                           f"not a multiple of {kv}")
-    num_blocks = gpu_block_id_tensor.numel()
+    num_blocks = gpu_block_id_tensor.numel()          # bindings.cpp:33
     if cpu_block_id_tensor.numel() != num_blocks:
         raise RuntimeError(
             f"gpu_block_id_tensor has {num_blocks} ids but cpu_block_id_tensor has "
             f"{cpu_block_id_tensor.numel()}")
-    if isinstance(use_ce_transfer, bool):
-        mode = _lib.FKV_XFER_CE if use_ce_transfer else _lib.FKV_XFER_KERNEL
-    else:
-        mode = int(use_ce_transfer)
+    if ptrs_tensor.numel() % per_layer:
+        raise RuntimeError(f"{ptrs_name} holds {ptrs_tensor.numel()} pointers, "
+                           f"not a multiple of {per_layer}")
     if stream is None:
-        stream = _stream_handle("transfer_kv_blocks_kv_ptrs")
-    rc = _lib.load().fkv_transfer_kv_blocks_kv_ptrs(
-        int(num_blocks), int(start_layer_id), int(gpu_kv_ptrs_tensor.numel() // kv),
-        gpu_block_id_tensor.data_ptr(), gpu_kv_ptrs_tensor.data_ptr(),
-        int(gpu_block_stride_in_bytes), cpu_block_id_tensor.data_ptr(), cpu_tensor.data_ptr(),
-        int(cpu_kv_stride_in_bytes), int(cpu_layer_stride_in_bytes),
-        int(cpu_block_stride_in_bytes), 0, int(chunk_size_in_bytes), stream,
-        int(transfer_sms), 1 if is_host_to_device else 0, mode, 1 if is_mla else 0)
-    if rc != 0:
-        raise RuntimeError(_lib.last_error() or f"fkv_transfer_kv_blocks_kv_ptrs failed ({rc})")
+        _stream_handle(fn_name)
+    raise RuntimeError(f"{fn_name}: arguments refused")
 
 
 def _contiguous(fn_name: str, gpu_block_id_tensor, gpu_layer_ptrs_tensor, gpu_kv_stride_in_bytes,

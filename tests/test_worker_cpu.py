@@ -184,3 +184,50 @@ def test_c_ext_argument_checks():
     if not torch.cuda.is_available():
         with pytest.raises(RuntimeError, match="HIP device"):
             c_ext.transfer_kv_blocks(ids, ptrs, 0, 0, ids, cache, 0, 0, 0, 16, 0)
+
+
+def test_c_ext_kv_ptrs_and_scalar_checks():
+    """The compiled per-call path refuses what the Python signature refuses,
+    with the same error types, for both entry points."""
+    from flexkv_amd import c_ext
+    ids = torch.tensor([1, 2], dtype=torch.int64)
+    cache = torch.zeros(16)
+    three = torch.tensor([0, 0, 0], dtype=torch.int64)
+    with pytest.raises(RuntimeError, match="not a multiple of 2"):
+        c_ext.transfer_kv_blocks_kv_ptrs(ids, three, 0, ids, cache, 0, 0, 0, 16, 0)
+    with pytest.raises(RuntimeError, match="ids"):
+        c_ext.transfer_kv_blocks_kv_ptrs(ids, three[:2], 0, ids[:1], cache, 0, 0, 0, 16, 0)
+    with pytest.raises(RuntimeError, match="host tensor"):
+        c_ext.transfer_kv_blocks(ids.to("meta"), three, 0, 0, ids, cache, 0, 0, 0, 16, 0)
+    with pytest.raises(TypeError):                      # strides are integers, as in bindings.cpp
+        c_ext.transfer_kv_blocks(ids, three, 0.5, 0, ids, cache, 0, 0, 0, 16, 0)
+    with pytest.raises(TypeError):
+        c_ext.transfer_kv_blocks(ids, three, 0, 0, ids, cache, 0, 0, 0, 16, 0, -1, True, "ce")
+    if not torch.cuda.is_available():
+        # integer-like scalars and an integer mode pass the checks; only the device is missing
+        with pytest.raises(RuntimeError, match="HIP device"):
+            c_ext.transfer_kv_blocks(ids, three, np.int64(0), 0, ids, cache, 0, 0, 0, 16, 0, -1,
+                                     True, 2, False)
+        with pytest.raises(RuntimeError, match="HIP device"):
+            c_ext.transfer_kv_blocks_kv_ptrs(ids, three, 0, ids, cache, 0, 0, 0, 16, 0, -1, True,
+                                             False, True)
+
+
+def test_c_ext_fast_module_shares_the_library():
+    """_fkv_py is bound to the functions of the library _lib loaded, and the
+    process maps that library once."""
+    import ctypes
+    from flexkv_amd import _lib
+    fast = _lib.fast()
+    assert _lib.fast() is fast
+    lib = _lib.load()
+    assert ctypes.cast(lib.fkv_transfer_kv_blocks, ctypes.c_void_p).value
+    paths = set()
+    with open("/proc/self/maps") as fh:
+        for line in fh:
+            parts = line.split()
+            if len(parts) >= 6 and parts[-1].endswith("libflexkv_hip.so"):
+                paths.add(parts[-1])
+    assert len(paths) == 1
+    with pytest.raises(TypeError):
+        fast.transfer_kv_blocks(1, 2, 3)
