@@ -135,8 +135,8 @@ class TransferWorkerBase(ABC):
     def create_worker_thread(cls, worker_id: int, finished_ops_queue: Any, *args: Any,
                              **kwargs: Any) -> "ThreadWorkerHandle":
         """Start the worker on a thread of this process.  The transfer call
-        releases the GIL (ctypes), and the worker shares this process's pinned
-        host cache and device tensors directly, with no IPC."""
+        releases the GIL while it runs, and the worker shares this process's
+        pinned host cache and device tensors directly, with no IPC."""
         conn = LocalChannel()
         ready_event = threading.Event()
         errors: List[BaseException] = []

@@ -829,6 +829,45 @@ def test_c_ext_dropin_on_side_stream(dev, use_ce):
         assert torch.equal(layers[l][:, gids].cpu(), src[l][:, gids])
 
 
+@pytest.mark.parametrize("use_ce", [False, True])
+def test_c_ext_releases_the_gil(dev, use_ce):
+    """Another Python thread runs while a transfer is in flight: the call
+    releases the GIL for as long as the library works (a 256 MiB transfer,
+    about 5 ms at the link's rate), so a thread of the serving engine or a
+    second worker is not stalled by it."""
+    import threading
+
+    from flexkv_amd import c_ext
+    from flexkv_amd.storage.allocator import pinned_empty
+    L, NG, chunk = 8, 512, 32768
+    layers = [torch.zeros(2 * NG * chunk, dtype=torch.uint8, device=dev) for _ in range(L)]
+    host = pinned_empty(NG * L * 2 * chunk, torch.uint8)
+    ids = torch.arange(NG, dtype=torch.int64)
+    ptrs = torch.tensor([t.data_ptr() for t in layers], dtype=torch.int64)
+    count = [0]
+    stop = threading.Event()
+
+    def spin():
+        while not stop.is_set():
+            count[0] += 1
+
+    th = threading.Thread(target=spin)
+    th.start()
+    try:
+        gained = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            before = count[0]
+            c_ext.transfer_kv_blocks(ids, ptrs, NG * chunk, chunk, ids, host, chunk, 2 * chunk,
+                                     L * 2 * chunk, chunk, 0, -1, False, use_ce, False)
+            gained.append(count[0] - before)
+    finally:
+        stop.set()
+        th.join()
+    # with the GIL held for the whole call the other thread could not count at all
+    assert max(gained) > 1000, gained
+
+
 @pytest.mark.parametrize("geo", [(4, 2, 64, 16, 8, 128, 37), (130, 2, 8, 1, 1, 64, 5),
                                  (5, 1, 30, 64, 1, 576, 11), (3, 2, 20, 1, 1, 24, 7),
                                  (3, 1, 24, 32, 1, 1024, 9)],
