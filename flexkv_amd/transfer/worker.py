@@ -75,7 +75,15 @@ class WorkerTransferOp:
 
 class LocalChannel:
     """In-process stand-in for a multiprocessing Connection pair: send() from
-    the engine, poll()/recv() in the worker thread."""
+    the engine, poll()/recv() in the worker thread.
+
+    send() wakes a waiting poll() at once, so a poll with a timeout waits at
+    least IDLE_WAIT_S: the worker loop's 100 us poll (the reference's, for a
+    pipe to another process) would otherwise wake an idle worker thread
+    10,000 times a second, each time taking the GIL from the engine's own
+    threads (a Python loop beside such an idle worker ran 5-11% slower)."""
+
+    IDLE_WAIT_S = 0.05
 
     def __init__(self) -> None:
         self._items: "collections.deque" = collections.deque()
@@ -89,7 +97,7 @@ class LocalChannel:
     def poll(self, timeout: float = 0.0) -> bool:
         with self._cv:
             if not self._items and timeout:
-                self._cv.wait(timeout)
+                self._cv.wait(max(timeout, self.IDLE_WAIT_S))
             return bool(self._items)
 
     def recv(self) -> Any:
