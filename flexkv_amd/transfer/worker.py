@@ -75,15 +75,8 @@ class WorkerTransferOp:
 
 class LocalChannel:
     """In-process stand-in for a multiprocessing Connection pair: send() from
-    the engine, poll()/recv() in the worker thread.
-
-    send() wakes a waiting poll() at once, so a poll with a timeout waits at
-    least IDLE_WAIT_S: the worker loop's 100 us poll (the reference's, for a
-    pipe to another process) would otherwise wake an idle worker thread
-    10,000 times a second, each time taking the GIL from the engine's own
-    threads (a Python loop beside such an idle worker ran 5-11% slower)."""
-
-    IDLE_WAIT_S = 0.05
+    the engine, poll()/recv() in the worker thread; send() wakes a waiting
+    poll() at once."""
 
     def __init__(self) -> None:
         self._items: "collections.deque" = collections.deque()
@@ -97,7 +90,7 @@ class LocalChannel:
     def poll(self, timeout: float = 0.0) -> bool:
         with self._cv:
             if not self._items and timeout:
-                self._cv.wait(max(timeout, self.IDLE_WAIT_S))
+                self._cv.wait(timeout)
             return bool(self._items)
 
     def recv(self) -> Any:
@@ -200,12 +193,19 @@ class TransferWorkerBase(ABC):
         if self.finished_ops_queue is not None:
             self.finished_ops_queue.put(op.transfer_op_id)
 
+    # How long the main loop's poll waits for an op.  A poll returns as soon
+    # as an op arrives, so this bounds only the wakeups of an idle worker.
+    # The reference polls every 100 us (worker.py:148), which keeps an idle
+    # worker process at about 4% of a host core (0.4% at 50 ms), per GPU
+    # and per SSD worker.
+    POLL_IDLE_S = 0.05
+
     def run(self) -> None:
-        """Main loop: poll the pipe (100 us), drain whatever else is queued,
-        run the batch in order, report each op id (worker.py:144-177)."""
+        """Main loop: wait for an op, drain whatever else is queued, run the
+        batch in order, report each op id (worker.py:144-177)."""
         while True:
             try:
-                if not self.transfer_conn.poll(timeout=0.0001):
+                if not self.transfer_conn.poll(timeout=self.POLL_IDLE_S):
                     continue
                 op = self.transfer_conn.recv()
                 if op is None:

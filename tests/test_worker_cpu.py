@@ -233,23 +233,32 @@ def test_c_ext_fast_module_shares_the_library():
         fast.transfer_kv_blocks(1, 2, 3)
 
 
-def test_local_channel_wakes_on_send_and_sleeps_when_idle():
-    """A waiting poll returns as soon as something is sent, however long its
-    idle wait; an idle poll sleeps at least the idle wait, not the 100 us the
-    worker loop asks for."""
+def test_idle_worker_waits_long_and_wakes_on_send():
+    """The run loop waits POLL_IDLE_S per poll while idle, not the
+    reference's 100 us, and a waiting poll returns as soon as an op is sent."""
     import threading
     import time
     ch = W.LocalChannel()
     assert ch.poll(0) is False
-    ch.IDLE_WAIT_S = 30.0
     got = []
-    th = threading.Thread(target=lambda: got.append(ch.poll(0.0001)))
+    th = threading.Thread(target=lambda: got.append(ch.poll(30.0)))
     th.start()
     time.sleep(0.05)
     ch.send("op")
     th.join(timeout=10)
     assert not th.is_alive() and got == [True] and ch.recv() == "op"
-    ch.IDLE_WAIT_S = 0.2
-    t0 = time.perf_counter()
-    assert ch.poll(0.0001) is False
-    assert time.perf_counter() - t0 >= 0.15
+
+    class Conn:
+        def __init__(self):
+            self.timeouts = []
+
+        def poll(self, timeout=0.0):
+            self.timeouts.append(timeout)
+            return len(self.timeouts) > 1      # idle once, then the stop message
+
+        def recv(self):
+            return None
+
+    w = RecordingWorker(0, Conn(), None)
+    w.run()
+    assert w.transfer_conn.timeouts[0] == W.TransferWorkerBase.POLL_IDLE_S >= 0.01
