@@ -15,7 +15,9 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/csrc/autograd/python_variable.h>
 
+#include <climits>
 #include <cstdint>
+#include <cstring>
 #include <exception>
 
 namespace {
@@ -51,10 +53,39 @@ bool as_i64(PyObject* o, int64_t* v) {
   return true;
 }
 
-// use_ce_transfer: a bool picks the copy engines or the kernel, an integer is a mode
+// an argument the C-ABI takes as int
+bool as_int(PyObject* o, int* v) {
+  const long x = PyLong_AsLong(o);
+  if (x == -1 && PyErr_Occurred()) return false;
+  if (x < INT_MIN || x > INT_MAX) {
+    PyErr_Format(PyExc_OverflowError, "%ld does not fit a C int", x);
+    return false;
+  }
+  *v = static_cast<int>(x);
+  return true;
+}
+
+// block and layer counts the C-ABI takes as int
+bool count_fits(int64_t n, const char* what) {
+  if (n <= INT_MAX) return true;
+  PyErr_Format(PyExc_RuntimeError, "%lld %s in one call; at most %d", static_cast<long long>(n),
+               what, INT_MAX);
+  return false;
+}
+
+// a numpy scalar bool (numpy 1.x names its type numpy.bool_, 2.x numpy.bool)
+bool is_numpy_bool(PyObject* o) {
+  const char* n = Py_TYPE(o)->tp_name;
+  return std::strcmp(n, "numpy.bool_") == 0 || std::strcmp(n, "numpy.bool") == 0;
+}
+
+// use_ce_transfer: a bool (Python or numpy) picks the copy engines or the
+// kernel, an integer is a mode
 bool as_mode(PyObject* o, int* mode) {
-  if (PyBool_Check(o)) {
-    *mode = o == Py_True ? g_mode_ce : g_mode_kernel;
+  if (PyBool_Check(o) || is_numpy_bool(o)) {
+    const int r = PyObject_IsTrue(o);
+    if (r < 0) return false;
+    *mode = r ? g_mode_ce : g_mode_kernel;
     return true;
   }
   int64_t v = 0;
@@ -124,12 +155,13 @@ PyObject* transfer_kv_blocks(PyObject*, PyObject* const* a, Py_ssize_t n) {
   const at::Tensor& cpu = THPVariable_Unpack(a[5]);
   const int64_t nb = gids->numel();
   if (cids->numel() != nb) Py_RETURN_FALSE;
-  int64_t gkv, gblk, ckv, clay, cblk, chunk, start, sms;
-  int h2d, mla, mode;
+  int64_t gkv, gblk, ckv, clay, cblk, chunk;
+  int start, sms, h2d, mla, mode;
   if (!as_i64(a[2], &gkv) || !as_i64(a[3], &gblk) || !as_i64(a[6], &ckv) ||
       !as_i64(a[7], &clay) || !as_i64(a[8], &cblk) || !as_i64(a[9], &chunk) ||
-      !as_i64(a[10], &start) || !as_i64(a[11], &sms) || !as_flag(a[12], &h2d) ||
-      !as_mode(a[13], &mode) || !as_flag(a[14], &mla))
+      !as_int(a[10], &start) || !as_int(a[11], &sms) || !as_flag(a[12], &h2d) ||
+      !as_mode(a[13], &mode) || !as_flag(a[14], &mla) || !count_fits(nb, "block ids") ||
+      !count_fits(ptrs->numel(), "layer pointers"))
     return nullptr;
   void* stream = nullptr;
   bool ok = true;
@@ -142,8 +174,8 @@ PyObject* transfer_kv_blocks(PyObject*, PyObject* const* a, Py_ssize_t n) {
   const int nl = static_cast<int>(ptrs->numel());
   int rc;
   Py_BEGIN_ALLOW_THREADS
-  rc = g_transfer(static_cast<int>(nb), static_cast<int>(start), nl, g, p, gkv, gblk, c, host,
-                  ckv, clay, cblk, 0, chunk, stream, static_cast<int>(sms), h2d, mode, mla);
+  rc = g_transfer(static_cast<int>(nb), start, nl, g, p, gkv, gblk, c, host, ckv, clay, cblk, 0,
+                  chunk, stream, sms, h2d, mode, mla);
   Py_END_ALLOW_THREADS
   return finish(rc);
 }
@@ -164,12 +196,13 @@ PyObject* transfer_kv_blocks_kv_ptrs(PyObject*, PyObject* const* a, Py_ssize_t n
     Py_RETURN_FALSE;
   const at::Tensor& cpu = THPVariable_Unpack(a[4]);
   const int64_t nb = gids->numel();
-  int64_t gblk, ckv, clay, cblk, chunk, start, sms;
-  int h2d, mla, mode;
+  int64_t gblk, ckv, clay, cblk, chunk;
+  int start, sms, h2d, mla, mode;
   if (!as_i64(a[2], &gblk) || !as_i64(a[5], &ckv) || !as_i64(a[6], &clay) ||
-      !as_i64(a[7], &cblk) || !as_i64(a[8], &chunk) || !as_i64(a[9], &start) ||
-      !as_i64(a[10], &sms) || !as_flag(a[11], &h2d) || !as_mode(a[12], &mode) ||
-      !as_flag(a[13], &mla))
+      !as_i64(a[7], &cblk) || !as_i64(a[8], &chunk) || !as_int(a[9], &start) ||
+      !as_int(a[10], &sms) || !as_flag(a[11], &h2d) || !as_mode(a[12], &mode) ||
+      !as_flag(a[13], &mla) || !count_fits(nb, "block ids") ||
+      !count_fits(ptrs->numel(), "layer pointers"))
     return nullptr;
   const int kv = mla ? 1 : 2;
   if (cids->numel() != nb || ptrs->numel() % kv) Py_RETURN_FALSE;
@@ -184,9 +217,8 @@ PyObject* transfer_kv_blocks_kv_ptrs(PyObject*, PyObject* const* a, Py_ssize_t n
   const int nl = static_cast<int>(ptrs->numel() / kv);
   int rc;
   Py_BEGIN_ALLOW_THREADS
-  rc = g_transfer_kv_ptrs(static_cast<int>(nb), static_cast<int>(start), nl, g, p, gblk, c, host,
-                          ckv, clay, cblk, 0, chunk, stream, static_cast<int>(sms), h2d, mode,
-                          mla);
+  rc = g_transfer_kv_ptrs(static_cast<int>(nb), start, nl, g, p, gblk, c, host, ckv, clay, cblk,
+                          0, chunk, stream, sms, h2d, mode, mla);
   Py_END_ALLOW_THREADS
   return finish(rc);
 }

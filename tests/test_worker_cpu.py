@@ -203,6 +203,8 @@ def test_c_ext_kv_ptrs_and_scalar_checks():
         c_ext.transfer_kv_blocks(ids, three, 0.5, 0, ids, cache, 0, 0, 0, 16, 0)
     with pytest.raises(TypeError):
         c_ext.transfer_kv_blocks(ids, three, 0, 0, ids, cache, 0, 0, 0, 16, 0, -1, True, "ce")
+    with pytest.raises(OverflowError):                  # start_layer_id is a C int
+        c_ext.transfer_kv_blocks(ids, three, 0, 0, ids, cache, 0, 0, 0, 16, 1 << 31)
     if not torch.cuda.is_available():
         # integer-like scalars and an integer mode pass the checks; only the device is missing
         with pytest.raises(RuntimeError, match="HIP device"):
@@ -211,6 +213,9 @@ def test_c_ext_kv_ptrs_and_scalar_checks():
         with pytest.raises(RuntimeError, match="HIP device"):
             c_ext.transfer_kv_blocks_kv_ptrs(ids, three, 0, ids, cache, 0, 0, 0, 16, 0, -1, True,
                                              False, True)
+        with pytest.raises(RuntimeError, match="HIP device"):   # numpy bools, as pybind takes them
+            c_ext.transfer_kv_blocks(ids, three, 0, 0, ids, cache, 0, 0, 0, 16, 0, -1,
+                                     np.True_, np.False_, np.False_)
 
 
 def test_c_ext_fast_module_shares_the_library():
