@@ -939,6 +939,21 @@ int staging_or_fallback(DeviceState& d, int dev, CopyLane& ln, size_t need_half)
   return kSdmaUnavailable;
 }
 
+// Edge pieces below kEdgePieceMinBytes: one of at least edge_small_min_bytes()
+// (FLEXKV_CE_EDGE_MIN_BYTES, default 32 MiB) gives 1 / kEdgeSmallDiv of its
+// blocks to a piece of its own.  Measured on MI355X, Llama-3-8B block rows
+// (2 MiB), copy-engine transfers with / without the cut: 16 blocks 628.8 /
+// 631.5 us D2H, 627.3 / 637.9 us H2D; 32 blocks 1216 / 1236 us D2H, 1214 /
+// 1237 us H2D; 4 blocks (8 MiB) 181 / 183 us D2H but 198 / 183 us H2D, where
+// the extra piece's host round trip is not hidden behind 2 MiB of copies.
+constexpr int kEdgeSmallDiv = 4;
+constexpr int64_t kEdgeSmallMinBytesDefault = int64_t(32) << 20;
+
+int64_t edge_small_min_bytes() {
+  const char* e = getenv("FLEXKV_CE_EDGE_MIN_BYTES");
+  return e ? std::max<int64_t>(1, atoll(e)) : kEdgeSmallMinBytesDefault;
+}
+
 int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   DeviceState& d = g_dev[dev];
   CopyLane& ln = d.lane[h2d ? 1 : 0];
@@ -1002,14 +1017,19 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   // The first piece's gather (D2H) and the last piece's scatter (H2D) run
   // with no engine copies beside them.  When that piece is large, an eighth
   // of a half is cut off it, so the engines start, or the transfer ends,
-  // after a short kernel; smaller pieces are not cut, since every piece costs
-  // a host round trip.
+  // after a short kernel.  A smaller edge piece of at least
+  // edge_small_min_bytes() gives a quarter of its blocks instead; below that
+  // it is not cut, since every piece costs a host round trip.
   if (!pieces.empty()) {
     const size_t edge = h2d ? pieces.size() - 1 : 0;
     const Piece p = pieces[edge];
     const int64_t bytes = static_cast<int64_t>(p.nb) * p.nl * g.kv * g.chunk;
-    const int cut = std::min(p.nb - 1, std::max(1, blocks_per_piece / kEdgePieceDiv));
-    if (bytes >= kEdgePieceMinBytes && cut >= 1) {
+    int cut = 0;
+    if (bytes >= kEdgePieceMinBytes)
+      cut = std::min(p.nb - 1, std::max(1, blocks_per_piece / kEdgePieceDiv));
+    else if (bytes >= edge_small_min_bytes())
+      cut = std::min(p.nb - 1, std::max(1, p.nb / kEdgeSmallDiv));
+    if (cut >= 1) {
       Piece first = p, second = p;
       first.nb = h2d ? p.nb - cut : cut;
       second.b0 = p.b0 + first.nb;

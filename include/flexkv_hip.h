@@ -62,8 +62,11 @@ enum {
    * does every transfer on a device whose engines cannot be set up (one
    * warning on stderr; FLEXKV_SDMA_ENGINES=0 turns them off) and every
    * transfer whose staging buffer cannot be allocated for want of device
-   * memory (one warning; the next transfer tries again).  Same role as
-   * the reference CE mode, csrc/transfer.cu:97-121. */
+   * memory (one warning; the next transfer tries again).  The pieces that
+   * run without engine copies beside them (the first gather, the last
+   * scatter) are cut short on transfers of FLEXKV_CE_EDGE_MIN_BYTES
+   * (default 32 MiB) and more.  Same role as the reference CE mode,
+   * csrc/transfer.cu:97-121. */
   FKV_XFER_CE = 1,
   /* The reference's copy-engine algorithm restated literally: one
    * hipMemcpyAsync per (layer, K|V, block) chunk, csrc/transfer.cu:97-121.

@@ -567,13 +567,15 @@ def test_staged_runs_and_small_staging(dev, run, heads):
         _lib.set_staging_bytes(0)
 
 
-@pytest.mark.parametrize("blocks,launches", [(384, 2), (192, 1)])
+@pytest.mark.parametrize("blocks,launches", [(384, 2), (192, 2), (48, 1)])
 def test_copy_engine_edge_piece(dev, blocks, launches):
     """A copy-engine transfer whose piece without engine copies beside it (the
     D2H's first gather, the H2D's last scatter) moves at least 128 MiB cuts
     an eighth of a staging half off it: 384 blocks of 512 KiB (192 MiB) in
-    256 MiB halves go as 64 + 320 blocks (D2H) and 320 + 64 (H2D), 192 blocks
-    (96 MiB) as one piece.  Bytes match the oracle either way."""
+    256 MiB halves go as 64 + 320 blocks (D2H) and 320 + 64 (H2D).  From
+    32 MiB to 128 MiB it cuts a quarter of its blocks: 192 blocks (96 MiB)
+    go as 48 + 144 and 144 + 48.  48 blocks (24 MiB) go as one piece.  Bytes
+    match the oracle either way."""
     from flexkv_amd import _lib
     _lib.set_staging_bytes(512 << 20)
     try:
