@@ -279,6 +279,8 @@ def transfer_kv_blocks_layerwise(gpu_block_id_tensor: torch.Tensor,
     _require_int64_host(gpu_block_id_tensor, "gpu_block_id_tensor")
     _require_int64_host(cpu_block_id_tensor, "cpu_block_id_tensor")
     _require_int64_host(gpu_layer_ptrs_tensor, "gpu_layer_ptrs_tensor")
+    if not isinstance(cpu_tensor, torch.Tensor):
+        raise TypeError(f"cpu_tensor must be a torch.Tensor, got {type(cpu_tensor).__name__}")
     if cpu_block_id_tensor.numel() != gpu_block_id_tensor.numel():
         raise RuntimeError("gpu and cpu block id tensors differ in length")
     stream = _stream_handle("transfer_kv_blocks_layerwise")

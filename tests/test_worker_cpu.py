@@ -267,3 +267,19 @@ def test_idle_worker_waits_long_and_wakes_on_send():
     w = RecordingWorker(0, Conn(), None)
     w.run()
     assert w.transfer_conn.timeouts[0] == W.TransferWorkerBase.POLL_IDLE_S >= 0.01
+
+
+def test_layerwise_argument_checks():
+    """The layer-wise entry refuses the same bad arguments before any device
+    work: non-tensor host cache, ids of different lengths, non-int64 ids."""
+    from flexkv_amd import c_ext
+    ids = torch.tensor([1, 2], dtype=torch.int64)
+    ptrs = torch.tensor([0], dtype=torch.int64)
+    with pytest.raises(TypeError, match="cpu_tensor"):
+        c_ext.transfer_kv_blocks_layerwise(ids, ptrs, 0, 0, ids, "cache", 0, 0, 0, 16, 0, 1)
+    with pytest.raises(RuntimeError, match="differ in length"):
+        c_ext.transfer_kv_blocks_layerwise(ids, ptrs, 0, 0, ids[:1], torch.zeros(4), 0, 0, 0,
+                                           16, 0, 1)
+    with pytest.raises(TypeError, match="int64"):
+        c_ext.transfer_kv_blocks_layerwise(ids.int(), ptrs, 0, 0, ids, torch.zeros(4), 0, 0, 0,
+                                           16, 0, 1)
