@@ -596,6 +596,53 @@ def test_copy_engine_edge_piece(dev, blocks, launches):
         _lib.set_staging_bytes(0)
 
 
+@pytest.mark.parametrize("order", ["block-major", "layer-major", "rect"])
+def test_copy_engine_small_edge_cut_every_staging_order(dev, order, monkeypatch):
+    """With the small edge cut forced on (FLEXKV_CE_EDGE_MIN_BYTES = 1 MiB), a
+    transfer of a few MiB splits its first gather (D2H) and its last scatter
+    (H2D) into one more piece, in each staging order: contiguous block rows,
+    layer-major runs of a layer-wise host cache, and one rect copy per block.
+    Bytes as the oracle's both ways, with and without the cut."""
+    from flexkv_amd import _lib
+    from gpu_util import DeviceCase, abi_transfer
+    layout = "BLOCKWISE" if order == "block-major" else "LAYERWISE"
+    case = KVCase(layers_total=4, num_layers=4, start_layer=0, kv=2, ng=64, nh=96, tokens=16,
+                  heads=4, dim=128, layout=layout).fill(seed=53)      # 16 KiB chunks
+    if order == "layer-major":
+        cids = np.concatenate([np.arange(8, 24), np.arange(50, 66)])  # 2 runs of 16 blocks
+        monkeypatch.setenv("FLEXKV_CE_LAYER_RUN_BYTES", str(4 * 16384))
+    else:
+        cids = inputs.distinct_ids(12, 32, 96)
+        monkeypatch.setenv("FLEXKV_CE_RECT_COPIES", "1")
+    cids = np.ascontiguousarray(cids, dtype=np.int64)
+    gids = inputs.distinct_ids(13, len(cids), 64)                     # 32 blocks, 4 MiB
+    launches = {}
+    for cut in (False, True):
+        if cut:
+            monkeypatch.setenv("FLEXKV_CE_EDGE_MIN_BYTES", str(1 << 20))
+        else:
+            monkeypatch.delenv("FLEXKV_CE_EDGE_MIN_BYTES", raising=False)
+        print(f"edge cut order={order} cut={cut}", flush=True)
+        dc = DeviceCase(case)
+        _lib.profile_enable(True)
+        abi_transfer(dc, gids, cids, h2d=False, mode=1)
+        d2h = _lib.profile_read()["kernel_launches"]
+        torch.cuda.synchronize()
+        assert np.array_equal(dc.host_np(), _oracle_d2h(case, gids, cids, 1)), (order, cut)
+        dc.set_gpu([np.zeros_like(g) for g in case.gpu])
+        _lib.profile_enable(True)
+        abi_transfer(dc, gids, cids, h2d=True, mode=1)
+        h2d = _lib.profile_read()["kernel_launches"]
+        _lib.profile_enable(False)
+        torch.cuda.synchronize()
+        for l, g in enumerate(dc.gpu_np()):
+            expect = np.zeros_like(case.gpu[l])
+            expect[:, gids] = case.gpu[l][:, gids]
+            assert np.array_equal(g, expect), (order, cut, l)
+        launches[cut] = (d2h, h2d)
+    assert launches[True] == (launches[False][0] + 1, launches[False][1] + 1), launches
+
+
 @pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("shape", [(1, 1, 32776, 1, 1), (3, 2, 32776, 1, 1),
                                    (1, 1, 128, 8, 16), (1, 1, 256, 16, 16)],
