@@ -586,8 +586,9 @@ def worker_ops(wl: Workload, reps: int = 40, process: bool = True):
     the copy-engine and the zero-copy path; on a worker thread of this
     process (this package's engine default) and, for 16 blocks, in a spawned
     worker process fed IPC handles of the device layers (the reference's
-    worker model; its own pinned host cache of 1024 blocks).  Each op runs
-    inside a roctx range named as the reference names its NVTX range."""
+    worker model; its own pinned host cache of 1024 blocks), reporting
+    finished ops over a pipe as TransferEngine's process mode does.  Each op
+    runs inside a roctx range named as the reference names its NVTX range."""
     import multiprocessing as mp
     import queue
 
@@ -595,7 +596,7 @@ def worker_ops(wl: Workload, reps: int = 40, process: bool = True):
     from flexkv_amd.common.storage import KVCacheLayout, KVCacheLayoutType
     from flexkv_amd.common.transfer import TransferDescriptor, TransferOp, TransferType
     from flexkv_amd.storage.allocator import HostCacheSpec
-    from flexkv_amd.transfer.worker import GPUCPUTransferWorker
+    from flexkv_amd.transfer.worker import FinishedOpsChannel, GPUCPUTransferWorker
     w = wl.w
     L = w["layers"]
     gl = KVCacheLayout(KVCacheLayoutType.LAYERWISE, L, w["ng"], w["tokens"], w["heads"],
@@ -642,7 +643,7 @@ def worker_ops(wl: Workload, reps: int = 40, process: bool = True):
             h.shutdown()
     if process:
         ctx = mp.get_context("spawn")
-        q = ctx.Queue()
+        q = FinishedOpsChannel(ctx)
         small = KVCacheLayout(wl.cl.type, L, 1024, w["tokens"], w["heads"], w["dim"],
                               is_mla=wl.mla)
         for path, ce in (("ce", True), ("kernel", False)):
@@ -660,7 +661,8 @@ def worker_ops(wl: Workload, reps: int = 40, process: bool = True):
             finally:
                 h.shutdown()
     out["what"] = ("16-block ops (32 MiB at this shape) and full-step ops, one at a time, "
-                   "submit to finished-ops queue; copy engines take ops of 8 MiB or more")
+                   "submit to finished-ops queue (spawned workers: a pipe, FinishedOpsChannel); "
+                   "copy engines take ops of 8 MiB or more")
     return out
 
 

@@ -40,7 +40,7 @@ from ..common.debug import flexkv_logger
 from ..common.transfer import TransferOp, TransferOpGraph, TransferType
 from ..storage.allocator import HostCacheSpec, StorageHandle
 from .scheduler import TransferScheduler
-from .worker import CPUSSDDiskTransferWorker, GPUCPUTransferWorker
+from .worker import CPUSSDDiskTransferWorker, FinishedOpsChannel, GPUCPUTransferWorker
 
 _GPU_CPU = (TransferType.H2D, TransferType.D2H)
 _CPU_SSD = (TransferType.DISK2H, TransferType.H2DISK)
@@ -122,9 +122,8 @@ class TransferEngine:
                     self._gpu_workers[("gpucpu", i, kind)] = w
                     self._workers.append(w)
             else:
-                import multiprocessing as mp
                 if self._mp_finished is None:
-                    self._mp_finished = mp.get_context("spawn").Queue()
+                    self._mp_finished = FinishedOpsChannel()
                 w = GPUCPUTransferWorker.create_worker(
                     i, self._mp_finished, gpu_blocks=g.get_tensor_handle_list(),
                     cpu_blocks=HostCacheSpec(self._cpu_handle.kv_layout, self._cpu_handle.dtype),

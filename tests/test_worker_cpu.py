@@ -283,3 +283,28 @@ def test_layerwise_argument_checks():
     with pytest.raises(TypeError, match="int64"):
         c_ext.transfer_kv_blocks_layerwise(ids.int(), ptrs, 0, 0, ids, torch.zeros(4), 0, 0, 0,
                                            16, 0, 1)
+
+
+def _put_ids(ch, ids):
+    for i in ids:
+        ch.put(i)
+
+
+def test_finished_ops_channel_across_processes():
+    """FinishedOpsChannel carries op ids from a spawned process in order, and
+    follows queue.Queue's get: a timeout or get_nowait on an empty channel
+    raises queue.Empty."""
+    import queue
+    ctx = mp.get_context("spawn")
+    ch = W.FinishedOpsChannel(ctx)
+    with pytest.raises(queue.Empty):
+        ch.get_nowait()
+    with pytest.raises(queue.Empty):
+        ch.get(timeout=0.01)
+    p = ctx.Process(target=_put_ids, args=(ch, list(range(200))))
+    p.start()
+    got = [ch.get(timeout=60) for _ in range(200)]
+    p.join(60)
+    assert got == list(range(200)) and p.exitcode == 0
+    ch.put("local")
+    assert ch.get() == "local"
