@@ -20,6 +20,7 @@ Differences from the reference:
 from __future__ import annotations
 
 import collections
+import contextlib
 import multiprocessing as mp
 import queue
 import threading
@@ -151,6 +152,9 @@ class TransferWorkerBase(ABC):
         self.transfer_conn = transfer_conn
         self.finished_ops_queue = finished_ops_queue
         self.failed_ops: List[int] = []
+        # failed op id -> host block ids that copy engines may still write
+        # (copies the library gave up waiting for); see _note_failure
+        self.unsafe_host_blocks: Dict[int, np.ndarray] = {}
 
     @staticmethod
     def _get_layer_ptrs(layer_blocks: Union[Sequence[torch.Tensor], torch.Tensor]) -> torch.Tensor:
@@ -190,8 +194,7 @@ class TransferWorkerBase(ABC):
                 errors.append(e)
                 ready_event.set()
                 return
-            ready_event.set()
-            worker.run()
+            worker.serve(ready_event)
 
         thread = threading.Thread(target=body, name=f"flexkv-worker-{worker_id}", daemon=True)
         thread.start()
@@ -200,9 +203,18 @@ class TransferWorkerBase(ABC):
     @classmethod
     def _worker_process(cls, worker_id: int, transfer_conn: Connection, finished_ops_queue: Any,
                         ready_event: Any, *args: Any, **kwargs: Any) -> None:
-        worker = cls(worker_id, transfer_conn, finished_ops_queue, *args, **kwargs)
+        """Body of a spawned worker process.  Its end of the op pipe is closed
+        whichever way it leaves, so the parent's next send fails at once
+        instead of writing into a pipe nobody reads.  A worker that cannot
+        be built never signals readiness; the parent's wait on ready_event
+        times out and the exception is in this process's stderr."""
+        with contextlib.closing(transfer_conn):
+            cls(worker_id, transfer_conn, finished_ops_queue, *args, **kwargs).serve(ready_event)
+
+    def serve(self, ready_event: Any) -> None:
+        """Announce readiness, then run the op loop until stopped."""
         ready_event.set()
-        worker.run()
+        self.run()
 
     @abstractmethod
     def _transfer_impl(self, src_block_ids: np.ndarray, dst_block_ids: np.ndarray,
@@ -231,8 +243,23 @@ class TransferWorkerBase(ABC):
         except Exception as e:
             self.failed_ops.append(op.transfer_op_id)
             flexkv_logger.error(f"Error launching transfer: {e}\nFailed transfer op: {op}")
+            self._note_failure(op)
         if self.finished_ops_queue is not None:
             self.finished_ops_queue.put(op.transfer_op_id)
+
+    def _note_failure(self, op: WorkerTransferOp) -> None:
+        """After a failed op: the host blocks whose rows a copy engine may
+        still write, because the library gave up waiting for its copies
+        (fkv_last_unsafe_host_blocks, read on the thread that made the
+        call), are kept in unsafe_host_blocks under the op id and logged.
+        The op is reported finished as any failed op is; those host blocks
+        must not be read or reused until abandoned_copies_pending() reads 0."""
+        ids = _lib.last_unsafe_host_blocks()
+        if ids:
+            self.unsafe_host_blocks[op.transfer_op_id] = np.asarray(ids, dtype=np.int64)
+            flexkv_logger.error(
+                f"transfer op {op.transfer_op_id}: copy engines may still write {len(ids)} host "
+                f"blocks after the failure; they stay unsafe until the abandoned copies finish")
 
     # How long the main loop's poll waits for an op.  A poll returns as soon
     # as an op arrives, so this bounds only the wakeups of an idle worker.
@@ -269,14 +296,20 @@ class TransferWorkerBase(ABC):
                 flexkv_logger.error(f"Error in worker run loop: {e}")
 
 
-class WorkerHandle:
-    """Parent-side handle of a worker process (worker.py:179-205)."""
+class _WorkerHandleBase:
+    """What the engine holds of a worker wherever it runs: ops go in through
+    submit_transfer, and shutdown() stops it.  A stop puts the sentinel None
+    behind the ops already sent (run() finishes those first), allows
+    STOP_GRACE_S for the worker to end, then forces the end where that is
+    possible.  Subclasses say how to wait for the worker and how to force it
+    (the reference waits 5 s for its process, then terminates it,
+    worker.py:189-198)."""
 
-    def __init__(self, worker_id: int, transfer_conn: Connection, process: Any,
-                 ready_event: Any) -> None:
+    STOP_GRACE_S = 5.0
+
+    def __init__(self, worker_id: int, transfer_conn: Any, ready_event: Any) -> None:
         self.worker_id = worker_id
         self.transfer_conn = transfer_conn
-        self.process = process
         self.ready_event = ready_event
 
     def submit_transfer(self, op: TransferOp) -> None:
@@ -285,32 +318,61 @@ class WorkerHandle:
     def shutdown(self) -> None:
         try:
             self.transfer_conn.send(None)
+        except OSError:
+            pass        # the worker's end is closed already: it has stopped or died
+        self._after_stop_sent()
+        if not self._ended_within(self.STOP_GRACE_S):
+            self._force_end()
+
+    def _after_stop_sent(self) -> None:
+        pass
+
+    def _ended_within(self, timeout: float) -> bool:
+        raise NotImplementedError
+
+    def _force_end(self) -> None:
+        raise NotImplementedError
+
+
+class WorkerHandle(_WorkerHandleBase):
+    """Parent-side handle of a worker process started by create_worker."""
+
+    def __init__(self, worker_id: int, transfer_conn: Connection, process: Any,
+                 ready_event: Any) -> None:
+        super().__init__(worker_id, transfer_conn, ready_event)
+        self.process = process
+
+    def _after_stop_sent(self) -> None:
+        # nothing more is sent; the worker sees EOF after the sentinel
+        with contextlib.suppress(OSError):
             self.transfer_conn.close()
-        except (BrokenPipeError, OSError):
-            pass
-        self.process.join(timeout=5)
-        if self.process.is_alive():
-            flexkv_logger.warning("force terminate the worker process")
-            self.process.terminate()
-            self.process.join()
+
+    def _ended_within(self, timeout: float) -> bool:
+        self.process.join(timeout)
+        return not self.process.is_alive()
+
+    def _force_end(self) -> None:
+        flexkv_logger.warning(f"worker {self.worker_id} did not stop within "
+                              f"{self.STOP_GRACE_S:.0f} s; terminating its process")
+        self.process.terminate()
+        self.process.join()
 
     def __del__(self) -> None:
-        try:
+        with contextlib.suppress(Exception):
             if self.process.is_alive():
                 self.shutdown()
-        except Exception:
-            pass
 
 
-class ThreadWorkerHandle:
-    """Handle of a worker running on a thread (same interface as WorkerHandle)."""
+class ThreadWorkerHandle(_WorkerHandleBase):
+    """Handle of a worker running on a thread of this process
+    (create_worker_thread).  A thread cannot be forced to end: one that
+    outlasts the grace period is left running (it is a daemon thread) and
+    logged."""
 
     def __init__(self, worker_id: int, conn: LocalChannel, thread: threading.Thread,
                  ready_event: threading.Event, errors: List[BaseException]) -> None:
-        self.worker_id = worker_id
-        self.transfer_conn = conn
+        super().__init__(worker_id, conn, ready_event)
         self.thread = thread
-        self.ready_event = ready_event
         self._errors = errors
 
     def wait_ready(self, timeout: float = 60.0) -> None:
@@ -320,12 +382,13 @@ class ThreadWorkerHandle:
             raise RuntimeError(f"worker {self.worker_id} failed to start: {self._errors[0]}") \
                 from self._errors[0]
 
-    def submit_transfer(self, op: TransferOp) -> None:
-        self.transfer_conn.send(WorkerTransferOp(op))
+    def _ended_within(self, timeout: float) -> bool:
+        self.thread.join(timeout)
+        return not self.thread.is_alive()
 
-    def shutdown(self) -> None:
-        self.transfer_conn.send(None)
-        self.thread.join(timeout=5)
+    def _force_end(self) -> None:
+        flexkv_logger.warning(f"worker thread {self.worker_id} did not stop within "
+                              f"{self.STOP_GRACE_S:.0f} s; leaving it running")
 
 
 class GPUCPUTransferWorker(TransferWorkerBase):

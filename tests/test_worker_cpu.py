@@ -168,7 +168,7 @@ class _NullCtx:
         return False
 
 
-def test_c_ext_argument_checks():
+def test_c_ext_argument_checks(per_call_path):
     from flexkv_amd import c_ext
     ids = torch.tensor([1, 2], dtype=torch.int64)
     ptrs = torch.tensor([0], dtype=torch.int64)
@@ -186,7 +186,7 @@ def test_c_ext_argument_checks():
             c_ext.transfer_kv_blocks(ids, ptrs, 0, 0, ids, cache, 0, 0, 0, 16, 0)
 
 
-def test_c_ext_kv_ptrs_and_scalar_checks():
+def test_c_ext_kv_ptrs_and_scalar_checks(per_call_path):
     """The compiled per-call path refuses what the Python signature refuses,
     with the same error types, for both entry points."""
     from flexkv_amd import c_ext
