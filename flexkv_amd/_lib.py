@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import atexit
 import ctypes
+import operator
 import os
 import threading
 
@@ -47,6 +48,8 @@ EXPORTED_SYMBOLS = (
     "fkv_ssd_close",
     "fkv_transfer_kv_blocks_ssd",
     "fkv_last_error",
+    "fkv_last_unsafe_host_blocks",
+    "fkv_abandoned_copies_pending",
     "fkv_host_alloc",
     "fkv_host_free",
     "fkv_host_register",
@@ -167,6 +170,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.fkv_profile_read.argtypes = [ctypes.POINTER(FkvProfile)]
     lib.fkv_version.restype = ctypes.c_char_p
     lib.fkv_version.argtypes = []
+    lib.fkv_last_unsafe_host_blocks.restype = c_int
+    lib.fkv_last_unsafe_host_blocks.argtypes = [c_vp, c_int]
+    lib.fkv_abandoned_copies_pending.restype = c_int
+    lib.fkv_abandoned_copies_pending.argtypes = [c_int]
 
 
 def hip_runtimes_loaded(name: str = "libamdhip64.so") -> list:
@@ -207,24 +214,127 @@ def load() -> ctypes.CDLL:
 
 
 _fast = None
+_INT_MAX = 2**31 - 1
+
+
+class _CtypesCalls:
+    """The per-call path of c_ext.transfer_kv_blocks and
+    transfer_kv_blocks_kv_ptrs over ctypes, with the compiled module's
+    argument conventions: the same 16 / 15 positional arguments, False
+    (nothing raised) when a tensor check fails so that c_ext names the
+    argument, RuntimeError with the library's message when the transfer
+    fails.  Used when _fkv_py cannot be imported (not built, or built for
+    another torch or Python); each call costs a few microseconds more."""
+
+    def __init__(self, lib: ctypes.CDLL):
+        self._lib = lib
+        self._device_visible = None
+
+    @staticmethod
+    def _i64_host(t) -> bool:
+        return (isinstance(t, torch.Tensor) and t.dtype == torch.int64 and t.is_cpu
+                and t.is_contiguous())
+
+    @staticmethod
+    def _mode(v) -> int:
+        if isinstance(v, bool) or type(v).__name__ in ("bool_", "bool"):
+            return FKV_XFER_CE if bool(v) else FKV_XFER_KERNEL
+        return operator.index(v)
+
+    @staticmethod
+    def _c_int(v, what: str) -> int:
+        v = operator.index(v)
+        if not -_INT_MAX - 1 <= v <= _INT_MAX:
+            raise OverflowError(f"{what} {v} does not fit a C int")
+        return v
+
+    def _stream(self, stream):
+        if stream is not None:
+            return int(stream)
+        if self._device_visible is None:
+            self._device_visible = torch.cuda.is_available()
+        if not self._device_visible:
+            return None
+        return torch.cuda.current_stream().cuda_stream
+
+    def _finish(self, rc: int) -> None:
+        if rc != 0:
+            msg = last_error()
+            raise RuntimeError(msg or f"transfer failed ({rc})")
+
+    def transfer_kv_blocks(self, gids, ptrs, gkv, gblk, cids, cpu, ckv, clay, cblk, chunk,
+                           start, sms, h2d, mode, mla, stream):
+        if not (self._i64_host(gids) and self._i64_host(ptrs) and self._i64_host(cids)
+                and isinstance(cpu, torch.Tensor)) or cids.numel() != gids.numel():
+            return False
+        for n, what in ((gids.numel(), "block ids"), (ptrs.numel(), "layer pointers")):
+            if n > _INT_MAX:
+                raise RuntimeError(f"{n} {what} in one call; at most {_INT_MAX}")
+        ix = operator.index
+        args = (ix(gkv), ix(gblk), ix(ckv), ix(clay), ix(cblk), ix(chunk),
+                self._c_int(start, "start_layer_id"), self._c_int(sms, "transfer_sms"),
+                1 if h2d else 0, self._mode(mode), 1 if mla else 0)
+        st = self._stream(stream)
+        if st is None:
+            return False
+        gkv, gblk, ckv, clay, cblk, chunk, start, sms, h2d, mode, mla = args
+        self._finish(self._lib.fkv_transfer_kv_blocks(
+            gids.numel(), start, ptrs.numel(), gids.data_ptr(), ptrs.data_ptr(), gkv, gblk,
+            cids.data_ptr(), cpu.data_ptr(), ckv, clay, cblk, 0, chunk, st, sms, h2d, mode, mla))
+        return None
+
+    def transfer_kv_blocks_kv_ptrs(self, gids, ptrs, gblk, cids, cpu, ckv, clay, cblk, chunk,
+                                   start, sms, h2d, mode, mla, stream):
+        if not (self._i64_host(gids) and self._i64_host(ptrs) and self._i64_host(cids)
+                and isinstance(cpu, torch.Tensor)):
+            return False
+        for n, what in ((gids.numel(), "block ids"), (ptrs.numel(), "layer pointers")):
+            if n > _INT_MAX:
+                raise RuntimeError(f"{n} {what} in one call; at most {_INT_MAX}")
+        ix = operator.index
+        args = (ix(gblk), ix(ckv), ix(clay), ix(cblk), ix(chunk),
+                self._c_int(start, "start_layer_id"), self._c_int(sms, "transfer_sms"),
+                1 if h2d else 0, self._mode(mode), 1 if mla else 0)
+        kv = 1 if mla else 2
+        if cids.numel() != gids.numel() or ptrs.numel() % kv:
+            return False
+        st = self._stream(stream)
+        if st is None:
+            return False
+        gblk, ckv, clay, cblk, chunk, start, sms, h2d, mode, mla = args
+        self._finish(self._lib.fkv_transfer_kv_blocks_kv_ptrs(
+            gids.numel(), start, ptrs.numel() // kv, gids.data_ptr(), ptrs.data_ptr(), gblk,
+            cids.data_ptr(), cpu.data_ptr(), ckv, clay, cblk, 0, chunk, st, sms, h2d, mode, mla))
+        return None
 
 
 def fast():
-    """Load (once) and return the compiled module ``_fkv_py`` that carries the
-    per-call path of c_ext.transfer_kv_blocks, bound to the functions of the
-    library that load() returns; raise if it is not built."""
+    """Load (once) and return the per-call path of c_ext.transfer_kv_blocks:
+    the compiled module ``_fkv_py`` bound to the functions of the library
+    that load() returns, or, when that module cannot be imported (not built,
+    or built against another torch or Python) or FLEXKV_PY_FASTCALL=0, the
+    ctypes calls of _CtypesCalls (logged once)."""
     global _fast
     if _fast is not None:
         return _fast
     lib = load()
     with _lock:
         if _fast is None:
-            try:
-                from . import _fkv_py
-            except ImportError as e:
-                raise ImportError(
-                    f"flexkv_amd/_fkv_py is not built ({e}); run `python -c 'import "
-                    "__graft_entry__ as g; g.build()'` from the repository root") from e
+            reason = None
+            if os.environ.get("FLEXKV_PY_FASTCALL", "1") == "0":
+                reason = "FLEXKV_PY_FASTCALL=0"
+            else:
+                try:
+                    from . import _fkv_py
+                except ImportError as e:
+                    reason = f"flexkv_amd/_fkv_py cannot be imported ({e})"
+            if reason is not None:
+                import logging
+                logging.getLogger("flexkv").warning(
+                    "%s; transfer_kv_blocks calls the library through ctypes (rebuild with "
+                    "`python -c 'import __graft_entry__ as g; g.build()'`)", reason)
+                _fast = _CtypesCalls(lib)
+                return _fast
 
             def addr(fn) -> int:
                 return ctypes.cast(fn, ctypes.c_void_p).value
@@ -232,6 +342,18 @@ def fast():
                          addr(lib.fkv_last_error), FKV_XFER_KERNEL, FKV_XFER_CE)
             _fast = _fkv_py
     return _fast
+
+
+def reset_fast() -> None:
+    """Forget the chosen per-call path, so the next fast() chooses again
+    (tests switch between the compiled module and the ctypes calls)."""
+    global _fast
+    import sys
+    with _lock:
+        _fast = None
+        c_ext = sys.modules.get(__package__ + ".c_ext")
+        if c_ext is not None:
+            c_ext._fast = None
 
 
 def finalize() -> None:
@@ -250,6 +372,27 @@ def finalize() -> None:
     if rc != 0:
         import sys
         print(f"flexkv: fkv_finalize failed (status {rc}): {last_error()}", file=sys.stderr)
+
+
+def last_unsafe_host_blocks() -> list:
+    """Host block ids that copy engines may still write after this thread's
+    last failed transfer (fkv_last_unsafe_host_blocks); [] when none."""
+    lib = load()
+    n = lib.fkv_last_unsafe_host_blocks(None, 0)
+    if n <= 0:
+        return []
+    buf = (ctypes.c_int64 * n)()
+    n = min(n, lib.fkv_last_unsafe_host_blocks(buf, n))
+    return list(buf[:n])
+
+
+def abandoned_copies_pending(device: int = -1) -> int:
+    """Copies given up on by timed-out copy-engine waits that have not
+    finished yet (fkv_abandoned_copies_pending)."""
+    n = load().fkv_abandoned_copies_pending(int(device))
+    if n < 0:
+        raise RuntimeError(last_error() or "fkv_abandoned_copies_pending failed")
+    return n
 
 
 def last_error() -> str:

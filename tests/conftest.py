@@ -32,3 +32,17 @@ def gpu_available() -> bool:
 def _skip_gpu_without_device(request):
     if request.node.get_closest_marker("gpu") is not None and not gpu_available():
         pytest.skip("no HIP device")
+
+
+@pytest.fixture(params=["compiled", "ctypes"])
+def per_call_path(request, monkeypatch):
+    """Run a test through the compiled per-call module of c_ext and through
+    the ctypes calls that stand in for it when the module cannot be imported."""
+    from flexkv_amd import _lib
+    monkeypatch.setenv("FLEXKV_PY_FASTCALL", "0" if request.param == "ctypes" else "1")
+    _lib.reset_fast()
+    fast = _lib.fast()
+    assert isinstance(fast, _lib._CtypesCalls) == (request.param == "ctypes")
+    yield request.param
+    monkeypatch.delenv("FLEXKV_PY_FASTCALL")
+    _lib.reset_fast()
