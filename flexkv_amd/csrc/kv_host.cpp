@@ -24,6 +24,11 @@ std::string& last_error() {
   return msg;
 }
 
+std::vector<int64_t>& last_unsafe_host_blocks() {
+  static thread_local std::vector<int64_t> ids;
+  return ids;
+}
+
 int fail(int code, const char* fmt, ...) {
   char buf[1024];
   va_list ap;
@@ -110,8 +115,11 @@ int ids_acquire(size_t bytes, IdBuf* out) {
       return 0;
     }
   }
+  // Capacities are powers of two (at least 64 KiB), so rising request sizes
+  // leave at most one buffer per size class in the pool, not one per size.
   IdBuf b;
-  b.cap = std::max<size_t>(bytes, 64 << 10);
+  b.cap = size_t(64) << 10;
+  while (b.cap < bytes) b.cap <<= 1;
   void* p = nullptr;
   FKV_HIP(hipHostMalloc(&p, b.cap, hipHostMallocPortable | hipHostMallocMapped | hipHostMallocCoherent));
   void* dp = nullptr;
@@ -160,6 +168,19 @@ int streams_destroy_all() {
       rc = fail(static_cast<int>(e), "destroying a library stream: %s", hipGetErrorString(e));
   }
   return rc;
+}
+
+bool geometry_vec16(const Geometry& g) {
+  const int64_t vals[] = {g.chunk, g.gks, g.gbs, g.cks, g.cls, g.cbs, g.startoff};
+  for (int64_t v : vals)
+    if (v % 16 != 0) return false;
+  if (reinterpret_cast<uintptr_t>(g.cpu_ptr) % 16 != 0) return false;
+  if (g.layer_ptrs && g.num_layers > 0) {
+    const int64_t nptr = static_cast<int64_t>(g.num_layers) * g.ptrs_per_layer;
+    for (int64_t i = 0; i < nptr; ++i)
+      if (reinterpret_cast<uintptr_t>(g.layer_ptrs[i]) % 16 != 0) return false;
+  }
+  return true;
 }
 
 int validate(Geometry& g, int mode) {
@@ -319,6 +340,13 @@ int fkv_stream_destroy(fkv_stream_t s) {
 }
 
 const char* fkv_last_error(void) { return last_error().c_str(); }
+
+int fkv_last_unsafe_host_blocks(int64_t* out, int cap) {
+  const std::vector<int64_t>& ids = last_unsafe_host_blocks();
+  const int n = static_cast<int>(ids.size());
+  if (out && cap > 0) std::memcpy(out, ids.data(), sizeof(int64_t) * std::min(n, cap));
+  return n;
+}
 
 int fkv_host_alloc(void** out_ptr, size_t bytes, unsigned flags) {
   last_error().clear();

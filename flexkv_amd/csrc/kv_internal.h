@@ -87,6 +87,9 @@ struct CopyLane {
   // on).  The signals of the copies given up on are kept here, never destroyed.
   bool stalled = false;
   std::vector<hsa_signal_t> abandoned;
+  // host block ids the device-to-host copies of each half write, and those
+  // of halves given up on (the device-to-host lane only)
+  HostRowLedger rows;
   // stream (own hardware queue) of the copy-engine layer-wise pipeline's
   // scatter kernels, made on first use under stream_mu
   std::mutex stream_mu;
@@ -183,6 +186,10 @@ struct Geometry {
 // Check ids, strides, alignment and that every byte the transfer touches lies
 // inside the host and device allocations; fills the id ranges and cpu_info.
 int validate(Geometry& g, int mode);
+// Whether the chunk size, every stride, the start offset, cpu_ptr and every
+// layer pointer are multiples of 16 bytes, as the kernels' 16-byte accesses
+// need.  Null pointers pass (validate reports them).
+bool geometry_vec16(const Geometry& g);
 
 // Profiling (fkv_profile_enable / fkv_profile_read)
 extern std::atomic<bool> g_prof_on;

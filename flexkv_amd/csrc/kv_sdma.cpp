@@ -204,12 +204,14 @@ int sdma_wait(DeviceState& dev, CopyLane& d, int half, bool spin) {
   // loads their values (any agent may) and never waits on them.
   HsaSignalOps ops;
   const int64_t limit_ms = sdma_timeout_ms();
-  const WaitOutcome w = wait_copies(ops, d.wake[half], d.queued[half], spin,
-                                    std::chrono::steady_clock::now() +
-                                        std::chrono::milliseconds(limit_ms));
+  const WaitOutcome w = wait_half(ops, d.wake[half], d.queued[half], spin,
+                                  std::chrono::steady_clock::now() +
+                                      std::chrono::milliseconds(limit_ms),
+                                  d.rows, half);
   if (!w.done) {
     // Give up on this half: its copies may still complete (or never), so
-    // their signals and the staging buffer are never reused or freed.
+    // their signals and the staging buffer are never reused or freed, and
+    // the host blocks they write are now in d.rows' unsafe list.
     for (hsa_signal_t s : d.queued[half]) d.abandoned.push_back(s);
     for (int h = 0; h < 2; ++h) {
       auto drop = [&](std::vector<hsa_signal_t>& pool) {
@@ -612,3 +614,20 @@ int sdma_prepare_lane(DeviceState& d, CopyLane& lane, bool h2d, size_t copies_pe
 bool sdma_rect_available() { return g_hsa.async_copy_rect != nullptr; }
 
 }  // namespace fkv_detail
+
+using namespace fkv_detail;
+
+extern "C" int fkv_abandoned_copies_pending(int device) {
+  last_error().clear();
+  int dev = device;
+  if (dev < 0 && hipGetDevice(&dev) != hipSuccess) return fail(-1, "no current device");
+  if (dev >= kMaxDevices) return fail(-1, "device %d out of range", dev);
+  int pending = 0;
+  for (CopyLane& ln : g_dev[dev].lane) {
+    std::lock_guard<std::mutex> lk(ln.mu);
+    if (ln.abandoned.empty() || !g_hsa_loaded) continue;
+    for (hsa_signal_t s : ln.abandoned)
+      if (g_hsa.signal_load_scacquire(s) >= 1) ++pending;
+  }
+  return pending;
+}

@@ -731,6 +731,7 @@ int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, voi
                                int64_t block_stride_bytes, int is_read, int round_robin,
                                int num_threads_per_device, int is_mla) try {
   fkv_detail::last_error().clear();
+  fkv_detail::last_unsafe_host_blocks().clear();
   if (!h) return ssd_fail("null SSD context");
   if (num_blocks <= 0 || num_layers <= 0) return 0;
   if (!cpu_ptr || !ssd_block_ids || !cpu_block_ids || chunk_size_bytes <= 0 || round_robin <= 0 ||

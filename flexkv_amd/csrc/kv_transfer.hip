@@ -814,7 +814,9 @@ int transfer_zero_copy(const Geometry& g, hipStream_t stream, int dev, int trans
 // holds its own copy of the array; host code reaches it only through the
 // address hipGetSymbolAddress returns for the device (the array's name is a
 // host-side stand-in, not a device address).  Every call on a device shares
-// that device's array, so calls that overlap on one device race.
+// that device's array, so a call holds the device's scratch mutex from the
+// copy of its ids into the array until its kernels have finished: calls
+// from several threads on one device take turns instead of racing.
 
 constexpr size_t kScratchBytes = size_t(1) << 20;
 // gpu ids in the first half, cpu ids in the second
@@ -824,6 +826,8 @@ static __device__ __align__(256) int64_t scratch[kScratchBytes / sizeof(int64_t)
 
 std::mutex g_scratch_mu;
 int64_t* g_scratch_dev[kMaxDevices];   // scratch's address on each device, once resolved
+// held by a call from its scratch copy until its stream is synchronised
+std::mutex g_scratch_use_mu[kMaxDevices];
 
 // scratch's device address on `dev` (resolved once per device, with the
 // device current).
@@ -869,6 +873,9 @@ int transfer_zero_copy_noalloc(const Geometry& g, hipStream_t stream, int dev, i
   int64_t pairs[2 * kInlineIds];
   IdBuf ids;
   int32_t split = 0;
+  // Declared before the DrainOnError below, so an error path drains the
+  // stream before the next call may overwrite the scratch.
+  std::unique_lock<std::mutex> scratch_use(g_scratch_use_mu[dev], std::defer_lock);
   if (g.num_blocks <= kInlineIds) {
     // the ids travel in the kernel arguments
     pack_ids_into(g, pairs);
@@ -877,9 +884,12 @@ int transfer_zero_copy_noalloc(const Geometry& g, hipStream_t stream, int dev, i
     int64_t* sp = nullptr;
     int rc = scratch_address(dev, &sp);
     if (rc) return rc;
+    scratch_use.lock();
     const size_t n = static_cast<size_t>(g.num_blocks) * sizeof(int64_t);
+    DrainOnError copy_drain{stream};   // a failed second copy still waits for the first
     FKV_HIP(hipMemcpyAsync(sp, g.gids, n, hipMemcpyHostToDevice, stream));
     FKV_HIP(hipMemcpyAsync(sp + kScratchMaxBlocks, g.cids, n, hipMemcpyHostToDevice, stream));
+    copy_drain.armed = false;
     ids.dev = reinterpret_cast<char*>(sp);
     split = kScratchMaxBlocks;
   }
@@ -1043,6 +1053,16 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   // Host-side waits order everything below against the caller's stream, so
   // work already queued on it comes first.
   FKV_HIP(hipStreamSynchronize(stream));
+  // After the drain below (declared later, so it runs first), hand the host
+  // blocks of device-to-host copies given up on to the calling thread
+  // (fkv_last_unsafe_host_blocks).
+  struct PublishUnsafeRows {
+    CopyLane& ln;
+    ~PublishUnsafeRows() {
+      std::vector<int64_t> ids = ln.rows.take_unsafe();
+      if (!ids.empty()) last_unsafe_host_blocks() = std::move(ids);
+    }
+  } publish{ln};
   DrainOnError drain{stream, &d, &ln};
   ProfRecorder prof;
   std::vector<Run> runs;
@@ -1058,6 +1078,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
     dma_bytes += piece_bytes;
     dma_copies += static_cast<int64_t>(runs.size());
     pending[h] = true;
+    if (!h2d) ln.rows.queued(h, g.cids + p.b0, static_cast<size_t>(p.nb));
     // Host-to-device copies shorter than kWideCopyBytes on average are bound
     // by the engines' per-copy cost and spread over the wide set
     const bool wide = h2d && !runs.empty() &&
@@ -1163,6 +1184,7 @@ int contiguous_entry(int num_blocks, int num_layers, const int64_t* gpu_block_id
                      size_t buffer_bytes, fkv_stream_t stream, int is_mla, bool to_gpu) {
   try {
     last_error().clear();
+    last_unsafe_host_blocks().clear();
     if (num_blocks == 0 || num_layers == 0) return 0;
     if (num_blocks < 0 || num_layers < 0)
       return fail(kInval, "negative count: num_blocks=%d num_layers=%d", num_blocks, num_layers);
@@ -1715,7 +1737,12 @@ bool ce_pays_off(const Geometry& g, bool h2d) {
 }
 
 // Validate, then run one synchronous transfer in the requested mode.
+// Copy-engine mode copies exact bytes for any geometry, as the reference's
+// CE loop does (csrc/transfer.cu:97-121): a chunk size, stride, offset or
+// pointer that is not a multiple of 16 bytes, which the kernels' 16-byte
+// accesses cannot take, sends the transfer to the per-chunk engine loop.
 int transfer_entry(Geometry& g, hipStream_t s, int transfer_cus, bool h2d, int mode) {
+  if (mode == FKV_XFER_CE && !geometry_vec16(g)) mode = FKV_XFER_CE_PER_CHUNK;
   int rc = validate(g, mode);
   if (rc) return rc;
   int dev = 0;
@@ -1747,6 +1774,7 @@ int fkv_transfer_kv_blocks(int num_blocks, int start_layer_id, int num_layers,
                            int is_host_to_device, int use_ce_transfer, int is_mla) {
   try {
     last_error().clear();
+    last_unsafe_host_blocks().clear();
     if (use_ce_transfer < FKV_XFER_KERNEL || use_ce_transfer > FKV_XFER_CE_PER_CHUNK)
       return fail(kInval, "use_ce_transfer must be 0 (kernel), 1 (CE) or 2 (CE per chunk), got %d",
                   use_ce_transfer);
@@ -1775,6 +1803,7 @@ int fkv_transfer_kv_blocks_kv_ptrs(int num_blocks, int start_layer_id, int num_l
                                    int use_ce_transfer, int is_mla) {
   try {
     last_error().clear();
+    last_unsafe_host_blocks().clear();
     if (use_ce_transfer < FKV_XFER_KERNEL || use_ce_transfer > FKV_XFER_CE_PER_CHUNK)
       return fail(kInval, "use_ce_transfer must be 0 (kernel), 1 (CE) or 2 (CE per chunk), got %d",
                   use_ce_transfer);
@@ -1804,15 +1833,25 @@ int fkv_transfer_kv_blocks_noalloc(int num_blocks, int start_layer_id, int num_l
                                    int is_mla) {
   try {
     last_error().clear();
+    last_unsafe_host_blocks().clear();
     if (num_blocks == 0 || num_layers == 0) return 0;
     Geometry g = make_geometry(num_blocks, start_layer_id, num_layers, gpu_block_ids,
                                gpu_layer_ptrs, gpu_kv_stride_bytes, gpu_block_stride_bytes,
                                cpu_block_ids, cpu_ptr, cpu_kv_stride_bytes,
                                cpu_layer_stride_bytes, cpu_block_stride_bytes,
                                cpu_startoff_inside_chunks, chunk_size_bytes, is_mla);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // The call is synchronous and resolves its ids and addresses on the host
+    // while it runs, so a captured call could not replay: refuse capture
+    // before anything reaches the stream (the null stream is never captured).
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (s) FKV_HIP(hipStreamIsCapturing(s, &cap));
+    if (cap != hipStreamCaptureStatusNone)
+      return fail(static_cast<int>(hipErrorStreamCaptureUnsupported),
+                  "fkv_transfer_kv_blocks_noalloc cannot run on a stream under HIP graph "
+                  "capture (it synchronises the stream and stages ids from host memory)");
     int rc = validate(g, FKV_XFER_KERNEL);
     if (rc) return rc;
-    hipStream_t s = static_cast<hipStream_t>(stream);
     int dev = 0;
     if ((rc = stream_device(s, &dev))) return rc;
     if ((rc = ensure_device_basics(dev))) return rc;
@@ -1853,6 +1892,7 @@ int fkv_transfer_kv_blocks_layerwise(
     fkv_transfer_handle* out) {
   try {
     last_error().clear();
+    last_unsafe_host_blocks().clear();
     if (!out) return fail(kInval, "out handle pointer is null");
     if (use_ce_transfer != FKV_XFER_KERNEL && use_ce_transfer != FKV_XFER_CE)
       return fail(kInval, "use_ce_transfer must be 0 (kernel) or 1 (copy engines), got %d",

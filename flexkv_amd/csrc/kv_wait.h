@@ -76,4 +76,44 @@ WaitOutcome wait_copies(Ops& ops, const std::vector<hsa_signal_t>& wake,
   return out;
 }
 
+// Which host blocks the device-to-host copies of each staging half write.
+// A half holds one piece at a time: queued() records the piece's host block
+// ids when its copies are queued, finished() forgets them once the wait on
+// the half succeeds, and abandoned() moves them to `unsafe` when the wait
+// gives up: an engine may still write those blocks' rows of the host cache
+// after the call has returned.  take_unsafe() hands the list to the caller
+// and empties it.
+struct HostRowLedger {
+  std::vector<int64_t> pending[2];
+  std::vector<int64_t> unsafe;
+
+  void queued(int half, const int64_t* ids, size_t n) { pending[half].assign(ids, ids + n); }
+  void finished(int half) { pending[half].clear(); }
+  void abandoned(int half) {
+    unsafe.insert(unsafe.end(), pending[half].begin(), pending[half].end());
+    pending[half].clear();
+  }
+  std::vector<int64_t> take_unsafe() {
+    std::vector<int64_t> out;
+    out.swap(unsafe);
+    return out;
+  }
+};
+
+// One bounded wait on the copies of staging half `half`, keeping the ledger:
+// the half's host blocks are forgotten when its copies have finished and
+// become unsafe when the wait gives up.
+template <class Ops>
+WaitOutcome wait_half(Ops& ops, const std::vector<hsa_signal_t>& wake,
+                      const std::vector<hsa_signal_t>& queued, bool spin,
+                      std::chrono::steady_clock::time_point deadline, HostRowLedger& rows,
+                      int half) {
+  const WaitOutcome w = wait_copies(ops, wake, queued, spin, deadline);
+  if (w.done)
+    rows.finished(half);
+  else
+    rows.abandoned(half);
+  return w;
+}
+
 }  // namespace fkv_detail

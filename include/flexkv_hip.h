@@ -136,19 +136,22 @@ int fkv_transfer_kv_blocks_kv_ptrs(int num_blocks, int start_layer_id, int num_l
                                    int is_host_to_device, int use_ce_transfer, int is_mla);
 
 /* As fkv_transfer_kv_blocks in kernel mode (FKV_XFER_KERNEL), for callers
- * that cannot allocate memory: code under HIP graph capture, tight serving
- * loops, harnesses that forbid allocation.  No counterpart in the reference.
- * It calls no hipMalloc, hipFree, pinned or other allocating routine:
- * fkv_transfer_kv_blocks stages the id lists in pinned buffers the library
- * allocates; this entry copies them (hipMemcpyAsync on `stream`) into a fixed
- * 1 MiB device array compiled into the library, one per GPU, held until the
- * process ends.  At most 65536 blocks per call; more is refused with
- * hipErrorInvalidValue.  Transfers of up to 32 blocks carry their ids in the
- * kernel arguments instead.  Every call on one GPU shares that GPU's array:
- * calls that overlap on one GPU (from several threads) race and must be
- * serialised by the caller.  Same arguments (without use_ce_transfer),
- * checks and synchronous return as fkv_transfer_kv_blocks; library
- * profiling does not see these calls. */
+ * that cannot allocate memory: tight serving loops and harnesses that forbid
+ * allocation.  No counterpart in the reference.  It calls no hipMalloc,
+ * hipFree, pinned or other allocating routine: fkv_transfer_kv_blocks stages
+ * the id lists in pinned buffers the library allocates; this entry copies
+ * them (hipMemcpyAsync on `stream`) into a fixed 1 MiB device array compiled
+ * into the library, one per GPU, held until the process ends.  At most 65536
+ * blocks per call; more is refused with hipErrorInvalidValue.  Transfers of
+ * up to 32 blocks carry their ids in the kernel arguments instead.  Calls on
+ * one GPU share that GPU's array: a call holds a per-GPU mutex from its copy
+ * into the array until its kernels have finished, so concurrent calls from
+ * several threads take turns.  Not for HIP graph capture: the call is
+ * synchronous and resolves ids and addresses on the host, so a stream under
+ * capture is refused with hipErrorStreamCaptureUnsupported before anything is
+ * queued.  Same arguments (without use_ce_transfer), checks and synchronous
+ * return as fkv_transfer_kv_blocks; library profiling does not see these
+ * calls. */
 int fkv_transfer_kv_blocks_noalloc(int num_blocks, int start_layer_id, int num_layers,
                                    const int64_t* gpu_block_ids, void* const* gpu_layer_ptrs,
                                    int64_t gpu_kv_stride_bytes, int64_t gpu_block_stride_bytes,
@@ -303,6 +306,26 @@ int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, voi
 
 /* Message of the last failed call made by this thread ("" if none). */
 const char* fkv_last_error(void);
+
+/* Host block ids (cpu_block_ids values) of this thread's last
+ * fkv_transfer_kv_blocks or fkv_transfer_kv_blocks_kv_ptrs call whose
+ * device-to-host copy-engine copies were given up on: a wait on the copy
+ * engines timed out (FLEXKV_SDMA_TIMEOUT_MS), so an engine may still write
+ * those blocks' rows of the host cache after the call returned its error.
+ * Writes up to `cap` ids to `out` (which may be null when cap is 0) and
+ * returns how many there are; 0 after a call that left no copy behind.
+ * Such a call fails; its caller must not read those host blocks, nor write
+ * them through another path, until the engines are known to be done (the
+ * process ends, or fkv_abandoned_copies_pending returns 0).  No counterpart
+ * in the reference, whose copy-engine path waits without a bound
+ * (csrc/transfer.cu:131). */
+int fkv_last_unsafe_host_blocks(int64_t* out, int cap);
+
+/* Copies on device `device` given up on by timed-out copy-engine waits whose
+ * completion signals have not yet reached zero (0: every such copy has
+ * finished, and the host blocks fkv_last_unsafe_host_blocks named are safe
+ * again); negative on error.  No counterpart in the reference. */
+int fkv_abandoned_copies_pending(int device);
 
 /* Pinned, device-mapped host allocation (hipHostMalloc).  flags: 0 = runtime
  * default, FKV_HOST_COHERENT / FKV_HOST_NONCOHERENT select the coherence

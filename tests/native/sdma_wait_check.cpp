@@ -8,8 +8,11 @@
 #include <cstdlib>
 #include <map>
 #include <thread>
+#include <vector>
 
+using fkv_detail::HostRowLedger;
 using fkv_detail::wait_copies;
+using fkv_detail::wait_half;
 using fkv_detail::WaitOutcome;
 using clk = std::chrono::steady_clock;
 
@@ -84,6 +87,32 @@ int main() {
     StubOps ops;
     const WaitOutcome w = wait_copies(ops, {}, {}, false, clk::now());
     check(w.done && ops.waits == 0 && ops.loads == 0, "an empty half returns at once");
+  }
+  {  // the host rows of a device-to-host transfer whose second half stalls
+    StubOps ops;
+    ops.remaining = {{1, 2}, {2, -1}, {3, -1}};   // half 0's copy finishes, 2 and 3 never
+    HostRowLedger rows;
+    const int64_t piece0[] = {10, 11, 12, 13}, piece1[] = {20, 21, 22}, piece2[] = {30, 31};
+    const auto soon = [] { return clk::now() + std::chrono::milliseconds(20); };
+    rows.queued(0, piece0, 4);
+    rows.queued(1, piece1, 3);
+    check(wait_half(ops, {sig(1)}, {sig(1)}, false, soon(), rows, 0).done,
+          "the first half's copies finish");
+    check(rows.unsafe.empty() && rows.pending[0].empty(),
+          "a finished half leaves no unsafe rows");
+    rows.queued(0, piece2, 2);   // the next piece reuses half 0
+    check(!wait_half(ops, {sig(2)}, {sig(2)}, true, soon(), rows, 1).done,
+          "the second half times out");
+    check((rows.unsafe == std::vector<int64_t>{20, 21, 22}),
+          "the timed-out half's host blocks are reported unsafe");
+    // the failing call's drain waits for the other half too, which also stalls
+    check(!wait_half(ops, {sig(3)}, {sig(3)}, false, soon(), rows, 0).done,
+          "the drain's wait on the other half times out");
+    const std::vector<int64_t> got = rows.take_unsafe();
+    check((got == std::vector<int64_t>{20, 21, 22, 30, 31}),
+          "both halves' host blocks are reported, in order");
+    check(rows.unsafe.empty() && rows.pending[0].empty() && rows.pending[1].empty(),
+          "the report empties the ledger");
   }
   return failures ? 1 : 0;
 }

@@ -3,8 +3,11 @@ with FLEXKV_SDMA_TIMEOUT_MS=1, so the host stops waiting for copies that are
 still in flight (the copies themselves finish normally): the worker reports
 the op as finished, records it in failed_ops and logs the timeout; the
 device's later copy-engine transfers move with the zero-copy kernel and are
-bit-exact.  The child sleeps before it exits, so the given-up copies end
-inside the process (their staging and signals are never freed or reused)."""
+bit-exact.  The worker records the host blocks the given-up copies may still write
+with the failed op (unsafe_host_blocks, from fkv_last_unsafe_host_blocks),
+and fkv_abandoned_copies_pending reads 0 once those copies have finished.
+The child sleeps before it exits, so the given-up copies end inside the
+process (their staging and signals are never freed or reused)."""
 import os
 import subprocess
 import sys
@@ -46,7 +49,14 @@ w._execute(WorkerTransferOp(bad))
 assert q.get(timeout=60) == bad.op_id
 assert w.failed_ops == [bad.op_id], w.failed_ops
 print("child: op failed and was reported", flush=True)
+from flexkv_amd import _lib
+unsafe = w.unsafe_host_blocks[bad.op_id]
+assert len(unsafe) > 0 and set(unsafe.tolist()) <= set(cids.tolist()), unsafe
+assert len(set(unsafe.tolist())) == len(unsafe)
+print(f"child: {{len(unsafe)}} host blocks reported unsafe", flush=True)
 time.sleep(1.0)                                 # the given-up copies finish
+assert _lib.abandoned_copies_pending(0) == 0
+print("child: the abandoned copies have finished", flush=True)
 cpu.view(torch.int16).zero_()
 good = op(TransferType.D2H, gids, cids)         # the zero-copy kernel from now on
 w._execute(WorkerTransferOp(good))
@@ -70,5 +80,7 @@ def test_copy_engine_wait_timeout_fails_the_op_and_falls_back(tmp_path):
     out = res.stdout + res.stderr
     assert res.returncode == 0, out[-3000:]
     assert "child: op failed and was reported" in res.stdout, out[-3000:]
+    assert "host blocks reported unsafe" in res.stdout, out[-3000:]
+    assert "child: the abandoned copies have finished" in res.stdout, out[-3000:]
     assert "child: the fallback transfer is bit-exact" in res.stdout, out[-3000:]
     assert "did not finish within 1 ms" in res.stderr, res.stderr[-3000:]

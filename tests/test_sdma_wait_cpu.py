@@ -2,8 +2,10 @@
 
 Builds tests/native/sdma_wait_check.cpp with g++ against
 flexkv_amd/csrc/kv_wait.h (header-only, no HIP) and runs it: stub signals
-that complete, an interrupt signal and a polled signal that never do, and an
-empty half.  No device is involved.
+that complete, an interrupt signal and a polled signal that never do, an
+empty half, and the host-row ledger of a device-to-host transfer whose
+halves stall (the host blocks their copies write are reported unsafe).  No
+device is involved.
 """
 import os
 import shutil
@@ -25,4 +27,4 @@ def test_bounded_sdma_wait(tmp_path):
     res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
     assert res.returncode == 0, res.stdout + res.stderr
     assert "FAIL" not in res.stdout
-    assert res.stdout.count("ok:") == 7
+    assert res.stdout.count("ok:") == 14

@@ -805,9 +805,9 @@ def test_rejected_arguments_launch_nothing(dev):
         for g, c, ov in bad_cases:
             with pytest.raises(RuntimeError):
                 abi_transfer(dc, g, c, h2d=False, mode=mode, **ov)
-    for mode in (0, 1):
-        with pytest.raises(RuntimeError, match="multiples of 16"):
-            abi_transfer(dc, ok, ok, h2d=False, mode=mode, chunk=24)
+    # kernel mode only: copy-engine mode copies such chunks exactly
+    with pytest.raises(RuntimeError, match="multiples of 16"):
+        abi_transfer(dc, ok, ok, h2d=False, mode=0, chunk=24)
     with pytest.raises(RuntimeError, match="use_ce_transfer"):
         abi_transfer(dc, ok, ok, h2d=False, mode=7)
     with pytest.raises(RuntimeError):
@@ -836,10 +836,65 @@ def test_unaligned_chunk_per_chunk_ce_matches_oracle(dev):
     check_case(case, inputs.distinct_ids(1, 6, 10), inputs.distinct_ids(2, 6, 12), 2)
 
 
+@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("heads,dim", [(1, 12), (4, 131)])
+def test_unaligned_chunk_ce_modes_match_oracle(dev, mode, heads, dim):
+    """Chunks of 24 and 1048 bytes (block strides that are not multiples of
+    16): both copy-engine modes copy them exactly, as the reference CE mode
+    does (csrc/transfer.cu:97-121)."""
+    case = KVCase(layers_total=3, num_layers=3, start_layer=0, kv=2, ng=10, nh=12, tokens=1,
+                  heads=heads, dim=dim).fill(seed=9)
+    assert case.strides()["chunk"] % 16 != 0
+    check_case(case, inputs.distinct_ids(3, 7, 10), inputs.distinct_ids(4, 7, 12), mode)
+
+
+@pytest.mark.parametrize("heads,dim", [(1, 12), (4, 131)])
+def test_c_ext_ce_transfer_copies_any_chunk_size(dev, heads, dim):
+    """The drop-in call with use_ce_transfer=True on chunks of 24 and 1048
+    bytes, both directions, byte for byte against the oracle's CE mode."""
+    from flexkv_amd import c_ext
+    from flexkv_amd.common.storage import KVCacheLayout, KVCacheLayoutType
+    from flexkv_amd.storage.allocator import CPUAllocator
+    L, NG, NH, T = 3, 10, 12, 1
+    dt = torch.float16
+    gl = KVCacheLayout(KVCacheLayoutType.LAYERWISE, L, NG, T, heads, dim)
+    cl = KVCacheLayout(KVCacheLayoutType.BLOCKWISE, L, NH, T, heads, dim)
+    chunk, gkv, _, gblk = gl.div_layer(L).byte_strides(dt)
+    _, ckv, clay, cblk = cl.byte_strides(dt)
+    assert chunk in (24, 1048)
+    gen = torch.Generator().manual_seed(11)
+    src = [torch.randn(gl.kv_shape[1:], generator=gen).to(dt) for _ in range(L)]
+    layers = [t.to(dev) for t in src]
+    ptrs = torch.tensor([t.data_ptr() for t in layers], dtype=torch.int64).pin_memory()
+    cache = CPUAllocator.allocate(cl, dt).get_tensor()
+    cache.view(torch.int16).fill_(0x2B2B)
+    gids = torch.tensor([7, 0, 9, 4, 2], dtype=torch.int64)
+    cids = torch.tensor([11, 3, 0, 6, 8], dtype=torch.int64)
+    want = cache.clone()
+    oracle.transfer_kv_blocks(gids, src, gkv, gblk, cids, want, ckv, clay, cblk, chunk, 0,
+                              False, use_ce_transfer=True)
+    c_ext.transfer_kv_blocks(gids.pin_memory(), ptrs, gkv, gblk, cids.pin_memory(), cache, ckv,
+                             clay, cblk, chunk, 0, -1, False, True, False)
+    assert torch.equal(cache.view(torch.int16), want.view(torch.int16)), "D2H"
+    # H2D of altered host blocks into sentinel-filled layers
+    cache.view(torch.int16).bitwise_xor_(0x0F0F)
+    init = [torch.full_like(t, 0).view(torch.int16).fill_(0x3C3C).view(dt) for t in src]
+    back = [t.to(dev) for t in init]
+    bptrs = torch.tensor([t.data_ptr() for t in back], dtype=torch.int64).pin_memory()
+    c_ext.transfer_kv_blocks(gids.pin_memory(), bptrs, gkv, gblk, cids.pin_memory(), cache, ckv,
+                             clay, cblk, chunk, 0, -1, True, True, False)
+    want_g = [t.clone() for t in init]
+    oracle.transfer_kv_blocks(gids, want_g, gkv, gblk, cids, cache, ckv, clay, cblk, chunk, 0,
+                              True, use_ce_transfer=True)
+    for l, (g, w) in enumerate(zip(back, want_g)):
+        assert torch.equal(g.cpu().view(torch.int16), w.view(torch.int16)), f"H2D layer {l}"
+
+
 @pytest.mark.parametrize("use_ce", [False, True])
-def test_c_ext_dropin_on_side_stream(dev, use_ce):
+def test_c_ext_dropin_on_side_stream(dev, use_ce, per_call_path):
     """The reference call shape: 15 positional args, pinned id tensors, on the
-    current (non-default) stream."""
+    current (non-default) stream; through the compiled per-call module and
+    through its ctypes stand-in."""
     from flexkv_amd import c_ext
     from flexkv_amd.common.storage import KVCacheLayout, KVCacheLayoutType
     from flexkv_amd.storage.allocator import CPUAllocator
