@@ -662,7 +662,7 @@ def worker_ops(wl: Workload, reps: int = 40, process: bool = True):
                 h.shutdown()
     out["what"] = ("16-block ops (32 MiB at this shape) and full-step ops, one at a time, "
                    "submit to finished-ops queue (spawned workers: a pipe, FinishedOpsChannel); "
-                   "copy engines take ops of 8 MiB or more")
+                   "copy engines take ops of 32 MiB or more (the default policy)")
     return out
 
 
@@ -758,13 +758,18 @@ def duplex(wl: Workload, reps: int = 3):
     return out
 
 
-def overlap_with_compute(wl: Workload, steps: int = 3, gemms: int = 160):
+def overlap_with_compute(wl: Workload, steps: int = 3, gemms: int = 160,
+                         rect_copies: bool = False, resident_probe: bool = True):
     """One full transfer op on its own stream (from a second host thread)
     while the main thread runs bf16 GEMMs [8192x4096]x[4096x4096] on a compute
     stream: GEMM time alone and beside each path and direction.  The
     zero-copy kernel shares compute units with the GEMMs; the copy-engine
     path leaves the PCIe copies to the SDMA engines.  Alone and beside, the
-    GEMMs run behind the same warm-up (gemm_window)."""
+    GEMMs run behind the same warm-up (gemm_window).  `rect_copies`: the
+    copy-engine runs use the rect-copy policy (layer-wise host caches with
+    scattered ids).  `resident_probe`: also time the GEMMs beside a kernel
+    that only spins in one single-thread workgroup (torch.cuda._sleep), as
+    long as a transfer, which shows what residency alone costs them."""
     import threading
 
     from flexkv_amd import c_ext
@@ -803,15 +808,29 @@ def overlap_with_compute(wl: Workload, steps: int = 3, gemms: int = 160):
                                     for _ in range(steps)], "gemm")}
     tf = {"gemm_alone_ms": med_ms([once(True, False, False, gemm_window_transfer_first)
                                    for _ in range(steps)], "gemm")}
+    ce_name = "_ce_rect" if rect_copies else "_ce"
     for h2d in (False, True):
         for ce in (False, True):
-            key = ("h2d" if h2d else "d2h") + ("_ce" if ce else "_kernel")
-            rs = [once(h2d, ce) for _ in range(steps)]
-            out[key] = {"gemm_ms": med_ms(rs, "gemm"), "transfer_ms": med_ms(rs, "xfer"),
-                        "gemm_slowdown": round(med_ms(rs, "gemm") / out["gemm_alone_ms"], 4)}
-            rs = [once(h2d, ce, True, gemm_window_transfer_first) for _ in range(steps)]
-            tf[key] = {"gemm_ms": med_ms(rs, "gemm"), "transfer_ms": med_ms(rs, "xfer"),
-                       "gemm_slowdown": round(med_ms(rs, "gemm") / tf["gemm_alone_ms"], 4)}
+            key = ("h2d" if h2d else "d2h") + (ce_name if ce else "_kernel")
+            if ce and rect_copies:
+                c_ext.set_copy_engine_policy(layerwise_scattered="rect_copies")
+            try:
+                rs = [once(h2d, ce) for _ in range(steps)]
+                out[key] = {"gemm_ms": med_ms(rs, "gemm"), "transfer_ms": med_ms(rs, "xfer"),
+                            "gemm_slowdown": round(med_ms(rs, "gemm") / out["gemm_alone_ms"], 4),
+                            "transfer_gbps": round(wl.bytes_per_op / med_ms(rs, "xfer") / 1e6,
+                                                   2)}
+                rs = [once(h2d, ce, True, gemm_window_transfer_first) for _ in range(steps)]
+                tf[key] = {"gemm_ms": med_ms(rs, "gemm"), "transfer_ms": med_ms(rs, "xfer"),
+                           "gemm_slowdown": round(med_ms(rs, "gemm") / tf["gemm_alone_ms"], 4),
+                           "transfer_gbps": round(wl.bytes_per_op / med_ms(rs, "xfer") / 1e6, 2)}
+            finally:
+                if ce and rect_copies:
+                    c_ext.set_copy_engine_policy(layerwise_scattered="unset")
+    if resident_probe:
+        spin = resident_spin_probe(a, b, c, comp, steps, gemms)
+        out["resident_spin"] = {k: v for k, v in spin.items() if k != "transfer_first"}
+        tf["resident_spin"] = spin["transfer_first"]
     c_ext.release_transfer_stream(xfer)
     out["transfer_first"] = tf
     out["what"] = (f"{gemms} GEMMs on a compute stream beside one {wl.bytes_per_op / 2**30:.0f} "
@@ -821,6 +840,53 @@ def overlap_with_compute(wl: Workload, steps: int = 3, gemms: int = 160):
                    f"{GEMM_QUIET_S * 1e3:.0f} ms and the GEMMs are queued after it; alone from "
                    "the same idle state")
     return out
+
+
+def resident_spin_probe(a, b, c, comp, steps: int, gemms: int, target_ms: float = 38.0):
+    """The GEMM windows of overlap_with_compute beside a kernel that touches
+    no memory: torch.cuda._sleep, one workgroup of one thread spinning on
+    the clock for about target_ms (the length of a 2 GiB transfer; the spin
+    count is calibrated first).  Both launch orders; alone from the same
+    state.  Any workgroup that stays resident on a compute unit slows these
+    GEMMs, which run one 256-thread workgroup per compute unit."""
+    spin_stream = torch.cuda.Stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    cycles = 1 << 20
+    for _ in range(3):                          # calibrate the spin's clock
+        with torch.cuda.stream(spin_stream):
+            e0.record()
+            torch.cuda._sleep(cycles)
+            e1.record()
+        e1.synchronize()
+        ms = max(e0.elapsed_time(e1), 1e-3)
+        cycles = int(cycles * min(64.0, target_ms / ms))
+    cycles = min(cycles, 1 << 40)
+
+    def start():
+        with torch.cuda.stream(spin_stream):
+            torch.cuda._sleep(cycles)
+
+    def med(fn):
+        return round(statistics.median(fn() for _ in range(steps)), 2)
+    out = {}
+    for key, window in (("gemm_first", gemm_window), ("transfer_first",
+                                                       gemm_window_transfer_first)):
+        alone = med(lambda: window(a, b, c, comp, None, gemms)[0])
+        beside = med(lambda: window(a, b, c, comp, start, gemms)[0])
+        torch.cuda.synchronize()
+        out[key] = {"gemm_alone_ms": alone, "gemm_ms": beside,
+                    "gemm_slowdown": round(beside / alone, 4)}
+    with torch.cuda.stream(spin_stream):
+        e0.record()
+        torch.cuda._sleep(cycles)
+        e1.record()
+    e1.synchronize()
+    res = out["gemm_first"]
+    res["spin_ms"] = round(e0.elapsed_time(e1), 2)
+    res["transfer_first"] = out["transfer_first"]
+    res["what"] = ("torch.cuda._sleep: one workgroup of one thread spinning on the clock, "
+                   "no memory access, started as the transfer would be")
+    return res
 
 
 def request_batch(wl: Workload, steps: int, num_requests: int = 32, max_blocks: int = 128):
@@ -986,11 +1052,14 @@ def other_workload(name: str, args, peaks: dict, host_layout: str = "BLOCKWISE",
         steps = max(3, args.steps // 2)
         out.update(path_rates(wl, steps, peaks))
         if rect_copies:
-            os.environ["FLEXKV_CE_RECT_COPIES"] = "1"
+            from flexkv_amd import c_ext
+            c_ext.set_copy_engine_policy(layerwise_scattered="rect_copies")
             try:
                 out["ce_rect_copies"] = path_rates(wl, steps, peaks, (("ce_rect", True),))["ce_rect"]
             finally:
-                os.environ.pop("FLEXKV_CE_RECT_COPIES", None)
+                c_ext.set_copy_engine_policy(layerwise_scattered="unset")
+            out["overlap_with_compute"] = overlap_with_compute(wl, 3, rect_copies=True,
+                                                               resident_probe=False)
         out["device_gather"] = standalone_gather(wl, steps)
         out["bit_exact"] = all(round_trip_bit_exact(wl, ce) for ce in (True, False))
         if wl.mla:
@@ -1348,6 +1417,10 @@ def main() -> int:
                     help="run only the worker-op section (thread and process workers, 16-block "
                          "and full-step ops, each inside a roctx range) and print its JSON "
                          "(for marker-trace profiling runs)")
+    ap.add_argument("--overlap-only", action="store_true",
+                    help="run only the overlap-with-compute section for --workload and "
+                         "--host-layout (layer-wise: the rect-copy policy on the copy-engine "
+                         "runs) and print its JSON (for kernel-trace profiling runs)")
     ap.add_argument("--seed", type=int, default=1001)
     ap.add_argument("--counters", action="store_true",
                     help="run only the kernels a PMC pass needs: a 1 GiB plain device copy "
@@ -1360,7 +1433,7 @@ def main() -> int:
               "multi-GPU runs are out of scope for this package", file=sys.stderr)
         return 2
     full_run = not (args.quick or args.counters or args.layerwise_only or args.worker_ops
-                    or args.duplex_only)
+                    or args.duplex_only or args.overlap_only)
     ceilings = device_ceilings() if full_run else None
     abi_latency = c_abi_latency() if full_run else None
     if not torch.cuda.is_available():
@@ -1377,7 +1450,7 @@ def main() -> int:
     default_ce = {"kernel": False, "ce": True}[args.path] if args.path else cfg.use_ce_transfer_d2h
     all_configs = (args.workload == "llama3-8b" and not args.run and args.host_layout == "BLOCKWISE"
                    and not (args.quick or args.layerwise_only or args.worker_ops
-                            or args.duplex_only))
+                            or args.duplex_only or args.overlap_only))
     wl = Workload(args.workload, args.seed, args.run, host_layout=args.host_layout)
     gb = wl.bytes_per_op / 1e9
     if args.layerwise_only:
@@ -1390,6 +1463,11 @@ def main() -> int:
         return 0
     if args.duplex_only:
         print(json.dumps({"duplex": duplex(wl, reps=max(3, args.steps))}), flush=True)
+        return 0
+    if args.overlap_only:
+        layerwise = args.host_layout == "LAYERWISE"
+        print(json.dumps({"overlap_with_compute": overlap_with_compute(
+            wl, 3, rect_copies=layerwise, resident_probe=True)}), flush=True)
         return 0
 
     # primary: D2H on the default path, library kernel timing on

@@ -57,6 +57,8 @@ EXPORTED_SYMBOLS = (
     "fkv_set_staging_bytes",
     "fkv_release_staging",
     "fkv_prepare",
+    "fkv_set_copy_engine_policy",
+    "fkv_get_copy_engine_policy",
     "fkv_finalize",
     "fkv_profile_enable",
     "fkv_profile_read",
@@ -170,6 +172,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.fkv_profile_read.argtypes = [ctypes.POINTER(FkvProfile)]
     lib.fkv_version.restype = ctypes.c_char_p
     lib.fkv_version.argtypes = []
+    lib.fkv_set_copy_engine_policy.restype = c_int
+    lib.fkv_set_copy_engine_policy.argtypes = [c_i64, c_int]
+    lib.fkv_get_copy_engine_policy.restype = c_int
+    lib.fkv_get_copy_engine_policy.argtypes = [ctypes.POINTER(c_i64), ctypes.POINTER(c_int)]
     lib.fkv_last_unsafe_host_blocks.restype = c_int
     lib.fkv_last_unsafe_host_blocks.argtypes = [c_vp, c_int]
     lib.fkv_abandoned_copies_pending.restype = c_int

@@ -16,7 +16,7 @@ from . import _lib
 __all__ = ["transfer_kv_blocks", "transfer_kv_blocks_kv_ptrs", "gather_kv_blocks",
            "scatter_kv_blocks",
            "transfer_kv_blocks_layerwise", "LayerwiseTransfer", "transfer_stream",
-           "release_transfer_stream",
+           "release_transfer_stream", "set_copy_engine_policy", "copy_engine_policy",
            "SSDIOCTX", "transfer_kv_blocks_ssd"]
 
 
@@ -300,6 +300,47 @@ def transfer_kv_blocks_layerwise(gpu_block_id_tensor: torch.Tensor,
     if rc != 0:
         raise RuntimeError(_lib.last_error() or f"fkv_transfer_kv_blocks_layerwise failed ({rc})")
     return LayerwiseTransfer(out.value, (cpu_tensor,))
+
+
+_LAYERWISE_SCATTERED = {"kernel": 0, "rect_copies": 1}
+
+
+def set_copy_engine_policy(min_bytes=None, layerwise_scattered=None) -> None:
+    """How use_ce_transfer=True chooses its path, process-wide (extension;
+    fkv_set_copy_engine_policy).  ``min_bytes``: transfers moving fewer
+    bytes take the zero-copy kernel (default 32 MiB).  ``layerwise_scattered``:
+    a layer-wise host cache with scattered ids moves with the zero-copy
+    kernel ("kernel", the default: link rate, but it holds compute units, and
+    a whole-device GEMM beside it slows 1.4-1.9x) or with one SDMA rect copy
+    per block ("rect_copies": one engine, about 47 GB/s at the Llama-3-8B
+    shape, compute keeps its speed).  None leaves a setting as it is; "unset"
+    returns it to the FLEXKV_CE_* environment variable or the default."""
+    keep = -2
+    mb = keep if min_bytes is None else (-1 if min_bytes == "unset" else min_bytes)
+    if not (mb in (keep, -1) or (isinstance(mb, int) and not isinstance(mb, bool) and mb >= 0)):
+        raise ValueError(f"min_bytes must be a non-negative int or 'unset', got {min_bytes!r}")
+    if layerwise_scattered is None:
+        rc = keep
+    elif layerwise_scattered == "unset":
+        rc = -1
+    elif layerwise_scattered in _LAYERWISE_SCATTERED:
+        rc = _LAYERWISE_SCATTERED[layerwise_scattered]
+    else:
+        raise ValueError("layerwise_scattered must be 'kernel', 'rect_copies' or 'unset', got "
+                         f"{layerwise_scattered!r}")
+    _lib.check(_lib.load().fkv_set_copy_engine_policy(int(mb), int(rc)),
+               "fkv_set_copy_engine_policy")
+
+
+def copy_engine_policy() -> dict:
+    """The copy-engine policy in force: {"min_bytes": int, "rect_copies": 0|1,
+    "layerwise_scattered": "kernel"|"rect_copies"}."""
+    import ctypes
+    mb, rc = ctypes.c_int64(), ctypes.c_int()
+    _lib.check(_lib.load().fkv_get_copy_engine_policy(ctypes.byref(mb), ctypes.byref(rc)),
+               "fkv_get_copy_engine_policy")
+    return {"min_bytes": mb.value, "rect_copies": rc.value,
+            "layerwise_scattered": "rect_copies" if rc.value else "kernel"}
 
 
 def transfer_stream(num_cus: int = 0) -> torch.cuda.ExternalStream:

@@ -153,9 +153,36 @@ constexpr int kAutoZeroCopyCus = 8;
 // CUs against 46.1 ms on 8.
 constexpr int kAutoLayerwiseH2DCus = 2;
 // Copy-engine size policy: smallest transfer, and smallest bytes per engine
-// copy, worth handing to the SDMA engines (ce_pays_off).
-constexpr int64_t kCeMinBytesDefault = int64_t(8) << 20;
+// copy, worth handing to the SDMA engines (ce_pays_off).  Measured on MI355X
+// (block-wise host caches, random ids, GB/s zero-copy kernel / engines): the
+// kernel is as fast or faster up to 32 MiB in both directions at every shape
+// (16 MiB of 256 KiB rows: D2H 48.9 / 46.1, H2D 53.8 / 49.5; 8 MiB of 2 MiB
+// rows: 46.1 / 45.9, 50.0 / 45.8), and from 32-64 MiB the engines come
+// within 1-3% (32 MiB of 2 MiB rows: D2H 53.1 / 53.5, H2D 55.2 / 53.5; 64 MiB:
+// 54.8 / 55.2, 56.2 / 55.2).  Below 32 MiB the kernel holds its compute units
+// for at most about 0.6 ms per transfer.
+constexpr int64_t kCeMinBytesDefault = int64_t(32) << 20;
 constexpr int64_t kCeMinRunBytes = int64_t(128) << 10;
+// The copy-engine policy set through fkv_set_copy_engine_policy; -1: unset,
+// so FLEXKV_CE_MIN_BYTES / FLEXKV_CE_RECT_COPIES, else the defaults, apply.
+std::atomic<int64_t> g_ce_min_bytes{-1};
+std::atomic<int> g_ce_rect_copies{-1};
+
+int64_t ce_min_bytes() {
+  const int64_t v = g_ce_min_bytes.load(std::memory_order_relaxed);
+  if (v >= 0) return v;
+  const char* e = getenv("FLEXKV_CE_MIN_BYTES");
+  return e ? std::max<int64_t>(0, atoll(e)) : kCeMinBytesDefault;
+}
+
+// Whether a layer-wise host cache with scattered ids stays on the engines
+// (rect copies) in copy-engine mode; default no (the zero-copy kernel).
+bool ce_rect_copies() {
+  const int v = g_ce_rect_copies.load(std::memory_order_relaxed);
+  if (v >= 0) return v == 1;
+  const char* r = getenv("FLEXKV_CE_RECT_COPIES");
+  return r && atoi(r) == 1;
+}
 // Host-to-device engine copies shorter than this on average spread over the
 // wide engine set (engines 0-7) instead of the direction's four.  Measured on
 // MI355X: 640 KiB copies (Llama-3-70B TP-8 shard) 51.9 -> 56.4 GB/s, 256 KiB
@@ -1700,7 +1727,7 @@ Geometry make_geometry(int num_blocks, int start_layer_id, int num_layers,
 }
 
 // Copy-engine mode hands a transfer to the SDMA engines only when the
-// engines pay off: the op moves at least FLEXKV_CE_MIN_BYTES (default 8 MiB)
+// engines pay off: the op moves at least ce_min_bytes() (default 32 MiB)
 // and each engine copy moves at least 128 KiB: a contiguous host run, or one
 // block's layer window as a rect copy when the host layout puts its chunks at
 // one stride (layer-wise).  Each engine copy costs about 6 us and the
@@ -1716,22 +1743,18 @@ Geometry make_geometry(int num_blocks, int start_layer_id, int num_layers,
 // 57.2 GB/s for the zero-copy kernel.  Such transfers therefore move with
 // the zero-copy kernel, which holds compute units for the whole transfer
 // (160 bf16 GEMMs queued after a 2 GiB D2H starts take 71 ms instead of
-// 36 ms beside the rect copies); FLEXKV_CE_RECT_COPIES=1 keeps them on the
-// engines.
+// 36 ms beside the rect copies); fkv_set_copy_engine_policy (or
+// FLEXKV_CE_RECT_COPIES=1) keeps them on the engines.
 bool ce_pays_off(const Geometry& g, bool h2d) {
   // a "host" cache that is device memory has no PCIe copy to offload
   if (g.cpu_info.device) return false;
-  const char* e = getenv("FLEXKV_CE_MIN_BYTES");
-  const int64_t min_bytes = e ? std::max<int64_t>(0, atoll(e)) : kCeMinBytesDefault;
+  const int64_t min_bytes = ce_min_bytes();
   const int64_t total = static_cast<int64_t>(g.num_blocks) * g.num_layers * g.kv * g.chunk;
   const bool row_contig = (g.kv == 1 || g.cks == g.chunk) &&
                           (g.num_layers == 1 || g.cls == g.kv * g.chunk);
   const int64_t row = static_cast<int64_t>(g.num_layers) * g.kv * g.chunk;
   const bool rect = !row_contig && host_slice_pitch(g, g.num_layers) > 0;
-  if (rect && !layer_major_pays_off(g, layer_run_bytes(h2d))) {
-    const char* r = getenv("FLEXKV_CE_RECT_COPIES");
-    if (!(r && atoi(r) == 1)) return false;
-  }
+  if (rect && !layer_major_pays_off(g, layer_run_bytes(h2d)) && !ce_rect_copies()) return false;
   const int64_t run = (row_contig || rect) ? row : g.chunk;
   return total >= min_bytes && (min_bytes == 0 || run >= kCeMinRunBytes);
 }
@@ -1987,6 +2010,27 @@ int fkv_handle_release(fkv_transfer_handle h) {
   if (!h) return 0;
   if (!handle_unregister(h)) return fail(kInval, "handle %p is released or unknown", (void*)h);
   return handle_destroy(h);
+}
+
+int fkv_set_copy_engine_policy(int64_t min_bytes, int rect_copies) {
+  last_error().clear();
+  if (min_bytes < -2)
+    return fail(kInval, "min_bytes must be >= 0, -1 to unset or -2 to keep, got %lld",
+                static_cast<long long>(min_bytes));
+  if (rect_copies < -2 || rect_copies > 1)
+    return fail(kInval, "rect_copies must be 0, 1, -1 to unset or -2 to keep, got %d",
+                rect_copies);
+  if (min_bytes != -2) g_ce_min_bytes.store(min_bytes);
+  if (rect_copies != -2) g_ce_rect_copies.store(rect_copies);
+  return 0;
+}
+
+int fkv_get_copy_engine_policy(int64_t* min_bytes, int* rect_copies) {
+  last_error().clear();
+  if (!min_bytes || !rect_copies) return fail(kInval, "null output pointer");
+  *min_bytes = ce_min_bytes();
+  *rect_copies = ce_rect_copies() ? 1 : 0;
+  return 0;
 }
 
 int fkv_prepare(int device) {

@@ -304,6 +304,25 @@ int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, voi
                                int64_t block_stride_bytes, int is_read, int round_robin,
                                int num_threads_per_device, int is_mla);
 
+/* How copy-engine mode (use_ce_transfer = FKV_XFER_CE) chooses between the
+ * SDMA engines and the zero-copy kernel, process-wide.  No counterpart in
+ * the reference, whose CE mode always copies on the engines.
+ *   min_bytes: transfers that move fewer bytes take the zero-copy kernel
+ *     (default 32 MiB: below it the kernel is as fast, and holds its compute
+ *     units for at most about 0.6 ms); 0 sends every transfer the engines can
+ *     take to them.
+ *   rect_copies: a layer-wise host cache with scattered ids (no contiguous
+ *     host run longer than one chunk) moves with one SDMA rect copy per
+ *     block when 1 (one engine: about 47 GB/s at the Llama-3-8B shape, and
+ *     compute beside it keeps its speed), with the zero-copy kernel when 0
+ *     (the default: about 57 GB/s, but any kernel resident on the compute
+ *     units slows a whole-device GEMM beside it 1.4-1.9x).
+ * -1 for either unsets it (FLEXKV_CE_MIN_BYTES / FLEXKV_CE_RECT_COPIES, else
+ * the default, apply again); -2 keeps it as it is.  fkv_get_copy_engine_policy
+ * reads the values in force. */
+int fkv_set_copy_engine_policy(int64_t min_bytes, int rect_copies);
+int fkv_get_copy_engine_policy(int64_t* min_bytes, int* rect_copies);
+
 /* Message of the last failed call made by this thread ("" if none). */
 const char* fkv_last_error(void);
 

@@ -7,7 +7,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
-# Copy-engine mode hands transfers under 8 MiB to the zero-copy kernel; the
+# Copy-engine mode hands transfers under 32 MiB to the zero-copy kernel; the
 # parity tests use small shapes and must reach the SDMA path itself.
 os.environ["FLEXKV_CE_MIN_BYTES"] = "0"
 # Layer-wise host caches with scattered ids move with the zero-copy kernel by

@@ -6,6 +6,7 @@ import re
 import subprocess
 
 import numpy as np
+import pytest
 
 from flexkv_amd import _lib
 
@@ -103,3 +104,42 @@ def test_profile_counters_roundtrip():
     d = _lib.profile_read()
     assert d["kernel_launches"] == 0 and d["dma_copies"] == 0
     _lib.profile_enable(False)
+
+
+def test_copy_engine_policy_setter_needs_no_device(monkeypatch):
+    """fkv_set/get_copy_engine_policy: the default (32 MiB, kernel for
+    scattered layer-wise ids), the environment variables while unset, explicit
+    values over them, -2 keeps a field, bad values are refused."""
+    import ctypes
+    from flexkv_amd import c_ext
+    lib = _lib.load()
+    monkeypatch.delenv("FLEXKV_CE_MIN_BYTES", raising=False)
+    monkeypatch.delenv("FLEXKV_CE_RECT_COPIES", raising=False)
+    try:
+        assert lib.fkv_set_copy_engine_policy(-1, -1) == 0
+        assert c_ext.copy_engine_policy() == {"min_bytes": 32 << 20, "rect_copies": 0,
+                                              "layerwise_scattered": "kernel"}
+        monkeypatch.setenv("FLEXKV_CE_MIN_BYTES", "4096")
+        monkeypatch.setenv("FLEXKV_CE_RECT_COPIES", "1")
+        assert c_ext.copy_engine_policy()["min_bytes"] == 4096
+        assert c_ext.copy_engine_policy()["rect_copies"] == 1
+        c_ext.set_copy_engine_policy(min_bytes=7 << 20)
+        assert c_ext.copy_engine_policy()["min_bytes"] == 7 << 20
+        assert c_ext.copy_engine_policy()["rect_copies"] == 1     # kept, from the variable
+        c_ext.set_copy_engine_policy(layerwise_scattered="kernel")
+        assert c_ext.copy_engine_policy() == {"min_bytes": 7 << 20, "rect_copies": 0,
+                                              "layerwise_scattered": "kernel"}
+        assert lib.fkv_set_copy_engine_policy(-3, -2) != 0
+        assert "min_bytes" in _lib.last_error()
+        assert lib.fkv_set_copy_engine_policy(-2, 2) != 0
+        assert "rect_copies" in _lib.last_error()
+        assert lib.fkv_get_copy_engine_policy(None, None) != 0
+        with pytest.raises(ValueError):
+            c_ext.set_copy_engine_policy(min_bytes=-5)
+        with pytest.raises(ValueError):
+            c_ext.set_copy_engine_policy(layerwise_scattered="engines")
+        mb, rc = ctypes.c_int64(), ctypes.c_int()
+        assert lib.fkv_get_copy_engine_policy(ctypes.byref(mb), ctypes.byref(rc)) == 0
+        assert (mb.value, rc.value) == (7 << 20, 0)
+    finally:
+        c_ext.set_copy_engine_policy(min_bytes="unset", layerwise_scattered="unset")

@@ -262,6 +262,43 @@ def test_rect_policy_default(dev, monkeypatch):
             assert np.array_equal(g, expect), f"{name} layer {l}"
 
 
+def test_copy_engine_policy_api_routes_transfers(dev, monkeypatch):
+    """c_ext.set_copy_engine_policy overrides the FLEXKV_CE_* variables: a
+    layer-wise host cache with scattered ids moves with rect copies under
+    layerwise_scattered="rect_copies" and with the zero-copy kernel under
+    "kernel"; a min_bytes above the transfer sends it to the kernel.  The
+    bytes match the oracle every time; "unset" returns to the variables."""
+    from flexkv_amd import _lib, c_ext
+    from gpu_util import DeviceCase, abi_transfer
+    monkeypatch.setenv("FLEXKV_CE_MIN_BYTES", "0")
+    monkeypatch.setenv("FLEXKV_CE_RECT_COPIES", "1")
+    case = KVCase(layers_total=4, num_layers=4, start_layer=0, kv=2, ng=64, nh=96, tokens=16,
+                  heads=4, dim=128, layout="LAYERWISE").fill(seed=54)   # 16 KiB chunks
+    gids = inputs.distinct_ids(14, 24, 64)
+    cids = inputs.distinct_ids(15, 24, 96)
+    total = 24 * 4 * 2 * 16384
+    want = _oracle_d2h(case, gids, cids, 1)
+    try:
+        for policy, engines in (({"layerwise_scattered": "kernel"}, False),
+                                ({"layerwise_scattered": "rect_copies"}, True),
+                                ({"min_bytes": total + 1}, False),
+                                ({"min_bytes": total}, True)):
+            c_ext.set_copy_engine_policy(**policy)
+            print(f"policy {policy}: {c_ext.copy_engine_policy()}", flush=True)
+            dc = DeviceCase(case)
+            _lib.profile_enable(True)
+            abi_transfer(dc, gids, cids, h2d=False, mode=1)
+            prof = _lib.profile_read()
+            _lib.profile_enable(False)
+            torch.cuda.synchronize()
+            assert (prof["dma_batches"] > 0) == engines, (policy, prof)
+            assert np.array_equal(dc.host_np(), want)
+    finally:
+        c_ext.set_copy_engine_policy(min_bytes="unset", layerwise_scattered="unset")
+    assert c_ext.copy_engine_policy() == {"min_bytes": 0, "rect_copies": 1,
+                                          "layerwise_scattered": "rect_copies"}
+
+
 @pytest.mark.parametrize("mla", [False, True])
 def test_layerwise_host_id_runs_stage_layer_major(dev, mla, monkeypatch):
     """On a layer-wise host cache whose ids come in runs of consecutive blocks
