@@ -660,6 +660,7 @@ def worker_ops(wl: Workload, reps: int = 40, process: bool = True):
                     for k in (TransferType.D2H, TransferType.H2D)}
             finally:
                 h.shutdown()
+        q.close()
     out["what"] = ("16-block ops (32 MiB at this shape) and full-step ops, one at a time, "
                    "submit to finished-ops queue (spawned workers: a pipe, FinishedOpsChannel); "
                    "copy engines take ops of 32 MiB or more (the default policy)")
@@ -1666,5 +1667,26 @@ def main() -> int:
     return 0 if (parity and gather_ok) else 1
 
 
+def end_helper_processes() -> None:
+    """Leave no process behind: join (or, after 5 s, terminate) any worker
+    process still alive, then stop the multiprocessing resource tracker that
+    spawned workers and their semaphores started.  The tracker would exit on
+    its own once this process has, but only after it notices."""
+    import multiprocessing as mp
+    from multiprocessing import resource_tracker
+    for p in mp.active_children():
+        p.join(timeout=5)
+        if p.is_alive():
+            p.terminate()
+            p.join(timeout=5)
+    tracker = resource_tracker._resource_tracker
+    if not mp.active_children() and getattr(tracker, "_pid", None) is not None:
+        tracker._stop()
+
+
 if __name__ == "__main__":
-    sys.exit(main())
+    try:
+        rc = main()
+    finally:
+        end_helper_processes()
+    sys.exit(rc)

@@ -247,5 +247,9 @@ class TransferEngine:
         self._ssd_workers = {}
         if self._forwarder is not None:
             self._forwarder.join(timeout=5)
+        if self._mp_finished is not None and (self._forwarder is None
+                                              or not self._forwarder.is_alive()):
+            self._mp_finished.close()
+            self._mp_finished = None
         if torch.cuda.is_available():
             torch.cuda.synchronize()

@@ -144,6 +144,13 @@ class FinishedOpsChannel:
     def get_nowait(self) -> Any:
         return self.get(block=False)
 
+    def close(self) -> None:
+        """Close this process's ends of the pipe (the engine, once every
+        worker using the channel has stopped)."""
+        for conn in (self._reader, self._writer):
+            with contextlib.suppress(OSError):
+                conn.close()
+
 
 class TransferWorkerBase(ABC):
     def __init__(self, worker_id: int, transfer_conn: Optional[Connection],
