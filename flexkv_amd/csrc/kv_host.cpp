@@ -95,6 +95,10 @@ fkv_profile g_prof{};
 std::mutex g_ids_mu;
 std::vector<IdBuf> g_ids_free;
 
+// The per-device pools of device id buffers (dev_ids_acquire / _release).
+std::mutex g_dev_ids_mu;
+std::vector<IdBuf> g_dev_ids_free[kMaxDevices];
+
 // Streams made by fkv_stream_create and not destroyed yet; fkv_finalize
 // destroys them.
 std::mutex g_streams_mu;
@@ -150,6 +154,61 @@ int ids_pool_free() {
     const hipError_t e = hipHostFree(b.host);
     if (e != hipSuccess && rc == 0)
       rc = fail(static_cast<int>(e), "hipHostFree of an id buffer: %s", hipGetErrorString(e));
+  }
+  return rc;
+}
+
+int dev_ids_acquire(int dev, size_t bytes, IdBuf* out) {
+  {
+    std::lock_guard<std::mutex> lk(g_dev_ids_mu);
+    std::vector<IdBuf>& pool = g_dev_ids_free[dev];
+    size_t best = pool.size();
+    for (size_t i = 0; i < pool.size(); ++i)
+      if (pool[i].cap >= bytes && (best == pool.size() || pool[i].cap < pool[best].cap)) best = i;
+    if (best != pool.size()) {
+      *out = pool[best];
+      pool.erase(pool.begin() + static_cast<long>(best));
+      return 0;
+    }
+  }
+  IdBuf b;
+  b.cap = size_t(64) << 10;
+  while (b.cap < bytes) b.cap <<= 1;
+  DeviceGuard guard;
+  int rc = guard.set(dev);
+  if (rc) return rc;
+  void* p = nullptr;
+  FKV_HIP(hipMalloc(&p, b.cap));
+  b.dev = static_cast<char*>(p);
+  *out = b;
+  return 0;
+}
+
+void dev_ids_release(int dev, const IdBuf& b) {
+  std::lock_guard<std::mutex> lk(g_dev_ids_mu);
+  g_dev_ids_free[dev].push_back(b);
+}
+
+int dev_ids_pool_free() {
+  int rc = 0;
+  for (int dev = 0; dev < kMaxDevices; ++dev) {
+    std::vector<IdBuf> bufs;
+    {
+      std::lock_guard<std::mutex> lk(g_dev_ids_mu);
+      bufs.swap(g_dev_ids_free[dev]);
+    }
+    if (bufs.empty()) continue;
+    DeviceGuard guard;
+    const int r = guard.set(dev);
+    if (r) {
+      if (!rc) rc = r;
+      continue;
+    }
+    for (const IdBuf& b : bufs) {
+      const hipError_t e = hipFree(b.dev);
+      if (e != hipSuccess && rc == 0)
+        rc = fail(static_cast<int>(e), "hipFree of a device id buffer: %s", hipGetErrorString(e));
+    }
   }
   return rc;
 }

@@ -118,6 +118,9 @@ struct DeviceState {
   // host-to-device engines of the copy-engine layer-wise pipeline: every
   // engine device-to-host did not take, up to FLEXKV_SDMA_ENGINES_LAYERWISE
   std::vector<hsa_amd_sdma_engine_id_t> engines_wide;
+  // the first few of them: short host-to-device copies of synchronous
+  // transfers (FLEXKV_SDMA_ENGINES_WIDE_SYNC)
+  std::vector<hsa_amd_sdma_engine_id_t> engines_wide_sync;
   // Engines each direction takes while the other direction's copy-engine
   // transfer is in flight (FLEXKV_SDMA_DUPLEX_D2H of engines 0-7 for
   // device-to-host, the rest of 0-7 for host-to-device); empty: no split.
@@ -222,6 +225,24 @@ struct ProfRecorder {
     spans.push_back({a, b, bytes, copies, dma});
     return 0;
   }
+  // A pair of events for one kernel launched with hipExtLaunchKernelGGL,
+  // which stamps the kernel's own start and end into them: no marker packets
+  // on the stream, so the span is the kernel alone.  Both null when off.
+  int kernel_events(hipEvent_t* a, hipEvent_t* b) {
+    *a = *b = nullptr;
+    if (!on) return 0;
+    FKV_HIP(hipEventCreate(a));
+    const hipError_t e = hipEventCreate(b);
+    if (e != hipSuccess) {
+      (void)hipEventDestroy(*a);
+      *a = nullptr;
+      return fail(static_cast<int>(e), "hipEventCreate: %s", hipGetErrorString(e));
+    }
+    return 0;
+  }
+  void kernel_span(hipEvent_t a, hipEvent_t b, int64_t bytes) {
+    if (a && b) spans.push_back({a, b, bytes, 0, false});
+  }
   void flush() {
     for (auto& sp : spans) {
       float ms = 0.f;
@@ -269,6 +290,26 @@ struct IdLease {
   IdLease& operator=(const IdLease&) = delete;
   ~IdLease() {
     if (buf.host) ids_release(buf);
+  }
+};
+// Device-memory id buffers for the staging kernels, one pool per device
+// (hipMalloc, power-of-two capacities from 64 KiB).  A staging transfer
+// copies its id pairs into one with a small kernel, so every workgroup reads
+// its tile's ids from HBM instead of over PCIe from the pinned buffer.
+// Freed by dev_ids_pool_free (fkv_finalize).
+int dev_ids_acquire(int dev, size_t bytes, IdBuf* out);
+void dev_ids_release(int dev, const IdBuf& b);
+int dev_ids_pool_free();
+// Holds a device id buffer for the scope of a synchronous call (declare it
+// before the call's DrainOnError).
+struct DevIdLease {
+  int dev = -1;
+  IdBuf buf;
+  DevIdLease() = default;
+  DevIdLease(const DevIdLease&) = delete;
+  DevIdLease& operator=(const DevIdLease&) = delete;
+  ~DevIdLease() {
+    if (buf.dev) dev_ids_release(dev, buf);
   }
 };
 // Synchronises and destroys every stream made by fkv_stream_create and not
@@ -339,8 +380,11 @@ int ensure_staging(CopyLane& lane, size_t need_half);
 // of `lane` on the direction's SDMA engines (`wide`: the layer-wise
 // pipeline's wider host-to-device set), round robin, each with its own
 // completion signal.  The half must have no copies queued (sdma_wait).
+// Engine sets issue_sdma may take: the direction's own, or for host-to-device
+// copies the synchronous transfers' wide set or the layer-wise pipeline's.
+enum EngineSet { kEnginesOwn = 0, kEnginesWideSync = 1, kEnginesWide = 2 };
 int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, char* staging,
-               bool h2d, int half, hsa_agent_t host_agent, bool wide = false);
+               bool h2d, int half, hsa_agent_t host_agent, int wide = kEnginesOwn);
 // Wait until every copy queued on a staging half has finished: block on the
 // interrupt signals of the engines' last copies, then check every copy's own
 // signal.  An engine runs its copies in order, so the check normally finds

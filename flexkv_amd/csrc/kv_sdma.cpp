@@ -41,6 +41,14 @@ constexpr uint32_t kComputeFriendlyEngines = 0xFFu;
 // and synchronous ones shorter than 1 MiB on average; taken from engines
 // 0-7, host-to-device's own first.
 constexpr int kDefaultWideEngines = 8;
+// Synchronous host-to-device transfers whose copies are short spread over the
+// first kSyncWideEngines of the wide set instead (FLEXKV_SDMA_ENGINES_WIDE_SYNC).
+// Their scatter kernels run while the next piece's copies are in flight, and
+// the engines' traffic slows them.  Measured on MI355X at the Llama-3-70B
+// TP-8 shard (640 KiB copies), 8 / 6 / 4 engines: H2D 56.4 / 56.6 / 52.7
+// GB/s, scatter pieces 4.26 / 4.65 / 4.90 TB/s.  The layer-wise pipeline
+// keeps all 8: its one-window copies need them (50.6 against 45.6 GB/s on 6).
+constexpr int kSyncWideEngines = 6;
 // The duplex split (FLEXKV_SDMA_DUPLEX_D2H; 0 turns it off): while a
 // transfer of the other direction is in flight, device-to-host copies take
 // this many of engines 0-7 and host-to-device copies the rest.  Measured on
@@ -428,6 +436,11 @@ int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr) {
         if (tier & (1u << b))
           d.engines_wide.push_back(static_cast<hsa_amd_sdma_engine_id_t>(1u << b));
     if (d.engines_wide.empty()) d.engines_wide = d.engines[1];
+    const char* es = getenv("FLEXKV_SDMA_ENGINES_WIDE_SYNC");
+    const size_t sync = static_cast<size_t>(std::max(1, es ? atoi(es) : kSyncWideEngines));
+    d.engines_wide_sync.assign(d.engines_wide.begin(),
+                               d.engines_wide.begin() +
+                                   static_cast<std::ptrdiff_t>(std::min(sync, d.engines_wide.size())));
   }
   {
     // the duplex split of engines 0-7: device-to-host takes the first
@@ -479,7 +492,7 @@ int ensure_staging(CopyLane& d, size_t need_half) {
 }
 
 int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, char* staging,
-               bool h2d, int half, hsa_agent_t host_agent, bool wide) {
+               bool h2d, int half, hsa_agent_t host_agent, int wide) {
   // While the other direction has a copy-engine transfer in flight, the
   // directions split engines 0-7 (the duplex sets); otherwise each takes its
   // one-way set, or host-to-device the wide set where asked.
@@ -488,7 +501,10 @@ int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, cha
                       d.busy[1 - dir].load(std::memory_order_relaxed) > 0;
   const std::vector<hsa_amd_sdma_engine_id_t>& eng =
       duplex ? d.engines_duplex[dir]
-             : (wide && h2d && !d.engines_wide.empty()) ? d.engines_wide : d.engines[dir];
+             : (wide == kEnginesWide && h2d && !d.engines_wide.empty()) ? d.engines_wide
+             : (wide == kEnginesWideSync && h2d && !d.engines_wide_sync.empty())
+                 ? d.engines_wide_sync
+                 : d.engines[dir];
   const size_t n = runs.size();
   // The engine of each copy (rect copies: the runtime's one engine, key
   // eng.size()) and whether it is that engine's last copy of the half.

@@ -24,6 +24,7 @@
 // transfer entry points of the C ABI; kv_host.cpp holds validation, id staging
 // and the host-only entry points, kv_sdma.cpp the copy engines.
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -494,6 +495,107 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
   }
 }
 
+// The staging gather / scatter over packed rows.  The packed (staging)
+// side of a launch is contiguous in row order, block -> layer -> K|V ->
+// row, each row 1 KiB, so row r lies at packed + r KiB.  The launch's rows
+// are cut into groups of kU consecutive rows and wavefront w of workgroup b
+// moves group 4b + w: no tile, no LDS, no barrier, and every wavefront moves
+// a full group.  A group is kC whole chunks of kU / kC rows (kC > 1: chunks
+// of 1-16 KiB, e.g. the Llama-3-70B TP-8 shard's 4 KiB) or kU rows inside
+// one chunk (kC == 1: chunks of a multiple of kU rows, e.g. Llama-3-8B's 32
+// and MLA's 72 rows at kU = 24).  The host checks the shape: full 1 KiB
+// rows, whole groups, a contiguous packed side, ids in device memory.
+struct PackArgs {
+  const int64_t* gids;       // device memory: gpu id of launch block i at gids[i]
+  char* packed;              // staging address of launch row 0
+  int64_t gpu_kv_stride;
+  int64_t gpu_block_stride;
+  uint32_t rows_per_chunk;
+  uint32_t items_per_block;  // layers x kv of the launch
+  uint32_t kv_dim;
+  uint32_t num_layers;       // layers of the launch
+  uint32_t num_groups;
+  int32_t ptrs_per_layer;    // 1: layer_ptr[l] + k*gpu_kv_stride; kv: layer_ptr[l*kv + k]
+  uint64_t layer_ptr[kMaxLayersPerLaunch];
+};
+
+template <bool kH2D, int kU, int kC>
+__global__ __launch_bounds__(kThreads) void kv_pack_kernel(PackArgs a) {
+  static_assert(kU % kC == 0, "a group is kC whole chunks");
+  constexpr int kR = kU / kC;                 // rows per chunk when kC > 1
+  constexpr int kRow = 64 * 16;               // bytes per row
+  const uint32_t lane_off = (threadIdx.x & 63) * 16;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t g = blockIdx.x * kWaves + wave;
+  if (g >= a.num_groups) return;
+  const uint32_t kv = a.kv_dim;
+  const uint32_t ppl = static_cast<uint32_t>(a.ptrs_per_layer);
+  // the group's first chunk and its first row inside that chunk
+  uint32_t c, rr;
+  if constexpr (kC > 1) {
+    c = g * kC;
+    rr = 0;
+  } else {
+    const uint32_t row0 = g * kU;
+    c = row0 / a.rows_per_chunk;
+    rr = row0 - c * a.rows_per_chunk;
+  }
+  uint32_t bi = c / a.items_per_block;
+  const uint32_t rem = c - bi * a.items_per_block;
+  uint32_t l = rem / kv;
+  uint32_t k = rem - l * kv;
+  // The ids do not change during the launch: read them through the constant
+  // address space, so the wave-uniform reads are scalar loads.
+  const __attribute__((address_space(4))) int64_t* gids =
+      (const __attribute__((address_space(4))) int64_t*)a.gids;
+  int64_t gid = gids[bi];
+  // scattered side: one base per chunk of the group
+  char* chunk_base[kC];
+#pragma unroll
+  for (int j = 0; j < kC; ++j) {
+    chunk_base[j] = reinterpret_cast<char*>(a.layer_ptr[l * ppl + k * (ppl - 1)]) +
+                    static_cast<int64_t>(k) * a.gpu_kv_stride + gid * a.gpu_block_stride +
+                    static_cast<int64_t>(rr) * kRow;
+    if (j + 1 < kC) {
+      if (++k == kv) {
+        k = 0;
+        if (++l == a.num_layers) {
+          l = 0;
+          gid = gids[++bi];
+        }
+      }
+    }
+  }
+  char* packed = a.packed + static_cast<int64_t>(g) * (kU * kRow);
+  u32x4 v[kU];
+#pragma unroll
+  for (int j = 0; j < kC; ++j)
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      const char* src = kH2D ? packed + (j * kR + r) * kRow : chunk_base[j] + r * kRow;
+      v[j * kR + r] = __builtin_nontemporal_load((const gvec*)(src + lane_off));
+    }
+#pragma unroll
+  for (int j = 0; j < kC; ++j)
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      char* dst = kH2D ? chunk_base[j] + r * kRow : packed + (j * kR + r) * kRow;
+      __builtin_nontemporal_store(v[j * kR + r], (gvec*)(dst + lane_off));
+    }
+}
+
+// Copies a transfer's (gpu_id, cpu_id) pairs from the pinned buffer into a
+// device buffer laid out [gpu ids | cpu ids], n entries each, which the
+// staging kernels then read with ids_split = n.
+__global__ __launch_bounds__(256) void stage_ids_kernel(const int64_t* pairs, int64_t* out,
+                                                        int n) {
+  const int i = blockIdx.x * 256 + static_cast<int>(threadIdx.x);
+  if (i < n) {
+    out[i] = pairs[2 * static_cast<int64_t>(i)];
+    out[static_cast<int64_t>(n) + i] = pairs[2 * static_cast<int64_t>(i) + 1];
+  }
+}
+
 // A system-scope acquire in every workgroup.  Launched with a workgroup per
 // compute unit (so every XCD's L2 takes part) before a kernel reads memory
 // the copy engines wrote outside any HIP stream: no stale line survives it.
@@ -606,6 +708,42 @@ int ensure_device_basics(int dev) {
   return 0;
 }
 
+// Staging launches take kv_pack_kernel where their shape allows (1), or
+// the row-by-row / whole-group kv_chunk_copy_kernel throughout (0).
+#ifndef FKV_PACK_KERNEL
+#define FKV_PACK_KERNEL 1
+#endif
+
+// Staging kernels read their tile's ids from a device copy of the pairs
+// (stage_ids_on_device) rather than the pinned buffer: every workgroup of a
+// staging launch starts with that read, and over PCIe it costs a host round
+// trip per tile.
+#ifndef FKV_STAGE_IDS_ON_DEVICE
+#define FKV_STAGE_IDS_ON_DEVICE 1
+#endif
+
+// Queue a copy of the n pairs in `ids` (pinned) into a device buffer held by
+// `lease`, on `stream`, and describe it in `out` (the pinned pairs stay its
+// host side, for launches that take their ids inline) with `split` = n.
+// Without FKV_STAGE_IDS_ON_DEVICE, `out` is `ids` and `split` 0.
+int stage_ids_on_device(const IdBuf& ids, int n, int dev, hipStream_t stream, DevIdLease& lease,
+                        IdBuf* out, int32_t* split) {
+  *out = ids;
+  *split = 0;
+  if (!FKV_STAGE_IDS_ON_DEVICE || n <= 0) return 0;
+  lease.dev = dev;
+  int rc = dev_ids_acquire(dev, static_cast<size_t>(n) * 16, &lease.buf);
+  if (rc) return rc;
+  (void)hipGetLastError();  // a stale error from elsewhere must not be blamed on this launch
+  hipLaunchKernelGGL(stage_ids_kernel, dim3((n + 255) / 256), dim3(256), 0, stream,
+                     reinterpret_cast<const int64_t*>(ids.dev),
+                     reinterpret_cast<int64_t*>(lease.buf.dev), n);
+  FKV_HIP(hipGetLastError());
+  out->dev = lease.buf.dev;
+  *split = n;
+  return 0;
+}
+
 // Tiles are tb blocks x tl layers.  Start from whole block rows (one block,
 // every layer) and halve the layer window until there are about `factor`
 // tiles per occupancy slot of the grid; when blocks are plentiful, group
@@ -681,6 +819,35 @@ void choose_tiles(int nb, int nl, int kv, int rpc, int grid_cap, int factor, int
 // `host` is null.  `grid_cap` is compute units x occupancy of the kernel the
 // launch takes; staging launches that take the whole-group variant use
 // `whole_grid_cap` instead when it is given.
+// The kv_pack_kernel instantiation (kU, kC) for a staging launch of `nb`
+// blocks x `nl` layers with chunks of `rpc` full rows, or {0, 0} when the
+// row-by-row kernel has to take it.
+struct PackShape {
+  int u = 0, c = 0;
+};
+PackShape pack_shape(int64_t rpc, int64_t chunks) {
+  if (rpc % 32 == 0) return {32, 1};
+  for (int c : {2, 4, 8})
+    if (rpc * c == 32 && chunks % c == 0) return {32, c};
+  if (rpc % 24 == 0) return {24, 1};
+  return {};
+}
+
+// Launch kv_pack_kernel<kH2D, kU, kC> over `groups` groups.
+// Dynamic LDS (unused by the kernel) that holds the 24-row variant to one
+// workgroup per compute unit.  Measured on MI355X, MLA 72 KiB chunks, HBM
+// TB/s at one / four workgroups per CU (the variant's occupancy): gather
+// 5.57 / 5.46 at 510 MiB, 5.56 / 5.50 at 1 GiB; scatter 5.36 / 5.22 and
+// 5.38 / 5.33.  The 32-row variants gained nothing from such a cap.
+constexpr unsigned kPackLds24 = 84 << 10;
+
+template <bool kH2D, int kU, int kC>
+void launch_pack(const PackArgs& pa, hipStream_t stream, hipEvent_t ea, hipEvent_t eb) {
+  const uint32_t grid = (pa.num_groups + kWaves - 1) / kWaves;
+  hipExtLaunchKernelGGL((kv_pack_kernel<kH2D, kU, kC>), dim3(grid), dim3(kThreads),
+                        kU == 24 ? kPackLds24 : 0u, stream, ea, eb, 0, pa);
+}
+
 template <bool kH2D, bool kIota>
 int launch_copy(const Geometry& g, const IdBuf& ids, char* cpu_base, int64_t cks, int64_t cls,
                 int64_t cbs, int b0, int nb, int l0, int nl, int grid_cap,
@@ -689,6 +856,46 @@ int launch_copy(const Geometry& g, const IdBuf& ids, char* cpu_base, int64_t cks
   if (nl < 1 || static_cast<int64_t>(nl) * g.ptrs_per_layer > kMaxLayersPerLaunch)
     return fail(kInval, "internal: a launch of %d layers exceeds the %d layer pointers of the "
                 "kernel arguments", nl, kMaxLayersPerLaunch / g.ptrs_per_layer);
+  // Staging launches whose packed side is contiguous in row order, with full
+  // rows and ids in device memory, take kv_pack_kernel.
+  if constexpr (kIota) {
+    const int64_t rpc = g.chunk / (64 * 16);
+    const bool packed_rows = FKV_PACK_KERNEL && split > 0 && g.chunk % (64 * 16) == 0 &&
+                             (g.kv == 1 || cks == g.chunk) && cls == g.kv * g.chunk &&
+                             cbs == static_cast<int64_t>(nl) * cls;
+    const int64_t chunks = static_cast<int64_t>(nb) * nl * g.kv;
+    const PackShape shape = packed_rows ? pack_shape(rpc, chunks) : PackShape{};
+    if (shape.u > 0 && chunks * rpc <= UINT32_MAX) {
+      PackArgs pa;
+      memset(&pa, 0, sizeof(pa));
+      pa.gids = reinterpret_cast<const int64_t*>(ids.dev) + b0;
+      pa.packed = cpu_base;
+      pa.gpu_kv_stride = g.gks;
+      pa.gpu_block_stride = g.gbs;
+      pa.rows_per_chunk = static_cast<uint32_t>(rpc);
+      pa.items_per_block = static_cast<uint32_t>(nl * g.kv);
+      pa.kv_dim = static_cast<uint32_t>(g.kv);
+      pa.num_layers = static_cast<uint32_t>(nl);
+      pa.num_groups = static_cast<uint32_t>(chunks * rpc / shape.u);
+      pa.ptrs_per_layer = g.ptrs_per_layer;
+      for (int i = 0; i < nl * g.ptrs_per_layer; ++i)
+        pa.layer_ptr[i] = reinterpret_cast<uint64_t>(g.layer_ptrs[l0 * g.ptrs_per_layer + i]);
+      hipEvent_t ea = nullptr, eb = nullptr;
+      int rc = prof.kernel_events(&ea, &eb);
+      if (rc) return rc;
+      prof.kernel_span(ea, eb, chunks * g.chunk);   // owns the events from here on
+      (void)hipGetLastError();  // a stale error from elsewhere must not be blamed on this launch
+      switch (shape.u * 16 + shape.c) {
+        case 32 * 16 + 1: launch_pack<kH2D, 32, 1>(pa, stream, ea, eb); break;
+        case 32 * 16 + 2: launch_pack<kH2D, 32, 2>(pa, stream, ea, eb); break;
+        case 32 * 16 + 4: launch_pack<kH2D, 32, 4>(pa, stream, ea, eb); break;
+        case 32 * 16 + 8: launch_pack<kH2D, 32, 8>(pa, stream, ea, eb); break;
+        default: launch_pack<kH2D, 24, 1>(pa, stream, ea, eb); break;
+      }
+      FKV_HIP(hipGetLastError());
+      return 0;
+    }
+  }
   CopyArgs a;
   memset(&a, 0, sizeof(a));
   a.ids = reinterpret_cast<const int64_t*>(ids.dev) + (split ? 1 : 2) * static_cast<int64_t>(b0);
@@ -730,18 +937,20 @@ int launch_copy(const Geometry& g, const IdBuf& ids, char* cpu_base, int64_t cks
   a.block_major = kIota && (kH2D ? FKV_BLOCK_MAJOR_SCATTER : FKV_BLOCK_MAJOR_GATHER);
   int grid = std::max(1, std::min(grid_cap, a.num_tiles));
   if (kIota && FKV_HBM_ONEPASS) grid = a.num_tiles;
-  hipEvent_t ev = nullptr;
-  if (prof.begin(stream, &ev)) return kInval;
+  hipEvent_t ea = nullptr, eb = nullptr;
+  int rc = prof.kernel_events(&ea, &eb);
+  if (rc) return rc;
+  prof.kernel_span(ea, eb, static_cast<int64_t>(nb) * nl * g.kv * g.chunk);
   (void)hipGetLastError();  // a stale error from elsewhere must not be blamed on this launch
   const unsigned lds = kIota ? FKV_HBM_LDS_PAD : 0;
   if (whole)
-    hipLaunchKernelGGL((kv_chunk_copy_kernel<kH2D, kIota, kIota>), dim3(grid), dim3(kThreads), lds,
-                       stream, a);
+    hipExtLaunchKernelGGL((kv_chunk_copy_kernel<kH2D, kIota, kIota>), dim3(grid), dim3(kThreads),
+                          lds, stream, ea, eb, 0, a);
   else
-    hipLaunchKernelGGL((kv_chunk_copy_kernel<kH2D, kIota>), dim3(grid), dim3(kThreads), lds,
-                       stream, a);
+    hipExtLaunchKernelGGL((kv_chunk_copy_kernel<kH2D, kIota>), dim3(grid), dim3(kThreads), lds,
+                          stream, ea, eb, 0, a);
   FKV_HIP(hipGetLastError());
-  return prof.end(stream, ev, static_cast<int64_t>(nb) * nl * g.kv * g.chunk, 0, false);
+  return 0;
 }
 
 // Pieces a call takes in kv_small_copy_kernel when it fits (at most
@@ -781,13 +990,15 @@ int transfer_small(const Geometry& g, char* cpu_dev, int n_pieces, hipStream_t s
       }
   if (p != n_pieces) return fail(kInval, "internal: %d small-transfer pieces, expected %d", p,
                                  n_pieces);
-  hipEvent_t ev = nullptr;
-  if (prof.begin(stream, &ev)) return kInval;
+  hipEvent_t ea = nullptr, eb = nullptr;
+  int rc = prof.kernel_events(&ea, &eb);
+  if (rc) return rc;
+  prof.kernel_span(ea, eb, static_cast<int64_t>(g.num_blocks) * g.num_layers * g.kv * g.chunk);
   (void)hipGetLastError();  // a stale error from elsewhere must not be blamed on this launch
-  hipLaunchKernelGGL(kv_small_copy_kernel<kH2D>, dim3(n_pieces), dim3(kThreads), 0, stream, a);
+  hipExtLaunchKernelGGL(kv_small_copy_kernel<kH2D>, dim3(n_pieces), dim3(kThreads), 0, stream,
+                        ea, eb, 0, a);
   FKV_HIP(hipGetLastError());
-  return prof.end(stream, ev, static_cast<int64_t>(g.num_blocks) * g.num_layers * g.kv * g.chunk,
-                  0, false);
+  return 0;
 }
 
 int transfer_zero_copy(const Geometry& g, hipStream_t stream, int dev, int transfer_cus,
@@ -1018,6 +1229,9 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   IdLease ids;
   rc = pack_ids(g, ids);
   if (rc) return rc;
+  DevIdLease dev_ids;   // released after the drain below
+  IdBuf kids;           // the ids the staging kernels read
+  int32_t kids_split = 0;
 
   // A piece is a run of whole blocks over a layer window; the window covers
   // all layers unless one block row would not fit a staging half.
@@ -1091,6 +1305,8 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
     }
   } publish{ln};
   DrainOnError drain{stream, &d, &ln};
+  if ((rc = stage_ids_on_device(ids.buf, g.num_blocks, dev, stream, dev_ids, &kids, &kids_split)))
+    return rc;
   ProfRecorder prof;
   std::vector<Run> runs;
   bool pending[2] = {false, false};
@@ -1110,7 +1326,8 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
     // by the engines' per-copy cost and spread over the wide set
     const bool wide = h2d && !runs.empty() &&
                       piece_bytes < kWideCopyBytes * static_cast<int64_t>(runs.size());
-    return issue_sdma(d, ln, runs, ln.staging + h * half, h2d, h, host_agent, wide);
+    return issue_sdma(d, ln, runs, ln.staging + h * half, h2d, h, host_agent,
+                      wide ? kEnginesWideSync : kEnginesOwn);
   };
   auto launch = [&](int pi) -> int {
     const Piece& p = pieces[pi];
@@ -1126,10 +1343,10 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
       cbs = static_cast<int64_t>(p.nl) * cls;
     }
     char* stg = ln.staging + (pi & 1) * half;
-    return h2d ? launch_copy<true, true>(g, ids.buf, stg, cks, cls, cbs, p.b0, p.nb, p.l0, p.nl,
-                                         grid_cap, stream, prof, 0, whole_cap)
-               : launch_copy<false, true>(g, ids.buf, stg, cks, cls, cbs, p.b0, p.nb, p.l0, p.nl,
-                                          grid_cap, stream, prof, 0, whole_cap);
+    return h2d ? launch_copy<true, true>(g, kids, stg, cks, cls, cbs, p.b0, p.nb, p.l0, p.nl,
+                                         grid_cap, stream, prof, kids_split, whole_cap)
+               : launch_copy<false, true>(g, kids, stg, cks, cls, cbs, p.b0, p.nb, p.l0, p.nl,
+                                          grid_cap, stream, prof, kids_split, whole_cap);
   };
   if (!h2d) {
     for (int pi = 0; pi < np; ++pi) {
@@ -1187,16 +1404,22 @@ int transfer_contiguous(const Geometry& g, hipStream_t stream, int dev, bool to_
   if (rc) return rc;
   const int grid_cap = d.num_cus * (to_gpu ? d.occ_staged[1] : d.occ_staged[0]);
   const int whole_cap = d.num_cus * (to_gpu ? d.occ_whole[1] : d.occ_whole[0]);
+  DevIdLease dev_ids;
+  IdBuf kids;
+  int32_t kids_split = 0;
   DrainOnError drain{stream};
+  if ((rc = stage_ids_on_device(ids.buf, g.num_blocks, dev, stream, dev_ids, &kids, &kids_split)))
+    return rc;
   ProfRecorder prof;
   const int per_launch = g.layers_per_launch();
   for (int l0 = 0; l0 < g.num_layers; l0 += per_launch) {
     const int nl = std::min(per_launch, g.num_layers - l0);
     char* base = g.cpu_info.dev_ptr + static_cast<int64_t>(l0) * g.cls;
-    rc = to_gpu ? launch_copy<true, true>(g, ids.buf, base, g.cks, g.cls, g.cbs, 0, g.num_blocks,
-                                          l0, nl, grid_cap, stream, prof, 0, whole_cap)
-                : launch_copy<false, true>(g, ids.buf, base, g.cks, g.cls, g.cbs, 0, g.num_blocks,
-                                           l0, nl, grid_cap, stream, prof, 0, whole_cap);
+    rc = to_gpu ? launch_copy<true, true>(g, kids, base, g.cks, g.cls, g.cbs, 0, g.num_blocks,
+                                          l0, nl, grid_cap, stream, prof, kids_split, whole_cap)
+                : launch_copy<false, true>(g, kids, base, g.cks, g.cls, g.cbs, 0, g.num_blocks,
+                                           l0, nl, grid_cap, stream, prof, kids_split,
+                                           whole_cap);
     if (rc) return rc;
   }
   FKV_HIP(hipStreamSynchronize(stream));
@@ -1580,7 +1803,7 @@ int layerwise_ce_run(fkv_transfer_handle_s* h, CopyLane& ln, hipStream_t work) {
     // Copies of one block's window are bound by the engines' per-copy cost,
     // so every window spreads over the wide engine set.
     return issue_sdma(d, ln, runs, ln.staging + (pi & 1) * half, true, pi & 1, d.cpu_agent,
-                      /*wide=*/true);
+                      kEnginesWide);
   };
   if (lead > 0) {
     if ((rc = layerwise_kernel_groups(h, work, 0, lead))) return rc;
@@ -2116,8 +2339,9 @@ int fkv_finalize(void) {
         keep(lane_release(d, ln));
       }
     }
-    // 4. pinned id buffers
+    // 4. pinned and device id buffers
     keep(ids_pool_free());
+    keep(dev_ids_pool_free());
     return rc;
   } catch (const std::exception& e) {
     return fail(static_cast<int>(hipErrorUnknown), "exception: %s", e.what());
