@@ -90,6 +90,12 @@ namespace {
 #ifndef FKV_WHOLE_SCATTER
 #define FKV_WHOLE_SCATTER 1
 #endif
+// Zero-copy launches whose chunks are whole groups of the unroll (8 rows
+// D2H, 4 H2D) take the whole-group variant, which keeps one base per group
+// instead of one address per row (no spills).
+#ifndef FKV_WHOLE_ZERO_COPY
+#define FKV_WHOLE_ZERO_COPY 1
+#endif
 // Cache hints: loads are non-temporal everywhere; stores are non-temporal
 // into HBM but plain into pinned host memory (about 2% faster D2H over PCIe).
 #ifndef FKV_NT_LOAD
@@ -147,6 +153,11 @@ constexpr int kInlineIds = 32;
 // loads/stores in flight to saturate the PCIe Gen5 x16 link (measured on
 // MI355X: 8 CUs reach the link's copy rate; more add contention).
 constexpr int kAutoZeroCopyCus = 8;
+// The whole-group variant of the device-to-host zero-copy kernel fills the
+// link with fewer compute units and loses rate with more (MI355X, Llama-3-8B
+// shape, 2 GiB: 56.4 / 56.7 / 56.2 / 55.8 GB/s on 3 / 4 / 6 / 8 CUs, against
+// 56.6 GB/s for the row-by-row variant on 8).
+constexpr int kAutoZeroCopyCusWholeD2H = 4;
 // Layer-wise host-to-device transfers run beside the caller's compute.  Two
 // CUs still fill the link for reads from host memory (56.9 vs 57.2 GB/s with
 // 8) and leave the rest of the chip to the compute kernels: a 32-layer
@@ -501,9 +512,9 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
 // are cut into groups of kU consecutive rows and wavefront w of workgroup b
 // moves group 4b + w: no tile, no LDS, no barrier, and every wavefront moves
 // a full group.  A group is kC whole chunks of kU / kC rows (kC > 1: chunks
-// of 1-16 KiB, e.g. the Llama-3-70B TP-8 shard's 4 KiB) or kU rows inside
+// of 4-16 KiB, e.g. the Llama-3-70B TP-8 shard's 4 KiB) or kU rows inside
 // one chunk (kC == 1: chunks of a multiple of kU rows, e.g. Llama-3-8B's 32
-// and MLA's 72 rows at kU = 24).  The host checks the shape: full 1 KiB
+// rows at kU = 32 and MLA's 72 at kU = 36).  The host checks the shape: full 1 KiB
 // rows, whole groups, a contiguous packed side, ids in device memory.
 struct PackArgs {
   const int64_t* gids;       // device memory: gpu id of launch block i at gids[i]
@@ -819,6 +830,18 @@ void choose_tiles(int nb, int nl, int kv, int rpc, int grid_cap, int factor, int
 // `host` is null.  `grid_cap` is compute units x occupancy of the kernel the
 // launch takes; staging launches that take the whole-group variant use
 // `whole_grid_cap` instead when it is given.
+// Whether the zero-copy launches of a transfer take the whole-group kernel
+// variant (launch_copy: full 1 KiB rows, chunks of whole unrolled groups).
+bool zero_copy_whole(const Geometry& g, bool h2d) {
+  const int64_t unroll = h2d ? FKV_UNROLL_ZC_H2D : FKV_UNROLL_ZC_D2H;
+  return FKV_WHOLE_ZERO_COPY && g.chunk % (64 * 16) == 0 && (g.chunk / (64 * 16)) % unroll == 0;
+}
+
+// Compute units of a zero-copy transfer when the caller passes -1.
+int auto_zero_copy_cus(const Geometry& g, bool h2d) {
+  return !h2d && zero_copy_whole(g, h2d) ? kAutoZeroCopyCusWholeD2H : kAutoZeroCopyCus;
+}
+
 // The kv_pack_kernel instantiation (kU, kC) for a staging launch of `nb`
 // blocks x `nl` layers with chunks of `rpc` full rows, or {0, 0} when the
 // row-by-row kernel has to take it.
@@ -829,23 +852,25 @@ PackShape pack_shape(int64_t rpc, int64_t chunks) {
   if (rpc % 32 == 0) return {32, 1};
   for (int c : {2, 4, 8})
     if (rpc * c == 32 && chunks % c == 0) return {32, c};
+  if (rpc % 36 == 0) return {36, 1};
   if (rpc % 24 == 0) return {24, 1};
   return {};
 }
 
 // Launch kv_pack_kernel<kH2D, kU, kC> over `groups` groups.
-// Dynamic LDS (unused by the kernel) that holds the 24-row variant to one
-// workgroup per compute unit.  Measured on MI355X, MLA 72 KiB chunks, HBM
-// TB/s at one / four workgroups per CU (the variant's occupancy): gather
-// 5.57 / 5.46 at 510 MiB, 5.56 / 5.50 at 1 GiB; scatter 5.36 / 5.22 and
-// 5.38 / 5.33.  The 32-row variants gained nothing from such a cap.
-constexpr unsigned kPackLds24 = 84 << 10;
+// Dynamic LDS (unused by the kernel) that holds the 36- and 24-row variants
+// to one workgroup per compute unit.  Measured on MI355X with MLA's 72 KiB
+// chunks, HBM TB/s of 506 MiB / 1 GiB launches, capped / uncapped: 36-row
+// groups gather 5.62-5.64 / 5.51-5.52 and 5.60-5.63 / 5.47-5.52, scatter
+// 5.29-5.30 / 5.27-5.30; 24-row groups gather 5.53 / 5.47 and 5.53-5.56 /
+// 5.42.  The 32-row variants gained nothing from such a cap.
+constexpr unsigned kPackLdsOneGroup = 84 << 10;
 
 template <bool kH2D, int kU, int kC>
 void launch_pack(const PackArgs& pa, hipStream_t stream, hipEvent_t ea, hipEvent_t eb) {
   const uint32_t grid = (pa.num_groups + kWaves - 1) / kWaves;
   hipExtLaunchKernelGGL((kv_pack_kernel<kH2D, kU, kC>), dim3(grid), dim3(kThreads),
-                        kU == 24 ? kPackLds24 : 0u, stream, ea, eb, 0, pa);
+                        kU != 32 ? kPackLdsOneGroup : 0u, stream, ea, eb, 0, pa);
 }
 
 template <bool kH2D, bool kIota>
@@ -890,6 +915,7 @@ int launch_copy(const Geometry& g, const IdBuf& ids, char* cpu_base, int64_t cks
         case 32 * 16 + 2: launch_pack<kH2D, 32, 2>(pa, stream, ea, eb); break;
         case 32 * 16 + 4: launch_pack<kH2D, 32, 4>(pa, stream, ea, eb); break;
         case 32 * 16 + 8: launch_pack<kH2D, 32, 8>(pa, stream, ea, eb); break;
+        case 36 * 16 + 1: launch_pack<kH2D, 36, 1>(pa, stream, ea, eb); break;
         default: launch_pack<kH2D, 24, 1>(pa, stream, ea, eb); break;
       }
       FKV_HIP(hipGetLastError());
@@ -928,8 +954,11 @@ int launch_copy(const Geometry& g, const IdBuf& ids, char* cpu_base, int64_t cks
       kH2D ? (FKV_WHOLE_SCATTER &&
               static_cast<int64_t>(nb) * nl * g.kv * g.chunk <= kWholeScatterMaxBytes)
            : FKV_WHOLE_GATHER;
-  const bool whole = kIota && whole_variant && a.chunk_vec % 64 == 0 &&
-                     a.rows_per_chunk % kStagedUnroll == 0;
+  // zero-copy launches whose chunks are whole groups of the launch's unroll
+  // take it too (FKV_WHOLE_ZERO_COPY)
+  const bool whole = kIota ? a.chunk_vec % 64 == 0 && whole_variant &&
+                                 a.rows_per_chunk % kStagedUnroll == 0
+                           : zero_copy_whole(g, kH2D);
   if (whole && whole_grid_cap > 0) grid_cap = whole_grid_cap;
   choose_tiles(nb, nl, g.kv, a.rows_per_chunk, grid_cap,
                kIota ? (kH2D ? FKV_TILE_FACTOR_SCATTER : FKV_TILE_FACTOR_HBM) : FKV_TILE_FACTOR,
@@ -944,7 +973,7 @@ int launch_copy(const Geometry& g, const IdBuf& ids, char* cpu_base, int64_t cks
   (void)hipGetLastError();  // a stale error from elsewhere must not be blamed on this launch
   const unsigned lds = kIota ? FKV_HBM_LDS_PAD : 0;
   if (whole)
-    hipExtLaunchKernelGGL((kv_chunk_copy_kernel<kH2D, kIota, kIota>), dim3(grid), dim3(kThreads),
+    hipExtLaunchKernelGGL((kv_chunk_copy_kernel<kH2D, kIota, true>), dim3(grid), dim3(kThreads),
                           lds, stream, ea, eb, 0, a);
   else
     hipExtLaunchKernelGGL((kv_chunk_copy_kernel<kH2D, kIota>), dim3(grid), dim3(kThreads), lds,
@@ -1023,7 +1052,7 @@ int transfer_zero_copy(const Geometry& g, hipStream_t stream, int dev, int trans
   int rc = pack_ids(g, ids);
   if (rc) return rc;
   DrainOnError drain{stream};
-  int cus = transfer_cus <= 0 ? std::min(kAutoZeroCopyCus, d.num_cus)
+  int cus = transfer_cus <= 0 ? std::min(auto_zero_copy_cus(g, h2d), d.num_cus)
                               : std::min(transfer_cus, d.num_cus);
   const int grid_cap = cus * (h2d ? d.occ_zero_copy[1] : d.occ_zero_copy[0]);
   char* cpu_dev = g.cpu_info.dev_ptr + g.startoff +
@@ -1132,7 +1161,7 @@ int transfer_zero_copy_noalloc(const Geometry& g, hipStream_t stream, int dev, i
     split = kScratchMaxBlocks;
   }
   DrainOnError drain{stream};
-  const int cus = transfer_cus <= 0 ? std::min(kAutoZeroCopyCus, d.num_cus)
+  const int cus = transfer_cus <= 0 ? std::min(auto_zero_copy_cus(g, h2d), d.num_cus)
                                     : std::min(transfer_cus, d.num_cus);
   const int grid_cap = cus * (h2d ? d.occ_zero_copy[1] : d.occ_zero_copy[0]);
   char* cpu_dev = g.cpu_info.dev_ptr + g.startoff + static_cast<int64_t>(g.start_layer) * g.cls;
@@ -1569,7 +1598,7 @@ int layerwise_enqueue(const Geometry& g, hipStream_t stream, int dev, int transf
   int rc = ids_acquire(static_cast<size_t>(g.num_blocks) * 16, &h->ids);
   if (rc) return rc;
   pack_ids_into(g, h->ids.host);
-  const int automatic = h2d ? kAutoLayerwiseH2DCus : kAutoZeroCopyCus;
+  const int automatic = h2d ? kAutoLayerwiseH2DCus : auto_zero_copy_cus(g, h2d);
   const int cus = transfer_cus <= 0 ? std::min(automatic, d.num_cus)
                                     : std::min(transfer_cus, d.num_cus);
   const int grid_cap = cus * (h2d ? d.occ_zero_copy[1] : d.occ_zero_copy[0]);
