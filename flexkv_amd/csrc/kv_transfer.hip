@@ -513,8 +513,8 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
 // moves group 4b + w: no tile, no LDS, no barrier, and every wavefront moves
 // a full group.  A group is kC whole chunks of kU / kC rows (kC > 1: chunks
 // of 4-16 KiB, e.g. the Llama-3-70B TP-8 shard's 4 KiB) or kU rows inside
-// one chunk (kC == 1: chunks of a multiple of kU rows, e.g. Llama-3-8B's 32
-// rows at kU = 32 and MLA's 72 at kU = 36).  The host checks the shape: full 1 KiB
+// one chunk (kC == 1: chunks of a multiple of kU rows, e.g. MLA's 72 rows
+// at kU = 36).  The host checks the shape: full 1 KiB
 // rows, whole groups, a contiguous packed side, ids in device memory.
 struct PackArgs {
   const int64_t* gids;       // device memory: gpu id of launch block i at gids[i]
@@ -848,8 +848,13 @@ int auto_zero_copy_cus(const Geometry& g, bool h2d) {
 struct PackShape {
   int u = 0, c = 0;
 };
+// Chunks of whole 32-row groups (32 KiB, 64 KiB, ...) keep the tiled
+// whole-group kernel: measured on MI355X at the Llama-3-8B shape it gathers
+// 0.3-1% faster than 32-row pack groups at 256 MiB-1 GiB (6.03 against 5.96
+// TB/s at 1 GiB) and in a copy-engine transfer's pieces moves the same
+// within 1% either way.
 PackShape pack_shape(int64_t rpc, int64_t chunks) {
-  if (rpc % 32 == 0) return {32, 1};
+  if (rpc % 32 == 0) return {};
   for (int c : {2, 4, 8})
     if (rpc * c == 32 && chunks % c == 0) return {32, c};
   if (rpc % 36 == 0) return {36, 1};
@@ -911,7 +916,6 @@ int launch_copy(const Geometry& g, const IdBuf& ids, char* cpu_base, int64_t cks
       prof.kernel_span(ea, eb, chunks * g.chunk);   // owns the events from here on
       (void)hipGetLastError();  // a stale error from elsewhere must not be blamed on this launch
       switch (shape.u * 16 + shape.c) {
-        case 32 * 16 + 1: launch_pack<kH2D, 32, 1>(pa, stream, ea, eb); break;
         case 32 * 16 + 2: launch_pack<kH2D, 32, 2>(pa, stream, ea, eb); break;
         case 32 * 16 + 4: launch_pack<kH2D, 32, 4>(pa, stream, ea, eb); break;
         case 32 * 16 + 8: launch_pack<kH2D, 32, 8>(pa, stream, ea, eb); break;

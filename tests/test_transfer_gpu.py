@@ -1022,11 +1022,12 @@ def test_c_ext_releases_the_gil(dev, use_ce):
 def test_gather_scatter_match_oracle(dev, geo, buffer_on_host):
     """fkv_gather/scatter_kv_blocks against the oracle with the contiguous
     buffer described as a block-wise cache [n, L, kv, chunk] and ids 0..n-1.
-    Every kv_pack_kernel shape is here: chunks of 32 / 64 KiB (32-row groups
-    inside a chunk), 72 KiB (36-row groups), 24 KiB (24-row groups), 16 / 8 /
-    4 KiB (groups of 2 / 4 / 8 whole chunks); and the row-by-row kernel's cases: partial
-    rows (128 B, 48 B), 1 KiB chunks, 4 KiB chunks whose count is not a
-    multiple of 8, more layers than one launch holds."""
+    Every kv_pack_kernel shape is here: chunks of 72 KiB (36-row groups),
+    24 KiB (24-row groups), 16 / 8 / 4 KiB (groups of 2 / 4 / 8 whole
+    chunks); the tiled whole-group kernel's 32 / 64 KiB chunks; and the
+    row-by-row kernel's cases: partial rows (128 B, 48 B), 1 KiB chunks,
+    4 KiB chunks whose count is not a multiple of 8, more layers than one
+    launch holds."""
     import ctypes
     from flexkv_amd import _lib
     from flexkv_amd.storage.allocator import pinned_empty
