@@ -313,10 +313,11 @@ int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, voi
  *     take to them.
  *   rect_copies: a layer-wise host cache with scattered ids (no contiguous
  *     host run longer than one chunk) moves with one SDMA rect copy per
- *     block when 1 (one engine: about 47 GB/s at the Llama-3-8B shape, and
- *     compute beside it keeps its speed), with the zero-copy kernel when 0
- *     (the default: about 57 GB/s, but any kernel resident on the compute
- *     units slows a whole-device GEMM beside it 1.4-1.9x).
+ *     block when 1 (the one engine the runtime assigns per direction: about
+ *     0.8 of the host link, and compute beside it keeps its speed), with the
+ *     zero-copy kernel when 0 (the default: the link's full rate, but any
+ *     kernel resident on the compute units slows a whole-device GEMM beside
+ *     it).  profiles/results.md holds the measured rates of both.
  * -1 for either unsets it (FLEXKV_CE_MIN_BYTES / FLEXKV_CE_RECT_COPIES, else
  * the default, apply again); -2 keeps it as it is.  fkv_get_copy_engine_policy
  * reads the values in force. */
