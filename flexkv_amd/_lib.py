@@ -75,6 +75,7 @@ class FkvProfile(ctypes.Structure):
         ("dma_copies", ctypes.c_int64),
         ("dma_ms", ctypes.c_double),
         ("dma_bytes", ctypes.c_int64),
+        ("dma_held_copies", ctypes.c_int64),
     ]
 
     def as_dict(self) -> dict:

@@ -323,12 +323,13 @@ void prof_add_kernel(double ms, int64_t bytes) {
   g_prof.kernel_bytes += bytes;
 }
 
-void prof_add_dma(double ms, int64_t copies, int64_t bytes) {
+void prof_add_dma(double ms, int64_t copies, int64_t bytes, int64_t held_copies) {
   std::lock_guard<std::mutex> lk(g_prof_mu);
   g_prof.dma_batches += 1;
   g_prof.dma_copies += copies;
   g_prof.dma_ms += ms;
   g_prof.dma_bytes += bytes;
+  g_prof.dma_held_copies += held_copies;
 }
 
 void pack_ids_into(const Geometry& g, int64_t* h) {

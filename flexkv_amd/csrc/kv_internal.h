@@ -80,6 +80,8 @@ struct CopyLane {
   std::vector<hsa_signal_t> polled_pool[2], irq_pool[2];   // created on demand, kept
   std::vector<hsa_signal_t> queued[2];   // signal of every copy queued on the half
   std::vector<hsa_signal_t> wake[2];     // the interrupt signals among them
+  // pool signals the half's queued copies use (issue_sdma appends after them)
+  size_t used_polled[2] = {0, 0}, used_irq[2] = {0, 0};
   hipEvent_t ev_compute[2] = {nullptr, nullptr};
   // A wait on this lane timed out: an engine may still write its staging
   // buffer or decrement its signals, so neither is freed or reused again
@@ -197,7 +199,7 @@ bool geometry_vec16(const Geometry& g);
 // Profiling (fkv_profile_enable / fkv_profile_read)
 extern std::atomic<bool> g_prof_on;
 void prof_add_kernel(double ms, int64_t bytes);
-void prof_add_dma(double ms, int64_t copies, int64_t bytes);
+void prof_add_dma(double ms, int64_t copies, int64_t bytes, int64_t held_copies = 0);
 
 // Event pairs recorded around launches when profiling is on; read after the
 // final synchronisation.
@@ -383,8 +385,24 @@ int ensure_staging(CopyLane& lane, size_t need_half);
 // Engine sets issue_sdma may take: the direction's own, or for host-to-device
 // copies the synchronous transfers' wide set or the layer-wise pipeline's.
 enum EngineSet { kEnginesOwn = 0, kEnginesWideSync = 1, kEnginesWide = 2 };
+// A half's copies whose first stretch runs beside a scatter kernel can hold
+// back the engines of the set beyond its first kHoldKeepEngines: issue_sdma
+// then queues only the kept engines' share of `runs` and leaves the held
+// engines' share, the tail of `runs`, in `deferred`, sized so that held
+// engines starting `held_fraction` of the half's time late finish with the
+// others.  The caller queues `deferred` (issue_sdma with `held_part`) once the
+// scatter is done.  A set of at most kHoldKeepEngines engines holds nothing.
+constexpr size_t kHoldKeepEngines = 4;
+struct SdmaHold {
+  double held_fraction = 0;
+  std::vector<Run> deferred;
+};
+// `held_part`: queue `runs` (a `deferred` list) on the held engines of the set,
+// after the copies already queued on the half (on every engine of the set when
+// it has no held engines now).
 int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, char* staging,
-               bool h2d, int half, hsa_agent_t host_agent, int wide = kEnginesOwn);
+               bool h2d, int half, hsa_agent_t host_agent, int wide = kEnginesOwn,
+               SdmaHold* hold = nullptr, bool held_part = false);
 // Wait until every copy queued on a staging half has finished: block on the
 // interrupt signals of the engines' last copies, then check every copy's own
 // signal.  An engine runs its copies in order, so the check normally finds

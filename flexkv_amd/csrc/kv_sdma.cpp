@@ -492,48 +492,83 @@ int ensure_staging(CopyLane& d, size_t need_half) {
 }
 
 int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, char* staging,
-               bool h2d, int half, hsa_agent_t host_agent, int wide) {
+               bool h2d, int half, hsa_agent_t host_agent, int wide, SdmaHold* hold,
+               bool held_part) {
   // While the other direction has a copy-engine transfer in flight, the
   // directions split engines 0-7 (the duplex sets); otherwise each takes its
   // one-way set, or host-to-device the wide set where asked.
   const int dir = h2d ? 1 : 0;
   const bool duplex = !d.engines_duplex[dir].empty() &&
                       d.busy[1 - dir].load(std::memory_order_relaxed) > 0;
-  const std::vector<hsa_amd_sdma_engine_id_t>& eng =
+  const std::vector<hsa_amd_sdma_engine_id_t>& set =
       duplex ? d.engines_duplex[dir]
              : (wide == kEnginesWide && h2d && !d.engines_wide.empty()) ? d.engines_wide
              : (wide == kEnginesWideSync && h2d && !d.engines_wide_sync.empty())
                  ? d.engines_wide_sync
                  : d.engines[dir];
-  const size_t n = runs.size();
-  // The engine of each copy (rect copies: the runtime's one engine, key
-  // eng.size()) and whether it is that engine's last copy of the half.
+  // The engines of this call: the whole set; its first kHoldKeepEngines when
+  // the held engines' share is deferred; the rest for a deferred share.
+  size_t e0 = 0, e1 = set.size();
+  size_t n = runs.size();
+  const bool linear = n > 0 && runs[0].slices == 0;
+  if (hold) hold->deferred.clear();
+  if (held_part) {
+    if (set.size() > kHoldKeepEngines) e0 = kHoldKeepEngines;
+  } else if (hold && hold->held_fraction > 0 && linear && set.size() > kHoldKeepEngines) {
+    // Held engines start held_fraction f of the half's time late.  Kept
+    // engines run faster while they are alone on the link: each moves about
+    // rho = (set / kept) * 0.93 times a held engine's rate then (MI355X,
+    // 640 KiB host-to-device copies: 52.7 GB/s on four engines, 56.6 on six).
+    // For all to end together a held engine takes 1 / (1 + rho f / (1 - f))
+    // of a kept engine's copies.
+    const double f = std::min(0.5, hold->held_fraction);
+    const double kept = static_cast<double>(kHoldKeepEngines);
+    const double held = static_cast<double>(set.size() - kHoldKeepEngines);
+    const double rho = static_cast<double>(set.size()) / kept * 0.93;
+    const double b = 1.0 / (1.0 + rho * f / (1.0 - f));
+    size_t nd = static_cast<size_t>(static_cast<double>(n) * held * b / (kept + held * b) + 0.5);
+    nd = std::min(nd, n > kHoldKeepEngines ? n - kHoldKeepEngines : size_t(0));
+    if (nd > 0) {
+      hold->deferred.assign(runs.end() - static_cast<std::ptrdiff_t>(nd), runs.end());
+      n -= nd;
+      e1 = kHoldKeepEngines;
+    }
+  }
+  const size_t ne = e1 - e0;
+  // The engine of each copy (rect copies: the runtime's one engine, key ne)
+  // and whether it is that engine's last copy of this call.
   std::vector<uint8_t> last(n, 0);
   uint64_t seen = 0;   // bit per engine key (at most 33)
   size_t tails = 0;
   for (size_t i = n; i-- > 0;) {
-    const size_t key = runs[i].slices > 0 ? eng.size() : i % eng.size();
+    const size_t key = runs[i].slices > 0 ? ne : i % ne;
     if (!(seen >> key & 1)) {
       seen |= uint64_t(1) << key;
       last[i] = 1;
       ++tails;
     }
   }
+  // A deferred share follows the copies already queued on the half, with
+  // signals of its own from the pools.
+  if (!held_part) {
+    lane.queued[half].clear();
+    lane.wake[half].clear();
+    lane.used_polled[half] = 0;
+    lane.used_irq[half] = 0;
+  }
   std::vector<hsa_signal_t>& polled = lane.polled_pool[half];
   std::vector<hsa_signal_t>& irq = lane.irq_pool[half];
-  while (polled.size() < n - tails) {
+  size_t np = lane.used_polled[half], ni = lane.used_irq[half];
+  while (polled.size() < np + (n - tails)) {
     hsa_signal_t sg;
     FKV_HSA(g_hsa.amd_signal_create(1, 0, nullptr, HSA_AMD_SIGNAL_AMD_GPU_ONLY, &sg));
     polled.push_back(sg);
   }
-  while (irq.size() < tails) {
+  while (irq.size() < ni + tails) {
     hsa_signal_t sg;
     FKV_HSA(g_hsa.signal_create(1, 0, nullptr, &sg));
     irq.push_back(sg);
   }
-  lane.queued[half].clear();
-  lane.wake[half].clear();
-  size_t np = 0, ni = 0;
   for (size_t i = 0; i < n; ++i) {
     const Run& r = runs[i];
     char* dev_p = staging + r.staging_off;
@@ -551,7 +586,7 @@ int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, cha
                : g_hsa.async_copy_rect(&hp, &zero, &sp, &zero, &range, d.gpu_agent,
                                        hsaDeviceToHost, 0, nullptr, sig);
     } else {
-      const hsa_amd_sdma_engine_id_t e = eng[i % eng.size()];
+      const hsa_amd_sdma_engine_id_t e = set[e0 + i % ne];
       st = h2d ? g_hsa.async_copy_on_engine(dev_p, d.gpu_agent, r.host, host_agent,
                                             static_cast<size_t>(r.bytes), 0, nullptr, sig, e,
                                             false)
@@ -562,6 +597,8 @@ int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, cha
     if (st != HSA_STATUS_SUCCESS) {
       const char* m = nullptr;
       (void)g_hsa.status_string(st, &m);
+      lane.used_polled[half] = np;
+      lane.used_irq[half] = ni;
       return fail(static_cast<int>(hipErrorUnknown), "SDMA %s of %lld bytes x %d failed: %s",
                   r.slices > 0 ? "rect copy" : "copy", static_cast<long long>(r.bytes),
                   std::max(1, static_cast<int>(r.slices)), m ? m : "?");
@@ -569,6 +606,8 @@ int issue_sdma(DeviceState& d, CopyLane& lane, const std::vector<Run>& runs, cha
     lane.queued[half].push_back(sig);
     if (last[i]) lane.wake[half].push_back(sig);
   }
+  lane.used_polled[half] = np;
+  lane.used_irq[half] = ni;
   return 0;
 }
 

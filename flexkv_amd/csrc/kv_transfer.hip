@@ -202,6 +202,24 @@ bool ce_rect_copies() {
 // keep the direction's four.  While a D2H is in flight, host-to-device copies
 // of any size take the duplex split instead (issue_sdma).
 constexpr int64_t kWideCopyBytes = int64_t(1) << 20;
+// Host-to-device copies on the wide set run beside the scatter of the
+// previous piece, and every engine in flight slows that scatter (MI355X,
+// Llama-3-70B TP-8 shard, 640 KiB copies: 512 MiB scatter pieces 4.26 /
+// 4.65 / 4.90 TB/s beside 8 / 6 / 4 engines).  So the engines of the set
+// beyond the first kHoldKeepEngines take their share of a piece only once
+// that scatter is done (issue_sdma, SdmaHold).  held_fraction is the
+// scatter's expected time, plus the host's wake-up, over the piece's time on
+// the link; FLEXKV_SDMA_HOLD_SCALE scales it (0: no engine is held).
+double held_fraction(int64_t prev_piece_bytes, int64_t piece_bytes) {
+  const char* e = getenv("FLEXKV_SDMA_HOLD_SCALE");
+  const double scale = e ? std::max(0.0, atof(e)) : 1.0;
+  if (scale <= 0 || piece_bytes <= 0) return 0.0;
+  constexpr double kScatterBytesPerS = 4.9e12;   // HBM bytes, read + write
+  constexpr double kLinkBytesPerS = 56e9;
+  constexpr double kWakeS = 20e-6;
+  const double d = 2.0 * static_cast<double>(prev_piece_bytes) / kScatterBytesPerS + kWakeS;
+  return scale * d / (static_cast<double>(piece_bytes) / kLinkBytesPerS);
+}
 // The piece of a copy-engine transfer that runs without engine copies beside
 // it (the first gather, the last scatter) is cut to 1 / kEdgePieceDiv of a
 // staging half when it moves at least kEdgePieceMinBytes.
@@ -1343,8 +1361,16 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   ProfRecorder prof;
   std::vector<Run> runs;
   bool pending[2] = {false, false};
-  int64_t dma_copies = 0, dma_bytes = 0;
+  int64_t dma_copies = 0, dma_bytes = 0, held_copies = 0;
   const auto t0 = std::chrono::steady_clock::now();
+  // Host-to-device copies into one half run beside the scatter of the other
+  // half's previous piece; the held engines' share of them waits for that
+  // scatter (issue_sdma, SdmaHold) and is queued by release_held.
+  SdmaHold hold[2];
+  auto piece_bytes_of = [&](int pi) {
+    const Piece& p = pieces[pi];
+    return static_cast<int64_t>(p.nb) * p.nl * g.kv * g.chunk;
+  };
   auto queue_copies = [&](int pi) -> int {
     const Piece& p = pieces[pi];
     const int h = pi & 1;
@@ -1359,8 +1385,19 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
     // by the engines' per-copy cost and spread over the wide set
     const bool wide = h2d && !runs.empty() &&
                       piece_bytes < kWideCopyBytes * static_cast<int64_t>(runs.size());
+    hold[h].held_fraction = wide && pi > 0 ? held_fraction(piece_bytes_of(pi - 1), piece_bytes)
+                                           : 0.0;
     return issue_sdma(d, ln, runs, ln.staging + h * half, h2d, h, host_agent,
-                      wide ? kEnginesWideSync : kEnginesOwn);
+                      wide ? kEnginesWideSync : kEnginesOwn, &hold[h]);
+  };
+  auto release_held = [&](int pi) -> int {
+    const int h = pi & 1;
+    if (hold[h].deferred.empty()) return 0;
+    held_copies += static_cast<int64_t>(hold[h].deferred.size());
+    const int rc2 = issue_sdma(d, ln, hold[h].deferred, ln.staging + h * half, h2d, h,
+                               host_agent, kEnginesWideSync, nullptr, /*held_part=*/true);
+    hold[h].deferred.clear();
+    return rc2;
   };
   auto launch = [&](int pi) -> int {
     const Piece& p = pieces[pi];
@@ -1404,10 +1441,13 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
       hipLaunchKernelGGL(acquire_system_kernel, dim3(d.num_cus), dim3(64), 0, stream);
       FKV_HIP(hipGetLastError());
       if ((rc = launch(pi))) return rc;
-      if (pi + 2 < np) {
+      if (pi + 1 < np) {
         FKV_HIP(hipEventRecord(ln.ev_compute[h], stream));
         FKV_HIP(hipEventSynchronize(ln.ev_compute[h]));
-        if ((rc = queue_copies(pi + 2))) return rc;
+        // the scatter of piece pi is done: the held engines take their share
+        // of piece pi + 1, and piece pi + 2 goes into the half it read
+        if ((rc = release_held(pi + 1))) return rc;
+        if (pi + 2 < np && (rc = queue_copies(pi + 2))) return rc;
       }
     }
   }
@@ -1421,7 +1461,7 @@ int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
   if (prof.on) {
     const double ms =
         std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-    prof_add_dma(ms, dma_copies, dma_bytes);
+    prof_add_dma(ms, dma_copies, dma_bytes, held_copies);
   }
   prof.flush();
   return 0;

@@ -52,11 +52,12 @@ enum {
    * double-buffered; the PCIe copies take no compute units.  Each direction
    * has its own staging and engines (device-to-host engines 0-3,
    * host-to-device 4-7; host-to-device copies shorter than 1 MiB on average
-   * spread over engines 0-7), so a D2H and an H2D transfer from different
-   * threads run at the same time; while both run, their copies split
-   * engines 0-7 (device-to-host 0-4, host-to-device 5-7;
+   * spread over six of engines 0-7, two of which wait for the scatter
+   * beside them to end before taking their share), so a D2H and an H2D
+   * transfer from different threads run at the same time; while both run,
+   * their copies split engines 0-7 (device-to-host 0-4, host-to-device 5-7;
    * FLEXKV_SDMA_DUPLEX_D2H), which balances the two.  Transfers under
-   * FLEXKV_CE_MIN_BYTES (default 8 MiB) or whose
+   * FLEXKV_CE_MIN_BYTES (default 32 MiB; fkv_set_copy_engine_policy) or whose
    * engine copies would move under 128 KiB each move with the zero-copy
    * kernel instead, where the engines' per-copy cost would dominate, and so
    * does every transfer on a device whose engines cannot be set up (one
@@ -98,10 +99,12 @@ enum {
  *   - cpu_ptr: pinned host memory (or device memory) for the kernel and CE
  *     modes; every addressed byte lies inside the allocation holding cpu_ptr,
  *     and every GPU chunk inside the allocation holding its layer pointer.
- *   - kernel and CE modes: chunk_size_bytes, every stride, cpu_startoff and
- *     every base pointer are multiples of 16 bytes.  (The reference kernel
+ *   - kernel mode: chunk_size_bytes, every stride, cpu_startoff and every
+ *     base pointer are multiples of 16 bytes.  (The reference kernel
  *     silently drops a tail of chunk_size % 16 bytes, csrc/transfer.cu:35;
- *     this library refuses such geometry instead.)
+ *     this library refuses such geometry instead.)  CE mode takes any
+ *     geometry: what the kernels cannot take moves on the per-chunk engine
+ *     loop (FKV_XFER_CE_PER_CHUNK), as the reference CE mode moves it.
  * The call is synchronous: it returns after `stream` has drained
  * (csrc/transfer.cu:131).  Different host threads may call concurrently.
  */
@@ -405,6 +408,7 @@ typedef struct fkv_profile {
   int64_t dma_copies;        /* individual contiguous DMA copies */
   double dma_ms;             /* sum of event-measured DMA batch durations */
   int64_t dma_bytes;
+  int64_t dma_held_copies;   /* DMA copies queued only after the scatter beside them ended */
 } fkv_profile;
 int fkv_profile_enable(int on);     /* also clears the counters */
 int fkv_profile_read(fkv_profile* out);

@@ -604,6 +604,37 @@ def test_staged_runs_and_small_staging(dev, run, heads):
         _lib.set_staging_bytes(0)
 
 
+@pytest.mark.parametrize("scale", ["0", "1", "40"])
+def test_held_engines_wait_for_the_scatter(dev, scale, monkeypatch):
+    """Host-to-device copies shorter than 1 MiB spread over the six-engine set,
+    and from the second piece on, the engines beyond the first four take their
+    share only once the scatter of the previous piece is done (queued
+    afterwards, counted as dma_held_copies).  64 KiB block rows in 512 KiB
+    staging halves: 16 pieces of 8 copies.  Scale 0 holds nothing, 1 is the
+    default, 40 defers the most the split allows; bytes match the oracle."""
+    from flexkv_amd import _lib
+    monkeypatch.setenv("FLEXKV_SDMA_HOLD_SCALE", scale)
+    _lib.set_staging_bytes(1 << 20)
+    try:
+        case = KVCase(layers_total=8, num_layers=8, start_layer=0, kv=2, ng=256, nh=512,
+                      tokens=16, heads=1, dim=128).fill(seed=int(scale) + 3)
+        gids = inputs.distinct_ids(7, 128, 256)
+        cids = inputs.distinct_ids(8, 128, 512)
+        _lib.profile_enable(True)
+        check_case(case, gids, cids, 1)
+        prof = _lib.profile_read()
+        _lib.profile_enable(False)
+        assert prof["dma_copies"] == 2 * 128, prof
+        if scale == "0":
+            assert prof["dma_held_copies"] == 0, prof
+        else:
+            assert 15 <= prof["dma_held_copies"] <= 15 * 4, prof
+    finally:
+        _lib.profile_enable(False)
+        _lib.release_staging()
+        _lib.set_staging_bytes(0)
+
+
 @pytest.mark.parametrize("blocks,launches", [(384, 2), (192, 2), (48, 1)])
 def test_copy_engine_edge_piece(dev, blocks, launches):
     """A copy-engine transfer whose piece without engine copies beside it (the
