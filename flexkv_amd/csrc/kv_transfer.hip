@@ -202,24 +202,6 @@ bool ce_rect_copies() {
 // keep the direction's four.  While a D2H is in flight, host-to-device copies
 // of any size take the duplex split instead (issue_sdma).
 constexpr int64_t kWideCopyBytes = int64_t(1) << 20;
-// Host-to-device copies on the wide set run beside the scatter of the
-// previous piece, and every engine in flight slows that scatter (MI355X,
-// Llama-3-70B TP-8 shard, 640 KiB copies: 512 MiB scatter pieces 4.26 /
-// 4.65 / 4.90 TB/s beside 8 / 6 / 4 engines).  So the engines of the set
-// beyond the first kHoldKeepEngines take their share of a piece only once
-// that scatter is done (issue_sdma, SdmaHold).  held_fraction is the
-// scatter's expected time, plus the host's wake-up, over the piece's time on
-// the link; FLEXKV_SDMA_HOLD_SCALE scales it (0: no engine is held).
-double held_fraction(int64_t prev_piece_bytes, int64_t piece_bytes) {
-  const char* e = getenv("FLEXKV_SDMA_HOLD_SCALE");
-  const double scale = e ? std::max(0.0, atof(e)) : 1.0;
-  if (scale <= 0 || piece_bytes <= 0) return 0.0;
-  constexpr double kScatterBytesPerS = 4.9e12;   // HBM bytes, read + write
-  constexpr double kLinkBytesPerS = 56e9;
-  constexpr double kWakeS = 20e-6;
-  const double d = 2.0 * static_cast<double>(prev_piece_bytes) / kScatterBytesPerS + kWakeS;
-  return scale * d / (static_cast<double>(piece_bytes) / kLinkBytesPerS);
-}
 // The piece of a copy-engine transfer that runs without engine copies beside
 // it (the first gather, the last scatter) is cut to 1 / kEdgePieceDiv of a
 // staging half when it moves at least kEdgePieceMinBytes.
@@ -1251,6 +1233,25 @@ constexpr int64_t kEdgeSmallMinBytesDefault = int64_t(32) << 20;
 int64_t edge_small_min_bytes() {
   const char* e = getenv("FLEXKV_CE_EDGE_MIN_BYTES");
   return e ? std::max<int64_t>(1, atoll(e)) : kEdgeSmallMinBytesDefault;
+}
+
+// Host-to-device copies on the wide set run beside the scatter of the
+// previous piece, and every engine in flight slows that scatter (MI355X,
+// Llama-3-70B TP-8 shard, 640 KiB copies: 512 MiB scatter pieces 4.26 /
+// 4.65 / 4.90 TB/s beside 8 / 6 / 4 engines).  So the engines of the set
+// beyond the first kHoldKeepEngines take their share of a piece only once
+// that scatter is done (issue_sdma, SdmaHold).  held_fraction is the
+// scatter's expected time, plus the host's wake-up, over the piece's time on
+// the link; FLEXKV_SDMA_HOLD_SCALE scales it (0: no engine is held).
+double held_fraction(int64_t prev_piece_bytes, int64_t piece_bytes) {
+  const char* e = getenv("FLEXKV_SDMA_HOLD_SCALE");
+  const double scale = e ? std::max(0.0, atof(e)) : 1.0;
+  if (scale <= 0 || piece_bytes <= 0) return 0.0;
+  constexpr double kScatterBytesPerS = 4.9e12;   // HBM bytes, read + write
+  constexpr double kLinkBytesPerS = 56e9;
+  constexpr double kWakeS = 20e-6;
+  const double d = 2.0 * static_cast<double>(prev_piece_bytes) / kScatterBytesPerS + kWakeS;
+  return scale * d / (static_cast<double>(piece_bytes) / kLinkBytesPerS);
 }
 
 int transfer_staged(const Geometry& g, hipStream_t stream, int dev, bool h2d) {
