@@ -961,16 +961,22 @@ def path_rates(wl: Workload, steps: int, peaks: dict, paths=(("ce", True), ("ker
     """D2H and H2D GB/s of the workload's step on each path, as fractions of
     the measured link and of the nominal PCIe Gen5 x16 rate; for the
     copy-engine path also the average rate of the gather and scatter pieces
-    it launched (the library's event timing, HBM bytes = 2 x moved)."""
+    it launched (the library's event timing, HBM bytes = 2 x moved).  The
+    rates come from a run without the library's profiling, which records
+    events around every launch and costs small ops several percent; it runs
+    at least 0.1 s (at 50 GB/s) so short ops are timed over many calls.  The
+    piece rates come from a second, profiled run of `steps` transfers."""
     from flexkv_amd import _lib
     gb = wl.bytes_per_op / 1e9
+    timed = max(steps, int(0.1 * 50e9 / wl.bytes_per_op) + 1)
     out = {}
     for name, ce in paths:
         res = {}
         for h2d in (False, True):
             d = "h2d" if h2d else "d2h"
+            s, _, _ = time_steps(lambda: wl.transfer(h2d, ce), timed, 1)
             _lib.profile_enable(True)
-            s, _, _ = time_steps(lambda: wl.transfer(h2d, ce), steps, 1)
+            time_steps(lambda: wl.transfer(h2d, ce), steps, 0)
             prof = _lib.profile_read()
             _lib.profile_enable(False)
             rate = gb / s
@@ -982,7 +988,7 @@ def path_rates(wl: Workload, steps: int, peaks: dict, paths=(("ce", True), ("ker
                 key = "scatter" if h2d else "gather"
                 res[f"{key}_piece_gbps_hbm"] = round(piece, 1)
                 res[f"{key}_piece_frac_hbm"] = round(piece / HBM_PEAK_GBS, 4)
-                res[f"{key}_pieces_per_step"] = prof["kernel_launches"] // (steps + 1)
+                res[f"{key}_pieces_per_step"] = prof["kernel_launches"] // steps
             elif ce:
                 res[f"{d}_moved_by"] = "zero-copy kernel (size or layout policy)"
         out[name] = res

@@ -156,7 +156,8 @@ constexpr int kAutoZeroCopyCus = 8;
 // The whole-group variant of the device-to-host zero-copy kernel fills the
 // link with fewer compute units and loses rate with more (MI355X, Llama-3-8B
 // shape, 2 GiB: 56.4 / 56.7 / 56.2 / 55.8 GB/s on 3 / 4 / 6 / 8 CUs, against
-// 56.6 GB/s for the row-by-row variant on 8).
+// 56.6 GB/s for the row-by-row variant on 8), for calls of at least
+// kZeroCopyFewCusMinBytes.
 constexpr int kAutoZeroCopyCusWholeD2H = 4;
 // Layer-wise host-to-device transfers run beside the caller's compute.  Two
 // CUs still fill the link for reads from host memory (56.9 vs 57.2 GB/s with
@@ -838,8 +839,16 @@ bool zero_copy_whole(const Geometry& g, bool h2d) {
 }
 
 // Compute units of a zero-copy transfer when the caller passes -1.
+// The whole-group device-to-host kernel's fewer compute units pay from this
+// many bytes per call; below it the ramp of a short call wants more (MI355X,
+// 4 / 8 / 16 CUs: 16 MiB ops 51.3 / 52.1 / 52.8 GB/s, 32 MiB 53.6 / 53.9 /
+// 53.9, 2 GiB 56.7 / 55.6 / 55.2).
+constexpr int64_t kZeroCopyFewCusMinBytes = int64_t(64) << 20;
 int auto_zero_copy_cus(const Geometry& g, bool h2d) {
-  return !h2d && zero_copy_whole(g, h2d) ? kAutoZeroCopyCusWholeD2H : kAutoZeroCopyCus;
+  const int64_t bytes = static_cast<int64_t>(g.num_blocks) * g.num_layers * g.kv * g.chunk;
+  return !h2d && zero_copy_whole(g, h2d) && bytes >= kZeroCopyFewCusMinBytes
+             ? kAutoZeroCopyCusWholeD2H
+             : kAutoZeroCopyCus;
 }
 
 // The kv_pack_kernel instantiation (kU, kC) for a staging launch of `nb`
