@@ -47,6 +47,9 @@ EXPORTED_SYMBOLS = (
     "fkv_ssd_stats_read",
     "fkv_ssd_close",
     "fkv_transfer_kv_blocks_ssd",
+    "fkv_tp_group_create",
+    "fkv_tp_group_transfer",
+    "fkv_tp_group_destroy",
     "fkv_last_error",
     "fkv_last_unsafe_host_blocks",
     "fkv_abandoned_copies_pending",
@@ -149,6 +152,15 @@ def _declare(lib: ctypes.CDLL) -> None:
     f.restype = c_int
     f.argtypes = [c_vp, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_i64, c_i64, c_i64, c_i64,
                   c_i64, c_i64, c_int, c_int, c_int, c_int]
+    lib.fkv_tp_group_create.restype = c_int
+    lib.fkv_tp_group_create.argtypes = [c_int, ctypes.POINTER(c_int), c_vp, c_int, c_vp,
+                                        ctypes.POINTER(c_vp)]
+    f = lib.fkv_tp_group_transfer
+    f.restype = c_int
+    f.argtypes = [c_vp, c_int, c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_int, c_int,
+                  c_int, c_int, c_int, c_int]
+    lib.fkv_tp_group_destroy.restype = c_int
+    lib.fkv_tp_group_destroy.argtypes = [c_vp]
     lib.fkv_last_error.restype = ctypes.c_char_p
     lib.fkv_last_error.argtypes = []
     lib.fkv_host_alloc.restype = c_int

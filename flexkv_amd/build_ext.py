@@ -18,7 +18,8 @@ import sysconfig
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SOURCES = [os.path.join(HERE, "csrc", f)
-           for f in ("kv_transfer.hip", "kv_host.cpp", "kv_sdma.cpp", "kv_ssd.cpp")]
+           for f in ("kv_transfer.hip", "kv_host.cpp", "kv_sdma.cpp", "kv_ssd.cpp",
+                     "kv_tp_group.cpp")]
 OUT = os.path.join(HERE, "libflexkv_hip.so")
 CEILING_SOURCE = os.path.join(HERE, "csrc", "hbm_ceiling.hip")
 CEILING_OUT = os.path.join(HERE, "hbm_ceiling")

@@ -17,7 +17,7 @@ __all__ = ["transfer_kv_blocks", "transfer_kv_blocks_kv_ptrs", "gather_kv_blocks
            "scatter_kv_blocks",
            "transfer_kv_blocks_layerwise", "LayerwiseTransfer", "transfer_stream",
            "release_transfer_stream", "set_copy_engine_policy", "copy_engine_policy",
-           "SSDIOCTX", "transfer_kv_blocks_ssd"]
+           "TPTransferThreadGroup", "SSDIOCTX", "transfer_kv_blocks_ssd"]
 
 
 _device_visible = None
@@ -371,6 +371,86 @@ def release_transfer_stream(stream: torch.cuda.ExternalStream) -> None:
         return                      # the library's finalize destroyed it already
     stream.synchronize()
     _lib.check(_lib.load().fkv_stream_destroy(stream.cuda_stream), "fkv_stream_destroy")
+
+
+class TPTransferThreadGroup:
+    """flexkv.c_ext.TPTransferThreadGroup (csrc/bindings.cpp:144-158,
+    csrc/tp_transfer_thread_group.h:30-57) over fkv_tp_group_*: the
+    ``num_gpus`` ranks of data-parallel group ``dp_group_id``, each with its
+    per-layer cache tensors ``gpu_blocks[rank]`` (its head slice of every
+    block), sharing the host cache ``cpu_blocks``.  Rank r's device is the one
+    its tensors live on (the reference computes dp_group_id * num_gpus + r),
+    so ranks may share a GPU.  The library keeps one thread and one stream per
+    rank until close()."""
+
+    def __init__(self, num_gpus: int, gpu_blocks, cpu_blocks: torch.Tensor,
+                 dp_group_id: int) -> None:
+        import ctypes
+
+        self._h = None
+        self._gen = _lib.generation
+        if num_gpus < 1 or len(gpu_blocks) != num_gpus:
+            raise ValueError(f"gpu_blocks needs one layer list per rank ({num_gpus})")
+        num_layers = len(gpu_blocks[0])
+        if num_layers == 0 or any(len(b) != num_layers for b in gpu_blocks):
+            raise ValueError("every rank needs the same, non-zero number of layers")
+        for r, blocks in enumerate(gpu_blocks):
+            dev = blocks[0].device
+            if dev.type != "cuda" or any(t.device != dev for t in blocks):
+                raise ValueError(f"rank {r}: every layer tensor must be on one GPU")
+        devices = (ctypes.c_int * num_gpus)(*[b[0].device.index for b in gpu_blocks])
+        ptrs = (ctypes.c_void_p * (num_gpus * num_layers))(
+            *[t.data_ptr() for b in gpu_blocks for t in b])
+        out = ctypes.c_void_p()
+        rc = _lib.load().fkv_tp_group_create(num_gpus, devices, ptrs, num_layers,
+                                             cpu_blocks.data_ptr(), ctypes.byref(out))
+        if rc != 0:
+            raise RuntimeError(_lib.last_error() or "fkv_tp_group_create failed")
+        self._h = out.value
+        # the tensors must outlive the group's pointers to them
+        self._keep = (list(map(list, gpu_blocks)), cpu_blocks)
+        self.num_gpus = num_gpus
+        self.num_layers = num_layers
+        self.dp_group_id = dp_group_id
+
+    def tp_group_transfer(self, gpu_block_id_tensor: torch.Tensor, gpu_kv_stride_in_bytes: int,
+                          gpu_block_stride_in_bytes: int, gpu_chunk_size_in_bytes: int,
+                          cpu_block_id_tensor: torch.Tensor, cpu_kv_stride_in_bytes: int,
+                          cpu_layer_stride_in_bytes: int, cpu_block_stride_in_bytes: int,
+                          cpu_chunk_size_in_bytes: int, transfer_sms: int,
+                          is_host_to_device: bool, use_ce_transfer: bool, layer_id: int,
+                          layer_granularity: int, is_mla: bool) -> None:
+        """The reference's arguments (csrc/tp_transfer_thread_group.cpp:48-59);
+        ``cpu_chunk_size_in_bytes`` only sizes the reference's log line.  Raises
+        RuntimeError("tp_group_transfer failed: ...") naming the first failing
+        rank, as the reference does (:107)."""
+        if self._h is None:
+            raise RuntimeError("TP transfer group is closed")
+        _require_int64_host(gpu_block_id_tensor, "gpu_block_id_tensor")
+        _require_int64_host(cpu_block_id_tensor, "cpu_block_id_tensor")
+        n = gpu_block_id_tensor.numel()
+        if cpu_block_id_tensor.numel() != n:
+            raise ValueError("gpu and cpu block id tensors differ in length")
+        rc = _lib.load().fkv_tp_group_transfer(
+            self._h, n, gpu_block_id_tensor.data_ptr(), int(gpu_kv_stride_in_bytes),
+            int(gpu_block_stride_in_bytes), int(gpu_chunk_size_in_bytes),
+            cpu_block_id_tensor.data_ptr(), int(cpu_kv_stride_in_bytes),
+            int(cpu_layer_stride_in_bytes), int(cpu_block_stride_in_bytes), int(transfer_sms),
+            int(bool(is_host_to_device)), int(use_ce_transfer), int(layer_id),
+            int(layer_granularity), int(bool(is_mla)))
+        if rc != 0:
+            raise RuntimeError("tp_group_transfer failed: " + _lib.last_error())
+
+    def close(self) -> None:
+        h, self._h = self._h, None
+        if h and self._gen == _lib.generation:   # else finalize destroyed it already
+            _lib.check(_lib.load().fkv_tp_group_destroy(h), "fkv_tp_group_destroy")
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class SSDIOCTX:

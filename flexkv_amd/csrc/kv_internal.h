@@ -317,6 +317,8 @@ struct DevIdLease {
 // Synchronises and destroys every stream made by fkv_stream_create and not
 // destroyed yet (fkv_finalize).
 int streams_destroy_all();
+// Stops and frees every TP transfer group not yet destroyed (kv_tp_group.cpp).
+int tp_groups_destroy_all();
 // The ids as (gpu_id, cpu_id) pairs.
 void pack_ids_into(const Geometry& g, int64_t* h);
 // Pack ids into a pool buffer held by `lease` as (gpu_id, cpu_id) pairs.

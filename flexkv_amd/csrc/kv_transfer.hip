@@ -2401,6 +2401,8 @@ int fkv_finalize(void) {
       handles.swap(g_handles);
     }
     for (fkv_transfer_handle_s* h : handles) keep(handle_destroy(h));
+    // TP groups: their rank threads and streams
+    keep(tp_groups_destroy_all());
     // 2. streams made by fkv_stream_create (each is synchronised first)
     keep(streams_destroy_all());
     // 3. copy-engine lanes: queued copies, signals, events, staging

@@ -40,7 +40,8 @@ from ..common.debug import flexkv_logger
 from ..common.transfer import TransferOp, TransferOpGraph, TransferType
 from ..storage.allocator import HostCacheSpec, StorageHandle
 from .scheduler import TransferScheduler
-from .worker import CPUSSDDiskTransferWorker, FinishedOpsChannel, GPUCPUTransferWorker
+from .worker import (CPUSSDDiskTransferWorker, FinishedOpsChannel, GPUCPUTransferWorker,
+                     tpGPUCPUTransferWorker)
 
 _GPU_CPU = (TransferType.H2D, TransferType.D2H)
 _CPU_SSD = (TransferType.DISK2H, TransferType.H2DISK)
@@ -54,9 +55,6 @@ class TransferEngine:
                  worker_mode: str = "thread", eager_dispatch: bool = True) -> None:
         if worker_mode not in ("thread", "process"):
             raise ValueError(f"worker_mode must be 'thread' or 'process', got {worker_mode!r}")
-        if model_config.tp_size != 1:
-            raise NotImplementedError("tensor-parallel groups need one worker per GPU group; "
-                                      "this engine drives one GPU per data-parallel group")
         if remote_handle is not None:
             raise NotImplementedError("the remote tier is not provided")
         if ssd_handle is not None and worker_mode != "thread":
@@ -105,18 +103,33 @@ class TransferEngine:
         if self._cpu_handle is None:
             raise ValueError("a CPU storage handle is required")
         cfg = self.cache_config
+        tp = self.model_config.tp_size
         for i in range(self.model_config.dp_size):
-            g = self.gpu_handles[i]
+            # a data-parallel group's ranks are handles [i * tp, (i + 1) * tp)
+            # (transfer_engine.py:105-122)
+            group = self.gpu_handles[i * tp:(i + 1) * tp]
+            g = group[0]
             common = dict(gpu_kv_layout=g.kv_layout, cpu_kv_layout=self._cpu_handle.kv_layout,
-                          dtype=g.dtype, gpu_device_id=g.gpu_device_id if g.gpu_device_id is not None else i,
+                          dtype=g.dtype,
                           use_ce_transfer_h2d=cfg.use_ce_transfer_h2d,
                           use_ce_transfer_d2h=cfg.use_ce_transfer_d2h,
                           transfer_sms_h2d=cfg.transfer_sms_h2d,
                           transfer_sms_d2h=cfg.transfer_sms_d2h)
+            if tp == 1:
+                cls = GPUCPUTransferWorker
+                common["gpu_device_id"] = g.gpu_device_id if g.gpu_device_id is not None else i
+            else:
+                cls = tpGPUCPUTransferWorker
+                common.update(tp_group_size=tp, dp_group_id=i)
+
+            def blocks(thread: bool):
+                lists = [h.get_tensor_list() if thread else h.get_tensor_handle_list()
+                         for h in group]
+                return lists[0] if tp == 1 else lists
             if self.worker_mode == "thread":
                 for kind in (TransferType.H2D, TransferType.D2H):
-                    w = GPUCPUTransferWorker.create_worker_thread(
-                        i, self._events, gpu_blocks=g.get_tensor_list(),
+                    w = cls.create_worker_thread(
+                        i, self._events, gpu_blocks=blocks(True),
                         cpu_blocks=self._cpu_handle.get_tensor(), **common)
                     w.wait_ready(60)
                     self._gpu_workers[("gpucpu", i, kind)] = w
@@ -124,8 +137,8 @@ class TransferEngine:
             else:
                 if self._mp_finished is None:
                     self._mp_finished = FinishedOpsChannel()
-                w = GPUCPUTransferWorker.create_worker(
-                    i, self._mp_finished, gpu_blocks=g.get_tensor_handle_list(),
+                w = cls.create_worker(
+                    i, self._mp_finished, gpu_blocks=blocks(False),
                     cpu_blocks=HostCacheSpec(self._cpu_handle.kv_layout, self._cpu_handle.dtype),
                     **common)
                 if not w.ready_event.wait(120):

@@ -34,8 +34,8 @@ import numpy as np
 import torch
 
 from .. import _lib
-from ..c_ext import (SSDIOCTX, transfer_kv_blocks, transfer_kv_blocks_kv_ptrs,
-                     transfer_kv_blocks_ssd)
+from ..c_ext import (SSDIOCTX, TPTransferThreadGroup, transfer_kv_blocks,
+                     transfer_kv_blocks_kv_ptrs, transfer_kv_blocks_ssd)
 from ..common import trace
 from ..common.debug import flexkv_logger
 from ..common.memory_handle import TensorSharedHandle
@@ -219,9 +219,16 @@ class TransferWorkerBase(ABC):
             cls(worker_id, transfer_conn, finished_ops_queue, *args, **kwargs).serve(ready_event)
 
     def serve(self, ready_event: Any) -> None:
-        """Announce readiness, then run the op loop until stopped."""
+        """Announce readiness, run the op loop until stopped, then release
+        what the worker holds (close)."""
         ready_event.set()
-        self.run()
+        try:
+            self.run()
+        finally:
+            self.close()
+
+    def close(self) -> None:
+        """Release the worker's own resources once its loop has ended."""
 
     @abstractmethod
     def _transfer_impl(self, src_block_ids: np.ndarray, dst_block_ids: np.ndarray,
@@ -513,6 +520,105 @@ class GPUCPUTransferWorker(TransferWorkerBase):
         kv_dim = 1 if self.is_mla else 2
         size = self.chunk_size_in_bytes * granularity * len(transfer_op.src_block_ids) * kv_dim
         self._log_transfer_performance(transfer_op, size, start, end)
+
+
+class tpGPUCPUTransferWorker(TransferWorkerBase):
+    """Moves KV blocks between the GPU caches of one tensor-parallel group
+    and the host cache (worker.py:344-480): ``gpu_blocks[r]`` is rank r's
+    per-layer cache (its head slice), and every op moves the same blocks on
+    all ranks at once through a c_ext.TPTransferThreadGroup, rank r into bytes
+    [r * chunk, (r + 1) * chunk) of each host chunk.  Ranks may share a GPU."""
+
+    def __init__(self, worker_id: int, transfer_conn: Optional[Connection],
+                 finished_ops_queue: Optional[Any],
+                 gpu_blocks: Sequence[Sequence[Union[TensorSharedHandle, torch.Tensor]]],
+                 cpu_blocks: Union[torch.Tensor, HostCacheSpec], gpu_kv_layout: KVCacheLayout,
+                 cpu_kv_layout: KVCacheLayout, dtype: torch.dtype, tp_group_size: int,
+                 dp_group_id: int, use_ce_transfer_h2d: bool = False,
+                 use_ce_transfer_d2h: bool = False, transfer_sms_h2d: int = 8,
+                 transfer_sms_d2h: int = 8) -> None:
+        super().__init__(worker_id, transfer_conn, finished_ops_queue)
+        if len(gpu_blocks) != tp_group_size:
+            raise ValueError(f"gpu_blocks holds {len(gpu_blocks)} ranks, the TP group "
+                             f"{tp_group_size}")
+        if gpu_kv_layout.type != KVCacheLayoutType.LAYERWISE:
+            raise ValueError("Only layerwise layout is supported for GPU")
+        if isinstance(cpu_blocks, HostCacheSpec):
+            cpu_blocks = cpu_blocks.allocate()
+        host_register(cpu_blocks)
+
+        def tensor(h):
+            return h.get_tensor() if isinstance(h, TensorSharedHandle) else h
+
+        self.gpu_blocks = [[tensor(h) for h in rank] for rank in gpu_blocks]
+        self.cpu_tensor = cpu_blocks
+        self.dtype = dtype
+        self.is_mla = gpu_kv_layout.is_mla
+        self.num_gpus = len(self.gpu_blocks)
+        self.tp_group_size = tp_group_size
+        self.dp_group_id = dp_group_id
+        self.num_layers = gpu_kv_layout.num_layer
+        per_layer = gpu_kv_layout.div_layer(self.num_layers)
+        es = dtype.itemsize
+        self.gpu_chunk_size_in_bytes = per_layer.get_chunk_size() * es
+        self.gpu_kv_stride_in_bytes = per_layer.get_kv_stride() * es
+        self.gpu_block_stride_in_bytes = per_layer.get_block_stride() * es
+        self.cpu_chunk_size_in_bytes = cpu_kv_layout.get_chunk_size() * es
+        self.cpu_layer_stride_in_bytes = cpu_kv_layout.get_layer_stride() * es
+        self.cpu_kv_stride_in_bytes = cpu_kv_layout.get_kv_stride() * es
+        self.cpu_block_stride_in_bytes = cpu_kv_layout.get_block_stride() * es
+        width = 1 if self.is_mla else tp_group_size
+        if self.cpu_chunk_size_in_bytes != width * self.gpu_chunk_size_in_bytes:
+            raise ValueError(f"the host chunk ({self.cpu_chunk_size_in_bytes} B) must hold "
+                             f"{width} rank chunk(s) of {self.gpu_chunk_size_in_bytes} B")
+        self.transfer_sms_h2d = transfer_sms_h2d
+        self.transfer_sms_d2h = transfer_sms_d2h
+        self.use_ce_transfer_h2d = use_ce_transfer_h2d
+        self.use_ce_transfer_d2h = use_ce_transfer_d2h
+        if use_ce_transfer_h2d or use_ce_transfer_d2h:
+            for dev in sorted({b[0].device.index for b in self.gpu_blocks}):
+                _lib.prepare(dev)
+        self.tp_transfer_thread_group = TPTransferThreadGroup(
+            self.num_gpus, self.gpu_blocks, cpu_blocks, dp_group_id)
+
+    def _transfer_impl(self, src_block_ids: np.ndarray, dst_block_ids: np.ndarray,
+                       transfer_type: TransferType, layer_id: int, layer_granularity: int,
+                       **kwargs: Any) -> None:
+        assert src_block_ids.dtype == np.int64
+        assert dst_block_ids.dtype == np.int64
+        assert len(src_block_ids) == len(dst_block_ids)
+        if transfer_type == TransferType.H2D:
+            gpu_ids, cpu_ids = dst_block_ids, src_block_ids
+            use_ce, sms = self.use_ce_transfer_h2d, self.transfer_sms_h2d
+        elif transfer_type == TransferType.D2H:
+            gpu_ids, cpu_ids = src_block_ids, dst_block_ids
+            use_ce, sms = self.use_ce_transfer_d2h, self.transfer_sms_d2h
+        else:
+            raise ValueError(f"Invalid transfer type: {transfer_type} for tpGPUCPUTransferWorker")
+        if len(gpu_ids) == 0:
+            return
+        self.tp_transfer_thread_group.tp_group_transfer(
+            torch.from_numpy(np.ascontiguousarray(gpu_ids)), self.gpu_kv_stride_in_bytes,
+            self.gpu_block_stride_in_bytes, self.gpu_chunk_size_in_bytes,
+            torch.from_numpy(np.ascontiguousarray(cpu_ids)), self.cpu_kv_stride_in_bytes,
+            self.cpu_layer_stride_in_bytes, self.cpu_block_stride_in_bytes,
+            self.cpu_chunk_size_in_bytes, sms, transfer_type == TransferType.H2D, use_ce,
+            layer_id, layer_granularity, self.is_mla)
+
+    def launch_transfer(self, transfer_op: WorkerTransferOp) -> None:
+        layer_id = 0 if transfer_op.layer_id == -1 else transfer_op.layer_id
+        granularity = self.num_layers if transfer_op.layer_granularity == -1 \
+            else transfer_op.layer_granularity
+        start = time.time()
+        self._transfer_impl(transfer_op.src_block_ids, transfer_op.dst_block_ids,
+                            transfer_op.transfer_type, layer_id, granularity)
+        end = time.time()
+        kv_dim = 1 if self.is_mla else 2
+        size = self.cpu_chunk_size_in_bytes * granularity * len(transfer_op.src_block_ids) * kv_dim
+        self._log_transfer_performance(transfer_op, size, start, end)
+
+    def close(self) -> None:
+        self.tp_transfer_thread_group.close()
 
 
 class CPUSSDDiskTransferWorker(TransferWorkerBase):

@@ -307,6 +307,46 @@ int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, voi
                                int64_t block_stride_bytes, int is_read, int round_robin,
                                int num_threads_per_device, int is_mla);
 
+/* Tensor-parallel transfer group: the ranks of one data-parallel group, each
+ * holding its own head slice (gpu chunk) of every block, move the same
+ * blocks at once, rank r into or out of bytes [r * gpu_chunk, (r + 1) *
+ * gpu_chunk) of each host chunk.  Replaces flexkv::TPTransferThreadGroup
+ * (csrc/tp_transfer_thread_group.h:30-57, .cpp:23-109).
+ *
+ * fkv_tp_group_create: `devices[r]` is rank r's device (ranks may share one);
+ * `gpu_layer_ptrs` holds num_ranks * num_layers per-layer cache pointers,
+ * [rank][layer], each layer laid out as for fkv_transfer_kv_blocks; the host
+ * cache `cpu_ptr` is shared.  The group keeps one host thread and one stream
+ * per rank until fkv_tp_group_destroy (or fkv_finalize).
+ *
+ * fkv_tp_group_transfer: tp_group_transfer's arguments
+ * (csrc/tp_transfer_thread_group.cpp:48-59) without the host chunk size,
+ * which only sizes the reference's log line.  Every rank makes one
+ * fkv_transfer_kv_blocks call on its own stream, host layers [layer_id,
+ * layer_id + layer_granularity) from rank r's pointers r * num_layers +
+ * layer_id onward, at cpu_startoff_inside_chunks = r * gpu_chunk_size_bytes.
+ * Synchronous: returns when every rank's call has; on failure, the first
+ * failing rank's status and message (fkv_last_error names the rank), and
+ * fkv_last_unsafe_host_blocks gathers every rank's.  Differences from the
+ * reference: rank r's layer pointers start at r * num_layers (the
+ * reference uses r * layer_granularity, which is another rank's table when
+ * the window is not every layer); under MLA (every rank holds the same
+ * latent) device-to-host is moved by rank 0 alone instead of every rank
+ * writing the same bytes, and host-to-device by every rank; devices come
+ * from the caller instead of dp_group_id * num_ranks + r.  One transfer of a
+ * group runs at a time; transfers of different groups may overlap. */
+typedef struct fkv_tp_group_s* fkv_tp_group_t;
+int fkv_tp_group_create(int num_ranks, const int* devices, void* const* gpu_layer_ptrs,
+                        int num_layers, void* cpu_ptr, fkv_tp_group_t* out);
+int fkv_tp_group_transfer(fkv_tp_group_t group, int num_blocks, const int64_t* gpu_block_ids,
+                          int64_t gpu_kv_stride_bytes, int64_t gpu_block_stride_bytes,
+                          int64_t gpu_chunk_size_bytes, const int64_t* cpu_block_ids,
+                          int64_t cpu_kv_stride_bytes, int64_t cpu_layer_stride_bytes,
+                          int64_t cpu_block_stride_bytes, int transfer_cus,
+                          int is_host_to_device, int use_ce_transfer, int layer_id,
+                          int layer_granularity, int is_mla);
+int fkv_tp_group_destroy(fkv_tp_group_t group);
+
 /* How copy-engine mode (use_ce_transfer = FKV_XFER_CE) chooses between the
  * SDMA engines and the zero-copy kernel, process-wide.  No counterpart in
  * the reference, whose CE mode always copies on the engines.

@@ -109,6 +109,34 @@ def transfer_kv_blocks(gpu_block_ids, gpu_layers: Sequence, gpu_kv_stride_in_byt
         raise ValueError(f"oracle rejected arguments (rc={rc})")
 
 
+def tp_group_transfer(rank_layers: Sequence[Sequence], gpu_block_ids,
+                      gpu_kv_stride_in_bytes: int, gpu_block_stride_in_bytes: int,
+                      gpu_chunk_size_in_bytes: int, cpu_block_ids, cpu_buffer,
+                      cpu_kv_stride_in_bytes: int, cpu_layer_stride_in_bytes: int,
+                      cpu_block_stride_in_bytes: int, is_host_to_device: bool,
+                      layer_id: int, layer_granularity: int, is_mla: bool = False) -> None:
+    """Oracle of a tensor-parallel group transfer, in place: rank r (its
+    per-layer host buffers ``rank_layers[r]``, all layers) moves host layers
+    [layer_id, layer_id + layer_granularity) from its own layers of that
+    window, at byte offset r * gpu_chunk inside each host chunk, as each
+    thread of csrc/tp_transfer_thread_group.cpp:66-99 calls transfer_kv_blocks
+    (startoff :79-80).  Rank r's window is rank_layers[r][layer_id:...]; the
+    reference's pointer arithmetic (:76-77) differs from that when the window
+    is not every layer, which the product does not follow.  Under MLA every
+    rank holds the same latent: device-to-host is rank 0's move (the
+    reference has every rank write the same bytes at offset 0), host-to-device
+    is every rank's."""
+    for r, layers in enumerate(rank_layers):
+        if is_mla and not is_host_to_device and r != 0:
+            continue
+        transfer_kv_blocks(gpu_block_ids, list(layers[layer_id:layer_id + layer_granularity]),
+                           gpu_kv_stride_in_bytes, gpu_block_stride_in_bytes, cpu_block_ids,
+                           cpu_buffer, cpu_kv_stride_in_bytes, cpu_layer_stride_in_bytes,
+                           cpu_block_stride_in_bytes, gpu_chunk_size_in_bytes, layer_id,
+                           is_host_to_device, use_ce_transfer=True, is_mla=is_mla,
+                           cpu_startoff_inside_chunks=0 if is_mla else r * gpu_chunk_size_in_bytes)
+
+
 def transfer_kv_blocks_ssd(files: Sequence, num_devices: int, files_per_device: int,
                            start_layer: int, num_layers: int, cpu_buffer, ssd_block_ids,
                            cpu_block_ids, cpu_layer_stride: int, cpu_kv_stride: int,

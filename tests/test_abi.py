@@ -143,3 +143,23 @@ def test_copy_engine_policy_setter_needs_no_device(monkeypatch):
         assert (mb.value, rc.value) == (7 << 20, 0)
     finally:
         c_ext.set_copy_engine_policy(min_bytes="unset", layerwise_scattered="unset")
+
+
+def test_tp_group_host_side_rejections_need_no_device():
+    """fkv_tp_group_create / _transfer / _destroy refuse bad arguments with a
+    message before any device work, and a null group is a no-op to destroy."""
+    lib = _lib.load()
+    out = ctypes.c_void_p()
+    devs = (ctypes.c_int * 2)(0, 0)
+    ptrs = (ctypes.c_void_p * 4)(16, 32, 48, 64)
+    assert lib.fkv_tp_group_create(0, devs, ptrs, 2, ctypes.c_void_p(64), ctypes.byref(out)) == 1
+    assert "ranks" in _lib.last_error()
+    assert lib.fkv_tp_group_create(2, None, ptrs, 2, ctypes.c_void_p(64), ctypes.byref(out)) == 1
+    assert "null" in _lib.last_error()
+    assert lib.fkv_tp_group_create(2, devs, ptrs, 2, ctypes.c_void_p(64), None) == 1
+    assert out.value is None
+    ids = np.zeros(1, dtype=np.int64)
+    rc = lib.fkv_tp_group_transfer(None, 1, ids.ctypes.data, 0, 0, 16, ids.ctypes.data, 0, 0, 0,
+                                   -1, 0, 0, 0, 1, 0)
+    assert rc == 1 and "null TP group" in _lib.last_error()
+    assert lib.fkv_tp_group_destroy(None) == 0

@@ -220,3 +220,80 @@ def test_config0_digests():
     back = run_h2d(case, gids, cids)
     assert hashlib.sha256(b"".join(g.tobytes() for g in back)).hexdigest() == \
         want["h2d_gpu_sha256"]
+
+
+def _tp_case(tp, layout, mla, seed, L=4, ng=6, nh=9, tokens=2, hpr=1, dim=4):
+    """Tiny tensor-parallel case: rank r's per-layer caches [kv, ng, chunk]
+    (uint16), a host cache whose chunk holds the tp ranks' chunks side by
+    side ([tp][chunk], one chunk under MLA), and its byte strides."""
+    rng = np.random.default_rng(seed)
+    kv = 1 if mla else 2
+    ce = tokens * hpr * dim
+    width = 1 if mla else tp
+    ranks = [[rng.integers(0, 65535, size=(kv, ng, ce), dtype=np.uint16) for _ in range(L)]
+             for _ in range(tp)]
+    if layout == "BLOCKWISE":
+        host = np.zeros((nh, L, kv, width, ce), np.uint16)
+        view = host
+        cblk, clay, ckv = L * kv * width * ce * 2, kv * width * ce * 2, width * ce * 2
+    else:
+        host = np.zeros((L, kv, nh, width, ce), np.uint16)
+        view = host.transpose(2, 0, 1, 3, 4)          # [nh, L, kv, width, ce]
+        cblk, clay, ckv = width * ce * 2, kv * nh * width * ce * 2, nh * width * ce * 2
+    strides = dict(gpu_kv_stride_in_bytes=ng * ce * 2, gpu_block_stride_in_bytes=ce * 2,
+                   gpu_chunk_size_in_bytes=ce * 2, cpu_kv_stride_in_bytes=ckv,
+                   cpu_layer_stride_in_bytes=clay, cpu_block_stride_in_bytes=cblk)
+    return ranks, host, view, strides
+
+
+@pytest.mark.parametrize("layout", ["BLOCKWISE", "LAYERWISE"])
+@pytest.mark.parametrize("tp,mla", [(2, False), (3, False), (4, True)])
+def test_tp_group_oracle_against_indexing(layout, tp, mla):
+    """oracle.tp_group_transfer pinned by numpy indexing: after a D2H of a
+    layer window, host chunk slot r of block cids[i], layer l, half k holds
+    rank r's chunk gids[i] of that layer and half (under MLA, rank 0's in the
+    one slot); every other host byte stays zero.  After an H2D into zeroed
+    rank caches, each rank holds its slot (under MLA, every rank the one
+    slot) in the window's layers and nothing else.  A planted mistake (every
+    rank at offset 0) breaks the D2H check."""
+    ranks, host, view, st = _tp_case(tp, layout, mla, seed=tp * 7 + mla)
+    gids = np.array([4, 0, 5], np.int64)
+    cids = np.array([2, 8, 5], np.int64)
+    lid, gran = 1, 2
+    oracle.tp_group_transfer(ranks, gids, st["gpu_kv_stride_in_bytes"],
+                             st["gpu_block_stride_in_bytes"], st["gpu_chunk_size_in_bytes"],
+                             cids, host, st["cpu_kv_stride_in_bytes"],
+                             st["cpu_layer_stride_in_bytes"], st["cpu_block_stride_in_bytes"],
+                             False, lid, gran, mla)
+    want = np.zeros_like(view)
+    for r in range(1 if mla else tp):
+        for l in range(lid, lid + gran):
+            want[cids, l, :, r] = ranks[r][l][:, gids].transpose(1, 0, 2)
+    assert np.array_equal(view, want)
+    # planted: every rank at offset 0
+    bad = np.zeros_like(host)
+    for r, layers in enumerate(ranks):
+        oracle.transfer_kv_blocks(gids, layers[lid:lid + gran], st["gpu_kv_stride_in_bytes"],
+                                  st["gpu_block_stride_in_bytes"], cids, bad,
+                                  st["cpu_kv_stride_in_bytes"], st["cpu_layer_stride_in_bytes"],
+                                  st["cpu_block_stride_in_bytes"], st["gpu_chunk_size_in_bytes"],
+                                  lid, False, True, mla)
+    bad_view = bad if layout == "BLOCKWISE" else bad.transpose(2, 0, 1, 3, 4)
+    if not mla:
+        assert not np.array_equal(bad_view, want)
+    # H2D from a filled host cache into zeroed rank caches
+    rng = np.random.default_rng(5)
+    host[...] = rng.integers(0, 65535, size=host.shape, dtype=np.uint16)
+    dst = [[np.zeros_like(a) for a in layers] for layers in ranks]
+    oracle.tp_group_transfer(dst, gids, st["gpu_kv_stride_in_bytes"],
+                             st["gpu_block_stride_in_bytes"], st["gpu_chunk_size_in_bytes"],
+                             cids, host, st["cpu_kv_stride_in_bytes"],
+                             st["cpu_layer_stride_in_bytes"], st["cpu_block_stride_in_bytes"],
+                             True, lid, gran, mla)
+    for r in range(tp):
+        slot = 0 if mla else r
+        for l in range(len(ranks[r])):
+            exp = np.zeros_like(ranks[r][l])
+            if lid <= l < lid + gran:
+                exp[:, gids] = view[cids, l, :, slot].transpose(1, 0, 2)
+            assert np.array_equal(dst[r][l], exp), (r, l)
