@@ -1380,11 +1380,107 @@ def configs_on_step(args, wl: Workload, peaks: dict, result: dict) -> dict:
     return cfg
 
 
+def tp_group(peaks: dict, reps: int = 3, tp: int = 8, seed: int = 1003) -> dict:
+    """The Llama-3-70B TP-8 shard's whole tensor-parallel group on this one
+    GPU: eight ranks, each with its own K/V [8192,16,1,128] bf16 per layer
+    (one KV head, 80 layers), sharing a pinned block-wise host cache whose
+    chunk holds the eight ranks' chunks side by side ([4096,80,2,16,8,128]).
+    One group transfer moves 2048 random blocks on every rank (10 GiB)
+    through c_ext.TPTransferThreadGroup (a thread and a stream per rank, rank
+    r at byte offset r * 4 KiB of each 32 KiB host chunk).  The ranks share
+    this GPU's host link, which bounds the aggregate; across GPUs each rank
+    has a link of its own.  Also: the same bytes as eight one-rank calls in
+    turn (fkv_transfer_kv_blocks with the rank's offset), a round trip
+    checked bit for bit, and 16 host blocks checked slot by slot."""
+    import ctypes
+    import gc
+    from flexkv_amd import _lib, c_ext
+    from flexkv_amd.common.storage import KVCacheLayout, KVCacheLayoutType
+    from flexkv_amd.storage.allocator import CPUAllocator
+    L, ng, nh, n, tokens, dim = 80, 8192, 4096, 2048, 16, 128
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    ranks = []
+    for _ in range(tp):
+        layers = []
+        for _ in range(L):
+            t = torch.empty((2, ng, tokens, 1, dim), dtype=torch.bfloat16, device=dev)
+            t.normal_(generator=gen)
+            layers.append(t)
+        ranks.append(layers)
+    cl = KVCacheLayout(KVCacheLayoutType.BLOCKWISE, L, nh, tokens, tp, dim)
+    host = CPUAllocator.allocate(cl, torch.bfloat16).get_tensor()
+    cpu_gen = torch.Generator().manual_seed(seed + 1)
+    gids = torch.randperm(ng, generator=cpu_gen)[:n].to(torch.int64)
+    cids = torch.randperm(nh, generator=cpu_gen)[:n].to(torch.int64)
+    chunk = tokens * dim * 2
+    gkv, gblk = ng * chunk, chunk
+    _, ckv, clay, cblk = cl.byte_strides(torch.bfloat16)
+    nbytes = tp * n * L * 2 * chunk
+    out = {"workload": f"Llama-3-70B at TP = 8 on one GPU: {tp} ranks x 80 layers, K/V "
+                       f"[8192,16,1,128] bf16 each <-> pinned host [4096,80,2,16,8,128]; "
+                       f"2048 random distinct ids on every rank",
+           "ranks": tp, "bytes_per_op": nbytes}
+    grp = c_ext.TPTransferThreadGroup(tp, ranks, host, 0)
+    lib = _lib.load()
+    try:
+        def group_move(h2d):
+            grp.tp_group_transfer(gids, gkv, gblk, chunk, cids, ckv, clay, cblk, tp * chunk, -1,
+                                  h2d, False, 0, L, False)
+
+        ptr_tables = [(ctypes.c_void_p * L)(*[t.data_ptr() for t in r]) for r in ranks]
+
+        def ranks_in_turn(h2d):
+            st = torch.cuda.current_stream().cuda_stream
+            for r in range(tp):
+                _lib.check(lib.fkv_transfer_kv_blocks(
+                    n, 0, L, gids.data_ptr(), ptr_tables[r], gkv, gblk, cids.data_ptr(),
+                    host.data_ptr(), ckv, clay, cblk, r * chunk, chunk, st, -1, int(h2d), 0, 0),
+                    "fkv_transfer_kv_blocks")
+        for name, fn in (("group", group_move), ("ranks_in_turn", ranks_in_turn)):
+            for h2d in (False, True):
+                d = "h2d" if h2d else "d2h"
+                s, _, _ = time_steps(lambda: fn(h2d), reps, 1)
+                out[f"{name}_{d}_gbps"] = round(nbytes / s / 1e9, 2)
+                if name == "group":
+                    out[f"group_{d}_frac_link"] = round(nbytes / s / 1e9 / peaks[d], 4)
+        # round trip: D2H, rank blocks zeroed in place, H2D, compared
+        g = gids.to(dev)
+        group_move(False)
+        torch.cuda.synchronize()
+        rows = host.view(nh, L, 2, tp, chunk // 2)
+        sample = torch.arange(16)
+        ok = True
+        for r in range(tp):
+            for l in range(0, L, 7):
+                want = ranks[r][l][:, g[sample]].reshape(2, 16, -1).transpose(0, 1).cpu()
+                ok &= bool(torch.equal(rows[cids[sample], l, :, r].view(torch.int16),
+                                       want.reshape(16, 2, -1).view(torch.int16)))
+        saved = [[t.index_select(1, g) for t in r] for r in ranks]
+        for r in ranks:
+            for t in r:
+                t.index_fill_(1, g, 0)
+        torch.cuda.synchronize()    # the ranks run on streams of their own
+        group_move(True)
+        torch.cuda.synchronize()
+        ok &= all(torch.equal(t.index_select(1, g), s)
+                  for r, sr in zip(ranks, saved) for t, s in zip(r, sr))
+        out["bit_exact"] = ok
+        del saved
+    finally:
+        grp.close()
+        del ranks, host
+        gc.collect()
+        release_device_memory()
+    return out
+
+
 def other_configs(args, peaks: dict, cfg: dict) -> dict:
     """The configurations with tensors of their own, each allocated and freed
     in turn: the CPU plumbing shape, Llama-3-8B on a layer-wise host cache,
     the Llama-3-70B TP-8 shard and the DeepSeek-V3 MLA latent cache with its
-    request mix.  Every entry of the benchmark set (with configs_on_step's)
+    request mix, and the 70B shard's whole eight-rank tensor-parallel group
+    sharing this GPU (tp_group).  Every entry of the benchmark set (with configs_on_step's)
     gives GB/s on both paths with fractions of the measured link and of
     nominal PCIe Gen5 x16, the copy-engine path's gather/scatter piece rates,
     the device gather/scatter in one launch, and a bit-exact round trip."""
@@ -1396,6 +1492,8 @@ def other_configs(args, peaks: dict, cfg: dict) -> dict:
                                     ("cfg4_mla-dsv3", "mla-dsv3", "BLOCKWISE", False)):
         cfg[key] = other_workload(name, args, peaks, layout, rect)
         log(f"{key}: {cfg[key]}")
+    cfg["cfg3_llama3-70b-tp8_group"] = tp_group(peaks)
+    log(f"cfg3_llama3-70b-tp8_group: {cfg['cfg3_llama3-70b-tp8_group']}")
     cfg["bit_exact"] = all(v.get("bit_exact", True) for v in cfg.values()
                            if isinstance(v, dict)) and all(
         r["bit_exact"] for r in cfg["cfg2_llama3-8b_fragmentation"].values())
@@ -1419,6 +1517,9 @@ def main() -> int:
     ap.add_argument("--layerwise-only", action="store_true",
                     help="run only the layer-wise H2D section (sync per layer, async handle, "
                          "overlap with per-layer GEMMs) and print its JSON (for profiling runs)")
+    ap.add_argument("--tp-group-only", action="store_true",
+                    help="run only the eight-rank tensor-parallel group section (the Llama-3-70B "
+                         "TP-8 shard's whole group on this GPU) and print its JSON")
     ap.add_argument("--duplex-only", action="store_true",
                     help="run only the both-directions-at-once section and print its JSON")
     ap.add_argument("--worker-ops", action="store_true",
@@ -1468,6 +1569,9 @@ def main() -> int:
     if args.worker_ops:
         print(json.dumps({"worker_ops": worker_ops(wl, reps=max(5, args.steps),
                                                    process=not args.quick)}), flush=True)
+        return 0
+    if args.tp_group_only:
+        print(json.dumps({"tp_group": tp_group(link_peaks(wl))}), flush=True)
         return 0
     if args.duplex_only:
         print(json.dumps({"duplex": duplex(wl, reps=max(3, args.steps))}), flush=True)

@@ -151,6 +151,15 @@ def table(p: dict, label: str) -> str:
               f"{mla['ce']['h2d_per_request_gbps']} GB/s, batched "
               f"{mla['ce']['d2h_batched_gbps']} / {mla['ce']['h2d_batched_gbps']} GB/s "
               f"(D2H / H2D)."]
+    tpg = p.get("configs", {}).get("cfg3_llama3-70b-tp8_group")
+    if tpg:
+        L += ["", f"Llama-3-70B TP-8 group on this GPU ({tpg['ranks']} ranks sharing its link, "
+              f"{tpg['bytes_per_op'] / 2**30:.0f} GiB per op, zero-copy kernel): group "
+              f"{tpg['group_d2h_gbps']} / {tpg['group_h2d_gbps']} GB/s "
+              f"({tpg['group_d2h_frac_link']} / {tpg['group_h2d_frac_link']} of the link), "
+              f"the ranks' calls in turn {tpg['ranks_in_turn_d2h_gbps']} / "
+              f"{tpg['ranks_in_turn_h2d_gbps']} GB/s (D2H / H2D); bit-exact "
+              f"{'yes' if tpg.get('bit_exact') else 'no'}."]
     L += ["", "## Beside compute", "",
           "160 bf16 GEMMs [8192x4096]x[4096x4096] beside one 2 GiB transfer, against the same",
           "GEMMs alone started the same way.", "",

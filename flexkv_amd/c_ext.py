@@ -381,7 +381,11 @@ class TPTransferThreadGroup:
     block), sharing the host cache ``cpu_blocks``.  Rank r's device is the one
     its tensors live on (the reference computes dp_group_id * num_gpus + r),
     so ranks may share a GPU.  The library keeps one thread and one stream per
-    rank until close()."""
+    rank until close().  Transfers run on those streams, not the current
+    torch stream: work the caller queued on other streams must have finished
+    (torch.cuda.synchronize()) before a transfer that reads or writes the
+    same memory, as with the reference's own streams
+    (csrc/tp_transfer_thread_group.cpp:39-43)."""
 
     def __init__(self, num_gpus: int, gpu_blocks, cpu_blocks: torch.Tensor,
                  dp_group_id: int) -> None:

@@ -334,7 +334,9 @@ int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, voi
  * latent) device-to-host is moved by rank 0 alone instead of every rank
  * writing the same bytes, and host-to-device by every rank; devices come
  * from the caller instead of dp_group_id * num_ranks + r.  One transfer of a
- * group runs at a time; transfers of different groups may overlap. */
+ * group runs at a time; transfers of different groups may overlap.  Each
+ * rank runs on the group's own stream, so work the caller queued elsewhere on
+ * the same memory must be finished first. */
 typedef struct fkv_tp_group_s* fkv_tp_group_t;
 int fkv_tp_group_create(int num_ranks, const int* devices, void* const* gpu_layer_ptrs,
                         int num_layers, void* cpu_ptr, fkv_tp_group_t* out);
