@@ -52,9 +52,11 @@ def test_finalize_then_library_works_again():
     stream = c_ext.transfer_stream()
     with torch.cuda.stream(stream):
         hnd = _layerwise(dc, gids, cids)                       # left unreleased
+    group = c_ext.TPTransferThreadGroup(2, [dc.gpu, dc.gpu], dc.host, 0)   # left open
     _lib.finalize()
     hnd.release()                                               # already released: no call
     c_ext.release_transfer_stream(stream)                       # already destroyed: no call
+    group.close()                                               # already destroyed: no call
     assert np.array_equal(dc.host_np(), _d2h_expected(case, gids, cids))
     # everything is made again on demand
     dc.set_host(case.host)
@@ -92,7 +94,9 @@ with torch.cuda.stream(stream):
     keep = c_ext.transfer_kv_blocks_layerwise(
         torch.from_numpy(gids), ptrs, s["gpu_kv"], s["gpu_block"], torch.from_numpy(cids),
         dc.host, s["cpu_kv"], s["cpu_layer"], s["cpu_block"], s["chunk"], 0, 1, -1, True)
-print("child: exiting with a stream, a handle and copy-engine state alive", flush=True)
+group = c_ext.TPTransferThreadGroup(2, [dc.gpu, dc.gpu], dc.host, 0)
+print("child: exiting with a stream, a handle, a TP group and copy-engine state alive",
+      flush=True)
 """
 
 
