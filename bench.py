@@ -281,7 +281,24 @@ def link_peaks(wl: Workload, reps: int = 8):
         b.synchronize()
         best = max(best, 2 * big.numel() / (a.elapsed_time(b) * 1e-3) / 1e9)
     res["d2d_copy_read_plus_write"] = best
-    del big, big2, dbuf
+    del big, big2
+    # both directions at once: a 1 GiB D2H and a 1 GiB H2D of other memory
+    # on two streams, started together; bytes of both over the wall time
+    host2 = wl.host.view(torch.uint8)[nbytes:2 * nbytes]
+    dbuf2 = torch.empty(nbytes, dtype=torch.uint8, device=wl.dev)
+    streams = (torch.cuda.Stream(), torch.cuda.Stream())
+    best = 0.0
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with torch.cuda.stream(streams[0]):
+            host.copy_(dbuf, non_blocking=True)
+        with torch.cuda.stream(streams[1]):
+            dbuf2.copy_(host2, non_blocking=True)
+        torch.cuda.synchronize()
+        best = max(best, 2 * nbytes / (time.perf_counter() - t0) / 1e9)
+    res["duplex"] = best
+    del dbuf, dbuf2
     release_device_memory()
     return res
 
@@ -717,7 +734,9 @@ def duplex(wl: Workload, reps: int = 3):
     free_c = torch.tensor(sorted(set(range(w["nh"])) - set(wl.cids.tolist())), dtype=torch.int64)
     g2 = free_g[torch.randperm(len(free_g), generator=g)[:n]].pin_memory()
     c2 = free_c[torch.randperm(len(free_c), generator=g)[:n]].pin_memory()
-    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    # streams on hardware queues of their own: two ordinary streams can share
+    # one of the process's queues, and then the two zero-copy kernels run in turn
+    streams = [c_ext.transfer_stream(), c_ext.transfer_stream()]
     out = {}
     for name, ce in (("kernel", False), ("ce", True)):
         best = None
@@ -753,6 +772,8 @@ def duplex(wl: Workload, reps: int = 3):
         out[f"{name}_aggregate_gbps"] = round(best[0], 3)
         out[f"{name}_d2h_gbps"] = round(best[1], 2)
         out[f"{name}_h2d_gbps"] = round(best[2], 2)
+    for st in streams:
+        c_ext.release_transfer_stream(st)
     out["what"] = ("one D2H and one H2D of 2 GiB each at once, two threads and streams; "
                    "aggregate: bytes of both over the wall time; per direction: its bytes "
                    "over its own call time (best run by aggregate)")
@@ -1574,7 +1595,11 @@ def main() -> int:
         print(json.dumps({"tp_group": tp_group(link_peaks(wl))}), flush=True)
         return 0
     if args.duplex_only:
-        print(json.dumps({"duplex": duplex(wl, reps=max(3, args.steps))}), flush=True)
+        pk = link_peaks(wl)
+        d = duplex(wl, reps=max(3, args.steps))
+        d["duplex_peak_gbps_measured"] = round(pk["duplex"], 2)
+        d["one_way_peaks_gbps"] = [round(pk["d2h"], 2), round(pk["h2d"], 2)]
+        print(json.dumps({"duplex": d}), flush=True)
         return 0
     if args.overlap_only:
         layerwise = args.host_layout == "LAYERWISE"
@@ -1712,8 +1737,11 @@ def main() -> int:
             **({} if default_ce else
                {"d2h_kernel_frac": round((gb / (z_ms * 1e-3)) / peaks["d2h"], 4)}),
             "d2d_copy_gbps_measured": round(peaks["d2d_copy_read_plus_write"], 1),
+            "duplex_peak_gbps_measured": round(peaks["duplex"], 2),
             "how": "best of 8 hipMemcpyAsync over 1 GiB contiguous pinned host memory per "
-                   "direction; D2D = 4 GiB device copy counted read+write",
+                   "direction; duplex = a 1 GiB D2H and a 1 GiB H2D on two streams at once, "
+                   "both directions' bytes over the wall time; D2D = 4 GiB device copy "
+                   "counted read+write",
         }
         paths = {}
         for name, h2d, ce, cus in (("d2h_kernel", False, False, -1), ("d2h_ce", False, True, -1),
@@ -1746,6 +1774,9 @@ def main() -> int:
         result["overlap_with_compute"] = overlap_with_compute(wl)
         log(f"overlap with compute: {result['overlap_with_compute']}")
         result["duplex"] = duplex(wl)
+        for name in ("ce", "kernel"):
+            result["duplex"][f"{name}_frac_duplex_peak"] = round(
+                result["duplex"][f"{name}_aggregate_gbps"] / peaks["duplex"], 4)
         log(f"duplex: {result['duplex']}")
         if wl.mla:
             result["request_batch"] = request_batch(wl, args.steps)

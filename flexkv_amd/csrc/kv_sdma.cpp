@@ -28,6 +28,15 @@ namespace {
 // (16 engines) with 2 MiB copies: four move 56-57 GB/s either way, and
 // device-to-host drops to 47 GB/s on eight.  While both directions run they
 // take the duplex split instead (kDefaultDuplexD2HEngines).
+//
+// Engines 0-3 are the fast ones across the host link.  One 1 GiB copy on
+// one engine (MI355X, HSA copies pinned to the engine): engines 0-3 move
+// 56.9 GB/s device-to-host and 57.4 host-to-device, engines 4-7 12.8 and
+// 51.0.  Host-to-device copies on four engines: 640 KiB copies 57.0 GB/s on
+// 0-3, 47.3 on 4-7; 2 MiB copies 56.8 / 56.5.  Copies on engines 4-7 also
+// slow a scatter kernel beside them more (Llama-3-8B, 512 MiB scatter
+// pieces: 0.605 of HBM peak beside engines 4-7, 0.625 beside 0-3).  So both
+// directions' one-way sets are engines 0-3.
 constexpr int kDefaultSdmaEngines[2] = {4, 4};   // [D2H, H2D]
 // Engines 0-7.  Host-to-device copies on engines 8-15 slow compute kernels
 // running beside them about twice over, at any copy size: 160 bf16 GEMMs
@@ -38,16 +47,18 @@ constexpr uint32_t kComputeFriendlyEngines = 0xFFu;
 // The wide engine set (FLEXKV_SDMA_ENGINES_WIDE): host-to-device copies bound
 // by the engines' per-copy cost spread over it, those of the copy-engine
 // layer-wise pipeline (one block's layer window, 64-256 KiB at Llama-3-8B)
-// and synchronous ones shorter than 1 MiB on average; taken from engines
-// 0-7, host-to-device's own first.
+// and synchronous ones shorter than kWideCopyBytes on average; engines 0-3
+// first, then 4-7 (256 KiB copies: 56.1 GB/s on engines 0-5, 51.7 on 0-3,
+// 50.7 on 4-7 with 0-1).
 constexpr int kDefaultWideEngines = 8;
 // Synchronous host-to-device transfers whose copies are short spread over the
 // first kSyncWideEngines of the wide set instead (FLEXKV_SDMA_ENGINES_WIDE_SYNC).
 // Their scatter kernels run while the next piece's copies are in flight, and
-// the engines' traffic slows them.  Measured on MI355X at the Llama-3-70B
-// TP-8 shard (640 KiB copies), 8 / 6 / 4 engines: H2D 56.4 / 56.6 / 52.7
-// GB/s, scatter pieces 4.26 / 4.65 / 4.90 TB/s.  The layer-wise pipeline
-// keeps all 8: its one-window copies need them (50.6 against 45.6 GB/s on 6).
+// the engines' traffic slows them: measured on MI355X with 640 KiB copies
+// over 8 / 6 / 4 engines (4-7 first): scatter pieces 4.26 / 4.65 / 4.90 TB/s.
+// The engines beyond the first four hold back while a scatter runs
+// (SdmaHold).  The layer-wise pipeline keeps all 8: its one-window copies
+// need them (50.6 against 45.6 GB/s on 6).
 constexpr int kSyncWideEngines = 6;
 // The duplex split (FLEXKV_SDMA_DUPLEX_D2H; 0 turns it off): while a
 // transfer of the other direction is in flight, device-to-host copies take
@@ -390,47 +401,36 @@ int ensure_sdma(DeviceState& d, int dev, const void* hip_ptr) {
   if (g_hsa.agent_get_info(q.gpu, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_NEAREST_CPU),
                            &nearest) == HSA_STATUS_SUCCESS && nearest.handle != 0)
     q.cpu = nearest;
-  // Each direction takes `want` engines, from engines 0-7 first;
-  // host-to-device takes those device-to-host did not take before those it
-  // did, so with the default four the two directions' one-way sets are
-  // disjoint (engines 0-3 and 4-7, 56-57 GB/s one way).
+  // Each direction takes `want` engines, from engines 0-7 first, so with the
+  // default four both directions' one-way sets are engines 0-3, the fast
+  // ones (kDefaultSdmaEngines).  While both directions have transfers in
+  // flight they take the duplex split.
   if (sdma_engines_wanted(0) == 0 || sdma_engines_wanted(1) == 0)
     return fail(kInval, "copy engines turned off (FLEXKV_SDMA_ENGINES=0)");
-  uint32_t taken = 0;
   for (int dir = 0; dir < 2; ++dir) {
     const int want = sdma_engines_wanted(dir);
     uint32_t mask = 0;
     FKV_HSA(dir == 0 ? g_hsa.copy_engine_status(q.cpu, q.gpu, &mask)
                      : g_hsa.copy_engine_status(q.gpu, q.cpu, &mask));
     d.engines[dir].clear();
-    const uint32_t tiers[3] = {mask & kComputeFriendlyEngines & ~taken,
-                               mask & kComputeFriendlyEngines & taken,
-                               mask & ~kComputeFriendlyEngines};
+    const uint32_t tiers[2] = {mask & kComputeFriendlyEngines, mask & ~kComputeFriendlyEngines};
     for (uint32_t tier : tiers)
       for (int b = 0; b < 32 && static_cast<int>(d.engines[dir].size()) < want; ++b)
-        if (tier & (1u << b)) {
-          d.engines[dir].push_back(static_cast<hsa_amd_sdma_engine_id_t>(1u << b));
-          taken |= 1u << b;
-        }
+        if (tier & (1u << b)) d.engines[dir].push_back(static_cast<hsa_amd_sdma_engine_id_t>(1u << b));
     if (d.engines[dir].empty())
       return fail(kInval, "device %d reports no SDMA engine for %s copies", dev,
                   dir == 0 ? "device-to-host" : "host-to-device");
   }
   {
-    // the layer-wise pipeline's set, in order of preference: host-to-device
-    // engines among 0-7 that device-to-host did not take, then those it
-    // took, then (only when more are asked for) the others
+    // the wide set, in order of preference: engines 0-7, then (only when
+    // more are asked for) the others
     const char* e = getenv("FLEXKV_SDMA_ENGINES_WIDE");
     if (!e) e = getenv("FLEXKV_SDMA_ENGINES_LAYERWISE");   // the earlier name
     const int wide = std::max(1, std::min(e ? atoi(e) : kDefaultWideEngines, 32));
     uint32_t mask = 0;
     FKV_HSA(g_hsa.copy_engine_status(q.gpu, q.cpu, &mask));
-    uint32_t d2h_taken = 0;
-    for (hsa_amd_sdma_engine_id_t id : d.engines[0]) d2h_taken |= static_cast<uint32_t>(id);
     d.engines_wide.clear();
-    const uint32_t tiers[3] = {mask & kComputeFriendlyEngines & ~d2h_taken,
-                               mask & kComputeFriendlyEngines & d2h_taken,
-                               mask & ~kComputeFriendlyEngines};
+    const uint32_t tiers[2] = {mask & kComputeFriendlyEngines, mask & ~kComputeFriendlyEngines};
     for (uint32_t tier : tiers)
       for (int b = 0; b < 32 && static_cast<int>(d.engines_wide.size()) < wide; ++b)
         if (tier & (1u << b))

@@ -149,89 +149,6 @@ constexpr int kMaxTileBlocks = 64;
 // the kernel arguments, so no workgroup reads them over PCIe first (one host
 // round trip less per call; a one-block zero-copy call is latency-bound).
 constexpr int kInlineIds = 32;
-// Compute units of the zero-copy kernel when the caller passes -1: enough
-// loads/stores in flight to saturate the PCIe Gen5 x16 link (measured on
-// MI355X: 8 CUs reach the link's copy rate; more add contention).
-constexpr int kAutoZeroCopyCus = 8;
-// The whole-group variant of the device-to-host zero-copy kernel fills the
-// link with fewer compute units and loses rate with more (MI355X, Llama-3-8B
-// shape, 2 GiB: 56.4 / 56.7 / 56.2 / 55.8 GB/s on 3 / 4 / 6 / 8 CUs, against
-// 56.6 GB/s for the row-by-row variant on 8), for calls of at least
-// kZeroCopyFewCusMinBytes.
-constexpr int kAutoZeroCopyCusWholeD2H = 4;
-// Layer-wise host-to-device transfers run beside the caller's compute.  Two
-// CUs still fill the link for reads from host memory (56.9 vs 57.2 GB/s with
-// 8) and leave the rest of the chip to the compute kernels: a 32-layer
-// Llama-3-8B load overlapped with per-layer GEMMs finishes in 42.8 ms on 2
-// CUs against 46.1 ms on 8.
-constexpr int kAutoLayerwiseH2DCus = 2;
-// Copy-engine size policy: smallest transfer, and smallest bytes per engine
-// copy, worth handing to the SDMA engines (ce_pays_off).  Measured on MI355X
-// (block-wise host caches, random ids, GB/s zero-copy kernel / engines): the
-// kernel is as fast or faster up to 32 MiB in both directions at every shape
-// (16 MiB of 256 KiB rows: D2H 48.9 / 46.1, H2D 53.8 / 49.5; 8 MiB of 2 MiB
-// rows: 46.1 / 45.9, 50.0 / 45.8), and from 32-64 MiB the engines come
-// within 1-3% (32 MiB of 2 MiB rows: D2H 53.1 / 53.5, H2D 55.2 / 53.5; 64 MiB:
-// 54.8 / 55.2, 56.2 / 55.2).  Below 32 MiB the kernel holds its compute units
-// for at most about 0.6 ms per transfer.
-constexpr int64_t kCeMinBytesDefault = int64_t(32) << 20;
-constexpr int64_t kCeMinRunBytes = int64_t(128) << 10;
-// The copy-engine policy set through fkv_set_copy_engine_policy; -1: unset,
-// so FLEXKV_CE_MIN_BYTES / FLEXKV_CE_RECT_COPIES, else the defaults, apply.
-std::atomic<int64_t> g_ce_min_bytes{-1};
-std::atomic<int> g_ce_rect_copies{-1};
-
-int64_t ce_min_bytes() {
-  const int64_t v = g_ce_min_bytes.load(std::memory_order_relaxed);
-  if (v >= 0) return v;
-  const char* e = getenv("FLEXKV_CE_MIN_BYTES");
-  return e ? std::max<int64_t>(0, atoll(e)) : kCeMinBytesDefault;
-}
-
-// Whether a layer-wise host cache with scattered ids stays on the engines
-// (rect copies) in copy-engine mode; default no (the zero-copy kernel).
-bool ce_rect_copies() {
-  const int v = g_ce_rect_copies.load(std::memory_order_relaxed);
-  if (v >= 0) return v == 1;
-  const char* r = getenv("FLEXKV_CE_RECT_COPIES");
-  return r && atoi(r) == 1;
-}
-// Host-to-device engine copies shorter than this on average spread over the
-// wide engine set (engines 0-7) instead of the direction's four.  Measured on
-// MI355X: 640 KiB copies (Llama-3-70B TP-8 shard) 51.9 -> 56.4 GB/s, 256 KiB
-// copies 39.5 -> 48.8 GB/s, 2 MiB copies 56.8 -> 57.0 GB/s, so longer copies
-// keep the direction's four.  While a D2H is in flight, host-to-device copies
-// of any size take the duplex split instead (issue_sdma).
-constexpr int64_t kWideCopyBytes = int64_t(1) << 20;
-// The piece of a copy-engine transfer that runs without engine copies beside
-// it (the first gather, the last scatter) is cut to 1 / kEdgePieceDiv of a
-// staging half when it moves at least kEdgePieceMinBytes.
-constexpr int kEdgePieceDiv = 8;
-constexpr int64_t kEdgePieceMinBytes = int64_t(128) << 20;
-// Default smallest engine copy per block of the copy-engine layer-wise
-// pipeline (see layerwise_min_copy_bytes).  Measured on MI355X, Llama-3-8B
-// one-layer groups (64 KiB per block), 1024 random blocks, engines 0-7:
-// 37.6 / 47.2 / 50.5 / 51.1 / 51.1 GB/s with windows up to 64 KiB / 128 KiB /
-// 256 KiB / 512 KiB / 1 MiB per block; per-layer GEMMs overlapped with it end
-// within 0.0 / 0.5 / 0.6 / 8.3 / 8.3% of the transfer plus one layer's
-// compute, and GEMMs beside it slow by the same few percent at every size.
-constexpr int64_t kLayerwiseCeMinCopyBytes = int64_t(256) << 10;
-// Average host run (bytes per (layer, K|V) run of consecutive blocks) from
-// which a layer-wise host cache is staged layer-major and copied run by run
-// instead of one rect copy per block.  Measured on MI355X at the Llama-3-8B
-// shape, layer-major against rect copies (46.8 GB/s either way): runs of
-// 128 KiB 41.2 / 32.4 GB/s (D2H / H2D), 256 KiB 51.1 / 42.0, 512 KiB
-// 55.3 / 51.7.
-constexpr int64_t kLayerRunBytes[2] = {int64_t(192) << 10, int64_t(384) << 10};   // [D2H, H2D]
-// The average run from which layer-major staging is used;
-// FLEXKV_CE_LAYER_RUN_BYTES overrides kLayerRunBytes.
-int64_t layer_run_bytes(bool h2d) {
-  const char* lr = getenv("FLEXKV_CE_LAYER_RUN_BYTES");
-  return lr ? std::max<int64_t>(1, atoll(lr)) : kLayerRunBytes[h2d ? 1 : 0];
-}
-// transfer_staged's return when the copy engines cannot be set up (nothing
-// was queued); not a hipError_t value
-constexpr int kSdmaUnavailable = -1000;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -684,6 +601,86 @@ __global__ __launch_bounds__(kThreads) void kv_small_copy_kernel(SmallArgs a) {
 }
 
 std::mutex g_init_mu;
+
+// ---------------------------------------------------------------------------
+// Host-side policy of the transfer paths
+
+// Compute units of the zero-copy kernel when the caller passes -1: enough
+// loads/stores in flight to saturate the PCIe Gen5 x16 link (measured on
+// MI355X: 8 CUs reach the link's copy rate; more add contention).
+constexpr int kAutoZeroCopyCus = 8;
+// The whole-group variant of the device-to-host zero-copy kernel fills the
+// link with fewer compute units and loses rate with more (MI355X, Llama-3-8B
+// shape, 2 GiB: 56.4 / 56.7 / 56.2 / 55.8 GB/s on 3 / 4 / 6 / 8 CUs, against
+// 56.6 GB/s for the row-by-row variant on 8), for calls of at least
+// kZeroCopyFewCusMinBytes.
+constexpr int kAutoZeroCopyCusWholeD2H = 4;
+// Layer-wise host-to-device transfers run beside the caller's compute.  Two
+// CUs still fill the link for reads from host memory (56.9 vs 57.2 GB/s with
+// 8) and leave the rest of the chip to the compute kernels: a 32-layer
+// Llama-3-8B load overlapped with per-layer GEMMs finishes in 42.8 ms on 2
+// CUs against 46.1 ms on 8.
+constexpr int kAutoLayerwiseH2DCus = 2;
+// Copy-engine size policy: smallest transfer, and smallest bytes per engine
+// copy, worth handing to the SDMA engines (ce_pays_off).  Measured on MI355X
+// (block-wise host caches, random ids, GB/s zero-copy kernel / engines): the
+// kernel is as fast or faster up to 32 MiB in both directions at every shape
+// (16 MiB of 256 KiB rows: D2H 48.9 / 46.1, H2D 53.8 / 49.5; 8 MiB of 2 MiB
+// rows: 46.1 / 45.9, 50.0 / 45.8), and from 32-64 MiB the engines come
+// within 1-3% (32 MiB of 2 MiB rows: D2H 53.1 / 53.5, H2D 55.2 / 53.5; 64 MiB:
+// 54.8 / 55.2, 56.2 / 55.2).  Below 32 MiB the kernel holds its compute units
+// for at most about 0.6 ms per transfer.
+constexpr int64_t kCeMinBytesDefault = int64_t(32) << 20;
+constexpr int64_t kCeMinRunBytes = int64_t(128) << 10;
+// The copy-engine policy set through fkv_set_copy_engine_policy; -1: unset,
+// so FLEXKV_CE_MIN_BYTES / FLEXKV_CE_RECT_COPIES, else the defaults, apply.
+std::atomic<int64_t> g_ce_min_bytes{-1};
+std::atomic<int> g_ce_rect_copies{-1};
+
+int64_t ce_min_bytes() {
+  const int64_t v = g_ce_min_bytes.load(std::memory_order_relaxed);
+  if (v >= 0) return v;
+  const char* e = getenv("FLEXKV_CE_MIN_BYTES");
+  return e ? std::max<int64_t>(0, atoll(e)) : kCeMinBytesDefault;
+}
+
+// Whether a layer-wise host cache with scattered ids stays on the engines
+// (rect copies) in copy-engine mode; default no (the zero-copy kernel).
+bool ce_rect_copies() {
+  const int v = g_ce_rect_copies.load(std::memory_order_relaxed);
+  if (v >= 0) return v == 1;
+  const char* r = getenv("FLEXKV_CE_RECT_COPIES");
+  return r && atoi(r) == 1;
+}
+// The piece of a copy-engine transfer that runs without engine copies beside
+// it (the first gather, the last scatter) is cut to 1 / kEdgePieceDiv of a
+// staging half when it moves at least kEdgePieceMinBytes.
+constexpr int kEdgePieceDiv = 8;
+constexpr int64_t kEdgePieceMinBytes = int64_t(128) << 20;
+// Default smallest engine copy per block of the copy-engine layer-wise
+// pipeline (see layerwise_min_copy_bytes).  Measured on MI355X, Llama-3-8B
+// one-layer groups (64 KiB per block), 1024 random blocks, engines 0-7:
+// 37.6 / 47.2 / 50.5 / 51.1 / 51.1 GB/s with windows up to 64 KiB / 128 KiB /
+// 256 KiB / 512 KiB / 1 MiB per block; per-layer GEMMs overlapped with it end
+// within 0.0 / 0.5 / 0.6 / 8.3 / 8.3% of the transfer plus one layer's
+// compute, and GEMMs beside it slow by the same few percent at every size.
+constexpr int64_t kLayerwiseCeMinCopyBytes = int64_t(256) << 10;
+// Average host run (bytes per (layer, K|V) run of consecutive blocks) from
+// which a layer-wise host cache is staged layer-major and copied run by run
+// instead of one rect copy per block.  Measured on MI355X at the Llama-3-8B
+// shape, layer-major against rect copies (46.8 GB/s either way): runs of
+// 128 KiB 41.2 / 32.4 GB/s (D2H / H2D), 256 KiB 51.1 / 42.0, 512 KiB
+// 55.3 / 51.7.
+constexpr int64_t kLayerRunBytes[2] = {int64_t(192) << 10, int64_t(384) << 10};   // [D2H, H2D]
+// The average run from which layer-major staging is used;
+// FLEXKV_CE_LAYER_RUN_BYTES overrides kLayerRunBytes.
+int64_t layer_run_bytes(bool h2d) {
+  const char* lr = getenv("FLEXKV_CE_LAYER_RUN_BYTES");
+  return lr ? std::max<int64_t>(1, atoll(lr)) : kLayerRunBytes[h2d ? 1 : 0];
+}
+// transfer_staged's return when the copy engines cannot be set up (nothing
+// was queued); not a hipError_t value
+constexpr int kSdmaUnavailable = -1000;
 
 template <bool H, bool I, bool W = false>
 void* kernel_ptr() {
@@ -1244,6 +1241,13 @@ int64_t edge_small_min_bytes() {
   return e ? std::max<int64_t>(1, atoll(e)) : kEdgeSmallMinBytesDefault;
 }
 
+// Host-to-device engine copies shorter than this on average spread over the
+// synchronous wide set (engines 0-5) instead of the direction's four (0-3).
+// Measured on MI355X: 256 KiB copies 51.7 GB/s on 0-3, 56.1 on 0-5; 640 KiB
+// copies (Llama-3-70B TP-8 shard) 57.0 on 0-3, 56.4 on 0-5.  While a D2H is
+// in flight, host-to-device copies of any size take the duplex split
+// instead (issue_sdma).
+constexpr int64_t kWideCopyBytes = int64_t(384) << 10;
 // Host-to-device copies on the wide set run beside the scatter of the
 // previous piece, and every engine in flight slows that scatter (MI355X,
 // Llama-3-70B TP-8 shard, 640 KiB copies: 512 MiB scatter pieces 4.26 /

@@ -50,12 +50,12 @@ enum {
    * transfer needs on a single engine (FLEXKV_CE_RECT_COPIES=1 keeps it on
    * the engines; a transfer of rect copies runs alone).  Staging is
    * double-buffered; the PCIe copies take no compute units.  Each direction
-   * has its own staging and engines (device-to-host engines 0-3,
-   * host-to-device 4-7; host-to-device copies shorter than 1 MiB on average
-   * spread over six of engines 0-7, two of which wait for the scatter
-   * beside them to end before taking their share), so a D2H and an H2D
-   * transfer from different threads run at the same time; while both run,
-   * their copies split engines 0-7 (device-to-host 0-4, host-to-device 5-7;
+   * has its own staging, and both take engines 0-3, the fast ones across
+   * the host link (host-to-device copies shorter than 384 KiB on average
+   * spread over engines 0-5, two of which wait for the scatter beside them
+   * to end before taking their share); a D2H and an H2D transfer from
+   * different threads run at the same time, and while both run their copies
+   * split engines 0-7 (device-to-host 0-4, host-to-device 5-7;
    * FLEXKV_SDMA_DUPLEX_D2H), which balances the two.  Transfers under
    * FLEXKV_CE_MIN_BYTES (default 32 MiB; fkv_set_copy_engine_policy) or whose
    * engine copies would move under 128 KiB each move with the zero-copy

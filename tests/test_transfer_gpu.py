@@ -469,9 +469,7 @@ def test_duplex_copy_engine_transfers(dev):
     two threads so that they overlap over many staging halves: while both
     are in flight their copies take the duplex engine split, and halves
     issued before, during and after the overlap land on different engine
-    sets.  The H2D's 512 KiB block rows take the six-engine set with held
-    engines outside the overlap, so held shares are queued on whichever set
-    is current then.  Every byte matches."""
+    sets.  Every byte matches."""
     import threading
     from gpu_util import DeviceCase, abi_transfer
     from flexkv_amd import _lib
