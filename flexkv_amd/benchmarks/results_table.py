@@ -187,8 +187,11 @@ def table(p: dict, label: str) -> str:
     wo = p.get("worker_ops", {})
     L += ["", "## Other measurements", "", "| Figure | Value |", "|---|---|"]
     if du:
+        peak = hl.get("duplex_peak_gbps_measured")
         L.append(f"| D2H and H2D at once, copy engines / zero-copy | "
-                 f"{du.get('ce_aggregate_gbps')} / {du.get('kernel_aggregate_gbps')} GB/s |")
+                 f"{du.get('ce_aggregate_gbps')} / {du.get('kernel_aggregate_gbps')} GB/s"
+                 + (f" ({du.get('ce_frac_duplex_peak')} / {du.get('kernel_frac_duplex_peak')} of "
+                    f"{peak} GB/s, two 1 GiB runtime copies at once)" if peak else "") + " |")
     if ep:
         L.append(f"| TransferEngine put / get / both | {ep['put']['gbps']} / {ep['get']['gbps']} / "
                  f"{ep['put_and_get']['gbps']} GB/s |")
