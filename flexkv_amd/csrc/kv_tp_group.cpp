@@ -102,10 +102,15 @@ void rank_loop(fkv_tp_group_s* g, int r) {
       rc = static_cast<int>(se);
       msg = std::string("hipSetDevice failed: ") + hipGetErrorString(se);
     } else {
-      rc = rank_transfer(g, r, job);
-      if (rc) {
-        msg = last_error();
-        unsafe = last_unsafe_host_blocks();
+      try {
+        rc = rank_transfer(g, r, job);
+        if (rc) {
+          msg = last_error();
+          unsafe = last_unsafe_host_blocks();
+        }
+      } catch (const std::exception& e) {   // nothing may end the rank thread
+        rc = static_cast<int>(hipErrorUnknown);
+        msg = std::string("exception: ") + e.what();
       }
     }
     std::lock_guard<std::mutex> lk(g->mu);
