@@ -200,7 +200,7 @@ CACHE = dict(tokens_per_block=16, num_cpu_blocks=128, use_ce_transfer_h2d=False,
              use_ce_transfer_d2h=True, transfer_sms_h2d=4, transfer_sms_d2h=4)
 
 
-def _wait(engine, gid, limit=30.0):
+def _wait(engine, gid, limit=120.0):
     t0 = time.time()
     seen = []
     while time.time() - t0 < limit:
@@ -210,15 +210,18 @@ def _wait(engine, gid, limit=30.0):
     raise AssertionError(f"graph {gid} did not complete")
 
 
-@pytest.mark.parametrize("tp,dp", [(2, 1), (2, 2), (4, 1)])
+@pytest.mark.parametrize("tp,dp,mode", [(2, 1, "thread"), (2, 2, "thread"), (4, 1, "thread"),
+                                         (2, 1, "process")])
 @pytest.mark.parametrize("use_mla", [False, True])
 @pytest.mark.parametrize("layout", [KVCacheLayoutType.LAYERWISE, KVCacheLayoutType.BLOCKWISE])
-def test_engine_tp_round_trip(tp, dp, use_mla, layout):
+def test_engine_tp_round_trip(tp, dp, mode, use_mla, layout):
     """GPU -> CPU -> GPU through StorageEngine + TransferEngine with tp ranks
     per data-parallel group, every rank's cache on cuda:0: each rank holds
     num_kv_heads / tp heads (all heads under MLA), dp group i writes host
     blocks [16 i, 16 i + 16), the rank caches are zeroed in place, and the
-    read graph restores every rank's every layer."""
+    read graph restores every rank's every layer.  In process mode the TP
+    worker is a spawned process fed IPC handles of the rank caches, with a
+    host cache of its own."""
     mc = ModelConfig(use_mla=use_mla, tp_size=tp, dp_size=dp, **MODEL)
     cc = CacheConfig(cpu_kv_layout_type=layout, **CACHE)
     heads = mc.num_kv_heads if use_mla else mc.num_kv_heads // tp
@@ -240,7 +243,8 @@ def test_engine_tp_round_trip(tp, dp, use_mla, layout):
         gpus.append(gpu)
         se.register_gpu_blocks(gpu, gl, device_id=j, dtype=mc.dtype)
     te = TransferEngine([se.get_storage_handle(DeviceType.GPU, j) for j in range(tp * dp)],
-                        mc, cc, cpu_handle=se.get_storage_handle(DeviceType.CPU))
+                        mc, cc, cpu_handle=se.get_storage_handle(DeviceType.CPU),
+                        worker_mode=mode)
     te.start()
     try:
         for i in range(dp):
