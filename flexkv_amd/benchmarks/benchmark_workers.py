@@ -52,7 +52,7 @@ from flexkv_amd.common.transfer import (TransferDescriptor, TransferOp,  # noqa:
                                         TransferType)
 from flexkv_amd.storage.allocator import HostCacheSpec, SSDAllocator  # noqa: E402
 from flexkv_amd.transfer.worker import (CPUSSDDiskTransferWorker,  # noqa: E402
-                                        GPUCPUTransferWorker)
+                                        GPUCPUTransferWorker, tpGPUCPUTransferWorker)
 
 DEFAULT_CONFIG = os.path.join(HERE, "example_config.json")
 
@@ -95,8 +95,6 @@ def make_configs(args: argparse.Namespace) -> Tuple[ModelConfig, CacheConfig, Be
                             num_blocks_to_transfer=args.num_blocks,
                             shuffle_ids=args.shuffle_ids, warmup_round=args.warmup_round,
                             benchmark_round=args.benchmark_round)
-    if model.tp_size != 1:
-        raise ValueError("this package runs one GPU per worker: tp_size must be 1")
     return model, cache, bench
 
 
@@ -108,19 +106,34 @@ def _layout(kind: KVCacheLayoutType, model: ModelConfig, cache: CacheConfig,
 
 def create_cpu_gpu_worker(model: ModelConfig, cache: CacheConfig, bench: BenchmarkConfig,
                           queue: Any):
+    """The GPU<->CPU worker of the reference harness (:43-117): with tp_size
+    > 1 a tpGPUCPUTransferWorker over tp_size ranks, each holding
+    num_kv_heads / tp_size heads (all heads under MLA).  Every rank's cache
+    is on cuda:0 (the reference puts rank r on GPU r and refuses a tp_size
+    above the device count, :185-187); the ranks then share one GPU's link."""
     n = bench.num_blocks_to_transfer
+    tp = model.tp_size
     gpu_layout = _layout(KVCacheLayoutType.LAYERWISE, model, cache, n)
+    if tp > 1 and not model.use_mla:
+        gpu_layout = gpu_layout.div_head(tp)
     cpu_layout = _layout(cache.cpu_kv_layout_type, model, cache, cache.num_cpu_blocks)
     per_layer = gpu_layout.get_total_elements() // model.num_layers
-    layers = [torch.zeros(per_layer, dtype=model.dtype, device="cuda:0")
-              for _ in range(model.num_layers)]
-    handle = GPUCPUTransferWorker.create_worker(
-        0, queue, [TensorSharedHandle(t) for t in layers],
-        HostCacheSpec(cpu_layout, model.dtype), gpu_layout, cpu_layout, model.dtype, 0,
-        use_ce_transfer_h2d=cache.use_ce_transfer_h2d,
-        use_ce_transfer_d2h=cache.use_ce_transfer_d2h,
-        transfer_sms_h2d=cache.transfer_sms_h2d, transfer_sms_d2h=cache.transfer_sms_d2h)
-    return handle, layers
+    ranks = [[torch.zeros(per_layer, dtype=model.dtype, device="cuda:0")
+              for _ in range(model.num_layers)] for _ in range(tp)]
+    common = dict(use_ce_transfer_h2d=cache.use_ce_transfer_h2d,
+                  use_ce_transfer_d2h=cache.use_ce_transfer_d2h,
+                  transfer_sms_h2d=cache.transfer_sms_h2d,
+                  transfer_sms_d2h=cache.transfer_sms_d2h)
+    spec = HostCacheSpec(cpu_layout, model.dtype)
+    if tp == 1:
+        handle = GPUCPUTransferWorker.create_worker(
+            0, queue, [TensorSharedHandle(t) for t in ranks[0]], spec, gpu_layout, cpu_layout,
+            model.dtype, 0, **common)
+    else:
+        handle = tpGPUCPUTransferWorker.create_worker(
+            0, queue, [[TensorSharedHandle(t) for t in layers] for layers in ranks], spec,
+            gpu_layout, cpu_layout, model.dtype, tp, 0, **common)
+    return handle, ranks
 
 
 def create_cpu_ssd_worker(model: ModelConfig, cache: CacheConfig, queue: Any, ssd_dir: str):

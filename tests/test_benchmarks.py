@@ -39,16 +39,20 @@ def test_example_config_parses():
     assert bench.transfer_type == TransferType.D2H and bench.num_blocks_to_transfer == 64
 
 
-def test_reference_style_keys_are_ignored_and_tp_refused(tmp_path):
+def _tp_config(tmp_path, tp=2, **cache):
+    p = tmp_path / "tp.json"
+    cfg = json.loads(open(_config(tmp_path, **cache)).read())
+    cfg["ModelConfig"]["tp_size"] = tp
+    p.write_text(json.dumps(cfg))
+    return str(p)
+
+
+def test_reference_style_keys_are_ignored_and_tp_accepted(tmp_path):
     args = bw.parse_args(["--config", _config(tmp_path)])
     model, cache, _ = bw.make_configs(args)
     assert model.dtype == torch.float16 and cache.num_ssd_blocks == 128
-    p = tmp_path / "tp.json"
-    cfg = json.loads(open(_config(tmp_path)).read())
-    cfg["ModelConfig"]["tp_size"] = 2
-    p.write_text(json.dumps(cfg))
-    with pytest.raises(ValueError, match="tp_size"):
-        bw.make_configs(bw.parse_args(["--config", str(p)]))
+    model, _, _ = bw.make_configs(bw.parse_args(["--config", _tp_config(tmp_path)]))
+    assert model.tp_size == 2
 
 
 @pytest.mark.parametrize("kind,shuffle,entries", [("H2DISK", False, 0), ("DISK2H", True, 0),
@@ -88,6 +92,20 @@ def test_gpu_benchmark_runs(tmp_path, kind, ce):
                                          "--benchmark-round", "3"]))
     assert res["bytes"] == 48 * 16 * 4 * 2 * 64 * 2 * 2
     assert res["path"] == ("ce" if ce else "kernel") and res["gb_per_s"] > 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind,ce", [("D2H", False), ("H2D", True)])
+def test_gpu_benchmark_runs_tp(tmp_path, kind, ce):
+    """tp_size = 2: a spawned tpGPUCPUTransferWorker over two ranks (each
+    holding half the heads) on cuda:0; the op moves every rank's bytes."""
+    cfg = _tp_config(tmp_path, use_pinned_memory=True, use_ce_transfer_h2d=ce,
+                     use_ce_transfer_d2h=ce)
+    res = bw.bench_worker(bw.parse_args(["--config", cfg, "--transfer-type", kind,
+                                         "--num-blocks", "48", "--shuffle-ids",
+                                         "--benchmark-round", "3"]))
+    assert res["bytes"] == 48 * 16 * 4 * 2 * 64 * 2 * 2
+    assert res["gb_per_s"] > 0
 
 
 REFERENCE_CONFIG = "/root/reference/benchmarks/example_config.json"
