@@ -90,9 +90,10 @@ namespace {
 #ifndef FKV_WHOLE_SCATTER
 #define FKV_WHOLE_SCATTER 1
 #endif
-// Zero-copy launches whose chunks are whole groups of the unroll (8 rows
-// D2H, 4 H2D) take the whole-group variant, which keeps one base per group
-// instead of one address per row (no spills).
+// Zero-copy launches whose chunks are whole sub-groups (4 rows D2H, whose
+// group of 8 rows in flight is addressed as two halves; 4 rows H2D) take the
+// whole-group variant, which keeps one base per sub-group instead of one
+// address per row (no spills).
 #ifndef FKV_WHOLE_ZERO_COPY
 #define FKV_WHOLE_ZERO_COPY 1
 #endif
@@ -144,6 +145,12 @@ constexpr int kThreads = 256;               // 4 wavefronts of 64 lanes
 constexpr int64_t kWholeScatterMaxBytes = int64_t(512) << 20;
 constexpr int kWaves = kThreads / 64;
 constexpr int kUnrollHbm = FKV_UNROLL_HBM;
+// Sub-groups per group of the whole-group variant: the zero-copy D2H group of
+// 8 rows in flight is two sub-groups of 4 rows, so chunks of 4 KiB (the
+// Llama-3-70B TP-8 shard) take it; every other instantiation addresses its
+// group as one.  Each sub-group lies inside one chunk.
+template <bool kH2D, bool kIotaCpu>
+constexpr int whole_sub_groups() { return (!kIotaCpu && !kH2D && FKV_UNROLL_ZC_D2H % 2 == 0) ? 2 : 1; }
 constexpr int kMaxTileBlocks = 64;
 // Transfers of at most this many blocks carry their (gpu_id, cpu_id) pairs in
 // the kernel arguments, so no workgroup reads them over PCIe first (one host
@@ -200,9 +207,10 @@ __device__ inline int64_t wave_uniform(int64_t x) {
 // block i of the launch sits at CPU-side block index i (ids[2i+1] unused).
 // Row addresses are wave-uniform (scalar registers); each lane adds its own
 // 16-byte slot, so one 32-bit lane offset serves every access.
-// kWhole: the launch's chunks are whole groups of kUnroll full rows (the
-// host checks rows_per_chunk % kUnroll == 0 and no partial row), so each
-// group lies inside one chunk and is addressed from one base per side.
+// kWhole: the launch's chunks are whole sub-groups of kUnroll / kSub full
+// rows (kSub = whole_sub_groups(); the host checks rows_per_chunk % (kUnroll /
+// kSub) == 0 and no partial row), so each sub-group lies inside one chunk and
+// is addressed from one base per side.
 template <bool kH2D, bool kIotaCpu, bool kWhole = false>
 __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
   constexpr bool kScatter = kIotaCpu && kH2D;
@@ -264,40 +272,64 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
     const uint32_t g_begin = static_cast<uint32_t>(tr) * a.split_rows;
     const uint32_t g_end = min(rows, g_begin + a.split_rows);
     if constexpr (kWhole) {
-      // Groups start at multiples of kUnroll, so each lies inside one chunk:
-      // consecutive 1 KiB rows on both sides.
+      // Groups start at multiples of kUnroll and sub-groups at multiples of
+      // kR, so each sub-group lies inside one chunk: consecutive 1 KiB rows
+      // on both sides.  A tile's rows are a multiple of kR, not always of
+      // kUnroll, so a group's later sub-groups may lie past g_end.
+      constexpr int kSub = whole_sub_groups<kH2D, kIotaCpu>();
+      constexpr int kR = kUnroll / kSub;
+      static_assert(kR * kSub == kUnroll, "a group is kSub sub-groups of kR rows");
       for (uint32_t g = g_begin + static_cast<uint32_t>(wave) * kUnroll; g < g_end;
            g += kWaves * kUnroll) {
-        const uint32_t item = g / rpc;
-        const uint32_t rr = g - item * rpc;
-        const uint32_t bi = item / items_per_block;
-        const uint32_t rem = item - bi * items_per_block;
-        const uint32_t l = rem / kv;
-        const uint32_t k = rem - l * kv;
-        const uint32_t layer = static_cast<uint32_t>(l0) + l;
-        const int64_t gid = wave_uniform(s_gid[bi]);
-        const int64_t cid = wave_uniform(s_cid[bi]);
-        const int64_t row_off = static_cast<int64_t>(rr) * (64 * 16);
-        char* gpu = reinterpret_cast<char*>(a.layer_ptr[layer * ppl + k * (ppl - 1)]) +
-                    static_cast<int64_t>(k) * a.gpu_kv_stride + gid * a.gpu_block_stride + row_off;
-        char* cpu = a.cpu_base + static_cast<int64_t>(layer) * a.cpu_layer_stride +
-                    static_cast<int64_t>(k) * a.cpu_kv_stride + cid * a.cpu_block_stride + row_off;
-        // Raw buffer accesses: the group's base in a buffer resource (scalar
-        // registers), the lane's 16-byte slot as the vector offset and the
-        // row as a scalar offset, so no per-row 64-bit address is kept.
-        const __amdgpu_buffer_rsrc_t rs =
-            __builtin_amdgcn_make_buffer_rsrc(kH2D ? cpu : gpu, 0, -1, kBufferRsrcWord3);
-        const __amdgpu_buffer_rsrc_t rd =
-            __builtin_amdgcn_make_buffer_rsrc(kH2D ? gpu : cpu, 0, -1, kBufferRsrcWord3);
+        // Raw buffer accesses: the sub-group's base in a buffer resource
+        // (scalar registers), the lane's 16-byte slot as the vector offset
+        // and the row as a scalar offset, so no per-row 64-bit address is
+        // kept.
+        __amdgpu_buffer_rsrc_t rs[kSub], rd[kSub];
+        bool live[kSub];
+#pragma unroll
+        for (int s = 0; s < kSub; ++s) {
+          const uint32_t gs = g + static_cast<uint32_t>(s * kR);
+          live[s] = s == 0 || gs < g_end;
+          // a sub-group past g_end takes the first one's row (never accessed)
+          const uint32_t row = live[s] ? gs : g;
+          const uint32_t item = row / rpc;
+          const uint32_t rr = row - item * rpc;
+          const uint32_t bi = item / items_per_block;
+          const uint32_t rem = item - bi * items_per_block;
+          const uint32_t l = rem / kv;
+          const uint32_t k = rem - l * kv;
+          const uint32_t layer = static_cast<uint32_t>(l0) + l;
+          const int64_t gid = wave_uniform(s_gid[bi]);
+          const int64_t cid = wave_uniform(s_cid[bi]);
+          const int64_t row_off = static_cast<int64_t>(rr) * (64 * 16);
+          char* gpu = reinterpret_cast<char*>(a.layer_ptr[layer * ppl + k * (ppl - 1)]) +
+                      static_cast<int64_t>(k) * a.gpu_kv_stride + gid * a.gpu_block_stride +
+                      row_off;
+          char* cpu = a.cpu_base + static_cast<int64_t>(layer) * a.cpu_layer_stride +
+                      static_cast<int64_t>(k) * a.cpu_kv_stride + cid * a.cpu_block_stride +
+                      row_off;
+          rs[s] = __builtin_amdgcn_make_buffer_rsrc(kH2D ? cpu : gpu, 0, -1, kBufferRsrcWord3);
+          rd[s] = __builtin_amdgcn_make_buffer_rsrc(kH2D ? gpu : cpu, 0, -1, kBufferRsrcWord3);
+        }
         i32x4 v[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u)
-          v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, u * (64 * 16),
-                                                       kNtLoad ? kCachePolicyNt : 0);
+        for (int s = 0; s < kSub; ++s)
+          if (live[s]) {
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u)
-          __builtin_amdgcn_raw_buffer_store_b128(v[u], rd, lane_off, u * (64 * 16),
-                                                 kNtStore ? kCachePolicyNt : 0);
+            for (int u = 0; u < kR; ++u)
+              v[s * kR + u] = __builtin_amdgcn_raw_buffer_load_b128(
+                  rs[s], lane_off, u * (64 * 16), kNtLoad ? kCachePolicyNt : 0);
+          }
+#pragma unroll
+        for (int s = 0; s < kSub; ++s)
+          if (live[s]) {
+#pragma unroll
+            for (int u = 0; u < kR; ++u)
+              __builtin_amdgcn_raw_buffer_store_b128(v[s * kR + u], rd[s], lane_off,
+                                                     u * (64 * 16),
+                                                     kNtStore ? kCachePolicyNt : 0);
+          }
       }
     } else {
       for (uint32_t g = g_begin + static_cast<uint32_t>(wave) * kUnroll; g < g_end;
@@ -829,10 +861,12 @@ void choose_tiles(int nb, int nl, int kv, int rpc, int grid_cap, int factor, int
 // launch takes; staging launches that take the whole-group variant use
 // `whole_grid_cap` instead when it is given.
 // Whether the zero-copy launches of a transfer take the whole-group kernel
-// variant (launch_copy: full 1 KiB rows, chunks of whole unrolled groups).
+// variant (launch_copy: full 1 KiB rows, chunks of whole sub-groups).
 bool zero_copy_whole(const Geometry& g, bool h2d) {
-  const int64_t unroll = h2d ? FKV_UNROLL_ZC_H2D : FKV_UNROLL_ZC_D2H;
-  return FKV_WHOLE_ZERO_COPY && g.chunk % (64 * 16) == 0 && (g.chunk / (64 * 16)) % unroll == 0;
+  const int64_t sub_rows = h2d ? FKV_UNROLL_ZC_H2D / whole_sub_groups<true, false>()
+                               : FKV_UNROLL_ZC_D2H / whole_sub_groups<false, false>();
+  return FKV_WHOLE_ZERO_COPY && g.chunk % (64 * 16) == 0 &&
+         (g.chunk / (64 * 16)) % sub_rows == 0;
 }
 
 // Compute units of a zero-copy transfer when the caller passes -1.

@@ -130,6 +130,12 @@ GEOMETRIES = [
     (130, 130, 0, 2, 6, 8, 1, 1, 64, np.uint16, "BLOCKWISE", 1, 0, 5),    # >128 layers: 2 launches
     (2, 2, 0, 2, 600, 700, 2, 2, 32, np.uint32, "BLOCKWISE", 1, 0, 520),  # many tiles
     (4, 4, 0, 2, 64, 96, 16, 8, 128, np.uint8, "LAYERWISE", 1, 0, 40),    # 1-byte (fp8) cache
+    # Zero-copy D2H groups of 8 rows as two 4-row sub-groups: MLA 4 KiB chunks
+    # over an odd number of chunks (a group's second sub-group past the end),
+    # and 12 KiB chunks (groups across two chunks); both over 128 chunks, so
+    # the general kernel takes them.
+    (3, 3, 0, 1, 60, 80, 16, 1, 128, np.uint16, "BLOCKWISE", 1, 0, 45),
+    (3, 3, 0, 1, 50, 60, 16, 3, 128, np.uint16, "BLOCKWISE", 1, 0, 43),
 ]
 
 
