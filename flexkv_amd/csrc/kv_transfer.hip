@@ -851,22 +851,25 @@ void choose_tiles(int nb, int nl, int kv, int rpc, int grid_cap, int factor, int
   a->num_tiles = static_cast<int32_t>(t * tr);
 }
 
-// Fill the per-launch part of CopyArgs and launch over `nb` blocks starting at
-// block `b0` of the (already packed) id list, for GPU layers [l0, l0 + nl).
-// `cpu_base` is the CPU-side address of launch layer 0 of block index 0.
-// `ids` holds the packed pairs: `host` for the host's view, `dev` for the
-// device's (the same pinned buffer).  With `split` > 0, `dev` instead holds
-// the gpu ids and, `split` entries later, the cpu ids (device memory), and
-// `host` is null.  `grid_cap` is compute units x occupancy of the kernel the
-// launch takes; staging launches that take the whole-group variant use
-// `whole_grid_cap` instead when it is given.
+int64_t op_bytes(const Geometry& g) {
+  return static_cast<int64_t>(g.num_blocks) * g.num_layers * g.kv * g.chunk;
+}
+
 // Whether the zero-copy launches of a transfer take the whole-group kernel
 // variant (launch_copy: full 1 KiB rows, chunks of whole sub-groups).
+// Host-to-device calls under kZeroCopyWholeH2DMinBytes keep the row-by-row
+// variant, which measured faster on short calls and slower on long ones
+// (MI355X, Llama-3-8B chunks, kernel mode, whole-group against row by row:
+// 1 block, 2 MiB, 34.4-34.6 against 35.6-36.1 GB/s; 16 blocks x 1 layer,
+// 36.2-36.7 against 34.5-34.7 us per call; 16 MiB equal; 64 MiB 56.33
+// against 56.21-56.22 GB/s; 2 GiB 57.34-57.35 against 57.19-57.20).
+constexpr int64_t kZeroCopyWholeH2DMinBytes = int64_t(32) << 20;
 bool zero_copy_whole(const Geometry& g, bool h2d) {
   const int64_t sub_rows = h2d ? FKV_UNROLL_ZC_H2D / whole_sub_groups<true, false>()
                                : FKV_UNROLL_ZC_D2H / whole_sub_groups<false, false>();
   return FKV_WHOLE_ZERO_COPY && g.chunk % (64 * 16) == 0 &&
-         (g.chunk / (64 * 16)) % sub_rows == 0;
+         (g.chunk / (64 * 16)) % sub_rows == 0 &&
+         (!h2d || op_bytes(g) >= kZeroCopyWholeH2DMinBytes);
 }
 
 // Compute units of a zero-copy transfer when the caller passes -1.
@@ -876,8 +879,7 @@ bool zero_copy_whole(const Geometry& g, bool h2d) {
 // 53.9, 2 GiB 56.7 / 55.6 / 55.2).
 constexpr int64_t kZeroCopyFewCusMinBytes = int64_t(64) << 20;
 int auto_zero_copy_cus(const Geometry& g, bool h2d) {
-  const int64_t bytes = static_cast<int64_t>(g.num_blocks) * g.num_layers * g.kv * g.chunk;
-  return !h2d && zero_copy_whole(g, h2d) && bytes >= kZeroCopyFewCusMinBytes
+  return !h2d && zero_copy_whole(g, h2d) && op_bytes(g) >= kZeroCopyFewCusMinBytes
              ? kAutoZeroCopyCusWholeD2H
              : kAutoZeroCopyCus;
 }
@@ -918,6 +920,15 @@ void launch_pack(const PackArgs& pa, hipStream_t stream, hipEvent_t ea, hipEvent
                         kU != 32 ? kPackLdsOneGroup : 0u, stream, ea, eb, 0, pa);
 }
 
+// Fill the per-launch part of CopyArgs and launch over `nb` blocks starting at
+// block `b0` of the (already packed) id list, for GPU layers [l0, l0 + nl).
+// `cpu_base` is the CPU-side address of launch layer 0 of block index 0.
+// `ids` holds the packed pairs: `host` for the host's view, `dev` for the
+// device's (the same pinned buffer).  With `split` > 0, `dev` instead holds
+// the gpu ids and, `split` entries later, the cpu ids (device memory), and
+// `host` is null.  `grid_cap` is compute units x occupancy of the kernel the
+// launch takes; staging launches that take the whole-group variant use
+// `whole_grid_cap` instead when it is given.
 template <bool kH2D, bool kIota>
 int launch_copy(const Geometry& g, const IdBuf& ids, char* cpu_base, int64_t cks, int64_t cls,
                 int64_t cbs, int b0, int nb, int l0, int nl, int grid_cap,
@@ -1066,7 +1077,7 @@ int transfer_small(const Geometry& g, char* cpu_dev, int n_pieces, hipStream_t s
   hipEvent_t ea = nullptr, eb = nullptr;
   int rc = prof.kernel_events(&ea, &eb);
   if (rc) return rc;
-  prof.kernel_span(ea, eb, static_cast<int64_t>(g.num_blocks) * g.num_layers * g.kv * g.chunk);
+  prof.kernel_span(ea, eb, op_bytes(g));
   (void)hipGetLastError();  // a stale error from elsewhere must not be blamed on this launch
   hipExtLaunchKernelGGL(kv_small_copy_kernel<kH2D>, dim3(n_pieces), dim3(kThreads), 0, stream,
                         ea, eb, 0, a);
@@ -2093,7 +2104,7 @@ bool ce_pays_off(const Geometry& g, bool h2d) {
   // a "host" cache that is device memory has no PCIe copy to offload
   if (g.cpu_info.device) return false;
   const int64_t min_bytes = ce_min_bytes();
-  const int64_t total = static_cast<int64_t>(g.num_blocks) * g.num_layers * g.kv * g.chunk;
+  const int64_t total = op_bytes(g);
   const bool row_contig = (g.kv == 1 || g.cks == g.chunk) &&
                           (g.num_layers == 1 || g.cls == g.kv * g.chunk);
   const int64_t row = static_cast<int64_t>(g.num_layers) * g.kv * g.chunk;
