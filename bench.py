@@ -693,6 +693,7 @@ def call_latency(wl: Workload, reps: int = 200):
     from flexkv_amd import c_ext
     out = {}
     L = wl.w["layers"]
+    warm = 50   # untimed calls first: the first of a series ran about 1 us slower
     for path, ce in (("zc", False), ("ce", True)):
         for nb, nl in ((1, 1), (16, 1), (16, L)):
             g = wl.gids_p[:nb].clone().pin_memory()
@@ -700,21 +701,21 @@ def call_latency(wl: Workload, reps: int = 200):
             p = wl.ptrs[:nl].clone().pin_memory()
             for name, h2d in (("h2d", True), ("d2h", False)):
                 ts = []
-                for i in range(reps + 5):
+                for i in range(reps + warm):
                     t0 = time.perf_counter()
                     c_ext.transfer_kv_blocks(g, p, wl.gkv, wl.gblk, c, wl.host, wl.ckv, wl.clay,
                                              wl.cblk, wl.chunk, 0, -1, h2d, ce, wl.mla)
                     ts.append(time.perf_counter() - t0)
-                out[f"{path}_{nb}blk_{nl}layer_{name}_us"] = round(statistics.median(ts[5:]) * 1e6, 1)
+                out[f"{path}_{nb}blk_{nl}layer_{name}_us"] = round(statistics.median(ts[warm:]) * 1e6, 1)
     x = torch.zeros(1, device=wl.dev)
     st = torch.cuda.current_stream()
     ts = []
-    for i in range(reps + 5):
+    for i in range(reps + warm):
         t0 = time.perf_counter()
         x.fill_(1.0)
         st.synchronize()
         ts.append(time.perf_counter() - t0)
-    out["torch_fill_sync_us"] = round(statistics.median(ts[5:]) * 1e6, 1)
+    out["torch_fill_sync_us"] = round(statistics.median(ts[warm:]) * 1e6, 1)
     return out
 
 
