@@ -91,7 +91,8 @@ enum {
  *
  * Arguments follow flexkv::transfer_kv_blocks (csrc/transfer.cu:63-70) one for
  * one; `transfer_cus` plays the role of `transfer_sms` (compute units the
- * zero-copy kernel may occupy; -1 = automatic).
+ * zero-copy kernel may occupy; -1 = automatic: 8, or 4 for device-to-host
+ * calls of 64 MiB and more whose chunks are whole multiples of 4 KiB).
  *
  * Host requirements (checked; violations return hipErrorInvalidValue):
  *   - gpu_block_ids, cpu_block_ids: host memory, num_blocks int64 each,
