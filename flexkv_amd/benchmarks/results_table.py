@@ -137,7 +137,7 @@ def table(p: dict, label: str) -> str:
          f"{cpu.get('value')} GB/s; one thread {cpu.get('single_thread_gbps')} GB/s |",
          f"| Reference copy-engine loop (one copy per chunk) | "
          f"{_f(p.get('ce_per_chunk_loop', {}).get('gbps'), 2)} GB/s |", "",
-         "## BASELINE configurations", "",
+         "## Benchmark configurations", "",
          "Fractions of the link are of the measured per-direction peak; piece and device",
          "fractions are of the 8 TB/s HBM peak.", "",
          "| Configuration | Copy-engine D2H / H2D GB/s | of link | Zero-copy D2H / H2D GB/s | "
