@@ -150,8 +150,10 @@ def test_geometries_match_oracle(dev, geo, mode):
     check_case(case, gids, cids, mode)
 
 
-@pytest.mark.parametrize("kv,layers,n", [(2, 8, 504), (2, 8, 520), (1, 9, 925), (1, 9, 939)],
-                         ids=["kv-31.5MiB", "kv-32.5MiB", "mla-32.5MiB-odd", "mla-33MiB-odd"])
+@pytest.mark.parametrize("kv,layers,n", [(2, 8, 504), (2, 8, 520), (1, 9, 925), (1, 9, 939),
+                                         (1, 9, 1851)],
+                         ids=["kv-31.5MiB", "kv-32.5MiB", "mla-32.5MiB-odd", "mla-33MiB-odd",
+                              "mla-65MiB-odd"])
 def test_zero_copy_variants_at_the_size_policy_edges(dev, kv, layers, n):
     """Kernel-mode calls on either side of the sizes where the zero-copy
     kernel changes variant: host-to-device calls take the whole-group kernel
@@ -159,10 +161,11 @@ def test_zero_copy_variants_at_the_size_policy_edges(dev, kv, layers, n):
     whole-group kernel of two 4-row sub-groups (4 CUs from 64 MiB).  4 KiB
     chunks; the MLA-shaped calls move an odd number of chunks (9 layers), so
     a group's second sub-group can lie past the end of a launch."""
-    case = KVCase(layers_total=layers, num_layers=layers, start_layer=0, kv=kv, ng=1200,
-                  nh=1300, tokens=16, heads=1, dim=128).fill(seed=kv * 1000 + n)
-    gids = inputs.distinct_ids(n + 5, n, 1200)
-    cids = inputs.distinct_ids(n + 6, n, 1300)
+    ng = max(1200, n + 200)
+    case = KVCase(layers_total=layers, num_layers=layers, start_layer=0, kv=kv, ng=ng,
+                  nh=ng + 100, tokens=16, heads=1, dim=128).fill(seed=kv * 1000 + n)
+    gids = inputs.distinct_ids(n + 5, n, ng)
+    cids = inputs.distinct_ids(n + 6, n, ng + 100)
     check_case(case, gids, cids, 0)
 
 
