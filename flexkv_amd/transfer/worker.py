@@ -27,7 +27,7 @@ import threading
 import time
 from abc import ABC, abstractmethod
 from multiprocessing.connection import Connection
-from typing import Any, Dict, List, Optional, Sequence, Union
+from typing import Any, Dict, List, Optional, Sequence, Tuple, Union
 
 import ctypes
 import numpy as np
@@ -405,6 +405,23 @@ class ThreadWorkerHandle(_WorkerHandleBase):
                               f"{self.STOP_GRACE_S:.0f} s; leaving it running")
 
 
+def _op_ids(src_block_ids: np.ndarray, dst_block_ids: np.ndarray,
+            transfer_type: TransferType, from_host: TransferType, to_host: TransferType,
+            worker: str) -> Tuple[np.ndarray, np.ndarray]:
+    """(ids on the worker's other tier, host cache ids) of one op: the host
+    cache is the source of `from_host` ops and the destination of `to_host`
+    ops (worker.py:272-283 for the GPU tier, :538-550 for SSD).  Ids are
+    int64 and pair up one to one; another op type is a ValueError."""
+    assert src_block_ids.dtype == np.int64 and dst_block_ids.dtype == np.int64, \
+        "block ids must be int64"
+    assert len(src_block_ids) == len(dst_block_ids), "source and destination ids must pair up"
+    if transfer_type == from_host:
+        return dst_block_ids, src_block_ids
+    if transfer_type == to_host:
+        return src_block_ids, dst_block_ids
+    raise ValueError(f"Invalid transfer type: {transfer_type} for {worker}")
+
+
 class GPUCPUTransferWorker(TransferWorkerBase):
     """Moves KV blocks between one GPU's per-layer cache and the host cache
     (worker.py:207-342; single GPU, no TP)."""
@@ -467,17 +484,12 @@ class GPUCPUTransferWorker(TransferWorkerBase):
     def _transfer_impl(self, src_block_ids: np.ndarray, dst_block_ids: np.ndarray,
                        transfer_type: TransferType, layer_id: int, layer_granularity: int,
                        **kwargs: Any) -> None:
-        assert src_block_ids.dtype == np.int64
-        assert dst_block_ids.dtype == np.int64
-        assert len(src_block_ids) == len(dst_block_ids)
+        gpu_ids, cpu_ids = _op_ids(src_block_ids, dst_block_ids, transfer_type,
+                                   TransferType.H2D, TransferType.D2H, "GPUCPUTransferWorker")
         if transfer_type == TransferType.H2D:
-            gpu_ids, cpu_ids = dst_block_ids, src_block_ids
             use_ce, sms = self.use_ce_transfer_h2d, self.transfer_sms_h2d
-        elif transfer_type == TransferType.D2H:
-            gpu_ids, cpu_ids = src_block_ids, dst_block_ids
-            use_ce, sms = self.use_ce_transfer_d2h, self.transfer_sms_d2h
         else:
-            raise ValueError(f"Invalid transfer type: {transfer_type} for GPUCPUTransferWorker")
+            use_ce, sms = self.use_ce_transfer_d2h, self.transfer_sms_d2h
         if len(gpu_ids) == 0:
             return
         if layer_id < 0 or layer_granularity < 1 or layer_id + layer_granularity > self.num_layers:
@@ -584,17 +596,12 @@ class tpGPUCPUTransferWorker(TransferWorkerBase):
     def _transfer_impl(self, src_block_ids: np.ndarray, dst_block_ids: np.ndarray,
                        transfer_type: TransferType, layer_id: int, layer_granularity: int,
                        **kwargs: Any) -> None:
-        assert src_block_ids.dtype == np.int64
-        assert dst_block_ids.dtype == np.int64
-        assert len(src_block_ids) == len(dst_block_ids)
+        gpu_ids, cpu_ids = _op_ids(src_block_ids, dst_block_ids, transfer_type,
+                                   TransferType.H2D, TransferType.D2H, "tpGPUCPUTransferWorker")
         if transfer_type == TransferType.H2D:
-            gpu_ids, cpu_ids = dst_block_ids, src_block_ids
             use_ce, sms = self.use_ce_transfer_h2d, self.transfer_sms_h2d
-        elif transfer_type == TransferType.D2H:
-            gpu_ids, cpu_ids = src_block_ids, dst_block_ids
-            use_ce, sms = self.use_ce_transfer_d2h, self.transfer_sms_d2h
         else:
-            raise ValueError(f"Invalid transfer type: {transfer_type} for tpGPUCPUTransferWorker")
+            use_ce, sms = self.use_ce_transfer_d2h, self.transfer_sms_d2h
         if len(gpu_ids) == 0:
             return
         self.tp_transfer_thread_group.tp_group_transfer(
@@ -670,15 +677,9 @@ class CPUSSDDiskTransferWorker(TransferWorkerBase):
     def _transfer_impl(self, src_block_ids: np.ndarray, dst_block_ids: np.ndarray,
                        transfer_type: TransferType, layer_id: int, layer_granularity: int,
                        **kwargs: Any) -> None:
-        assert src_block_ids.dtype == np.int64
-        assert dst_block_ids.dtype == np.int64
-        assert len(src_block_ids) == len(dst_block_ids)
-        if transfer_type == TransferType.H2DISK:
-            ssd_ids, cpu_ids = dst_block_ids, src_block_ids
-        elif transfer_type == TransferType.DISK2H:
-            ssd_ids, cpu_ids = src_block_ids, dst_block_ids
-        else:
-            raise ValueError(f"Invalid transfer type: {transfer_type} for CPUSSDDiskTransferWorker")
+        ssd_ids, cpu_ids = _op_ids(src_block_ids, dst_block_ids, transfer_type,
+                                   TransferType.H2DISK, TransferType.DISK2H,
+                                   "CPUSSDDiskTransferWorker")
         if len(ssd_ids) == 0:
             return
         if layer_id < 0 or layer_granularity < 1 or layer_id + layer_granularity > self.num_layers:
