@@ -337,7 +337,11 @@ int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, voi
  * from the caller instead of dp_group_id * num_ranks + r.  One transfer of a
  * group runs at a time; transfers of different groups may overlap.  Each
  * rank runs on the group's own stream, so work the caller queued elsewhere on
- * the same memory must be finished first. */
+ * the same memory must be finished first.
+ *
+ * fkv_tp_group_destroy: waits for a transfer of the group that is running,
+ * then stops the rank threads and destroys their streams.  The handle is
+ * gone when it returns: no call on it may start during or after it. */
 typedef struct fkv_tp_group_s* fkv_tp_group_t;
 int fkv_tp_group_create(int num_ranks, const int* devices, void* const* gpu_layer_ptrs,
                         int num_layers, void* cpu_ptr, fkv_tp_group_t* out);
