@@ -9,6 +9,8 @@ the HIP C-ABI entry ``fkv_transfer_kv_blocks``.
 """
 from __future__ import annotations
 
+import contextlib
+
 import torch
 
 from . import _lib
@@ -390,9 +392,13 @@ class TPTransferThreadGroup:
     def __init__(self, num_gpus: int, gpu_blocks, cpu_blocks: torch.Tensor,
                  dp_group_id: int) -> None:
         import ctypes
+        import threading
 
         self._h = None
         self._gen = _lib.generation
+        # held across each transfer and by close(), so a close() from another
+        # thread cannot free the group under a running call
+        self._lock = threading.Lock()
         if num_gpus < 1 or len(gpu_blocks) != num_gpus:
             raise ValueError(f"gpu_blocks needs one layer list per rank ({num_gpus})")
         num_layers = len(gpu_blocks[0])
@@ -428,27 +434,30 @@ class TPTransferThreadGroup:
         ``cpu_chunk_size_in_bytes`` only sizes the reference's log line.  Raises
         RuntimeError("tp_group_transfer failed: ...") naming the first failing
         rank, as the reference does (:107)."""
-        if self._h is None:
-            raise RuntimeError("TP transfer group is closed")
         _require_int64_host(gpu_block_id_tensor, "gpu_block_id_tensor")
         _require_int64_host(cpu_block_id_tensor, "cpu_block_id_tensor")
         n = gpu_block_id_tensor.numel()
         if cpu_block_id_tensor.numel() != n:
             raise ValueError("gpu and cpu block id tensors differ in length")
-        rc = _lib.load().fkv_tp_group_transfer(
-            self._h, n, gpu_block_id_tensor.data_ptr(), int(gpu_kv_stride_in_bytes),
-            int(gpu_block_stride_in_bytes), int(gpu_chunk_size_in_bytes),
-            cpu_block_id_tensor.data_ptr(), int(cpu_kv_stride_in_bytes),
-            int(cpu_layer_stride_in_bytes), int(cpu_block_stride_in_bytes), int(transfer_sms),
-            int(bool(is_host_to_device)), int(use_ce_transfer), int(layer_id),
-            int(layer_granularity), int(bool(is_mla)))
-        if rc != 0:
-            raise RuntimeError("tp_group_transfer failed: " + _lib.last_error())
+        with self._lock:
+            if self._h is None:
+                raise RuntimeError("TP transfer group is closed")
+            rc = _lib.load().fkv_tp_group_transfer(
+                self._h, n, gpu_block_id_tensor.data_ptr(), int(gpu_kv_stride_in_bytes),
+                int(gpu_block_stride_in_bytes), int(gpu_chunk_size_in_bytes),
+                cpu_block_id_tensor.data_ptr(), int(cpu_kv_stride_in_bytes),
+                int(cpu_layer_stride_in_bytes), int(cpu_block_stride_in_bytes),
+                int(transfer_sms), int(bool(is_host_to_device)), int(use_ce_transfer),
+                int(layer_id), int(layer_granularity), int(bool(is_mla)))
+            if rc != 0:
+                raise RuntimeError("tp_group_transfer failed: " + _lib.last_error())
 
     def close(self) -> None:
-        h, self._h = self._h, None
-        if h and self._gen == _lib.generation:   # else finalize destroyed it already
-            _lib.check(_lib.load().fkv_tp_group_destroy(h), "fkv_tp_group_destroy")
+        lock = getattr(self, "_lock", None)   # None: __init__ failed before making it
+        with lock if lock is not None else contextlib.nullcontext():
+            h, self._h = self._h, None
+            if h and self._gen == _lib.generation:   # else finalize destroyed it already
+                _lib.check(_lib.load().fkv_tp_group_destroy(h), "fkv_tp_group_destroy")
 
     def __del__(self) -> None:
         try:

@@ -161,6 +161,43 @@ def test_tp_group_error_names_the_rank():
         case.move(grp, gids, cids, False, False)
 
 
+def test_close_from_another_thread_waits_for_the_transfer():
+    """close() from a second thread while the first keeps transferring:
+    every transfer that starts finishes whole (the group is freed only
+    between transfers), the ones after close() raise, and the last D2H's host
+    bytes match the oracle."""
+    import threading
+
+    case = TpCase(4, "BLOCKWISE", False, seed=9)
+    gids = inputs.distinct_ids(41, 24, case.ng)
+    cids = inputs.distinct_ids(42, 24, case.nh)
+    grp = case.group()
+    done, refused, errors = [], [], []
+
+    def mover():
+        for _ in range(200):
+            try:
+                case.move(grp, gids, cids, False, False)
+                done.append(1)
+            except RuntimeError as e:
+                (refused if "closed" in str(e) else errors).append(str(e))
+                return
+
+    t = threading.Thread(target=mover)
+    t.start()
+    while not done:
+        time.sleep(0.001)
+    grp.close()
+    t.join(timeout=60)
+    assert not t.is_alive() and not errors, errors
+    assert done and len(done) + len(refused) <= 200
+    want = np.zeros(case.shape, np.uint16)
+    case.oracle([[a.copy() for a in r] for r in case.np_ranks], want, gids, cids, False)
+    assert np.array_equal(case.host_np().reshape(case.shape), want)
+    with pytest.raises(RuntimeError, match="closed"):
+        case.move(grp, gids, cids, False, False)
+
+
 def test_two_groups_at_once():
     """Two data-parallel groups' transfers from two host threads at once,
     each group's ranks on their own host blocks (as dp groups own disjoint
