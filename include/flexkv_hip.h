@@ -221,7 +221,9 @@ int fkv_scatter_kv_blocks(int num_blocks, int num_layers, const int64_t* gpu_blo
  * Arguments and checks as in fkv_transfer_kv_blocks; the id lists and layer
  * pointers are copied before the call returns.  The caller keeps the GPU
  * cache and host cache alive until the handle is released;
- * fkv_handle_release waits for all groups and frees the handle.
+ * fkv_handle_release waits for all groups and frees the handle.  A handle
+ * may be waited on and queried from several threads, but its release must
+ * not overlap another call on it, and no call may follow it.
  *
  * The reference reaches the same layer-wise schedule with one synchronous
  * call per layer group (worker.py:293-295, layer-wise ops of
@@ -299,6 +301,9 @@ typedef struct {
   int64_t fallbacks;
 } fkv_ssd_stats;
 int fkv_ssd_stats_read(fkv_ssd_t h, fkv_ssd_stats* out);
+/* Closes the files and frees the context: no transfer on it may be running
+ * or start afterwards (transfers on one context from several threads are
+ * fine; they take turns on its ring). */
 int fkv_ssd_close(fkv_ssd_t h);
 int fkv_transfer_kv_blocks_ssd(fkv_ssd_t h, int start_layer, int num_layers, void* cpu_ptr,
                                const int64_t* ssd_block_ids, const int64_t* cpu_block_ids,
