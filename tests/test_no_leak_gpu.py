@@ -84,3 +84,29 @@ def test_repeated_layerwise_handles_hold_no_memory(setup, ce):
     rss1, free1 = _snapshot()
     assert rss1 - rss0 < (8 << 20), f"host memory grew {(rss1 - rss0) >> 10} KiB"
     assert free0 - free1 < (16 << 20), f"device memory fell {(free0 - free1) >> 20} MiB"
+
+
+def test_tp_groups_release_threads_and_streams(setup):
+    """Creating, using and closing TP groups leaves the process's thread
+    count and the device's free memory where they were."""
+    layers, ptrs, host, (gkv, gblk, ckv, clay, cblk, chunk) = setup
+    gids = torch.from_numpy(inputs.distinct_ids(11, 16, NG))
+    cids = torch.from_numpy(inputs.distinct_ids(12, 16, NH))
+    ranks = [layers] * 2           # two ranks on one GPU, same caches (reads only)
+
+    def groups(k):
+        for _ in range(k):
+            g = c_ext.TPTransferThreadGroup(2, ranks, host, 0)
+            # D2H of half chunks: rank r into bytes [r * chunk / 2, ...) of each
+            g.tp_group_transfer(gids, gkv, gblk, chunk // 2, cids, ckv, clay, cblk, chunk, -1,
+                                False, False, 0, L, False)
+            g.close()
+
+    groups(3)
+    proc = psutil.Process(os.getpid())
+    threads0 = proc.num_threads()
+    _, free0 = _snapshot()
+    groups(30)
+    _, free1 = _snapshot()
+    assert proc.num_threads() <= threads0 + 2, (threads0, proc.num_threads())   # 2 rank threads each would add 60
+    assert free0 - free1 < (16 << 20), f"device memory fell {(free0 - free1) >> 20} MiB"

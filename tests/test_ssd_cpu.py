@@ -691,3 +691,22 @@ def test_random_geometries_match_oracle(tmp_path_factory, layout, mla, n_dev, mb
     c["worker"]._transfer_impl(sids, dst, TransferType.DISK2H, start, nl)
     assert np.array_equal(c["host"], expect)
     c["worker"].close()
+
+
+@pytest.mark.parametrize("entries", [0, 8])
+def test_contexts_release_their_files(tmp_path, entries):
+    """Opening and closing contexts (threads, and a ring where the kernel
+    allows one) leaves the process's open descriptors where they were."""
+    import psutil
+    paths = []
+    for i in range(3):
+        p = tmp_path / f"f{i}.bin"
+        p.write_bytes(b"\0" * 8192)
+        paths.append(str(p))
+    proc = psutil.Process(os.getpid())
+    c_ext.SSDIOCTX({0: paths[:2], 1: paths[1:]}, 2, iouring_entries=entries).close()
+    before = proc.num_fds()
+    for _ in range(100):
+        ctx = c_ext.SSDIOCTX({0: paths[:2], 1: paths[1:]}, 2, iouring_entries=entries)
+        ctx.close()
+    assert proc.num_fds() == before
