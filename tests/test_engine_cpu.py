@@ -208,3 +208,18 @@ def test_engine_multiple_graphs_and_virtual(fake_engine):
         assert sorted(k for _, k, _ in worker.log) == ["D2H", "H2D"]
     finally:
         eng.shutdown()
+
+
+def test_engine_shutdown_leaves_no_threads(fake_engine):
+    """Engines started and shut down one after another (thread-mode workers
+    and the scheduler) leave the process's threads where they were."""
+    import threading
+    make, _ = fake_engine
+    eng = make(True)
+    eng.shutdown()
+    before = {t.ident for t in threading.enumerate()}
+    for _ in range(5):
+        eng = make(True)
+        eng.shutdown()
+    left = [t.name for t in threading.enumerate() if t.ident not in before and t.is_alive()]
+    assert not left, left
