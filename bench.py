@@ -802,14 +802,14 @@ def overlap_with_compute(wl: Workload, steps: int = 3, gemms: int = 160,
     b = torch.randn(4096, 4096, device=wl.dev, dtype=torch.bfloat16)
     c = torch.empty(8192, 4096, device=wl.dev, dtype=torch.bfloat16)
 
-    def once(h2d, ce, with_xfer=True, window=gemm_window):
+    def once(h2d, ce, with_xfer=True, window=gemm_window, cus=-1):
         torch.cuda.synchronize()
         res = {}
 
         def move():
             with torch.cuda.stream(xfer):
                 t0 = time.perf_counter()
-                wl.transfer(h2d, ce)
+                wl.transfer(h2d, ce, cus)
                 res["xfer"] = time.perf_counter() - t0
 
         def start():
@@ -850,6 +850,18 @@ def overlap_with_compute(wl: Workload, steps: int = 3, gemms: int = 160,
             finally:
                 if ce and rect_copies:
                     c_ext.set_copy_engine_policy(layerwise_scattered="unset")
+    # The zero-copy H2D with its grid spread over the chip (transfer_cus = a
+    # CU count / 8: about one workgroup per compute unit) instead of 8 CUs'
+    # worth: the automatic grid keeps 8, and this shows the trade.
+    spread = max(1, torch.cuda.get_device_properties(wl.dev).multi_processor_count // 8)
+    for key, window, store, alone in (("h2d_kernel_spread", gemm_window, out, out),
+                                      ("h2d_kernel_spread", gemm_window_transfer_first, tf,
+                                       tf)):
+        rs = [once(True, False, True, window, cus=spread) for _ in range(steps)]
+        store[key] = {"gemm_ms": med_ms(rs, "gemm"), "transfer_ms": med_ms(rs, "xfer"),
+                      "gemm_slowdown": round(med_ms(rs, "gemm") / alone["gemm_alone_ms"], 4),
+                      "transfer_gbps": round(wl.bytes_per_op / med_ms(rs, "xfer") / 1e6, 2),
+                      "transfer_cus": spread}
     if resident_probe:
         spin = resident_spin_probe(a, b, c, comp, steps, gemms)
         out["resident_spin"] = {k: v for k, v in spin.items() if k != "transfer_first"}

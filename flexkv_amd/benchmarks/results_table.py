@@ -162,7 +162,9 @@ def table(p: dict, label: str) -> str:
               f"{'yes' if tpg.get('bit_exact') else 'no'}."]
     L += ["", "## Beside compute", "",
           "160 bf16 GEMMs [8192x4096]x[4096x4096] beside one 2 GiB transfer, against the same",
-          "GEMMs alone started the same way.", "",
+          "GEMMs alone started the same way. `h2d_kernel_spread`: the zero-copy H2D with its",
+          "grid spread over the chip (`transfer_cus` = CUs / 8, about one workgroup per CU)",
+          "instead of the automatic 8 CUs' worth.", "",
           "| Host cache | Path | Transfer GB/s | GEMMs first | Transfer first |",
           "|---|---|---|---|---|"]
     L += overlap_rows(p.get("overlap_with_compute", {}), "block-wise")
