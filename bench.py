@@ -866,6 +866,12 @@ def overlap_with_compute(wl: Workload, steps: int = 3, gemms: int = 160,
         spin = resident_spin_probe(a, b, c, comp, steps, gemms)
         out["resident_spin"] = {k: v for k, v in spin.items() if k != "transfer_first"}
         tf["resident_spin"] = spin["transfer_first"]
+        for key, grid, block in (("resident_sleep_1wave", 1, 64),
+                                 ("resident_sleep_256wg", 256, 256)):
+            res = resident_sleep_probe(a, b, c, comp, steps, gemms, grid, block)
+            if res is None:
+                break
+            out[key], tf[key] = res
     c_ext.release_transfer_stream(xfer)
     out["transfer_first"] = tf
     out["what"] = (f"{gemms} GEMMs on a compute stream beside one {wl.bytes_per_op / 2**30:.0f} "
@@ -922,6 +928,46 @@ def resident_spin_probe(a, b, c, comp, steps: int, gemms: int, target_ms: float 
     res["what"] = ("torch.cuda._sleep: one workgroup of one thread spinning on the clock, "
                    "no memory access, started as the transfer would be")
     return res
+
+
+def resident_sleep_probe(a, b, c, comp, steps: int, gemms: int, grid: int, block: int,
+                         target_ms: float = 38.0):
+    """The GEMM windows beside a kernel whose wavefronts only sleep
+    (flexkv_amd/libresident_probe.so: s_sleep between wall-clock reads for
+    target_ms, no memory access), `grid` workgroups of `block` threads, in
+    both launch orders against GEMMs alone started the same way.  Set beside
+    resident_spin, it shows whether a resident kernel costs the GEMMs by what
+    it issues or by occupying compute units.  None when the probe library is
+    not built."""
+    import ctypes
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "flexkv_amd",
+                        "libresident_probe.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    lib.fkv_probe_resident.argtypes = [ctypes.c_void_p, ctypes.c_double, ctypes.c_int,
+                                       ctypes.c_int]
+    side = torch.cuda.Stream()
+
+    def start():
+        rc = lib.fkv_probe_resident(ctypes.c_void_p(side.cuda_stream), target_ms, grid, block)
+        if rc != 0:
+            raise RuntimeError(f"fkv_probe_resident failed ({rc})")
+
+    def med(fn):
+        return round(statistics.median(fn() for _ in range(steps)), 2)
+    out = []
+    for window in (gemm_window, gemm_window_transfer_first):
+        alone = med(lambda: window(a, b, c, comp, None, gemms)[0])
+
+        def beside():
+            ms = window(a, b, c, comp, start, gemms)[0]
+            side.synchronize()
+            return ms
+        ms = med(beside)
+        out.append({"gemm_alone_ms": alone, "gemm_ms": ms, "gemm_slowdown": round(ms / alone, 4),
+                    "grid": grid, "block": block})
+    return out[0], out[1]
 
 
 def request_batch(wl: Workload, steps: int, num_requests: int = 32, max_blocks: int = 128):

@@ -84,6 +84,11 @@ def overlap_rows(o: dict, label: str) -> list:
         rows.append(f"| {label} | one-thread spin kernel (no memory access) | — | "
                     f"{_f(o['resident_spin'].get('gemm_slowdown'), 3)} | "
                     f"{_f(tf.get('resident_spin', {}).get('gemm_slowdown'), 3)} |")
+    for key, what in (("resident_sleep_1wave", "one sleeping wavefront (no memory access)"),
+                      ("resident_sleep_256wg", "256 sleeping workgroups of 256 threads")):
+        if key in o:
+            rows.append(f"| {label} | {what} | — | {_f(o[key].get('gemm_slowdown'), 3)} | "
+                        f"{_f(tf.get(key, {}).get('gemm_slowdown'), 3)} |")
     return rows
 
 

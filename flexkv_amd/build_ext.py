@@ -2,8 +2,10 @@
 program that measures the device's plain read / write / copy rates
 (bench.py reports them beside the gather's roofline), and the call_latency
 program that times small fkv_transfer_kv_blocks calls against the launch
-floors beside them, and the CPython module _fkv_py (host C++ against torch's
-headers, built with g++) that carries c_ext.transfer_kv_blocks' per-call path.
+floors beside them, libresident_probe.so (a kernel that only occupies compute
+units, which bench.py runs beside GEMMs), and the CPython module _fkv_py (host
+C++ against torch's headers, built with g++) that carries
+c_ext.transfer_kv_blocks' per-call path.
 
     python -m flexkv_amd.build_ext
 """
@@ -25,6 +27,8 @@ CEILING_SOURCE = os.path.join(HERE, "csrc", "hbm_ceiling.hip")
 CEILING_OUT = os.path.join(HERE, "hbm_ceiling")
 LATENCY_SOURCE = os.path.join(HERE, "csrc", "call_latency.hip")
 LATENCY_OUT = os.path.join(HERE, "call_latency")
+PROBE_SOURCE = os.path.join(HERE, "csrc", "resident_probe.hip")
+PROBE_OUT = os.path.join(HERE, "libresident_probe.so")
 PY_SOURCE = os.path.join(HERE, "csrc", "py_fastcall.cpp")
 PY_OUT = os.path.join(HERE, "_fkv_py" + sysconfig.get_config_var("EXT_SUFFIX"))
 ARCH = "gfx950"
@@ -59,6 +63,11 @@ def latency_command() -> list:
             "-Wl,-rpath,$ORIGIN"]
 
 
+def probe_command() -> list:
+    return [hipcc(), f"--offload-arch={ARCH}", *COMMON, "-fPIC", "-shared", PROBE_SOURCE,
+            "-o", PROBE_OUT + ".tmp"]
+
+
 def py_command() -> list:
     import torch
     tdir = os.path.dirname(os.path.abspath(torch.__file__))
@@ -88,6 +97,7 @@ def build(verbose: bool = False) -> str:
     _run(command(), OUT, verbose)
     _run(ceiling_command(), CEILING_OUT, verbose)
     _run(latency_command(), LATENCY_OUT, verbose)
+    _run(probe_command(), PROBE_OUT, verbose)
     _run(py_command(), PY_OUT, verbose)
     return OUT
 
