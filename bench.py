@@ -1370,8 +1370,9 @@ KERNEL_SECTION_END = b"// A system-scope acquire in every workgroup."
 def kernel_section_sha16(path: str = KERNEL_SOURCE) -> str:
     """sha256 prefix of the transfer kernels' source: kv_transfer.hip from its
     start (build macros, CopyArgs, PackArgs) to the end of the data-moving
-    kernels (kv_chunk_copy_kernel, kv_pack_kernel, stage_ids_kernel), the
-    part that decides which bytes the kernels read and write.  Comments,
+    kernels (kv_chunk_copy_kernel, kv_pack_kernel, kv_pack_span_kernel,
+    stage_ids_kernel), the part that decides which bytes the kernels read and
+    write.  Comments,
     blank lines and indentation are left out, so a change to a comment keeps
     the key and any change to the code changes it."""
     import hashlib

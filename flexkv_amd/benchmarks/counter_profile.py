@@ -42,9 +42,11 @@ def kind_of(name: str) -> str:
     """Which transfer kernel a dispatch is: staging gather / scatter,
     zero-copy D2H / H2D, or '' for anything else (the calibration copy,
     id staging, cache acquires, torch's own kernels)."""
-    if "kv_pack_kernel<false" in name or "kv_chunk_copy_kernel<false, true" in name:
+    if "kv_pack_kernel<false" in name or "kv_pack_span_kernel<false" in name or \
+            "kv_chunk_copy_kernel<false, true" in name:
         return "gather"
-    if "kv_pack_kernel<true" in name or "kv_chunk_copy_kernel<true, true" in name:
+    if "kv_pack_kernel<true" in name or "kv_pack_span_kernel<true" in name or \
+            "kv_chunk_copy_kernel<true, true" in name:
         return "scatter"
     if "kv_chunk_copy_kernel<false, false" in name or "kv_small_copy_kernel<false>" in name:
         return "zero_copy_d2h"

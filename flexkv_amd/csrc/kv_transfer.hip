@@ -82,8 +82,9 @@ namespace {
 // size 128 MiB / 256 MiB / 512 MiB / 2 GiB): gather 5.41/5.71/5.89/6.07
 // against 5.46/5.67/5.89/6.05 row by row; scatter 4.67/4.97/5.08/5.26
 // against 4.01/4.67/5.10/5.42.  So the scatter takes the whole-group
-// variant up to kWholeScatterMaxBytes per launch (every copy-engine piece)
-// and the row-by-row one above.
+// variant up to kWholeScatterMaxBytes per launch and the row-by-row one
+// above, where kv_pack_span_kernel does not take it (a packed side that is
+// not contiguous in row order; pack_shape).
 #ifndef FKV_WHOLE_GATHER
 #define FKV_WHOLE_GATHER 1
 #endif
@@ -476,6 +477,7 @@ struct PackArgs {
   uint32_t kv_dim;
   uint32_t num_layers;       // layers of the launch
   uint32_t num_groups;
+  uint32_t num_rows;         // packed rows of the launch
   int32_t ptrs_per_layer;    // 1: layer_ptr[l] + k*gpu_kv_stride; kv: layer_ptr[l*kv + k]
   uint64_t layer_ptr[kMaxLayersPerLaunch];
 };
@@ -543,6 +545,70 @@ __global__ __launch_bounds__(kThreads) void kv_pack_kernel(PackArgs a) {
       char* dst = kH2D ? chunk_base[j] + r * kRow : packed + (j * kR + r) * kRow;
       __builtin_nontemporal_store(v[j * kR + r], (gvec*)(dst + lane_off));
     }
+}
+
+// 32-row packed groups over chunks of 32 rows or more: group g moves packed
+// rows [32g, 32g + 32), fewer in the launch's last group.  They lie in chunk
+// c = 32g / rows_per_chunk and, past its end, in chunk c + 1, so a wavefront
+// holds at most two scattered bases (MLA's 72-row chunks: a group reads 32
+// rows of one chunk, or the tail of one and the head of the next).  Walk
+// order, id reads and accesses as in kv_pack_kernel.
+template <bool kH2D>
+__global__ __launch_bounds__(kThreads) void kv_pack_span_kernel(PackArgs a) {
+  constexpr int kU = 32;
+  constexpr int kRow = 64 * 16;
+  const uint32_t lane_off = (threadIdx.x & 63) * 16;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t g = blockIdx.x * kWaves + wave;
+  if (g >= a.num_groups) return;
+  const uint32_t rpc = a.rows_per_chunk;
+  const uint32_t row0 = g * kU;
+  const uint32_t c = row0 / rpc;
+  const uint32_t rr = row0 - c * rpc;
+  const uint32_t rows = min(static_cast<uint32_t>(kU), a.num_rows - row0);
+  const uint32_t head = min(rows, rpc - rr);   // rows of the group in chunk c
+  const uint32_t kv = a.kv_dim;
+  const uint32_t ppl = static_cast<uint32_t>(a.ptrs_per_layer);
+  uint32_t bi = c / a.items_per_block;
+  const uint32_t rem = c - bi * a.items_per_block;
+  uint32_t l = rem / kv;
+  uint32_t k = rem - l * kv;
+  const __attribute__((address_space(4))) int64_t* gids =
+      (const __attribute__((address_space(4))) int64_t*)a.gids;
+  int64_t gid = gids[bi];
+  // row r of the group lies at first + r * kRow (r < head) or next + r * kRow
+  char* const first = reinterpret_cast<char*>(a.layer_ptr[l * ppl + k * (ppl - 1)]) +
+                      static_cast<int64_t>(k) * a.gpu_kv_stride + gid * a.gpu_block_stride +
+                      static_cast<int64_t>(rr) * kRow;
+  char* next = first;
+  if (head < rows) {
+    if (++k == kv) {
+      k = 0;
+      if (++l == a.num_layers) {
+        l = 0;
+        gid = gids[++bi];
+      }
+    }
+    next = reinterpret_cast<char*>(a.layer_ptr[l * ppl + k * (ppl - 1)]) +
+           static_cast<int64_t>(k) * a.gpu_kv_stride + gid * a.gpu_block_stride -
+           static_cast<int64_t>(head) * kRow;
+  }
+  char* packed = a.packed + static_cast<int64_t>(g) * (kU * kRow);
+  u32x4 v[kU];
+#pragma unroll
+  for (int r = 0; r < kU; ++r) {
+    if (r < rows) {
+      const char* src = kH2D ? packed + r * kRow : (r < head ? first : next) + r * kRow;
+      v[r] = __builtin_nontemporal_load((const gvec*)(src + lane_off));
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kU; ++r) {
+    if (r < rows) {
+      char* dst = kH2D ? (r < head ? first : next) + r * kRow : packed + r * kRow;
+      __builtin_nontemporal_store(v[r], (gvec*)(dst + lane_off));
+    }
+  }
 }
 
 // Copies a transfer's (gpu_id, cpu_id) pairs from the pinned buffer into a
@@ -749,8 +815,9 @@ int ensure_device_basics(int dev) {
   return 0;
 }
 
-// Staging launches take kv_pack_kernel where their shape allows (1), or
-// the row-by-row / whole-group kv_chunk_copy_kernel throughout (0).
+// Staging launches take kv_pack_kernel / kv_pack_span_kernel where their
+// shape allows (1), or the row-by-row / whole-group kv_chunk_copy_kernel
+// throughout (0).
 #ifndef FKV_PACK_KERNEL
 #define FKV_PACK_KERNEL 1
 #endif
@@ -884,40 +951,55 @@ int auto_zero_copy_cus(const Geometry& g, bool h2d) {
              : kAutoZeroCopyCus;
 }
 
-// The kv_pack_kernel instantiation (kU, kC) for a staging launch of `nb`
-// blocks x `nl` layers with chunks of `rpc` full rows, or {0, 0} when the
-// row-by-row kernel has to take it.
+// The packed-row kernel for a staging launch of chunks of `rpc` full rows:
+// kv_pack_kernel<kU, kC>, kv_pack_span_kernel ({32, 0}), or {0, 0} when the
+// row-by-row or whole-group kv_chunk_copy_kernel takes it.
 struct PackShape {
   int u = 0, c = 0;
 };
-// Chunks of whole 32-row groups (32 KiB, 64 KiB, ...) keep the tiled
-// whole-group kernel: measured on MI355X at the Llama-3-8B shape it gathers
-// 0.3-1% faster than 32-row pack groups at 256 MiB-1 GiB (6.03 against 5.96
-// TB/s at 1 GiB) and in a copy-engine transfer's pieces moves the same
-// within 1% either way.
-PackShape pack_shape(int64_t rpc, int64_t chunks) {
-  if (rpc % 32 == 0) return {};
+// Measured on MI355X (HBM TB/s, interleaved A/B in one process):
+// - chunks of whole 32-row groups (32 KiB, 64 KiB, ...): gathers keep the
+//   tiled whole-group kernel (Llama-3-8B, 2 GiB: 6.07-6.10 against 6.01-6.08
+//   for 32-row span groups); scatters take the span kernel (5.53-5.54 against
+//   5.47-5.50; the copy-engine path's pieces 0.628 -> 0.650 of 8 TB/s);
+// - longer chunks that are not (MLA's 72 rows): 32-row span groups gather
+//   6.15-6.20 and scatter 5.70 against 5.60-5.62 and 5.48-5.49 for 36-row
+//   kv_pack_kernel groups (pieces: gather 0.695 -> 0.731, scatter 0.665 ->
+//   0.682);
+// - 4-16 KiB chunks: groups of 32 / rpc whole chunks.
+PackShape pack_shape(int64_t rpc, int64_t chunks, bool h2d) {
+  if (rpc % 32 == 0) return h2d ? PackShape{32, 0} : PackShape{};
+  if (rpc > 32) return {32, 0};
   for (int c : {2, 4, 8})
     if (rpc * c == 32 && chunks % c == 0) return {32, c};
-  if (rpc % 36 == 0) return {36, 1};
-  if (rpc % 24 == 0) return {24, 1};
+  if (rpc == 24) return {24, 1};
   return {};
 }
 
-// Launch kv_pack_kernel<kH2D, kU, kC> over `groups` groups.
-// Dynamic LDS (unused by the kernel) that holds the 36- and 24-row variants
-// to one workgroup per compute unit.  Measured on MI355X with MLA's 72 KiB
-// chunks, HBM TB/s of 506 MiB / 1 GiB launches, capped / uncapped: 36-row
-// groups gather 5.62-5.64 / 5.51-5.52 and 5.60-5.63 / 5.47-5.52, scatter
-// 5.29-5.30 / 5.27-5.30; 24-row groups gather 5.53 / 5.47 and 5.53-5.56 /
-// 5.42.  The 32-row variants gained nothing from such a cap.
+// Dynamic LDS (unused by the kernels) that holds the span kernel and the
+// 24-row variant to one workgroup per compute unit.  Measured on MI355X,
+// capped / uncapped HBM TB/s: span groups gather 6.15-6.20 / 5.94-5.96 (MLA)
+// and 6.01-6.08 / 5.77-5.83 (Llama-3-8B), scatter 5.70-5.71 / 5.61-5.65 and
+// 5.53-5.54 / 5.37-5.43; two workgroups per CU (64 KiB) fall between; 24-row
+// groups gather 5.53 / 5.47.  The 4-16 KiB chunk groups gain nothing from it
+// (the Llama-3-70B TP-8 shard: gather 5.92-5.98 / 5.96-6.02, scatter 5.29 /
+// 5.24-5.28).
 constexpr unsigned kPackLdsOneGroup = 84 << 10;
 
+// Launch kv_pack_kernel<kH2D, kU, kC> over the launch's groups.
 template <bool kH2D, int kU, int kC>
 void launch_pack(const PackArgs& pa, hipStream_t stream, hipEvent_t ea, hipEvent_t eb) {
   const uint32_t grid = (pa.num_groups + kWaves - 1) / kWaves;
   hipExtLaunchKernelGGL((kv_pack_kernel<kH2D, kU, kC>), dim3(grid), dim3(kThreads),
                         kU != 32 ? kPackLdsOneGroup : 0u, stream, ea, eb, 0, pa);
+}
+
+// Launch kv_pack_span_kernel<kH2D> over the launch's groups.
+template <bool kH2D>
+void launch_pack_span(const PackArgs& pa, hipStream_t stream, hipEvent_t ea, hipEvent_t eb) {
+  const uint32_t grid = (pa.num_groups + kWaves - 1) / kWaves;
+  hipExtLaunchKernelGGL((kv_pack_span_kernel<kH2D>), dim3(grid), dim3(kThreads),
+                        kPackLdsOneGroup, stream, ea, eb, 0, pa);
 }
 
 // Fill the per-launch part of CopyArgs and launch over `nb` blocks starting at
@@ -938,15 +1020,16 @@ int launch_copy(const Geometry& g, const IdBuf& ids, char* cpu_base, int64_t cks
     return fail(kInval, "internal: a launch of %d layers exceeds the %d layer pointers of the "
                 "kernel arguments", nl, kMaxLayersPerLaunch / g.ptrs_per_layer);
   // Staging launches whose packed side is contiguous in row order, with full
-  // rows and ids in device memory, take kv_pack_kernel.
+  // rows and ids in device memory, take kv_pack_kernel or kv_pack_span_kernel
+  // where pack_shape says so.
   if constexpr (kIota) {
     const int64_t rpc = g.chunk / (64 * 16);
     const bool packed_rows = FKV_PACK_KERNEL && split > 0 && g.chunk % (64 * 16) == 0 &&
                              (g.kv == 1 || cks == g.chunk) && cls == g.kv * g.chunk &&
                              cbs == static_cast<int64_t>(nl) * cls;
     const int64_t chunks = static_cast<int64_t>(nb) * nl * g.kv;
-    const PackShape shape = packed_rows ? pack_shape(rpc, chunks) : PackShape{};
-    if (shape.u > 0 && chunks * rpc <= UINT32_MAX) {
+    const PackShape shape = packed_rows ? pack_shape(rpc, chunks, kH2D) : PackShape{};
+    if (shape.u > 0 && chunks * rpc + shape.u <= UINT32_MAX) {
       PackArgs pa;
       memset(&pa, 0, sizeof(pa));
       pa.gids = reinterpret_cast<const int64_t*>(ids.dev) + b0;
@@ -957,7 +1040,8 @@ int launch_copy(const Geometry& g, const IdBuf& ids, char* cpu_base, int64_t cks
       pa.items_per_block = static_cast<uint32_t>(nl * g.kv);
       pa.kv_dim = static_cast<uint32_t>(g.kv);
       pa.num_layers = static_cast<uint32_t>(nl);
-      pa.num_groups = static_cast<uint32_t>(chunks * rpc / shape.u);
+      pa.num_rows = static_cast<uint32_t>(chunks * rpc);
+      pa.num_groups = (pa.num_rows + shape.u - 1) / shape.u;   // whole groups but for span launches
       pa.ptrs_per_layer = g.ptrs_per_layer;
       for (int i = 0; i < nl * g.ptrs_per_layer; ++i)
         pa.layer_ptr[i] = reinterpret_cast<uint64_t>(g.layer_ptrs[l0 * g.ptrs_per_layer + i]);
@@ -970,8 +1054,8 @@ int launch_copy(const Geometry& g, const IdBuf& ids, char* cpu_base, int64_t cks
         case 32 * 16 + 2: launch_pack<kH2D, 32, 2>(pa, stream, ea, eb); break;
         case 32 * 16 + 4: launch_pack<kH2D, 32, 4>(pa, stream, ea, eb); break;
         case 32 * 16 + 8: launch_pack<kH2D, 32, 8>(pa, stream, ea, eb); break;
-        case 36 * 16 + 1: launch_pack<kH2D, 36, 1>(pa, stream, ea, eb); break;
-        default: launch_pack<kH2D, 24, 1>(pa, stream, ea, eb); break;
+        case 24 * 16 + 1: launch_pack<kH2D, 24, 1>(pa, stream, ea, eb); break;
+        default: launch_pack_span<kH2D>(pa, stream, ea, eb); break;
       }
       FKV_HIP(hipGetLastError());
       return 0;
