@@ -464,8 +464,8 @@ __global__ __launch_bounds__(kThreads) void kv_chunk_copy_kernel(CopyArgs a) {
 // moves group 4b + w: no tile, no LDS, no barrier, and every wavefront moves
 // a full group.  A group is kC whole chunks of kU / kC rows (kC > 1: chunks
 // of 4-16 KiB, e.g. the Llama-3-70B TP-8 shard's 4 KiB) or kU rows inside
-// one chunk (kC == 1: chunks of a multiple of kU rows, e.g. MLA's 72 rows
-// at kU = 36).  The host checks the shape: full 1 KiB
+// one chunk (kC == 1: 24 KiB chunks at kU = 24).  The host checks the
+// shape: full 1 KiB
 // rows, whole groups, a contiguous packed side, ids in device memory.
 struct PackArgs {
   const int64_t* gids;       // device memory: gpu id of launch block i at gids[i]
