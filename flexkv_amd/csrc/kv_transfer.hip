@@ -547,13 +547,16 @@ __global__ __launch_bounds__(kThreads) void kv_pack_kernel(PackArgs a) {
     }
 }
 
-// 32-row packed groups over chunks of 32 rows or more: group g moves packed
+// 32-row packed groups over chunks of 8 rows or more: group g moves packed
 // rows [32g, 32g + 32), fewer in the launch's last group.  They lie in chunk
-// c = 32g / rows_per_chunk and, past its end, in chunk c + 1, so a wavefront
-// holds at most two scattered bases (MLA's 72-row chunks: a group reads 32
-// rows of one chunk, or the tail of one and the head of the next).  Walk
-// order, id reads and accesses as in kv_pack_kernel.
-template <bool kH2D>
+// c = 32g / rows_per_chunk and the chunks after it, at most kB = 2 + 30 /
+// rows_per_chunk chunks in all (2 from 31 rows per chunk, 3 from 16, 4 from
+// 11, 5 from 8; span_bases), so a wavefront
+// holds kB bases and picks one per row with wave-uniform compares (MLA's
+// 72-row chunks: a group reads 32 rows of one chunk, or the tail of one and
+// the head of the next).  Walk order, id reads and accesses as in
+// kv_pack_kernel.
+template <bool kH2D, int kB>
 __global__ __launch_bounds__(kThreads) void kv_pack_span_kernel(PackArgs a) {
   constexpr int kU = 32;
   constexpr int kRow = 64 * 16;
@@ -566,7 +569,6 @@ __global__ __launch_bounds__(kThreads) void kv_pack_span_kernel(PackArgs a) {
   const uint32_t c = row0 / rpc;
   const uint32_t rr = row0 - c * rpc;
   const uint32_t rows = min(static_cast<uint32_t>(kU), a.num_rows - row0);
-  const uint32_t head = min(rows, rpc - rr);   // rows of the group in chunk c
   const uint32_t kv = a.kv_dim;
   const uint32_t ppl = static_cast<uint32_t>(a.ptrs_per_layer);
   uint32_t bi = c / a.items_per_block;
@@ -576,36 +578,52 @@ __global__ __launch_bounds__(kThreads) void kv_pack_span_kernel(PackArgs a) {
   const __attribute__((address_space(4))) int64_t* gids =
       (const __attribute__((address_space(4))) int64_t*)a.gids;
   int64_t gid = gids[bi];
-  // row r of the group lies at first + r * kRow (r < head) or next + r * kRow
-  char* const first = reinterpret_cast<char*>(a.layer_ptr[l * ppl + k * (ppl - 1)]) +
-                      static_cast<int64_t>(k) * a.gpu_kv_stride + gid * a.gpu_block_stride +
-                      static_cast<int64_t>(rr) * kRow;
-  char* next = first;
-  if (head < rows) {
-    if (++k == kv) {
-      k = 0;
-      if (++l == a.num_layers) {
-        l = 0;
-        gid = gids[++bi];
+  // Row r of the group lies at base[j] + r * kRow for the last j with
+  // edge[j] <= r: chunk c + j starts at group row edge[j] (edge[0] = 0).
+  char* base[kB];
+  uint32_t edge[kB];
+  base[0] = reinterpret_cast<char*>(a.layer_ptr[l * ppl + k * (ppl - 1)]) +
+            static_cast<int64_t>(k) * a.gpu_kv_stride + gid * a.gpu_block_stride +
+            static_cast<int64_t>(rr) * kRow;
+  edge[0] = 0;
+#pragma unroll
+  for (int j = 1; j < kB; ++j) {
+    edge[j] = rpc - rr + (j - 1) * rpc;
+    base[j] = base[j - 1];
+    if (edge[j] < rows) {
+      if (++k == kv) {
+        k = 0;
+        if (++l == a.num_layers) {
+          l = 0;
+          gid = gids[++bi];
+        }
       }
+      base[j] = reinterpret_cast<char*>(a.layer_ptr[l * ppl + k * (ppl - 1)]) +
+                static_cast<int64_t>(k) * a.gpu_kv_stride + gid * a.gpu_block_stride -
+                static_cast<int64_t>(edge[j]) * kRow;
     }
-    next = reinterpret_cast<char*>(a.layer_ptr[l * ppl + k * (ppl - 1)]) +
-           static_cast<int64_t>(k) * a.gpu_kv_stride + gid * a.gpu_block_stride -
-           static_cast<int64_t>(head) * kRow;
   }
   char* packed = a.packed + static_cast<int64_t>(g) * (kU * kRow);
   u32x4 v[kU];
 #pragma unroll
   for (int r = 0; r < kU; ++r) {
     if (r < rows) {
-      const char* src = kH2D ? packed + r * kRow : (r < head ? first : next) + r * kRow;
+      char* b = base[0];
+#pragma unroll
+      for (int j = 1; j < kB; ++j)
+        if (r >= edge[j]) b = base[j];
+      const char* src = kH2D ? packed + r * kRow : b + r * kRow;
       v[r] = __builtin_nontemporal_load((const gvec*)(src + lane_off));
     }
   }
 #pragma unroll
   for (int r = 0; r < kU; ++r) {
     if (r < rows) {
-      char* dst = kH2D ? (r < head ? first : next) + r * kRow : packed + r * kRow;
+      char* b = base[0];
+#pragma unroll
+      for (int j = 1; j < kB; ++j)
+        if (r >= edge[j]) b = base[j];
+      char* dst = kH2D ? b + r * kRow : packed + r * kRow;
       __builtin_nontemporal_store(v[r], (gvec*)(dst + lane_off));
     }
   }
@@ -966,15 +984,23 @@ struct PackShape {
 //   6.15-6.20 and scatter 5.70 against 5.60-5.62 and 5.48-5.49 for 36-row
 //   kv_pack_kernel groups (pieces: gather 0.695 -> 0.731, scatter 0.665 ->
 //   0.682);
-// - 4-16 KiB chunks: groups of 32 / rpc whole chunks.
+// - 4-16 KiB chunks: groups of 32 / rpc whole chunks;
+// - other chunks of 8-31 rows: span groups with 3-5 bases (DeepSeek MLA at
+//   16 tokens per block, 18 KiB chunks: gather 6.03-6.07 and scatter
+//   5.41-5.43 against 5.48-5.49 and 5.14-5.15 for the two-walk kernel;
+//   pieces 0.656 -> 0.712 and 0.614 -> 0.644).
 PackShape pack_shape(int64_t rpc, int64_t chunks, bool h2d) {
   if (rpc % 32 == 0) return h2d ? PackShape{32, 0} : PackShape{};
   if (rpc > 32) return {32, 0};
   for (int c : {2, 4, 8})
     if (rpc * c == 32 && chunks % c == 0) return {32, c};
   if (rpc == 24) return {24, 1};
+  if (rpc >= 8) return {32, 0};
   return {};
 }
+
+// Chunks a 32-row span group can touch with chunks of `rpc` rows (rpc >= 8).
+int span_bases(int64_t rpc) { return 2 + static_cast<int>(30 / rpc); }
 
 // Dynamic LDS (unused by the kernels) that holds the span kernel and the
 // 24-row variant to one workgroup per compute unit.  Measured on MI355X,
@@ -994,11 +1020,11 @@ void launch_pack(const PackArgs& pa, hipStream_t stream, hipEvent_t ea, hipEvent
                         kU != 32 ? kPackLdsOneGroup : 0u, stream, ea, eb, 0, pa);
 }
 
-// Launch kv_pack_span_kernel<kH2D> over the launch's groups.
-template <bool kH2D>
+// Launch kv_pack_span_kernel<kH2D, kB> over the launch's groups.
+template <bool kH2D, int kB>
 void launch_pack_span(const PackArgs& pa, hipStream_t stream, hipEvent_t ea, hipEvent_t eb) {
   const uint32_t grid = (pa.num_groups + kWaves - 1) / kWaves;
-  hipExtLaunchKernelGGL((kv_pack_span_kernel<kH2D>), dim3(grid), dim3(kThreads),
+  hipExtLaunchKernelGGL((kv_pack_span_kernel<kH2D, kB>), dim3(grid), dim3(kThreads),
                         kPackLdsOneGroup, stream, ea, eb, 0, pa);
 }
 
@@ -1055,7 +1081,14 @@ int launch_copy(const Geometry& g, const IdBuf& ids, char* cpu_base, int64_t cks
         case 32 * 16 + 4: launch_pack<kH2D, 32, 4>(pa, stream, ea, eb); break;
         case 32 * 16 + 8: launch_pack<kH2D, 32, 8>(pa, stream, ea, eb); break;
         case 24 * 16 + 1: launch_pack<kH2D, 24, 1>(pa, stream, ea, eb); break;
-        default: launch_pack_span<kH2D>(pa, stream, ea, eb); break;
+        default:
+          switch (span_bases(rpc)) {
+            case 2: launch_pack_span<kH2D, 2>(pa, stream, ea, eb); break;
+            case 3: launch_pack_span<kH2D, 3>(pa, stream, ea, eb); break;
+            case 4: launch_pack_span<kH2D, 4>(pa, stream, ea, eb); break;
+            default: launch_pack_span<kH2D, 5>(pa, stream, ea, eb); break;
+          }
+          break;
       }
       FKV_HIP(hipGetLastError());
       return 0;

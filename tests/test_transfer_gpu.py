@@ -1071,21 +1071,25 @@ def test_c_ext_releases_the_gil(dev, use_ce):
                                  (3, 2, 40, 16, 1, 128, 13), (5, 2, 32, 16, 2, 128, 12),
                                  (3, 2, 32, 16, 4, 128, 9), (4, 1, 30, 16, 6, 128, 7),
                                  (3, 2, 16, 4, 1, 128, 6), (3, 2, 20, 16, 10, 128, 7),
-                                 (2, 1, 16, 33, 1, 512, 5)],
+                                 (2, 1, 16, 33, 1, 512, 5), (3, 1, 20, 18, 1, 512, 7),
+                                 (2, 2, 16, 12, 1, 512, 5), (3, 1, 16, 9, 1, 512, 5),
+                                 (3, 1, 16, 16, 1, 512, 5)],
                          ids=["8b-like", "130-layers", "mla", "48B-chunk", "mla-64KiB",
                               "4KiB-8-chunk-groups", "4KiB-ragged", "8KiB", "16KiB", "24KiB-mla",
-                              "1KiB", "40KiB", "33KiB-mla"])
+                              "1KiB", "40KiB", "33KiB-mla", "18KiB-mla", "12KiB", "9KiB-mla",
+                              "16KiB-odd"])
 @pytest.mark.parametrize("buffer_on_host", [False, True])
 def test_gather_scatter_match_oracle(dev, geo, buffer_on_host):
     """fkv_gather/scatter_kv_blocks against the oracle with the contiguous
     buffer described as a block-wise cache [n, L, kv, chunk] and ids 0..n-1.
     Every packed-row kernel shape is here: 32-row span groups over chunks of
-    72, 40 and 33 KiB (groups that cross into the next chunk, a short last
-    group) and, scattering, over 32 / 64 KiB chunks; 24 KiB (24-row groups);
-    16 / 8 / 4 KiB (groups of 2 / 4 / 8 whole chunks); the tiled whole-group
-    gather of 32 / 64 KiB chunks; and the row-by-row kernel's cases: partial
-    rows (128 B, 48 B), 1 KiB chunks, 4 KiB chunks whose count is not a
-    multiple of 8, more layers than one launch holds."""
+    72, 40 and 33 KiB (two bases), 18 and 16 KiB (three), 12 KiB (four), 9
+    and 8 KiB (five), with groups that cross chunk edges and a short last
+    group, and, scattering, over 32 / 64 KiB chunks; 24 KiB (24-row groups);
+    16 / 8 / 4 KiB chunk counts that fill groups of 2 / 4 / 8 whole chunks;
+    the tiled whole-group gather of 32 / 64 KiB chunks; and the row-by-row
+    kernel's cases: partial rows (128 B, 48 B), 1 KiB chunks, 4 KiB chunks
+    whose count is not a multiple of 8, more layers than one launch holds."""
     import ctypes
     from flexkv_amd import _lib
     from flexkv_amd.storage.allocator import pinned_empty
